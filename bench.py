@@ -1,0 +1,346 @@
+"""Benchmark: the 311M-parameter GPT training step (config 3) on one MI355X.
+
+Workload (the configuration the metric is quoted on):
+24 layers, hidden 1024, 16 heads (MHA, head_dim 64), SwiGLU ffn 2736, vocab 8192
+tied, bf16 parameters and activations with fp32 master weights and AdamW
+(lr 3e-4, betas (0.9, 0.95), eps 1e-8, weight decay 0.1, grad-norm clip 1.0),
+micro-batch 16 x seq 512 of uniform random tokens resident in HBM, full
+per-layer activation recompute.  One step = forward + backward + clip +
+optimizer update.  The same step without checkpointing gives the recompute
+overhead.
+
+Prints ONE JSON line.  ``value`` = tokens/s of the full-recompute step.
+``roofline`` is measured live with HIP events on the launch stream for each
+hand-written kernel at the config-3 shapes (``kernels``); the dominant one
+(largest time per training step) is ``roofline``.  ``cpu_baseline`` times the
+CPU oracle (the repo's PyTorch-CPU restatement) on a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+METRIC = "train tokens/s + peak act GB/layer, 311M seq512 recompute, 1 MI355X; HBM/MFMA %"
+
+C3 = dict(layers=24, hidden_size=1024, ffn_hidden_size=2736, heads=16, seq_length=512,
+          vocab_size=8192, norm_epsilon=1e-5, rope_theta=1e4)
+BATCH, SEQ = 16, 512
+
+
+def parse() -> argparse.Namespace:
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-kernels", action="store_true", help="skip the per-kernel roofline timing")
+    p.add_argument("--no-eager", action="store_true", help="skip the no-checkpoint comparison run")
+    p.add_argument("--only-kernels", action="store_true", help="time the kernels only (for profiling)")
+    return p.parse_args()
+
+
+class MasterAdamW:
+    """fp32-master AdamW over bf16 parameters (data_parallel/_zero.py:166-199 at DP=1)
+    with global grad-norm clipping (data_parallel/_zero.py:130-164)."""
+
+    def __init__(self, params, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, clip=1.0):
+        import torch
+
+        self.params = [p for p in params if p.requires_grad]
+        self.master = [p.detach().float().clone().requires_grad_(True) for p in self.params]
+        self.opt = torch.optim.AdamW(self.master, lr=lr, betas=betas, eps=eps,
+                                     weight_decay=weight_decay, fused=True)
+        self.clip = clip
+
+    def step(self) -> None:
+        import torch
+
+        for p, m in zip(self.params, self.master):
+            m.grad = p.grad.float()
+        torch.nn.utils.clip_grad_norm_(self.master, self.clip, foreach=True)
+        self.opt.step()
+        with torch.no_grad():
+            torch._foreach_copy_([p.data for p in self.params], [m.data for m in self.master])
+
+    def zero_grad(self) -> None:
+        for p in self.params:
+            p.grad = None
+        for m in self.master:
+            m.grad = None
+
+
+def run_steps(mode: str, steps: int, warmup: int, device) -> dict:
+    import torch
+
+    import nano_megatron_amd as nm
+
+    torch.manual_seed(1234)
+    cfg = nm.GPTConfig(**C3)
+    model = nm.GPTModel(cfg, activation_checkpoint_config=nm.ActivationCheckpointConfig(mode=mode))
+    model = model.to(device=device, dtype=torch.bfloat16).train()
+    opt = MasterAdamW(model.parameters())
+    g = torch.Generator(device=device).manual_seed(1234)
+    ids = torch.randint(0, cfg.vocab_size, (BATCH, SEQ + 1), device=device, generator=g)
+    x, y = ids[:, :SEQ].contiguous(), ids[:, 1:].contiguous()
+
+    def step():
+        opt.zero_grad()
+        loss = model(x, labels=y).loss
+        loss.backward()
+        opt.step()
+        return loss
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    # memory: activations = peak during a step minus what is resident at its start
+    torch.cuda.reset_peak_memory_stats()
+    start_alloc = torch.cuda.memory_allocated()
+    opt.zero_grad()
+    out = model(x, labels=y)
+    torch.cuda.synchronize()
+    saved_after_fwd = torch.cuda.memory_allocated() - start_alloc
+    out.loss.backward()
+    opt.step()
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated() - start_alloc
+    del out
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss = step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    result = dict(
+        ms_per_step=1e3 * elapsed / steps,
+        tokens_per_s=BATCH * SEQ * steps / elapsed,
+        loss=float(loss.item()),
+        peak_act_gib_per_layer=peak / cfg.layers / 2**30,
+        saved_act_mib_per_layer=saved_after_fwd / cfg.layers / 2**20,
+    )
+    del model, opt, x, y, ids
+    torch.cuda.empty_cache()
+    return result
+
+
+def kernel_rooflines(device) -> list[dict]:
+    """Average launch time (HIP events on the launch stream) of each hand-written
+    kernel at the config-3 shapes, with algorithmic bytes / FLOPs per launch."""
+    import torch
+
+    import nano_megatron_amd as nm
+    from nano_megatron_amd import functional as Fn
+
+    T, H, F, V = BATCH * SEQ, C3["hidden_size"], C3["ffn_hidden_size"], C3["vocab_size"]
+    nh, d = C3["heads"], C3["hidden_size"] // C3["heads"]
+    L = C3["layers"]
+    g = torch.Generator(device=device).manual_seed(1)
+    bf = torch.bfloat16
+
+    def randn(*shape, scale=1.0):
+        return (scale * torch.randn(*shape, device=device, generator=g)).to(bf)
+
+    x = randn(T, H)
+    w = (1 + randn(H, scale=0.02).float()).to(bf)
+    dy = randn(T, H)
+    qkv = randn(T, 3 * H)
+    q = qkv[:, :H].view(BATCH, SEQ, nh, d)
+    k = qkv[:, H:2 * H].view(BATCH, SEQ, nh, d)
+    v = qkv[:, 2 * H:].view(BATCH, SEQ, nh, d)
+    gu = randn(T, 2 * F)
+    gate, up = gu[:, :F], gu[:, F:]
+    dh = randn(T, F)
+    dgu = torch.empty_like(gu)
+    act = torch.empty(T, F, dtype=bf, device=device)
+    tab = nm.RotaryEmbedding(d).tables(device, SEQ)
+    o, lse = Fn.attn_fwd_bshd(q, [k], [v], (0,), causal=True, q_offset=0, scale=None)
+    do = randn(BATCH, SEQ, nh, d)
+    dqkv = torch.empty_like(qkv)
+    dq = dqkv[:, :H].view(BATCH, SEQ, nh, d)
+    dk = dqkv[:, H:2 * H].view(BATCH, SEQ, nh, d)
+    dv = dqkv[:, 2 * H:].view(BATCH, SEQ, nh, d)
+    chunk = 2048
+    logits = randn(chunk, V)
+    targets = torch.randint(0, V, (chunk,), device=device, generator=g)
+    loss = torch.empty(chunk, dtype=torch.float32, device=device)
+    lse_c = torch.empty_like(loss)
+    grad_c = torch.full((chunk,), 1.0 / T, device=device)
+    Fn.ce_fwd(logits, targets, -100, loss, lse_c)
+    rope_out = torch.empty_like(q)
+
+    causal_flops = 2 * 2 * BATCH * nh * SEQ * SEQ * d / 2
+    E = 2  # bytes per bf16 element
+    cases = [
+        # name, fn, algorithmic bytes, flops, bound, launches per training step (full recompute)
+        ("rmsnorm_fwd", lambda: Fn.rmsnorm_fwd(x, w, 1e-5), 2 * T * H * E + H * E, 0, "hbm", 4 * L + 1),
+        ("rmsnorm_bwd", lambda: Fn.rmsnorm_bwd(x, w, dy, 1e-5), 3 * T * H * E + 2 * H * E, 0, "hbm", 2 * L + 1),
+        ("rope_apply", lambda: Fn.rope_apply(q, rope_out, tab.cos, tab.sin), 2 * T * H * E, 0, "hbm", 6 * L),
+        ("swiglu_fwd", lambda: Fn.swiglu_fwd(gate, up, act), 3 * T * F * E, 0, "hbm", L),
+        ("swiglu_bwd", lambda: Fn.swiglu_bwd(gate, up, dh, dgu[:, :F], dgu[:, F:], act), 6 * T * F * E, 0, "hbm", L),
+        ("attn_fwd", lambda: Fn.attn_fwd_bshd(q, [k], [v], (0,), causal=True, q_offset=0, scale=None, out=o, lse=lse),
+         4 * T * H * E + BATCH * nh * SEQ * 4, causal_flops, "hbm", 2 * L),
+        ("attn_bwd", lambda: Fn.attn_bwd_bshd(q, [k], [v], (0,), o, do, lse, dq, [dk], [dv], causal=True, q_offset=0, scale=None),
+         8 * T * H * E + BATCH * nh * SEQ * 4, 2.5 * causal_flops, "hbm", L),
+        ("ce_fwd", lambda: Fn.ce_fwd(logits, targets, -100, loss, lse_c), chunk * V * E + chunk * 16, 0, "hbm", T // chunk),
+        ("ce_bwd", lambda: Fn.ce_bwd_(logits, targets, -100, lse_c, grad_c), 2 * chunk * V * E + chunk * 16, 0, "hbm", T // chunk),
+    ]
+    out = []
+    stream = torch.cuda.current_stream(device)
+    for name, fn, nbytes, flops, bound, per_step in cases:
+        for _ in range(3):
+            fn()
+        n = 50
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(n):
+            fn()
+        end.record(stream)
+        end.synchronize()
+        us = start.elapsed_time(end) * 1e3 / n
+        gbs = nbytes / us / 1e3
+        entry = dict(kernel=name, us=round(us, 2), bytes=int(nbytes), gbs=round(gbs, 1),
+                     hbm_frac=round(gbs / HBM_PEAK_GBS, 3), bound=bound,
+                     us_per_step=round(us * per_step, 1))
+        if flops:
+            tf = flops / us / 1e6
+            entry.update(flops=int(flops), tflops=round(tf, 1), mfma_frac=round(tf / BF16_PEAK_TFLOPS, 4))
+        out.append(entry)
+    return out
+
+
+def cpu_baseline() -> dict:
+    """The CPU oracle on a bounded sample of the config-3 step: 2 of the 24 layers
+    plus embedding/final norm/LM head/CE, one 512-token sequence, full recompute,
+    fp32 on the host cores; scaled to tokens/s of the 24-layer step."""
+    import torch
+
+    from oracle import reference as R
+
+    threads = torch.get_num_threads()
+
+    class Ck:
+        mode = "full"
+        block_interval = 1
+
+    def time_layers(n_layers: int, reps: int) -> float:
+        cfg = dict(C3, layers=n_layers)
+
+        class Cfg:
+            pass
+
+        for k_, v_ in cfg.items():
+            setattr(Cfg, k_, v_)
+        torch.manual_seed(0)
+        model = R.OracleGPTModel(Cfg(), activation_checkpoint_config=Ck()).train()
+        ids = torch.randint(0, C3["vocab_size"], (1, SEQ + 1))
+        x, y = ids[:, :SEQ], ids[:, 1:]
+        model(x, labels=y).loss.backward()  # warm-up
+        ts = []
+        for _ in range(reps):
+            model.zero_grad(set_to_none=True)
+            t0 = time.perf_counter()
+            model(x, labels=y).loss.backward()
+            ts.append(time.perf_counter() - t0)
+        ts.sort()
+        return ts[len(ts) // 2]
+
+    t1 = time_layers(1, 3)
+    t2 = time_layers(2, 3)
+    per_layer = max(t2 - t1, 1e-9)
+    base = max(t1 - per_layer, 0.0)
+    t_step = base + C3["layers"] * per_layer
+    return dict(
+        value=round(SEQ / t_step, 1),
+        unit="tokens/s",
+        cores=threads,
+        kind="port",
+        sample=(f"CPU oracle (PyTorch fp32, {threads} threads), one 512-token sequence, 1- and "
+                f"2-layer models with full recompute; per-layer time {per_layer:.3f} s "
+                f"extrapolated to 24 layers + head ({t_step:.2f} s per 512 tokens)"),
+    )
+
+
+def main() -> None:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(this build has no collectives)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X (no HIP device visible)", file=sys.stderr)
+        sys.exit(2)
+    device = torch.device("cuda", 0)
+    import nano_megatron_amd  # noqa: F401  (fails loudly without libnmb.so)
+    from nano_megatron_amd import _lib
+
+    _lib.load()
+
+    kernels = None
+    if not args.no_kernels:
+        kernels = kernel_rooflines(device)
+        print("kernels: " + json.dumps(kernels), file=sys.stderr, flush=True)
+    if args.only_kernels:
+        return
+    full = run_steps("full", args.steps, args.warmup, device)
+    print("full: " + json.dumps(full), file=sys.stderr, flush=True)
+    eager = None
+    if not args.no_eager:
+        eager = run_steps("none", args.steps, args.warmup, device)
+        print("none: " + json.dumps(eager), file=sys.stderr, flush=True)
+
+    roofline = None
+    if kernels:
+        dom = max(kernels, key=lambda k: k["us_per_step"])
+        roofline = dict(bound="hbm", achieved=dom["gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
+                        frac=dom["hbm_frac"], traffic=None, kernel=dom["kernel"])
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline()
+    line = dict(
+        metric=METRIC,
+        value=round(full["tokens_per_s"], 1),
+        unit="tokens/s",
+        n_gpus=1,
+        steps=args.steps,
+        warmup=args.warmup,
+        ms_per_step=round(full["ms_per_step"], 3),
+        higher_is_better=True,
+        scaling="weak",
+        vs_baseline=None,
+        dtype="bf16",
+        data="synthetic",
+        config=dict(
+            workload="C3: 310.8M GPT (24L, H1024, 16 heads MHA D64, ffn 2736, vocab 8192 tied) "
+                     "training step, full per-layer recompute, bf16 + fp32-master AdamW",
+            global_batch=BATCH, seq_len=SEQ, parallelism="single GPU",
+        ),
+        peak_act_gib_per_layer=round(full["peak_act_gib_per_layer"], 4),
+        saved_act_mib_per_layer=round(full["saved_act_mib_per_layer"], 2),
+        act_floor_mib_per_layer=16.5,
+        loss=round(full["loss"], 4),
+        roofline=roofline,
+        cpu_baseline=cpu,
+        kernels=kernels,
+    )
+    if eager:
+        line["no_checkpoint_tokens_per_s"] = round(eager["tokens_per_s"], 1)
+        line["no_checkpoint_saved_act_mib_per_layer"] = round(eager["saved_act_mib_per_layer"], 2)
+        line["recompute_overhead"] = round(full["ms_per_step"] / eager["ms_per_step"] - 1.0, 4)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,157 @@
+/*
+ * nmb.h -- C ABI of libnmb.so, the MI355X (gfx950) kernels behind the
+ * activation-checkpointed GPT block of pyy233/Nano-Megatron.
+ *
+ * Every entry point:
+ *   - takes raw device pointers owned by the caller, plain sizes and strides
+ *     (in elements), a dtype code and the caller's hipStream_t;
+ *   - enqueues work on that stream and returns without synchronising;
+ *   - returns NMB_OK or an error status, never throws, and records a message
+ *     readable with nmb_last_error() on the same thread;
+ *   - allocates no device memory: scratch comes in as a caller workspace.
+ * All functions are reentrant; the PyTorch autograd device thread calls the
+ * backward entry points while the main thread may call forward ones.
+ *
+ * The "replaces" notes cite the reference interface, as file:line under
+ * pyy233/Nano-Megatron src/nano_megatron/.
+ */
+#ifndef NMB_H
+#define NMB_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes; the Python host maps EINVAL/EUNSUPPORTED to ValueError and
+ * EHIP to RuntimeError, as the reference raises ValueError on contract
+ * violations (nn/kernels/torch_backend.py:45-55, nn/norms.py:34-37). */
+#define NMB_OK 0
+#define NMB_EINVAL 1
+#define NMB_EUNSUPPORTED 2
+#define NMB_EHIP 3
+
+/* dtype codes: the path computes in fp32 (config 1) or bf16 storage with fp32
+ * arithmetic (configs 2-5). */
+#define NMB_F32 0
+#define NMB_BF16 1
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* nmb_last_error(void);
+
+/* ABI version; bumped on any signature change. */
+int nmb_abi_version(void);
+
+/* ------------------------------------------------------------ RMSNorm
+ * replaces RMSNorm.forward (nn/norms.py:33-41) and its autograd backward;
+ * seam: KernelBackend.rms_norm (nn/kernels/interface.py:20-21,
+ * nn/kernels/torch_backend.py:22-23).
+ * x, y: [rows, cols] contiguous; w: [cols]; rstd (nullable): [rows] fp32.
+ * y = cast(x * rsqrt(mean(x^2) + eps)) * w with fp32 statistics. */
+int nmb_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd, int64_t rows,
+                    int64_t cols, float eps, int dtype, hipStream_t stream);
+
+/* Bytes of workspace nmb_rmsnorm_bwd needs for this shape. */
+int nmb_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols, size_t* bytes);
+
+/* dx = rstd * (g - n * mean(g * n)) with g = dy * w, n = x * rstd (rstd
+ * recomputed from x), plus residual_grad if non-null; dw = sum_rows(dy * n)
+ * reduced deterministically through the workspace. */
+int nmb_rmsnorm_bwd(const void* x, const void* w, const void* dy, const void* residual_grad,
+                    void* dx, void* dw, void* workspace, size_t workspace_bytes, int64_t rows,
+                    int64_t cols, float eps, int dtype, hipStream_t stream);
+
+/* ------------------------------------------------------------ RoPE
+ * replaces RotaryEmbedding.forward + apply_rotary_pos_emb
+ * (nn/rotary.py:27-38, 55-70) as called at models/gpt/attention.py:180-181.
+ * nmb_rope_table fills cos/sin [n_pos, half] fp32 with cos(p * inv_freq[i]).
+ * nmb_rope_apply rotates x [batch, seq, heads, 2*half] (strides in elements
+ * for b, s, h; the last dim contiguous) into out (same strides; may alias x):
+ *   out = x * cos + rotate_half(x) * sin        (inverse = 0)
+ *   out = x * cos - rotate_half(x) * sin        (inverse = 1, the backward)
+ * position of (b, s) = positions[b * pos_batch_stride + s] if positions is
+ * non-null, else pos_offset + s. */
+int nmb_rope_table(float* cos_table, float* sin_table, const float* inv_freq, int64_t n_pos,
+                   int64_t half, hipStream_t stream);
+
+int nmb_rope_apply(const void* x, void* out, const float* cos_table, const float* sin_table,
+                   int64_t n_pos, const int32_t* positions, int64_t pos_batch_stride,
+                   int64_t pos_offset, int64_t batch, int64_t seq, int64_t heads,
+                   int64_t head_dim, const int64_t* x_strides, const int64_t* out_strides,
+                   int inverse, int dtype, hipStream_t stream);
+
+/* ------------------------------------------------------------ SwiGLU
+ * replaces F.silu(gate) * up (models/gpt/mlp.py:77).
+ * All operands are [rows, cols] with a row stride (elements). */
+int nmb_swiglu_fwd(const void* gate, int64_t gate_ld, const void* up, int64_t up_ld, void* out,
+                   int64_t out_ld, int64_t rows, int64_t cols, int dtype, hipStream_t stream);
+
+/* Fused recompute-backward: from gate, up and d_out produce d_gate, d_up and
+ * (if out is non-null) the recomputed out = silu(gate) * up that the
+ * down-projection weight gradient needs. */
+int nmb_swiglu_bwd(const void* gate, int64_t gate_ld, const void* up, int64_t up_ld,
+                   const void* dout, int64_t dout_ld, void* dgate, int64_t dgate_ld, void* dup,
+                   int64_t dup_ld, void* out, int64_t out_ld, int64_t rows, int64_t cols,
+                   int dtype, hipStream_t stream);
+
+/* ------------------------------------------------------------ attention
+ * replaces TorchKernelBackend.local_attention (nn/kernels/torch_backend.py:
+ * 25-76; seam nn/kernels/interface.py:22-25) and the ring maths of
+ * _ring_forward/_ring_backward (context_parallel/ring.py:104-250).
+ *
+ * q: [batch, seq_q, q_heads, head_dim]; each of the n_blocks K/V blocks:
+ * [batch, seq_k, kv_heads, head_dim]; o like q.  Strides are arrays of 3
+ * int64 (batch, seq, head) in elements; head_dim is contiguous.  K and V (and
+ * dK, dV) share kv_strides; dq shares q_strides; dO shares o_strides.
+ * Query i has absolute position q_offset + i; key j of block b has position
+ * k_offsets[b] + j.  With causal != 0 a key is visible iff its position is
+ * <= the query's.  Query head h reads KV head h / (q_heads / kv_heads) (GQA
+ * without materialised repeats).  The blocks are one concatenated key
+ * sequence for the online softmax.  lse: [batch, q_heads, seq_q] fp32,
+ * natural log; a query with no visible key gets o = 0 and lse = -inf.
+ * scale <= 0 selects 1/sqrt(head_dim). */
+int nmb_attn_fwd(const void* q, const void* const* k_blocks, const void* const* v_blocks,
+                 const int64_t* k_offsets, int n_blocks, void* o, float* lse, int64_t batch,
+                 int64_t q_heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k,
+                 int64_t head_dim, const int64_t* q_strides, const int64_t* kv_strides,
+                 const int64_t* o_strides, int causal, int64_t q_offset, float scale, int dtype,
+                 hipStream_t stream);
+
+/* Bytes of workspace nmb_attn_bwd needs (the fp32 delta = rowsum(dO * O)). */
+int nmb_attn_bwd_workspace_bytes(int64_t batch, int64_t q_heads, int64_t seq_q, size_t* bytes);
+
+/* Backward from the saved lse: dq (overwritten), and per block dk, dv
+ * (overwritten).  Deterministic: no atomics. */
+int nmb_attn_bwd(const void* q, const void* const* k_blocks, const void* const* v_blocks,
+                 const int64_t* k_offsets, int n_blocks, const void* o, const void* dout,
+                 const float* lse, void* dq, void* const* dk_blocks, void* const* dv_blocks,
+                 void* workspace, size_t workspace_bytes, int64_t batch, int64_t q_heads,
+                 int64_t kv_heads, int64_t seq_q, int64_t seq_k, int64_t head_dim,
+                 const int64_t* q_strides, const int64_t* kv_strides, const int64_t* o_strides,
+                 int causal, int64_t q_offset, float scale, int dtype, hipStream_t stream);
+
+/* ------------------------------------------------------------ cross entropy
+ * replaces _VocabParallelCrossEntropy.forward/backward at TP=1
+ * (tensor_parallel/cross_entropy.py:30-86) applied to one chunk of tied
+ * LM-head logits (tensor_parallel/layers.py:207-214).
+ * logits: [rows, vocab] with row stride ld; targets: int64 [rows].
+ * Forward: loss[r] = lse[r] - z[r, t_r] (0 if t_r == ignore_index), lse in
+ * fp32 over fp32-converted logits. */
+int nmb_ce_fwd(const void* logits, int64_t ld, const int64_t* targets, int64_t rows,
+               int64_t vocab, int64_t ignore_index, float* loss, float* lse, int dtype,
+               hipStream_t stream);
+
+/* Backward in place: logits[r, j] <- (exp(z - lse[r]) - [j == t_r]) * grad[r],
+ * rows with an ignored target become 0. grad: fp32 [rows]. */
+int nmb_ce_bwd(void* logits, int64_t ld, const int64_t* targets, int64_t rows, int64_t vocab,
+               int64_t ignore_index, const float* lse, const float* grad, int dtype,
+               hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NMB_H */

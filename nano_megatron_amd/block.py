@@ -1,0 +1,175 @@
+"""The GPT transformer block as two autograd Functions: checkpointed and eager.
+
+Both run the same device sequence (reference GPTLayer.forward,
+models/gpt/layer.py:91-137):
+
+    n1 = RMSNorm(x)                          nmb_rmsnorm_fwd
+    [q|k|v] = n1 [Wq;Wk;Wv]^T                one GEMM (hipBLASLt)
+    q, k = RoPE(q, k)                        nmb_rope_apply, in place
+    o, lse = attention(q, k, v)              nmb_attn_fwd (MFMA, online softmax)
+    h = x + o Wo^T                           GEMM with the residual as C input
+    n2 = RMSNorm(h)                          nmb_rmsnorm_fwd
+    [g|u] = n2 [Wg;Wu]^T                     one GEMM
+    s = silu(g) * u                          nmb_swiglu_fwd
+    y = h + s Wd^T                           GEMM with the residual as C input
+
+``CheckpointedBlockFunction`` is the full-recompute policy of
+``activation_checkpoint`` (nn/activation_checkpoint.py:73-100, selected by
+models/gpt/model.py:162-170, 215-233): it saves only the block input x and
+the attention lse.  Its backward re-runs the sequence above up to [g|u] with
+the same kernels and shapes (so the recomputed tensors are bit-identical to
+the forward's) and never re-runs the down projection, whose output the
+backward does not need; ``nmb_swiglu_bwd`` re-emits s for the Wd gradient.
+``EagerBlockFunction`` (activation_checkpoint.mode = "none") keeps the
+intermediates instead and shares the backward.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+from torch import Tensor
+
+from nano_megatron_amd import functional as Fn
+
+
+@dataclass(frozen=True)
+class BlockMeta:
+    heads: int
+    kv_heads: int
+    head_dim: int
+    eps: float
+    sequence_offset: int
+    cos: Tensor          # fp32 [n_pos, head_dim/2]
+    sin: Tensor
+    positions: Tensor | None  # int32 [S] or [B,S], or None for offset + arange
+
+
+def _qkv_views(qkv: Tensor, b: int, s: int, m: BlockMeta) -> tuple[Tensor, Tensor, Tensor]:
+    """[B*S, (Hq+2Hkv)*D] -> q [B,S,Hq,D], k, v [B,S,Hkv,D] strided views."""
+    qd = m.heads * m.head_dim
+    kd = m.kv_heads * m.head_dim
+    t = qkv.view(b, s, qkv.shape[-1])
+    q = t[:, :, :qd].unflatten(2, (m.heads, m.head_dim))
+    k = t[:, :, qd : qd + kd].unflatten(2, (m.kv_heads, m.head_dim))
+    v = t[:, :, qd + kd :].unflatten(2, (m.kv_heads, m.head_dim))
+    return q, k, v
+
+
+def block_forward(x: Tensor, w: tuple[Tensor, ...], m: BlockMeta, *, recompute: bool) -> dict:
+    """Run the block on x [B,S,H].  With recompute=True stop after [g|u] (no s, no y)."""
+    w_in, wq, wk, wv, wo, w_post, wg, wu, wd = w
+    b, s, hdim = x.shape
+    x2 = x.reshape(b * s, hdim)
+    n1 = Fn.rmsnorm_fwd(x2, w_in, m.eps)
+    qkv = torch.mm(n1, torch.cat((wq, wk, wv)).t())
+    q, k, v = _qkv_views(qkv, b, s, m)
+    Fn.rope_apply(q, q, m.cos, m.sin, pos_offset=m.sequence_offset, positions=m.positions)
+    Fn.rope_apply(k, k, m.cos, m.sin, pos_offset=m.sequence_offset, positions=m.positions)
+    o, lse = Fn.attn_fwd_bshd(q, [k], [v], (0,), causal=True, q_offset=m.sequence_offset, scale=None)
+    o2 = o.view(b * s, m.heads * m.head_dim)
+    h = torch.addmm(x2, o2, wo.t())
+    n2 = Fn.rmsnorm_fwd(h, w_post, m.eps)
+    gu = torch.mm(n2, torch.cat((wg, wu)).t())
+    acts = dict(x2=x2, n1=n1, qkv=qkv, o2=o2, lse=lse, h=h, n2=n2, gu=gu)
+    if recompute:
+        return acts
+    f = wg.shape[0]
+    act = Fn.swiglu_fwd(gu[:, :f], gu[:, f:])
+    acts["s"] = act
+    acts["y"] = torch.addmm(h, act, wd.t()).view(b, s, hdim)
+    return acts
+
+
+def block_backward(acts: dict, dy: Tensor, w: tuple[Tensor, ...], m: BlockMeta, shape) -> tuple:
+    """Gradients (dx, dw_in, dWq, dWk, dWv, dWo, dw_post, dWg, dWu, dWd) of the block."""
+    w_in, wq, wk, wv, wo, w_post, wg, wu, wd = w
+    b, s, hdim = shape
+    f = wg.shape[0]
+    dy2 = dy.reshape(b * s, hdim)
+    if not dy2.is_contiguous():
+        dy2 = dy2.contiguous()
+    x2, n1, qkv, o2, lse, h, n2, gu = (acts[k] for k in ("x2", "n1", "qkv", "o2", "lse", "h", "n2", "gu"))
+
+    # MLP: y = h + s Wd^T, s = silu(g) * u, [g|u] = n2 [Wg;Wu]^T
+    ds = torch.mm(dy2, wd)
+    dgu = torch.empty_like(gu)
+    act = torch.empty(b * s, f, dtype=gu.dtype, device=gu.device)
+    Fn.swiglu_bwd(gu[:, :f], gu[:, f:], ds, dgu[:, :f], dgu[:, f:], act)
+    dwd = torch.mm(dy2.t(), act)
+    dn2 = torch.mm(dgu, torch.cat((wg, wu)))
+    dwgu = torch.mm(dgu.t(), n2)
+    dh, dw_post = Fn.rmsnorm_bwd(h, w_post, dn2, m.eps, residual_grad=dy2)
+
+    # attention: h = x + o Wo^T
+    do2 = torch.mm(dh, wo)
+    dwo = torch.mm(dh.t(), o2)
+    q, k, v = _qkv_views(qkv, b, s, m)
+    dqkv = torch.empty_like(qkv)
+    dq, dk, dv = _qkv_views(dqkv, b, s, m)
+    o4 = o2.view(b, s, m.heads, m.head_dim)
+    do4 = do2.view(b, s, m.heads, m.head_dim)
+    Fn.attn_bwd_bshd(q, [k], [v], (0,), o4, do4, lse, dq, [dk], [dv],
+                     causal=True, q_offset=m.sequence_offset, scale=None)
+    Fn.rope_apply(dq, dq, m.cos, m.sin, pos_offset=m.sequence_offset, positions=m.positions, inverse=True)
+    Fn.rope_apply(dk, dk, m.cos, m.sin, pos_offset=m.sequence_offset, positions=m.positions, inverse=True)
+    dn1 = torch.mm(dqkv, torch.cat((wq, wk, wv)))
+    dwqkv = torch.mm(dqkv.t(), n1)
+    dx, dw_in = Fn.rmsnorm_bwd(x2, w_in, dn1, m.eps, residual_grad=dh)
+
+    qd = m.heads * m.head_dim
+    kd = m.kv_heads * m.head_dim
+    return (
+        dx.view(b, s, hdim), dw_in,
+        dwqkv[:qd], dwqkv[qd : qd + kd], dwqkv[qd + kd :],
+        dwo, dw_post, dwgu[:f], dwgu[f:], dwd,
+    )
+
+
+class CheckpointedBlockFunction(torch.autograd.Function):
+    """Full per-layer recompute: saves x (the block input) and the lse only."""
+
+    @staticmethod
+    def forward(ctx: Any, x: Tensor, meta: BlockMeta, *weights: Tensor) -> Tensor:
+        with torch.no_grad():
+            acts = block_forward(x.contiguous(), weights, meta, recompute=False)
+        ctx.meta = meta
+        ctx.shape = tuple(x.shape)
+        ctx.save_for_backward(x, acts["lse"], *weights)
+        return acts["y"]
+
+    @staticmethod
+    def backward(ctx: Any, dy: Tensor):
+        x, lse, *weights = ctx.saved_tensors
+        with torch.no_grad():
+            acts = block_forward(x.contiguous(), tuple(weights), ctx.meta, recompute=True)
+            acts["lse"] = lse
+            grads = block_backward(acts, dy, tuple(weights), ctx.meta, ctx.shape)
+        return (grads[0], None, *grads[1:])
+
+
+class EagerBlockFunction(torch.autograd.Function):
+    """No checkpoint: keeps every intermediate the backward reads."""
+
+    @staticmethod
+    def forward(ctx: Any, x: Tensor, meta: BlockMeta, *weights: Tensor) -> Tensor:
+        with torch.no_grad():
+            acts = block_forward(x.contiguous(), weights, meta, recompute=False)
+        ctx.meta = meta
+        ctx.shape = tuple(x.shape)
+        keys = ("x2", "n1", "qkv", "o2", "lse", "h", "n2", "gu")
+        ctx.keys = keys
+        ctx.save_for_backward(*(acts[k] for k in keys), *weights)
+        return acts["y"]
+
+    @staticmethod
+    def backward(ctx: Any, dy: Tensor):
+        saved = ctx.saved_tensors
+        n = len(ctx.keys)
+        acts = dict(zip(ctx.keys, saved[:n]))
+        weights = tuple(saved[n:])
+        with torch.no_grad():
+            grads = block_backward(acts, dy, weights, ctx.meta, ctx.shape)
+        return (grads[0], None, *grads[1:])

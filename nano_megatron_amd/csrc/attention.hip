@@ -1,0 +1,921 @@
+// Causal / non-causal MHA-GQA attention forward and backward for gfx950.
+//
+// Follows TorchKernelBackend.local_attention (reference
+// nn/kernels/torch_backend.py:25-76: softmax(Q K^T * scale + mask) V with the
+// mask key_pos <= sequence_offset + query_pos) and the ring maths of
+// context_parallel/ring.py:104-250 (online max/sum merge over K/V blocks with
+// absolute-position causal masks, lse = m + log l; backward
+// delta = rowsum(dO * O), P = exp(S - lse), dS = P (dP - delta)).
+//
+// bf16 path (head_dim 64 or 128): v_mfma_f32_16x16x32_bf16, fp32 accumulate.
+//   Forward and dQ kernels compute S^T = K Q^T so that every lane holds the
+//   scores of ONE query (lane % 16) for 16 keys: the softmax statistics are
+//   per-lane scalars, the O^T / dQ^T accumulators are rescaled per lane, and the
+//   probabilities feed the next MFMA as its B operand straight from registers
+//   (the 32-deep K index of that MFMA is a fixed permutation of keys that the
+//   A operand, read from a transposed LDS tile, follows as well).
+//   The dK/dV kernel uses S = Q K^T the same way with the roles of queries and
+//   keys exchanged.  K/V (or Q/dO) tiles are staged through LDS, once per
+//   workgroup; transposed copies are written as packed 32-bit key pairs.
+//   GQA reads KV head h / (Hq / Hkv) directly; the dK/dV workgroup of a KV
+//   head loops over its query heads, so no repeat is materialised and no
+//   atomics are used (deterministic).
+// fp32 path: one wavefront per query (or key) row, fp32 FMA, for the fp32
+//   parity configuration.
+#include <math.h>
+
+#include "common.h"
+
+namespace nmb {
+namespace {
+
+constexpr int kMaxBlocks = 8;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+struct KVBlocks {
+  const void* k[kMaxBlocks];
+  const void* v[kMaxBlocks];
+  void* dk[kMaxBlocks];
+  void* dv[kMaxBlocks];
+  int64_t koff[kMaxBlocks];
+};
+
+struct AttnShape {
+  int B, Hq, Hkv, Sq, Sk, nblk, causal;
+  int64_t q_sb, q_ss, q_sh;
+  int64_t kv_sb, kv_ss, kv_sh;
+  int64_t o_sb, o_ss, o_sh;
+  int64_t q_offset;
+  float scale;       // softmax scale
+  float scale_log2;  // scale * log2(e)
+};
+
+__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 zero8() {
+  bf16x8 z;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) z[i] = static_cast<bf16>(0.f);
+  return z;
+}
+
+__device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
+
+// Two 4-element halves at p and p + 16 (the key permutation of a 32-deep MFMA
+// K index: lane group g holds keys 4g..4g+3 and 16+4g..16+4g+3).
+__device__ __forceinline__ bf16x8 ld4x2(const bf16* p) {
+  const bf16x4 lo = *reinterpret_cast<const bf16x4*>(p);
+  const bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + 16);
+  bf16x8 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    r[i] = lo[i];
+    r[4 + i] = hi[i];
+  }
+  return r;
+}
+
+// Stage rows [r0, r0 + R) x D of a strided bf16 matrix into LDS, row-major with
+// row stride LD; rows at or beyond nrows are zero.
+template <int R, int D, int LD>
+__device__ __forceinline__ void stage_rows(bf16* __restrict__ dst, const bf16* __restrict__ src,
+                                           int64_t row_stride, int r0, int nrows) {
+  for (int c = threadIdx.x; c < R * D / 8; c += 256) {
+    const int r = c / (D / 8), dc = c % (D / 8);
+    bf16x8 val = zero8();
+    if (r0 + r < nrows) val = ld8(src + static_cast<int64_t>(r0 + r) * row_stride + dc * 8);
+    *reinterpret_cast<bf16x8*>(dst + r * LD + dc * 8) = val;
+  }
+}
+
+// Stage the transpose: dst[d][r] (row stride LD) for rows [r0, r0 + R).  Each
+// thread moves a pair of rows so that LDS writes are 32-bit words.
+template <int R, int D, int LD>
+__device__ __forceinline__ void stage_rows_t(bf16* __restrict__ dst, const bf16* __restrict__ src,
+                                             int64_t row_stride, int r0, int nrows) {
+  for (int c = threadIdx.x; c < (R / 2) * (D / 8); c += 256) {
+    const int rp = c % (R / 2), dc = c / (R / 2);
+    const int ra = r0 + 2 * rp;
+    bf16x8 v0 = zero8(), v1 = zero8();
+    if (ra < nrows) v0 = ld8(src + static_cast<int64_t>(ra) * row_stride + dc * 8);
+    if (ra + 1 < nrows) v1 = ld8(src + static_cast<int64_t>(ra + 1) * row_stride + dc * 8);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      bf16 pr[2] = {v0[i], v1[i]};
+      uint32_t w;
+      __builtin_memcpy(&w, pr, 4);
+      *reinterpret_cast<uint32_t*>(dst + (dc * 8 + i) * LD + 2 * rp) = w;
+    }
+  }
+}
+
+// Number of 64-key tiles of a block that any query up to absolute position
+// q_last can see.
+__device__ __forceinline__ int visible_key_tiles(const AttnShape& p, int64_t koff, int64_t q_last) {
+  int n = (p.Sk + 63) / 64;
+  if (p.causal) {
+    const int64_t lim = q_last - koff;
+    if (lim < 0) return 0;
+    const int64_t t = lim / 64 + 1;
+    if (t < n) n = static_cast<int>(t);
+  }
+  return n;
+}
+
+// ---------------------------------------------------------------- forward
+template <int D>
+__global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16* __restrict__ q, KVBlocks kv,
+                                                       bf16* __restrict__ o,
+                                                       float* __restrict__ lse, AttnShape p) {
+  constexpr int BQ = 128, BK = 64, KS = D / 32, DT = D / 16;
+  constexpr int LDK = D + 8, LDV = BK + 8;
+  __shared__ __attribute__((aligned(16))) bf16 sK[BK * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sVt[D * LDV];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int n_qt = (p.Sq + BQ - 1) / BQ;
+  const int qt = n_qt - 1 - static_cast<int>(blockIdx.x);  // heavy causal tiles first
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int hk = h / (p.Hq / p.Hkv);
+  const int q0 = qt * BQ + wave * 32;
+
+  const bf16* qb = q + b * p.q_sb + h * p.q_sh;
+  bf16x8 qf[2][KS];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int qi = q0 + 16 * t + l16;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qf[t][ks] = qi < p.Sq ? ld8(qb + static_cast<int64_t>(qi) * p.q_ss + ks * 32 + g * 8) : zero8();
+  }
+  float m[2] = {-__builtin_inff(), -__builtin_inff()};
+  float l[2] = {0.f, 0.f};
+  f32x4 acc[2][DT];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int64_t qa_wave_first = p.q_offset + q0;
+  const int64_t qa_wave_last = p.q_offset + min(q0 + 31, p.Sq - 1);
+  const int64_t qa_wg_last = p.q_offset + min(qt * BQ + BQ - 1, p.Sq - 1);
+
+  for (int blk = 0; blk < p.nblk; ++blk) {
+    const bf16* kb = static_cast<const bf16*>(kv.k[blk]) + b * p.kv_sb + hk * p.kv_sh;
+    const bf16* vb = static_cast<const bf16*>(kv.v[blk]) + b * p.kv_sb + hk * p.kv_sh;
+    const int64_t koff = kv.koff[blk];
+    const int n_kt = visible_key_tiles(p, koff, qa_wg_last);
+    for (int kt = 0; kt < n_kt; ++kt) {
+      const int k0 = kt * BK;
+      __syncthreads();
+      stage_rows<BK, D, LDK>(sK, kb, p.kv_ss, k0, p.Sk);
+      stage_rows_t<BK, D, LDV>(sVt, vb, p.kv_ss, k0, p.Sk);
+      __syncthreads();
+      if (p.causal && koff + k0 > qa_wave_last) continue;  // wave-uniform: nothing visible
+      const bool need_mask =
+          (k0 + BK > p.Sk) || (p.causal && koff + k0 + BK - 1 > qa_wave_first);
+
+      f32x4 s[4][2];
+#pragma unroll
+      for (int mk = 0; mk < 4; ++mk) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) s[mk][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const bf16x8 a = ld8(sK + (mk * 16 + l16) * LDK + ks * 32 + g * 8);
+#pragma unroll
+          for (int t = 0; t < 2; ++t) s[mk][t] = mfma16(a, qf[t][ks], s[mk][t]);
+        }
+      }
+      bf16x8 pf[2][2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int64_t qa = p.q_offset + q0 + 16 * t + l16;
+        float tmax = -__builtin_inff();
+#pragma unroll
+        for (int mk = 0; mk < 4; ++mk)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float val = s[mk][t][e] * p.scale_log2;
+            if (need_mask) {
+              const int kl = k0 + mk * 16 + g * 4 + e;
+              if (kl >= p.Sk || (p.causal && koff + kl > qa)) val = -__builtin_inff();
+            }
+            s[mk][t][e] = val;
+            tmax = fmaxf(tmax, val);
+          }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float mnew = fmaxf(m[t], tmax);
+        const bool dead = mnew == -__builtin_inff();
+        const float alpha = dead ? 1.f : exp2f(m[t] - mnew);
+        const float msub = dead ? 0.f : mnew;
+        float rs = 0.f;
+#pragma unroll
+        for (int mk = 0; mk < 4; ++mk)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float pv = exp2f(s[mk][t][e] - msub);
+            s[mk][t][e] = pv;
+            rs += pv;
+          }
+        rs += __shfl_xor(rs, 16, 64);
+        rs += __shfl_xor(rs, 32, 64);
+        l[t] = l[t] * alpha + rs;
+        m[t] = mnew;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[t][dt] *= alpha;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            pf[s2][t][e] = static_cast<bf16>(s[2 * s2][t][e]);
+            pf[s2][t][4 + e] = static_cast<bf16>(s[2 * s2 + 1][t][e]);
+          }
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const bf16x8 a = ld4x2(sVt + (dt * 16 + l16) * LDV + 32 * s2 + g * 4);
+#pragma unroll
+          for (int t = 0; t < 2; ++t) acc[t][dt] = mfma16(a, pf[s2][t], acc[t][dt]);
+        }
+      }
+    }
+  }
+  bf16* ob = o + b * p.o_sb + h * p.o_sh;
+  float* lb = lse + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int qi = q0 + 16 * t + l16;
+    if (qi >= p.Sq) continue;
+    const float inv = l[t] > 0.f ? 1.f / l[t] : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      bf16x4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] = static_cast<bf16>(acc[t][dt][e] * inv);
+      *reinterpret_cast<bf16x4*>(ob + static_cast<int64_t>(qi) * p.o_ss + dt * 16 + g * 4) = w;
+    }
+    if (g == 0) lb[qi] = l[t] > 0.f ? (m[t] + log2f(l[t])) * kLn2 : -__builtin_inff();
+  }
+}
+
+// ---------------------------------------------------------------- delta
+// delta[b, h, i] = sum_d dO[b, i, h, d] * O[b, i, h, d] (fp32).
+template <typename T>
+__global__ __launch_bounds__(256) void attn_delta_kernel(const T* __restrict__ o,
+                                                         const T* __restrict__ dout,
+                                                         float* __restrict__ delta, AttnShape p,
+                                                         int D) {
+  const int64_t rows = static_cast<int64_t>(p.B) * p.Sq * p.Hq;
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; r < rows;
+       r += static_cast<int64_t>(gridDim.x) * 256) {
+    const int h = static_cast<int>(r % p.Hq);
+    const int64_t bi = r / p.Hq;
+    const int i = static_cast<int>(bi % p.Sq);
+    const int b = static_cast<int>(bi / p.Sq);
+    const int64_t off = b * p.o_sb + static_cast<int64_t>(i) * p.o_ss + h * p.o_sh;
+    float s = 0.f;
+    for (int d = 0; d < D; ++d) s += to_f32(o[off + d]) * to_f32(dout[off + d]);
+    delta[(static_cast<int64_t>(b) * p.Hq + h) * p.Sq + i] = s;
+  }
+}
+
+// log2-domain lse for P = exp2(S * scale_log2 - lse2); a query with no visible
+// key (lse = -inf) maps to +inf so that every P of its row is 0.
+__device__ __forceinline__ float lse_to_log2(float v) {
+  return v == -__builtin_inff() ? __builtin_inff() : v * kLog2e;
+}
+
+// ---------------------------------------------------------------- dQ
+template <int D>
+__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const bf16* __restrict__ q, KVBlocks kv,
+                                                          const bf16* __restrict__ dout,
+                                                          const float* __restrict__ lse,
+                                                          const float* __restrict__ delta,
+                                                          bf16* __restrict__ dq, AttnShape p) {
+  constexpr int BQ = 128, BK = 64, KS = D / 32, DT = D / 16;
+  constexpr int LDK = D + 8, LDT = BK + 8;
+  __shared__ __attribute__((aligned(16))) bf16 sK[BK * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sKt[D * LDT];
+  __shared__ __attribute__((aligned(16))) bf16 sV[BK * LDK];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int n_qt = (p.Sq + BQ - 1) / BQ;
+  const int qt = n_qt - 1 - static_cast<int>(blockIdx.x);
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int hk = h / (p.Hq / p.Hkv);
+  const int q0 = qt * BQ + wave * 32;
+
+  const bf16* qb = q + b * p.q_sb + h * p.q_sh;
+  const bf16* db = dout + b * p.o_sb + h * p.o_sh;
+  const float* lb = lse + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
+  const float* deb = delta + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
+  bf16x8 qf[2][KS], df[2][KS];
+  float lse2[2], dl[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int qi = q0 + 16 * t + l16;
+    const bool ok = qi < p.Sq;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qf[t][ks] = ok ? ld8(qb + static_cast<int64_t>(qi) * p.q_ss + ks * 32 + g * 8) : zero8();
+      df[t][ks] = ok ? ld8(db + static_cast<int64_t>(qi) * p.o_ss + ks * 32 + g * 8) : zero8();
+    }
+    lse2[t] = ok ? lse_to_log2(lb[qi]) : __builtin_inff();
+    dl[t] = ok ? deb[qi] : 0.f;
+  }
+  f32x4 acc[2][DT];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int64_t qa_wave_first = p.q_offset + q0;
+  const int64_t qa_wave_last = p.q_offset + min(q0 + 31, p.Sq - 1);
+  const int64_t qa_wg_last = p.q_offset + min(qt * BQ + BQ - 1, p.Sq - 1);
+
+  for (int blk = 0; blk < p.nblk; ++blk) {
+    const bf16* kb = static_cast<const bf16*>(kv.k[blk]) + b * p.kv_sb + hk * p.kv_sh;
+    const bf16* vb = static_cast<const bf16*>(kv.v[blk]) + b * p.kv_sb + hk * p.kv_sh;
+    const int64_t koff = kv.koff[blk];
+    const int n_kt = visible_key_tiles(p, koff, qa_wg_last);
+    for (int kt = 0; kt < n_kt; ++kt) {
+      const int k0 = kt * BK;
+      __syncthreads();
+      stage_rows<BK, D, LDK>(sK, kb, p.kv_ss, k0, p.Sk);
+      stage_rows_t<BK, D, LDT>(sKt, kb, p.kv_ss, k0, p.Sk);
+      stage_rows<BK, D, LDK>(sV, vb, p.kv_ss, k0, p.Sk);
+      __syncthreads();
+      if (p.causal && koff + k0 > qa_wave_last) continue;
+      const bool need_mask =
+          (k0 + BK > p.Sk) || (p.causal && koff + k0 + BK - 1 > qa_wave_first);
+
+      f32x4 s[4][2], dp[4][2];
+#pragma unroll
+      for (int mk = 0; mk < 4; ++mk) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          s[mk][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+          dp[mk][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const bf16x8 ak = ld8(sK + (mk * 16 + l16) * LDK + ks * 32 + g * 8);
+          const bf16x8 av = ld8(sV + (mk * 16 + l16) * LDK + ks * 32 + g * 8);
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            s[mk][t] = mfma16(ak, qf[t][ks], s[mk][t]);
+            dp[mk][t] = mfma16(av, df[t][ks], dp[mk][t]);
+          }
+        }
+      }
+      bf16x8 dsf[2][2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int64_t qa = p.q_offset + q0 + 16 * t + l16;
+#pragma unroll
+        for (int mk = 0; mk < 4; ++mk)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float pv = exp2f(s[mk][t][e] * p.scale_log2 - lse2[t]);
+            if (need_mask) {
+              const int kl = k0 + mk * 16 + g * 4 + e;
+              if (kl >= p.Sk || (p.causal && koff + kl > qa)) pv = 0.f;
+            }
+            s[mk][t][e] = pv * (dp[mk][t][e] - dl[t]);
+          }
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            dsf[s2][t][e] = static_cast<bf16>(s[2 * s2][t][e]);
+            dsf[s2][t][4 + e] = static_cast<bf16>(s[2 * s2 + 1][t][e]);
+          }
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const bf16x8 a = ld4x2(sKt + (dt * 16 + l16) * LDT + 32 * s2 + g * 4);
+#pragma unroll
+          for (int t = 0; t < 2; ++t) acc[t][dt] = mfma16(a, dsf[s2][t], acc[t][dt]);
+        }
+      }
+    }
+  }
+  bf16* dqb = dq + b * p.q_sb + h * p.q_sh;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int qi = q0 + 16 * t + l16;
+    if (qi >= p.Sq) continue;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      bf16x4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] = static_cast<bf16>(acc[t][dt][e] * p.scale);
+      *reinterpret_cast<bf16x4*>(dqb + static_cast<int64_t>(qi) * p.q_ss + dt * 16 + g * 4) = w;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- dK, dV
+// Workgroup = 64 keys of one (batch, KV head, block); wave w owns keys
+// 16w..16w+15.  Loops over the query heads of the GQA group and over the
+// 64-query tiles that can see these keys.
+template <int D>
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const bf16* __restrict__ q,
+                                                            KVBlocks kv,
+                                                            const bf16* __restrict__ dout,
+                                                            const float* __restrict__ lse,
+                                                            const float* __restrict__ delta,
+                                                            AttnShape p) {
+  constexpr int BQ = 64, BK = 64, KS = D / 32, DT = D / 16;
+  constexpr int LDQ = D + 8, LDT = BQ + 8;
+  __shared__ __attribute__((aligned(16))) bf16 sQ[BQ * LDQ];
+  __shared__ __attribute__((aligned(16))) bf16 sQt[D * LDT];
+  __shared__ __attribute__((aligned(16))) bf16 sD[BQ * LDQ];
+  __shared__ __attribute__((aligned(16))) bf16 sDt[D * LDT];
+  __shared__ float sL[BQ], sDl[BQ];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int blk = static_cast<int>(blockIdx.z) % p.nblk;
+  const int b = static_cast<int>(blockIdx.z) / p.nblk;
+  const int hk = blockIdx.y;
+  const int k0 = static_cast<int>(blockIdx.x) * BK;
+  const int kw0 = k0 + wave * 16;
+  const int64_t koff = kv.koff[blk];
+  const int group = p.Hq / p.Hkv;
+
+  const bf16* kb = static_cast<const bf16*>(kv.k[blk]) + b * p.kv_sb + hk * p.kv_sh;
+  const bf16* vb = static_cast<const bf16*>(kv.v[blk]) + b * p.kv_sb + hk * p.kv_sh;
+  bf16x8 kf[KS], vf[KS];
+  {
+    const int key = kw0 + l16;
+    const bool ok = key < p.Sk;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      kf[ks] = ok ? ld8(kb + static_cast<int64_t>(key) * p.kv_ss + ks * 32 + g * 8) : zero8();
+      vf[ks] = ok ? ld8(vb + static_cast<int64_t>(key) * p.kv_ss + ks * 32 + g * 8) : zero8();
+    }
+  }
+  f32x4 dka[DT], dva[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    dka[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    dva[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  // first query (local index) that can see key k0 of this tile
+  int first_q = 0;
+  if (p.causal) {
+    const int64_t fq = koff + k0 - p.q_offset;
+    first_q = fq <= 0 ? 0 : (fq >= p.Sq ? p.Sq : static_cast<int>(fq));
+  }
+  const int qt_begin = first_q / BQ;
+  const int n_qt = (p.Sq + BQ - 1) / BQ;
+  const int64_t ka_wave_first = koff + kw0;
+  const int64_t ka_wave_last = koff + kw0 + 15;
+
+  for (int hi = 0; hi < group; ++hi) {
+    const int h = hk * group + hi;
+    const bf16* qb = q + b * p.q_sb + h * p.q_sh;
+    const bf16* db = dout + b * p.o_sb + h * p.o_sh;
+    const float* lb = lse + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
+    const float* deb = delta + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
+    for (int qt = qt_begin; qt < n_qt; ++qt) {
+      const int q0 = qt * BQ;
+      __syncthreads();
+      stage_rows<BQ, D, LDQ>(sQ, qb, p.q_ss, q0, p.Sq);
+      stage_rows_t<BQ, D, LDT>(sQt, qb, p.q_ss, q0, p.Sq);
+      stage_rows<BQ, D, LDQ>(sD, db, p.o_ss, q0, p.Sq);
+      stage_rows_t<BQ, D, LDT>(sDt, db, p.o_ss, q0, p.Sq);
+      if (threadIdx.x < BQ) {
+        const int qi = q0 + threadIdx.x;
+        sL[threadIdx.x] = qi < p.Sq ? lse_to_log2(lb[qi]) : __builtin_inff();
+        sDl[threadIdx.x] = qi < p.Sq ? deb[qi] : 0.f;
+      }
+      __syncthreads();
+      const int64_t qa_last = p.q_offset + min(q0 + BQ - 1, p.Sq - 1);
+      if (kw0 >= p.Sk) continue;
+      if (p.causal && ka_wave_first > qa_last) continue;
+      const bool need_mask =
+          (kw0 + 16 > p.Sk) || (p.causal && ka_wave_last > p.q_offset + q0);
+
+      // S = Q K^T and dP = dO V^T for this wave's 16 keys: lane holds
+      // S[q = 16 mq + 4 g + e][key = kw0 + l16].
+      f32x4 s[4], dp[4];
+#pragma unroll
+      for (int mq = 0; mq < 4; ++mq) {
+        s[mq] = f32x4{0.f, 0.f, 0.f, 0.f};
+        dp[mq] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const bf16x8 aq = ld8(sQ + (mq * 16 + l16) * LDQ + ks * 32 + g * 8);
+          const bf16x8 ad = ld8(sD + (mq * 16 + l16) * LDQ + ks * 32 + g * 8);
+          s[mq] = mfma16(aq, kf[ks], s[mq]);
+          dp[mq] = mfma16(ad, vf[ks], dp[mq]);
+        }
+      }
+      const int64_t ka = koff + kw0 + l16;
+#pragma unroll
+      for (int mq = 0; mq < 4; ++mq)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int ql = mq * 16 + g * 4 + e;
+          float pv = exp2f(s[mq][e] * p.scale_log2 - sL[ql]);
+          if (need_mask) {
+            if (kw0 + l16 >= p.Sk || (p.causal && ka > p.q_offset + q0 + ql)) pv = 0.f;
+          }
+          s[mq][e] = pv;
+          dp[mq][e] = pv * (dp[mq][e] - sDl[ql]);
+        }
+      bf16x8 pa[2], da[2];
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pa[s2][e] = static_cast<bf16>(s[2 * s2][e]);
+          pa[s2][4 + e] = static_cast<bf16>(s[2 * s2 + 1][e]);
+          da[s2][e] = static_cast<bf16>(dp[2 * s2][e]);
+          da[s2][4 + e] = static_cast<bf16>(dp[2 * s2 + 1][e]);
+        }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const bf16x8 bd = ld4x2(sDt + (dt * 16 + l16) * LDT + 32 * s2 + g * 4);
+          const bf16x8 bq = ld4x2(sQt + (dt * 16 + l16) * LDT + 32 * s2 + g * 4);
+          dva[dt] = mfma16(pa[s2], bd, dva[dt]);
+          dka[dt] = mfma16(da[s2], bq, dka[dt]);
+        }
+      }
+    }
+  }
+  // lane holds dK[key = kw0 + 4 g + e][d = 16 dt + l16]
+  bf16* dkb = static_cast<bf16*>(kv.dk[blk]) + b * p.kv_sb + hk * p.kv_sh;
+  bf16* dvb = static_cast<bf16*>(kv.dv[blk]) + b * p.kv_sb + hk * p.kv_sh;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int key = kw0 + g * 4 + e;
+    if (key >= p.Sk) continue;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      dkb[static_cast<int64_t>(key) * p.kv_ss + dt * 16 + l16] =
+          static_cast<bf16>(dka[dt][e] * p.scale);
+      dvb[static_cast<int64_t>(key) * p.kv_ss + dt * 16 + l16] = static_cast<bf16>(dva[dt][e]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- fp32 path
+// One wavefront per query row; lane owns head_dim elements lane and lane + 64.
+__device__ __forceinline__ float dot_row(const float* a, const float* b, int D, int lane) {
+  float s = 0.f;
+  for (int d = lane; d < D; d += 64) s += a[d] * b[d];
+  return wave_sum(s);
+}
+
+__global__ __launch_bounds__(64) void attn_fwd_f32_kernel(const float* __restrict__ q, KVBlocks kv,
+                                                          float* __restrict__ o,
+                                                          float* __restrict__ lse, AttnShape p,
+                                                          int D) {
+  const int lane = threadIdx.x;
+  const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int hk = h / (p.Hq / p.Hkv);
+  const float* qr = q + b * p.q_sb + static_cast<int64_t>(i) * p.q_ss + h * p.q_sh;
+  const int64_t qa = p.q_offset + i;
+  float m = -__builtin_inff(), l = 0.f;
+  float acc[2] = {0.f, 0.f};
+  for (int blk = 0; blk < p.nblk; ++blk) {
+    const float* kb = static_cast<const float*>(kv.k[blk]) + b * p.kv_sb + hk * p.kv_sh;
+    const float* vb = static_cast<const float*>(kv.v[blk]) + b * p.kv_sb + hk * p.kv_sh;
+    const int64_t koff = kv.koff[blk];
+    for (int j = 0; j < p.Sk; ++j) {
+      if (p.causal && koff + j > qa) break;
+      const float* kr = kb + static_cast<int64_t>(j) * p.kv_ss;
+      const float* vr = vb + static_cast<int64_t>(j) * p.kv_ss;
+      const float sc = dot_row(qr, kr, D, lane) * p.scale;
+      const float mnew = fmaxf(m, sc);
+      const float alpha = expf(m - mnew);
+      const float pv = expf(sc - mnew);
+      l = l * alpha + pv;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int d = lane + 64 * c;
+        if (d < D) acc[c] = acc[c] * alpha + pv * vr[d];
+      }
+      m = mnew;
+    }
+  }
+  float* orow = o + b * p.o_sb + static_cast<int64_t>(i) * p.o_ss + h * p.o_sh;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int d = lane + 64 * c;
+    if (d < D) orow[d] = acc[c] * inv;
+  }
+  if (lane == 0)
+    lse[(static_cast<int64_t>(b) * p.Hq + h) * p.Sq + i] = l > 0.f ? m + logf(l) : -__builtin_inff();
+}
+
+__global__ __launch_bounds__(64) void attn_bwd_dq_f32_kernel(
+    const float* __restrict__ q, KVBlocks kv, const float* __restrict__ dout,
+    const float* __restrict__ lse, const float* __restrict__ delta, float* __restrict__ dq,
+    AttnShape p, int D) {
+  const int lane = threadIdx.x;
+  const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int hk = h / (p.Hq / p.Hkv);
+  const float* qr = q + b * p.q_sb + static_cast<int64_t>(i) * p.q_ss + h * p.q_sh;
+  const float* dr = dout + b * p.o_sb + static_cast<int64_t>(i) * p.o_ss + h * p.o_sh;
+  const int64_t row = (static_cast<int64_t>(b) * p.Hq + h) * p.Sq + i;
+  const float ls = lse[row], dl = delta[row];
+  const int64_t qa = p.q_offset + i;
+  float acc[2] = {0.f, 0.f};
+  if (ls != -__builtin_inff()) {
+    for (int blk = 0; blk < p.nblk; ++blk) {
+      const float* kb = static_cast<const float*>(kv.k[blk]) + b * p.kv_sb + hk * p.kv_sh;
+      const float* vb = static_cast<const float*>(kv.v[blk]) + b * p.kv_sb + hk * p.kv_sh;
+      const int64_t koff = kv.koff[blk];
+      for (int j = 0; j < p.Sk; ++j) {
+        if (p.causal && koff + j > qa) break;
+        const float* kr = kb + static_cast<int64_t>(j) * p.kv_ss;
+        const float* vr = vb + static_cast<int64_t>(j) * p.kv_ss;
+        const float pv = expf(dot_row(qr, kr, D, lane) * p.scale - ls);
+        const float ds = pv * (dot_row(dr, vr, D, lane) - dl);
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const int d = lane + 64 * c;
+          if (d < D) acc[c] += ds * kr[d];
+        }
+      }
+    }
+  }
+  float* out = dq + b * p.q_sb + static_cast<int64_t>(i) * p.q_ss + h * p.q_sh;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int d = lane + 64 * c;
+    if (d < D) out[d] = acc[c] * p.scale;
+  }
+}
+
+__global__ __launch_bounds__(64) void attn_bwd_dkdv_f32_kernel(
+    const float* __restrict__ q, KVBlocks kv, const float* __restrict__ dout,
+    const float* __restrict__ lse, const float* __restrict__ delta, AttnShape p, int D) {
+  const int lane = threadIdx.x;
+  const int j = blockIdx.x, hk = blockIdx.y;
+  const int blk = static_cast<int>(blockIdx.z) % p.nblk;
+  const int b = static_cast<int>(blockIdx.z) / p.nblk;
+  const int group = p.Hq / p.Hkv;
+  const int64_t koff = kv.koff[blk];
+  const int64_t kvo = b * p.kv_sb + static_cast<int64_t>(j) * p.kv_ss + hk * p.kv_sh;
+  const float* kr = static_cast<const float*>(kv.k[blk]) + kvo;
+  const float* vr = static_cast<const float*>(kv.v[blk]) + kvo;
+  float dk[2] = {0.f, 0.f}, dv[2] = {0.f, 0.f};
+  int i0 = 0;
+  if (p.causal) {
+    const int64_t fq = koff + j - p.q_offset;
+    i0 = fq <= 0 ? 0 : (fq >= p.Sq ? p.Sq : static_cast<int>(fq));
+  }
+  for (int hi = 0; hi < group; ++hi) {
+    const int h = hk * group + hi;
+    for (int i = i0; i < p.Sq; ++i) {
+      const int64_t row = (static_cast<int64_t>(b) * p.Hq + h) * p.Sq + i;
+      const float ls = lse[row];
+      if (ls == -__builtin_inff()) continue;
+      const float* qr = q + b * p.q_sb + static_cast<int64_t>(i) * p.q_ss + h * p.q_sh;
+      const float* dr = dout + b * p.o_sb + static_cast<int64_t>(i) * p.o_ss + h * p.o_sh;
+      const float pv = expf(dot_row(qr, kr, D, lane) * p.scale - ls);
+      const float ds = pv * (dot_row(dr, vr, D, lane) - delta[row]);
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int d = lane + 64 * c;
+        if (d < D) {
+          dv[c] += pv * dr[d];
+          dk[c] += ds * qr[d];
+        }
+      }
+    }
+  }
+  float* dkr = static_cast<float*>(kv.dk[blk]) + kvo;
+  float* dvr = static_cast<float*>(kv.dv[blk]) + kvo;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int d = lane + 64 * c;
+    if (d < D) {
+      dkr[d] = dk[c] * p.scale;
+      dvr[d] = dv[c];
+    }
+  }
+}
+
+// ---------------------------------------------------------------- host side
+int fill_shape(AttnShape* p, KVBlocks* kv, const void* q, const void* const* kb,
+               const void* const* vb, const int64_t* koff, int nblk, int64_t B, int64_t Hq,
+               int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D, const int64_t* qs,
+               const int64_t* kvs, const int64_t* os, int causal, int64_t q_offset, float scale,
+               int dtype) {
+  NMB_REQUIRE(q != nullptr && kb != nullptr && vb != nullptr && koff != nullptr && qs != nullptr &&
+                  kvs != nullptr && os != nullptr,
+              "attention: null argument");
+  NMB_REQUIRE(nblk >= 1 && nblk <= kMaxBlocks, "attention: n_blocks must be in [1, %d], got %d",
+              kMaxBlocks, nblk);
+  NMB_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Sq >= 0 && Sk >= 0 && D > 0,
+              "attention: invalid shape");
+  NMB_REQUIRE(Hq % Hkv == 0, "query heads (%lld) must be divisible by KV heads (%lld)",
+              (long long)Hq, (long long)Hkv);
+  NMB_REQUIRE(B <= 65535 && Hq <= 65535 && Sq <= 0x3fffffff && Sk <= 0x3fffffff,
+              "attention: shape exceeds the launch grid");
+  if (dtype == NMB_BF16) {
+    NMB_REQUIRE_SUPPORTED(D == 64 || D == 128, "attention (bf16): head_dim must be 64 or 128, got %lld",
+                          (long long)D);
+    for (int i = 0; i < 3; ++i)
+      NMB_REQUIRE_SUPPORTED(qs[i] % 8 == 0 && kvs[i] % 8 == 0 && os[i] % 8 == 0,
+                            "attention (bf16): strides must be multiples of 8 elements");
+    NMB_REQUIRE(aligned16(q), "attention: q must be 16-byte aligned");
+  } else if (dtype == NMB_F32) {
+    NMB_REQUIRE_SUPPORTED(D <= 128, "attention (fp32): head_dim must be <= 128, got %lld",
+                          (long long)D);
+  } else {
+    NMB_REQUIRE_SUPPORTED(false, "attention: unsupported dtype code %d", dtype);
+  }
+  for (int i = 0; i < nblk; ++i) {
+    NMB_REQUIRE(kb[i] != nullptr && vb[i] != nullptr, "attention: null K/V block %d", i);
+    NMB_REQUIRE(dtype != NMB_BF16 || (aligned16(kb[i]) && aligned16(vb[i])),
+                "attention: K/V blocks must be 16-byte aligned");
+    kv->k[i] = kb[i];
+    kv->v[i] = vb[i];
+    kv->koff[i] = koff[i];
+    kv->dk[i] = nullptr;
+    kv->dv[i] = nullptr;
+  }
+  p->B = static_cast<int>(B);
+  p->Hq = static_cast<int>(Hq);
+  p->Hkv = static_cast<int>(Hkv);
+  p->Sq = static_cast<int>(Sq);
+  p->Sk = static_cast<int>(Sk);
+  p->nblk = nblk;
+  p->causal = causal ? 1 : 0;
+  p->q_sb = qs[0];
+  p->q_ss = qs[1];
+  p->q_sh = qs[2];
+  p->kv_sb = kvs[0];
+  p->kv_ss = kvs[1];
+  p->kv_sh = kvs[2];
+  p->o_sb = os[0];
+  p->o_ss = os[1];
+  p->o_sh = os[2];
+  p->q_offset = q_offset;
+  p->scale = scale > 0.f ? scale : static_cast<float>(1.0 / sqrt(static_cast<double>(D)));
+  p->scale_log2 = p->scale * kLog2e;
+  return NMB_OK;
+}
+
+}  // namespace
+}  // namespace nmb
+
+using nmb::AttnShape;
+using nmb::KVBlocks;
+
+extern "C" int nmb_attn_fwd(const void* q, const void* const* k_blocks,
+                            const void* const* v_blocks, const int64_t* k_offsets, int n_blocks,
+                            void* o, float* lse, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                            int64_t seq_q, int64_t seq_k, int64_t head_dim,
+                            const int64_t* q_strides, const int64_t* kv_strides,
+                            const int64_t* o_strides, int causal, int64_t q_offset, float scale,
+                            int dtype, hipStream_t stream) {
+  AttnShape p;
+  KVBlocks kv;
+  int st = nmb::fill_shape(&p, &kv, q, k_blocks, v_blocks, k_offsets, n_blocks, batch, q_heads,
+                           kv_heads, seq_q, seq_k, head_dim, q_strides, kv_strides, o_strides,
+                           causal, q_offset, scale, dtype);
+  if (st != NMB_OK) return st;
+  NMB_REQUIRE(o != nullptr && lse != nullptr, "attn_fwd: null output");
+  if (batch == 0 || seq_q == 0) return NMB_OK;
+  if (dtype == NMB_BF16) {
+    NMB_REQUIRE(nmb::aligned16(o), "attn_fwd: o must be 16-byte aligned");
+    const dim3 grid(static_cast<unsigned>((seq_q + 127) / 128), static_cast<unsigned>(q_heads),
+                    static_cast<unsigned>(batch));
+    const nmb::bf16* qp = static_cast<const nmb::bf16*>(q);
+    nmb::bf16* op = static_cast<nmb::bf16*>(o);
+    if (head_dim == 64)
+      hipLaunchKernelGGL(nmb::attn_fwd_kernel<64>, grid, dim3(256), 0, stream, qp, kv, op, lse, p);
+    else
+      hipLaunchKernelGGL(nmb::attn_fwd_kernel<128>, grid, dim3(256), 0, stream, qp, kv, op, lse, p);
+  } else {
+    const dim3 grid(static_cast<unsigned>(seq_q), static_cast<unsigned>(q_heads),
+                    static_cast<unsigned>(batch));
+    hipLaunchKernelGGL(nmb::attn_fwd_f32_kernel, grid, dim3(64), 0, stream,
+                       static_cast<const float*>(q), kv, static_cast<float*>(o), lse, p,
+                       static_cast<int>(head_dim));
+  }
+  NMB_CHECK_LAUNCH("attn_fwd");
+  return NMB_OK;
+}
+
+extern "C" int nmb_attn_bwd_workspace_bytes(int64_t batch, int64_t q_heads, int64_t seq_q,
+                                            size_t* bytes) {
+  NMB_REQUIRE(bytes != nullptr && batch >= 0 && q_heads >= 0 && seq_q >= 0,
+              "attn_bwd_workspace_bytes: bad args");
+  *bytes = static_cast<size_t>(batch * q_heads * seq_q) * sizeof(float);
+  return NMB_OK;
+}
+
+extern "C" int nmb_attn_bwd(const void* q, const void* const* k_blocks,
+                            const void* const* v_blocks, const int64_t* k_offsets, int n_blocks,
+                            const void* o, const void* dout, const float* lse, void* dq,
+                            void* const* dk_blocks, void* const* dv_blocks, void* workspace,
+                            size_t workspace_bytes, int64_t batch, int64_t q_heads,
+                            int64_t kv_heads, int64_t seq_q, int64_t seq_k, int64_t head_dim,
+                            const int64_t* q_strides, const int64_t* kv_strides,
+                            const int64_t* o_strides, int causal, int64_t q_offset, float scale,
+                            int dtype, hipStream_t stream) {
+  AttnShape p;
+  KVBlocks kv;
+  int st = nmb::fill_shape(&p, &kv, q, k_blocks, v_blocks, k_offsets, n_blocks, batch, q_heads,
+                           kv_heads, seq_q, seq_k, head_dim, q_strides, kv_strides, o_strides,
+                           causal, q_offset, scale, dtype);
+  if (st != NMB_OK) return st;
+  NMB_REQUIRE(o != nullptr && dout != nullptr && lse != nullptr && dq != nullptr &&
+                  dk_blocks != nullptr && dv_blocks != nullptr,
+              "attn_bwd: null argument");
+  for (int i = 0; i < n_blocks; ++i) {
+    NMB_REQUIRE(dk_blocks[i] != nullptr && dv_blocks[i] != nullptr, "attn_bwd: null dK/dV block");
+    kv.dk[i] = dk_blocks[i];
+    kv.dv[i] = dv_blocks[i];
+  }
+  const size_t need = static_cast<size_t>(batch * q_heads * seq_q) * sizeof(float);
+  NMB_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+              "attn_bwd: workspace of %zu bytes is smaller than the %zu required",
+              workspace_bytes, need);
+  if (batch == 0) return NMB_OK;
+  float* delta = static_cast<float*>(workspace);
+  const int D = static_cast<int>(head_dim);
+  if (seq_q > 0) {
+    int64_t rows = batch * q_heads * seq_q;
+    int64_t blocks = (rows + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    if (dtype == NMB_BF16)
+      hipLaunchKernelGGL(nmb::attn_delta_kernel<nmb::bf16>, dim3(static_cast<unsigned>(blocks)),
+                         dim3(256), 0, stream, static_cast<const nmb::bf16*>(o),
+                         static_cast<const nmb::bf16*>(dout), delta, p, D);
+    else
+      hipLaunchKernelGGL(nmb::attn_delta_kernel<float>, dim3(static_cast<unsigned>(blocks)),
+                         dim3(256), 0, stream, static_cast<const float*>(o),
+                         static_cast<const float*>(dout), delta, p, D);
+    NMB_CHECK_LAUNCH("attn_bwd(delta)");
+  }
+  if (dtype == NMB_BF16) {
+    NMB_REQUIRE(nmb::aligned16(dq) && nmb::aligned16(dout), "attn_bwd: dq/dout must be aligned");
+    const nmb::bf16* qp = static_cast<const nmb::bf16*>(q);
+    const nmb::bf16* dp = static_cast<const nmb::bf16*>(dout);
+    nmb::bf16* dqp = static_cast<nmb::bf16*>(dq);
+    if (seq_q > 0) {
+      const dim3 grid(static_cast<unsigned>((seq_q + 127) / 128), static_cast<unsigned>(q_heads),
+                      static_cast<unsigned>(batch));
+      if (D == 64)
+        hipLaunchKernelGGL(nmb::attn_bwd_dq_kernel<64>, grid, dim3(256), 0, stream, qp, kv, dp,
+                           lse, delta, dqp, p);
+      else
+        hipLaunchKernelGGL(nmb::attn_bwd_dq_kernel<128>, grid, dim3(256), 0, stream, qp, kv, dp,
+                           lse, delta, dqp, p);
+      NMB_CHECK_LAUNCH("attn_bwd(dq)");
+    }
+    if (seq_k > 0) {
+      const dim3 grid(static_cast<unsigned>((seq_k + 63) / 64), static_cast<unsigned>(kv_heads),
+                      static_cast<unsigned>(batch * n_blocks));
+      if (D == 64)
+        hipLaunchKernelGGL(nmb::attn_bwd_dkdv_kernel<64>, grid, dim3(256), 0, stream, qp, kv, dp,
+                           lse, delta, p);
+      else
+        hipLaunchKernelGGL(nmb::attn_bwd_dkdv_kernel<128>, grid, dim3(256), 0, stream, qp, kv, dp,
+                           lse, delta, p);
+      NMB_CHECK_LAUNCH("attn_bwd(dkdv)");
+    }
+  } else {
+    const float* qp = static_cast<const float*>(q);
+    const float* dp = static_cast<const float*>(dout);
+    if (seq_q > 0) {
+      const dim3 grid(static_cast<unsigned>(seq_q), static_cast<unsigned>(q_heads),
+                      static_cast<unsigned>(batch));
+      hipLaunchKernelGGL(nmb::attn_bwd_dq_f32_kernel, grid, dim3(64), 0, stream, qp, kv, dp, lse,
+                         delta, static_cast<float*>(dq), p, D);
+      NMB_CHECK_LAUNCH("attn_bwd(dq,f32)");
+    }
+    if (seq_k > 0) {
+      const dim3 grid(static_cast<unsigned>(seq_k), static_cast<unsigned>(kv_heads),
+                      static_cast<unsigned>(batch * n_blocks));
+      hipLaunchKernelGGL(nmb::attn_bwd_dkdv_f32_kernel, grid, dim3(64), 0, stream, qp, kv, dp,
+                         lse, delta, p, D);
+      NMB_CHECK_LAUNCH("attn_bwd(dkdv,f32)");
+    }
+  }
+  return NMB_OK;
+}

@@ -1,0 +1,321 @@
+// RMSNorm forward/backward for gfx950.
+//
+// Follows RMSNorm.forward (reference nn/norms.py:38-41):
+//   var = mean(fp32(x)^2); n = fp32(x) * rsqrt(var + eps); y = cast(n) * cast(w)
+// and the gradient of that expression:
+//   g = dy * w;  dx = rstd * (g - n * mean(g * n));  dw = sum_rows(dy * cast(n)).
+//
+// Layout: one 64-lane wavefront owns one row; each lane holds ITERS 16-byte
+// vectors of the row in registers, so x is read from HBM exactly once.  The
+// row statistic is a wavefront butterfly reduction.  dw is reduced
+// deterministically: per-workgroup partial sums (fixed row order) into an fp32
+// workspace, then a column-sum kernel with a fixed order.
+#include "common.h"
+#include "vec.h"
+
+namespace nmb {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kBwdBlocks = 512;
+
+template <typename T>
+__device__ __forceinline__ float inv_rms(float sum_sq, int cols, float eps) {
+  const float var = __fdiv_rn(sum_sq, static_cast<float>(cols));
+  return __fdiv_rn(1.0f, __fsqrt_rn(add_rn(var, eps)));
+}
+
+template <typename T, int ITERS>
+__global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const T* __restrict__ x,
+                                                          const T* __restrict__ w,
+                                                          T* __restrict__ y,
+                                                          float* __restrict__ rstd, int64_t rows,
+                                                          int cols, float eps) {
+  constexpr int V = VecTraits<T>::N;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;  // wave-uniform
+  const T* xr = x + row * cols;
+  float v[ITERS][V];
+  float ss = 0.f;
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const int c = (it * 64 + lane) * V;
+    if (c < cols) {
+      load_vec<T>(xr + c, v[it]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < V; ++i) v[it][i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < V; ++i) ss += v[it][i] * v[it][i];
+  }
+  ss = wave_sum(ss);
+  const float r = inv_rms<T>(ss, cols, eps);
+  T* yr = y + row * cols;
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const int c = (it * 64 + lane) * V;
+    if (c < cols) {
+      float wv[V], o[V];
+      load_vec<T>(w + c, wv);
+#pragma unroll
+      for (int i = 0; i < V; ++i) o[i] = mul_rn(round_as<T>(mul_rn(v[it][i], r)), wv[i]);
+      store_vec<T>(yr + c, o);
+    }
+  }
+  if (rstd != nullptr && lane == 0) rstd[row] = r;
+}
+
+template <typename T, int ITERS>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
+    const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ dy,
+    const T* __restrict__ dres, T* __restrict__ dx, float* __restrict__ partial, int64_t rows,
+    int cols, float eps, int64_t rows_per_block) {
+  constexpr int V = VecTraits<T>::N;
+  extern __shared__ float s_dw[];  // [kWaves][cols]
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  float wv[ITERS][V];
+  float acc[ITERS][V];
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const int c = (it * 64 + lane) * V;
+    if (c < cols) {
+      load_vec<T>(w + c, wv[it]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < V; ++i) wv[it][i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[it][i] = 0.f;
+  }
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rows_per_block;
+  const int64_t r1 = min(rows, r0 + rows_per_block);
+  for (int64_t row = r0 + wave; row < r1; row += kWaves) {
+    const T* xr = x + row * cols;
+    const T* dyr = dy + row * cols;
+    float xv[ITERS][V], dv[ITERS][V];
+    float ss = 0.f;
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      const int c = (it * 64 + lane) * V;
+      if (c < cols) {
+        load_vec<T>(xr + c, xv[it]);
+        load_vec<T>(dyr + c, dv[it]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i) xv[it][i] = dv[it][i] = 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < V; ++i) ss += xv[it][i] * xv[it][i];
+    }
+    ss = wave_sum(ss);
+    const float r = inv_rms<T>(ss, cols, eps);
+    float dot = 0.f;
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float n = mul_rn(xv[it][i], r);
+        const float g = round_as<T>(mul_rn(dv[it][i], wv[it][i]));
+        dot += g * n;
+        // weight gradient of y = cast(n) * w: dy * cast(n), rounded as the
+        // reference's per-element product tensor is.
+        acc[it][i] += round_as<T>(mul_rn(dv[it][i], round_as<T>(n)));
+        xv[it][i] = n;   // keep n
+        dv[it][i] = g;   // keep g
+      }
+    }
+    dot = wave_sum(dot);
+    const float mean_dot = __fdiv_rn(dot, static_cast<float>(cols));
+    T* dxr = dx + row * cols;
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      const int c = (it * 64 + lane) * V;
+      if (c < cols) {
+        float o[V];
+#pragma unroll
+        for (int i = 0; i < V; ++i) o[i] = r * (dv[it][i] - xv[it][i] * mean_dot);
+        if (dres != nullptr) {
+          float rv[V];
+          load_vec<T>(dres + row * cols + c, rv);
+#pragma unroll
+          for (int i = 0; i < V; ++i) o[i] += rv[i];
+        }
+        store_vec<T>(dxr + c, o);
+      }
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const int c = (it * 64 + lane) * V;
+    if (c < cols) {
+#pragma unroll
+      for (int i = 0; i < V; ++i) s_dw[wave * cols + c + i] = acc[it][i];
+    }
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < cols; c += 256) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < kWaves; ++k) s += s_dw[k * cols + c];
+    partial[static_cast<int64_t>(blockIdx.x) * cols + c] = s;
+  }
+}
+
+// dw[c] = sum_b partial[b][c] in a fixed order.  Block: 16 column groups of 16
+// columns each (64-byte segments); the 16 row groups are combined in LDS.
+template <typename T>
+__global__ __launch_bounds__(256) void column_sum_kernel(const float* __restrict__ partial,
+                                                         int nblocks, int cols,
+                                                         T* __restrict__ out) {
+  __shared__ float s[16][17];
+  const int cl = threadIdx.x & 15;
+  const int rg = threadIdx.x >> 4;
+  const int c = blockIdx.x * 16 + cl;
+  float acc = 0.f;
+  if (c < cols) {
+    for (int b = rg; b < nblocks; b += 16) acc += partial[static_cast<int64_t>(b) * cols + c];
+  }
+  s[rg][cl] = acc;
+  __syncthreads();
+  if (rg == 0 && c < cols) {
+    float t = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) t += s[k][cl];
+    out[c] = from_f32<T>(t);
+  }
+}
+
+int iters_for(int cols, int vec) { return (cols + 64 * vec - 1) / (64 * vec); }
+
+void bwd_grid(int64_t rows, int* nblocks, int64_t* rows_per_block) {
+  int64_t nb = (rows + kWaves - 1) / kWaves;
+  if (nb > kBwdBlocks) nb = kBwdBlocks;
+  if (nb < 1) nb = 1;
+  int64_t rpb = (rows + nb - 1) / nb;
+  rpb = (rpb + kWaves - 1) / kWaves * kWaves;
+  nb = (rows + rpb - 1) / rpb;
+  if (nb < 1) nb = 1;
+  *nblocks = static_cast<int>(nb);
+  *rows_per_block = rpb;
+}
+
+template <typename T>
+int check_common(const void* x, const void* w, int64_t rows, int64_t cols) {
+  constexpr int V = VecTraits<T>::N;
+  NMB_REQUIRE(x != nullptr && w != nullptr, "rmsnorm: null tensor pointer");
+  NMB_REQUIRE(rows >= 0 && cols > 0, "rmsnorm: invalid shape rows=%lld cols=%lld",
+              (long long)rows, (long long)cols);
+  NMB_REQUIRE_SUPPORTED(cols % V == 0, "rmsnorm: hidden size %lld must be a multiple of %d",
+                        (long long)cols, V);
+  NMB_REQUIRE_SUPPORTED(iters_for(static_cast<int>(cols), V) <= 8,
+                        "rmsnorm: hidden size %lld exceeds the supported maximum %d",
+                        (long long)cols, 8 * 64 * V);
+  return NMB_OK;
+}
+
+template <typename T>
+int fwd_impl(const void* x, const void* w, void* y, float* rstd, int64_t rows, int64_t cols,
+             float eps, hipStream_t stream) {
+  int st = check_common<T>(x, w, rows, cols);
+  if (st != NMB_OK) return st;
+  NMB_REQUIRE(y != nullptr, "rmsnorm_fwd: null output");
+  NMB_REQUIRE(aligned16(x) && aligned16(w) && aligned16(y),
+              "rmsnorm_fwd: tensors must be 16-byte aligned");
+  if (rows == 0) return NMB_OK;
+  const dim3 grid(static_cast<unsigned>((rows + kWaves - 1) / kWaves));
+  const int c = static_cast<int>(cols);
+  const T* xp = static_cast<const T*>(x);
+  const T* wp = static_cast<const T*>(w);
+  T* yp = static_cast<T*>(y);
+  switch (iters_for(c, VecTraits<T>::N)) {
+#define NMB_CASE(I)                                                                        \
+  case I:                                                                                  \
+    hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, I>), grid, dim3(256), 0, stream, xp, wp, yp, \
+                       rstd, rows, c, eps);                                                \
+    break;
+    NMB_CASE(1) NMB_CASE(2) NMB_CASE(3) NMB_CASE(4) NMB_CASE(5) NMB_CASE(6) NMB_CASE(7)
+    NMB_CASE(8)
+#undef NMB_CASE
+  }
+  NMB_CHECK_LAUNCH("rmsnorm_fwd");
+  return NMB_OK;
+}
+
+template <typename T>
+int bwd_impl(const void* x, const void* w, const void* dy, const void* dres, void* dx, void* dw,
+             void* ws, size_t ws_bytes, int64_t rows, int64_t cols, float eps,
+             hipStream_t stream) {
+  int st = check_common<T>(x, w, rows, cols);
+  if (st != NMB_OK) return st;
+  NMB_REQUIRE(dy != nullptr && dx != nullptr && dw != nullptr, "rmsnorm_bwd: null tensor");
+  NMB_REQUIRE(aligned16(x) && aligned16(w) && aligned16(dy) && aligned16(dx) &&
+                  (dres == nullptr || aligned16(dres)),
+              "rmsnorm_bwd: tensors must be 16-byte aligned");
+  int nblocks;
+  int64_t rpb;
+  bwd_grid(rows, &nblocks, &rpb);
+  const size_t need = static_cast<size_t>(nblocks) * static_cast<size_t>(cols) * sizeof(float);
+  NMB_REQUIRE(ws != nullptr && ws_bytes >= need,
+              "rmsnorm_bwd: workspace of %zu bytes is smaller than the %zu required", ws_bytes,
+              need);
+  const int c = static_cast<int>(cols);
+  const T* xp = static_cast<const T*>(x);
+  const T* wp = static_cast<const T*>(w);
+  const T* dyp = static_cast<const T*>(dy);
+  const T* drp = static_cast<const T*>(dres);
+  T* dxp = static_cast<T*>(dx);
+  float* part = static_cast<float*>(ws);
+  const size_t lds = static_cast<size_t>(kWaves) * cols * sizeof(float);
+  switch (iters_for(c, VecTraits<T>::N)) {
+#define NMB_CASE(I)                                                                       \
+  case I:                                                                                 \
+    hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, I>), dim3(nblocks), dim3(256), lds, stream, \
+                       xp, wp, dyp, drp, dxp, part, rows, c, eps, rpb);                   \
+    break;
+    NMB_CASE(1) NMB_CASE(2) NMB_CASE(3) NMB_CASE(4) NMB_CASE(5) NMB_CASE(6) NMB_CASE(7)
+    NMB_CASE(8)
+#undef NMB_CASE
+  }
+  NMB_CHECK_LAUNCH("rmsnorm_bwd");
+  hipLaunchKernelGGL((column_sum_kernel<T>), dim3((c + 15) / 16), dim3(256), 0, stream, part,
+                     nblocks, c, static_cast<T*>(dw));
+  NMB_CHECK_LAUNCH("rmsnorm_bwd(dw)");
+  return NMB_OK;
+}
+
+}  // namespace
+}  // namespace nmb
+
+extern "C" int nmb_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd, int64_t rows,
+                               int64_t cols, float eps, int dtype, hipStream_t stream) {
+  NMB_REQUIRE(eps > 0.f, "rmsnorm_fwd: eps must be positive, got %g", (double)eps);
+  if (dtype == NMB_BF16) return nmb::fwd_impl<nmb::bf16>(x, w, y, rstd, rows, cols, eps, stream);
+  if (dtype == NMB_F32) return nmb::fwd_impl<float>(x, w, y, rstd, rows, cols, eps, stream);
+  NMB_REQUIRE_SUPPORTED(false, "rmsnorm_fwd: unsupported dtype code %d", dtype);
+}
+
+extern "C" int nmb_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols, size_t* bytes) {
+  NMB_REQUIRE(bytes != nullptr && rows >= 0 && cols > 0, "rmsnorm_bwd_workspace_bytes: bad args");
+  int nb;
+  int64_t rpb;
+  nmb::bwd_grid(rows, &nb, &rpb);
+  *bytes = static_cast<size_t>(nb) * static_cast<size_t>(cols) * sizeof(float);
+  return NMB_OK;
+}
+
+extern "C" int nmb_rmsnorm_bwd(const void* x, const void* w, const void* dy,
+                               const void* residual_grad, void* dx, void* dw, void* workspace,
+                               size_t workspace_bytes, int64_t rows, int64_t cols, float eps,
+                               int dtype, hipStream_t stream) {
+  NMB_REQUIRE(eps > 0.f, "rmsnorm_bwd: eps must be positive, got %g", (double)eps);
+  if (dtype == NMB_BF16)
+    return nmb::bwd_impl<nmb::bf16>(x, w, dy, residual_grad, dx, dw, workspace, workspace_bytes,
+                                    rows, cols, eps, stream);
+  if (dtype == NMB_F32)
+    return nmb::bwd_impl<float>(x, w, dy, residual_grad, dx, dw, workspace, workspace_bytes,
+                                rows, cols, eps, stream);
+  NMB_REQUIRE_SUPPORTED(false, "rmsnorm_bwd: unsupported dtype code %d", dtype);
+}

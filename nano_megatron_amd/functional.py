@@ -1,0 +1,577 @@
+"""Device ops of the GPT block: thin wrappers over libnmb.so plus autograd Functions.
+
+Every op runs on the GPU through the C ABI; a CPU tensor is an error, never a
+fallback.  Dense projections are plain library GEMMs (``torch.mm`` /
+``torch.addmm`` -> hipBLASLt); everything else is a hand-written gfx950
+kernel.
+
+Attention tensors use one memory layout throughout: ``[batch, seq, heads,
+head_dim]`` (the layout of the Q/K/V projection outputs), seen through a
+``[batch, heads, seq, head_dim]`` view where the reference API expects it
+(nn/kernels/torch_backend.py:25-76).  That makes the reference's
+``transpose(1, 2).contiguous()`` (models/gpt/attention.py:176-178, 207) free.
+"""
+
+from __future__ import annotations
+
+import math
+import threading
+from typing import Any, Sequence
+
+import torch
+from torch import Tensor
+
+from nano_megatron_amd import _lib
+
+IGNORE_INDEX = -100
+
+
+def _require_gpu(*tensors: Tensor) -> None:
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise ValueError(
+                "nano_megatron_amd runs its kernels on the GPU only; got a tensor on "
+                f"{t.device} (there is no CPU fallback)"
+            )
+
+
+def _workspace(nbytes: int, device: torch.device) -> Tensor:
+    return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
+
+
+# ---------------------------------------------------------------- RMSNorm
+def rmsnorm_fwd(x2: Tensor, weight: Tensor, eps: float) -> Tensor:
+    """y = RMSNorm(x2) for a contiguous [rows, hidden] tensor (nn/norms.py:38-41)."""
+    _require_gpu(x2, weight)
+    rows, cols = x2.shape
+    y = torch.empty_like(x2)
+    _lib.call(
+        "nmb_rmsnorm_fwd", x2.data_ptr(), weight.data_ptr(), y.data_ptr(), None, rows, cols,
+        float(eps), _lib.dtype_code(x2.dtype), _lib.stream_of(x2),
+    )
+    return y
+
+
+def rmsnorm_bwd(
+    x2: Tensor, weight: Tensor, dy2: Tensor, eps: float, residual_grad: Tensor | None = None
+) -> tuple[Tensor, Tensor]:
+    """(dx [+ residual_grad], dw) of RMSNorm, with dw reduced deterministically."""
+    _require_gpu(x2, weight, dy2)
+    rows, cols = x2.shape
+    nbytes = _lib.ctypes.c_size_t(0)
+    _lib.call("nmb_rmsnorm_bwd_workspace_bytes", rows, cols, _lib.ctypes.byref(nbytes))
+    ws = _workspace(nbytes.value, x2.device)
+    dx = torch.empty_like(x2)
+    dw = torch.empty_like(weight)
+    _lib.call(
+        "nmb_rmsnorm_bwd", x2.data_ptr(), weight.data_ptr(), dy2.data_ptr(),
+        _lib.ptr(residual_grad), dx.data_ptr(), dw.data_ptr(), ws.data_ptr(), ws.numel(),
+        rows, cols, float(eps), _lib.dtype_code(x2.dtype), _lib.stream_of(x2),
+    )
+    return dx, dw
+
+
+class RMSNormFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx: Any, x: Tensor, weight: Tensor, eps: float) -> Tensor:
+        if x.shape[-1] != weight.shape[0]:
+            raise ValueError(f"expected the last dimension to be {weight.shape[0]}, got {x.shape[-1]}")
+        if weight.dtype != x.dtype:
+            weight = weight.to(x.dtype)
+        x2 = x.reshape(-1, x.shape[-1]).contiguous()
+        y = rmsnorm_fwd(x2, weight.contiguous(), eps)
+        ctx.save_for_backward(x2, weight)
+        ctx.eps = eps
+        ctx.shape = x.shape
+        return y.view(x.shape)
+
+    @staticmethod
+    def backward(ctx: Any, dy: Tensor):
+        x2, weight = ctx.saved_tensors
+        dx, dw = rmsnorm_bwd(x2, weight, dy.reshape(x2.shape).contiguous(), ctx.eps)
+        return dx.view(ctx.shape), dw, None
+
+
+def rms_norm(x: Tensor, weight: Tensor, eps: float) -> Tensor:
+    return RMSNormFunction.apply(x, weight, eps)
+
+
+# ---------------------------------------------------------------- RoPE tables
+class RopeTables:
+    """fp32 cos/sin tables [n_pos, head_dim/2] on one device, grown on demand.
+
+    ``inv_freq`` is computed on the host exactly as nn/rotary.py:52 does; the
+    table rows are ``cos(p * inv_freq)`` / ``sin(p * inv_freq)`` computed by
+    ``nmb_rope_table``.  Because ``emb = cat(f, f)`` only half a row is kept.
+    """
+
+    _cache: dict[tuple, "RopeTables"] = {}
+    _lock = threading.Lock()
+
+    def __init__(self, device: torch.device, head_dim: int, theta: float) -> None:
+        self.device = device
+        self.head_dim = head_dim
+        self.theta = theta
+        inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
+        self.inv_freq = inv.to(device)
+        self.n_pos = 0
+        self.cos = self.sin = None
+
+    @classmethod
+    def get(cls, device: torch.device, head_dim: int, theta: float, n_pos: int) -> "RopeTables":
+        key = (device.type, device.index, head_dim, float(theta))
+        with cls._lock:
+            tab = cls._cache.get(key)
+            if tab is None:
+                tab = cls._cache[key] = RopeTables(device, head_dim, theta)
+            tab._ensure(n_pos)
+            return tab
+
+    def _ensure(self, n_pos: int) -> None:
+        if n_pos <= self.n_pos:
+            return
+        if self.device.type != "cuda":
+            raise ValueError("RoPE tables are built on the GPU only (there is no CPU fallback)")
+        n = 1 << max(10, int(math.ceil(math.log2(max(n_pos, 1)))))
+        half = self.head_dim // 2
+        cos = torch.empty(n, half, dtype=torch.float32, device=self.device)
+        sin = torch.empty_like(cos)
+        _lib.call(
+            "nmb_rope_table", cos.data_ptr(), sin.data_ptr(), self.inv_freq.data_ptr(), n, half,
+            _lib.stream_of(cos),
+        )
+        self.cos, self.sin, self.n_pos = cos, sin, n
+
+
+def rope_apply(
+    x: Tensor,
+    out: Tensor,
+    cos: Tensor,
+    sin: Tensor,
+    *,
+    pos_offset: int = 0,
+    positions: Tensor | None = None,
+    inverse: bool = False,
+) -> None:
+    """Rotate x [B, S, H, D] (any strides, last dim contiguous) into out.
+
+    cos/sin are fp32 [n_pos, D/2] tables; position of (b, s) is
+    positions[b, s] (int32 [S] or [B, S]) or pos_offset + s.
+    """
+    _require_gpu(x, out, cos, sin)
+    b, s, h, d = x.shape
+    if x.stride(3) != 1 or out.stride(3) != 1:
+        raise ValueError("rope_apply: head_dim must be the contiguous dimension")
+    pos_ptr, pos_bstride = None, 0
+    if positions is not None:
+        if positions.dtype != torch.int32:
+            raise ValueError("rope_apply: positions must be int32")
+        pos_ptr = positions.data_ptr()
+        pos_bstride = positions.stride(0) if positions.ndim == 2 else 0
+    _lib.call(
+        "nmb_rope_apply", x.data_ptr(), out.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+        cos.shape[0], pos_ptr, pos_bstride, int(pos_offset), b, s, h, d,
+        _lib.i64x3((x.stride(0), x.stride(1), x.stride(2))),
+        _lib.i64x3((out.stride(0), out.stride(1), out.stride(2))),
+        1 if inverse else 0, _lib.dtype_code(x.dtype), _lib.stream_of(x),
+    )
+
+
+def _bshd_view(t_bhsd: Tensor) -> Tensor:
+    """[B,H,S,D] tensor -> [B,S,H,D] view of the same memory."""
+    return t_bhsd.transpose(1, 2)
+
+
+def _new_bhsd(shape_bhsd: Sequence[int], like: Tensor) -> Tensor:
+    """Allocate a [B,H,S,D] tensor stored as [B,S,H,D] memory."""
+    b, h, s, d = shape_bhsd
+    return torch.empty(b, s, h, d, dtype=like.dtype, device=like.device).transpose(1, 2)
+
+
+def _canonical_bhsd(t: Tensor) -> Tensor:
+    """Return t ([B,H,S,D]) with [B,S,H,D]-contiguous memory, copying only if needed."""
+    b, h, s, d = t.shape
+    want = (s * h * d, d, h * d, 1)
+    if tuple(t.stride()) == want or t.numel() == 0:
+        return t
+    return t.transpose(1, 2).contiguous().transpose(1, 2)
+
+
+class RotaryFunction(torch.autograd.Function):
+    """``q*cos + rotate_half(q)*sin`` for one [B,H,S,D] tensor, backward by -theta."""
+
+    @staticmethod
+    def forward(ctx: Any, x: Tensor, cos: Tensor, sin: Tensor, positions: Tensor | None,
+                pos_offset: int) -> Tensor:
+        out = _new_bhsd(x.shape, x)
+        rope_apply(_bshd_view(x), _bshd_view(out), cos, sin, pos_offset=pos_offset,
+                   positions=positions)
+        ctx.save_for_backward(cos, sin, positions)
+        ctx.pos_offset = pos_offset
+        return out
+
+    @staticmethod
+    def backward(ctx: Any, grad: Tensor):
+        cos, sin, positions = ctx.saved_tensors
+        grad = _canonical_bhsd(grad)
+        dx = _new_bhsd(grad.shape, grad)
+        rope_apply(_bshd_view(grad), _bshd_view(dx), cos, sin, pos_offset=ctx.pos_offset,
+                   positions=positions, inverse=True)
+        return dx, None, None, None, None
+
+
+def rope_tables_from_cos_sin(
+    cos: Tensor, sin: Tensor, batch: int, seq: int
+) -> tuple[Tensor, Tensor, Tensor]:
+    """Turn reference-style cos/sin ([S,D] or [B,S,D], emb = cat(f, f)) into
+    fp32 half tables plus an int32 row index per (b, s)."""
+    half = cos.shape[-1] // 2
+    if cos.ndim == 2:
+        ct = cos[:, :half].float().contiguous()
+        st = sin[:, :half].float().contiguous()
+        pos = torch.arange(seq, dtype=torch.int32, device=cos.device)
+    elif cos.ndim == 3:
+        ct = cos[..., :half].float().reshape(-1, half).contiguous()
+        st = sin[..., :half].float().reshape(-1, half).contiguous()
+        pos = torch.arange(cos.shape[0] * seq, dtype=torch.int32, device=cos.device).view(-1, seq)
+    else:
+        raise ValueError(
+            "RoPE cos/sin tensors must have shape [sequence, head_dim] or "
+            f"[batch, sequence, head_dim], got {tuple(cos.shape)}"
+        )
+    return ct, st, pos
+
+
+# ---------------------------------------------------------------- SwiGLU
+def swiglu_fwd(g: Tensor, u: Tensor, out: Tensor | None = None) -> Tensor:
+    _require_gpu(g, u)
+    rows, cols = g.shape
+    if out is None:
+        out = torch.empty(rows, cols, dtype=g.dtype, device=g.device)
+    _lib.call(
+        "nmb_swiglu_fwd", g.data_ptr(), g.stride(0), u.data_ptr(), u.stride(0), out.data_ptr(),
+        out.stride(0), rows, cols, _lib.dtype_code(g.dtype), _lib.stream_of(g),
+    )
+    return out
+
+
+def swiglu_bwd(
+    g: Tensor, u: Tensor, dout: Tensor, dg: Tensor, du: Tensor, out: Tensor | None = None
+) -> None:
+    _require_gpu(g, u, dout, dg, du)
+    rows, cols = g.shape
+    _lib.call(
+        "nmb_swiglu_bwd", g.data_ptr(), g.stride(0), u.data_ptr(), u.stride(0), dout.data_ptr(),
+        dout.stride(0), dg.data_ptr(), dg.stride(0), du.data_ptr(), du.stride(0),
+        _lib.ptr(out), out.stride(0) if out is not None else cols, rows, cols,
+        _lib.dtype_code(g.dtype), _lib.stream_of(g),
+    )
+
+
+class SwiGLUFunction(torch.autograd.Function):
+    """``silu(gate) * up`` (models/gpt/mlp.py:77)."""
+
+    @staticmethod
+    def forward(ctx: Any, gate: Tensor, up: Tensor) -> Tensor:
+        if gate.shape != up.shape:
+            raise ValueError("gate and up must have the same shape")
+        shape = gate.shape
+        g2 = gate.reshape(-1, shape[-1]).contiguous()
+        u2 = up.reshape(-1, shape[-1]).contiguous()
+        out = swiglu_fwd(g2, u2)
+        ctx.save_for_backward(g2, u2)
+        ctx.shape = shape
+        return out.view(shape)
+
+    @staticmethod
+    def backward(ctx: Any, grad: Tensor):
+        g2, u2 = ctx.saved_tensors
+        d2 = grad.reshape(g2.shape).contiguous()
+        dg = torch.empty_like(g2)
+        du = torch.empty_like(u2)
+        swiglu_bwd(g2, u2, d2, dg, du)
+        return dg.view(ctx.shape), du.view(ctx.shape)
+
+
+def swiglu(gate: Tensor, up: Tensor) -> Tensor:
+    return SwiGLUFunction.apply(gate, up)
+
+
+# ---------------------------------------------------------------- attention
+def _check_attn(q: Tensor, ks: Sequence[Tensor], vs: Sequence[Tensor]) -> tuple[int, ...]:
+    if q.ndim != 4 or any(k.ndim != 4 for k in ks) or any(v.ndim != 4 for v in vs):
+        raise ValueError("q, k and v must have [batch, heads, sequence, head_dim] shape")
+    for k, v in zip(ks, vs):
+        if k.shape != v.shape:
+            raise ValueError("k and v must have identical shapes")
+        if k.shape != ks[0].shape:
+            raise ValueError("all K/V blocks must have the same shape")
+    k = ks[0]
+    if q.shape[0] != k.shape[0] or q.shape[-1] != k.shape[-1]:
+        raise ValueError("q and k/v must agree on batch size and head_dim")
+    if q.shape[1] % k.shape[1]:
+        raise ValueError(f"query heads ({q.shape[1]}) must be divisible by KV heads ({k.shape[1]})")
+    return q.shape[0], q.shape[1], k.shape[1], q.shape[2], k.shape[2], q.shape[3]
+
+
+def attn_fwd_bshd(
+    q: Tensor,
+    ks: Sequence[Tensor],
+    vs: Sequence[Tensor],
+    k_offsets: Sequence[int],
+    *,
+    causal: bool,
+    q_offset: int,
+    scale: float | None,
+    out: Tensor | None = None,
+    lse: Tensor | None = None,
+) -> tuple[Tensor, Tensor]:
+    """Attention over [B,S,H,D]-strided q and K/V blocks; returns (o [B,S,Hq,D], lse [B,Hq,S])."""
+    _require_gpu(q, *ks, *vs)
+    b, sq, hq, d = q.shape
+    _, sk, hkv, _ = ks[0].shape
+    if out is None:
+        out = torch.empty(b, sq, hq, d, dtype=q.dtype, device=q.device)
+    if lse is None:
+        lse = torch.empty(b, hq, sq, dtype=torch.float32, device=q.device)
+    kv_strides = (ks[0].stride(0), ks[0].stride(1), ks[0].stride(2))
+    for t in (*ks, *vs):
+        if (t.stride(0), t.stride(1), t.stride(2)) != kv_strides or t.stride(3) != 1:
+            raise ValueError("attention: all K/V blocks must share one [B,S,H,D] stride layout")
+    if q.stride(3) != 1 or out.stride(3) != 1:
+        raise ValueError("attention: head_dim must be the contiguous dimension")
+    _lib.call(
+        "nmb_attn_fwd", q.data_ptr(), _lib.ptr_array(k.data_ptr() for k in ks),
+        _lib.ptr_array(v.data_ptr() for v in vs), _lib.i64_array(k_offsets), len(ks),
+        out.data_ptr(), lse.data_ptr(), b, hq, hkv, sq, sk, d,
+        _lib.i64x3(q.stride()[:3]), _lib.i64x3(kv_strides), _lib.i64x3(out.stride()[:3]),
+        1 if causal else 0, int(q_offset), float(scale) if scale else 0.0,
+        _lib.dtype_code(q.dtype), _lib.stream_of(q),
+    )
+    return out, lse
+
+
+def attn_bwd_bshd(
+    q: Tensor,
+    ks: Sequence[Tensor],
+    vs: Sequence[Tensor],
+    k_offsets: Sequence[int],
+    o: Tensor,
+    do: Tensor,
+    lse: Tensor,
+    dq: Tensor,
+    dks: Sequence[Tensor],
+    dvs: Sequence[Tensor],
+    *,
+    causal: bool,
+    q_offset: int,
+    scale: float | None,
+) -> None:
+    """Backward of attn_fwd_bshd into caller-provided dq / dK / dV (same strides as q / K / V)."""
+    _require_gpu(q, o, do, lse, dq)
+    b, sq, hq, d = q.shape
+    _, sk, hkv, _ = ks[0].shape
+    kv_strides = (ks[0].stride(0), ks[0].stride(1), ks[0].stride(2))
+    for t in (*ks, *vs, *dks, *dvs):
+        if (t.stride(0), t.stride(1), t.stride(2)) != kv_strides:
+            raise ValueError("attention backward: K, V, dK, dV must share one stride layout")
+    if tuple(dq.stride()) != tuple(q.stride()) or tuple(do.stride()) != tuple(o.stride()):
+        raise ValueError("attention backward: dq must match q's strides and dO must match O's")
+    nbytes = _lib.ctypes.c_size_t(0)
+    _lib.call("nmb_attn_bwd_workspace_bytes", b, hq, sq, _lib.ctypes.byref(nbytes))
+    ws = _workspace(nbytes.value, q.device)
+    _lib.call(
+        "nmb_attn_bwd", q.data_ptr(), _lib.ptr_array(k.data_ptr() for k in ks),
+        _lib.ptr_array(v.data_ptr() for v in vs), _lib.i64_array(k_offsets), len(ks),
+        o.data_ptr(), do.data_ptr(), lse.data_ptr(), dq.data_ptr(),
+        _lib.ptr_array(t.data_ptr() for t in dks), _lib.ptr_array(t.data_ptr() for t in dvs),
+        ws.data_ptr(), ws.numel(), b, hq, hkv, sq, sk, d,
+        _lib.i64x3(q.stride()[:3]), _lib.i64x3(kv_strides), _lib.i64x3(o.stride()[:3]),
+        1 if causal else 0, int(q_offset), float(scale) if scale else 0.0,
+        _lib.dtype_code(q.dtype), _lib.stream_of(q),
+    )
+
+
+class AttentionFunction(torch.autograd.Function):
+    """Attention over K/V blocks for [B,H,S,D] tensors (views of [B,S,H,D] memory).
+
+    One block with offset 0 is ``local_attention`` (nn/kernels/torch_backend.py:25-76,
+    key positions arange(Sk), query positions sequence_offset + arange(Sq)); several
+    blocks with absolute key offsets are one ring rank's share
+    (context_parallel/ring.py:104-250).  Saves only q, K/V, the output and the lse.
+    """
+
+    @staticmethod
+    def forward(ctx: Any, q: Tensor, causal: bool, q_offset: int, scale: float | None,
+                k_offsets: tuple[int, ...], *kv: Tensor) -> Tensor:
+        n = len(kv) // 2
+        ks = [_canonical_bhsd(t) for t in kv[:n]]
+        vs = [_canonical_bhsd(t) for t in kv[n:]]
+        _check_attn(q, ks, vs)
+        q = _canonical_bhsd(q)
+        o, lse = attn_fwd_bshd(
+            _bshd_view(q), [_bshd_view(k) for k in ks], [_bshd_view(v) for v in vs], k_offsets,
+            causal=causal, q_offset=q_offset, scale=scale,
+        )
+        o_bhsd = o.transpose(1, 2)
+        ctx.save_for_backward(q, o_bhsd, lse, *ks, *vs)
+        ctx.meta = (causal, q_offset, scale, tuple(k_offsets), n)
+        return o_bhsd
+
+    @staticmethod
+    def backward(ctx: Any, grad: Tensor):
+        causal, q_offset, scale, k_offsets, n = ctx.meta
+        q, o, lse, *kv = ctx.saved_tensors
+        ks, vs = kv[:n], kv[n:]
+        do = _canonical_bhsd(grad)
+        dq = _new_bhsd(q.shape, q)
+        dks = [_new_bhsd(k.shape, k) for k in ks]
+        dvs = [_new_bhsd(v.shape, v) for v in vs]
+        attn_bwd_bshd(
+            _bshd_view(q), [_bshd_view(k) for k in ks], [_bshd_view(v) for v in vs], k_offsets,
+            _bshd_view(o), _bshd_view(do), lse, _bshd_view(dq),
+            [_bshd_view(t) for t in dks], [_bshd_view(t) for t in dvs],
+            causal=causal, q_offset=q_offset, scale=scale,
+        )
+        return (dq, None, None, None, None, *dks, *dvs)
+
+
+def attention(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    *,
+    causal: bool = True,
+    sequence_offset: int = 0,
+    scale: float | None = None,
+) -> Tensor:
+    """``local_attention`` for [B,H,S,D] tensors, GQA without repeated K/V."""
+    _check_attn(q, [k], [v])
+    return AttentionFunction.apply(q, causal, int(sequence_offset), scale, (0,), k, v)
+
+
+def ring_attention(
+    q: Tensor,
+    kv_blocks: Sequence[tuple[Tensor, Tensor]],
+    key_offsets: Sequence[int],
+    *,
+    causal: bool = True,
+    query_offset: int = 0,
+    scale: float | None = None,
+) -> Tensor:
+    """One context-parallel rank's attention over streamed K/V blocks, merged by
+    online softmax in one kernel (context_parallel/ring.py:104-250 on one GPU)."""
+    if not 1 <= len(kv_blocks) <= 8:
+        raise ValueError("ring_attention supports 1 to 8 K/V blocks")
+    ks = [k for k, _ in kv_blocks]
+    vs = [v for _, v in kv_blocks]
+    _check_attn(q, ks, vs)
+    return AttentionFunction.apply(
+        q, causal, int(query_offset), scale, tuple(int(o) for o in key_offsets), *ks, *vs
+    )
+
+
+# ---------------------------------------------------------------- LM head + CE
+def ce_fwd(logits2: Tensor, targets: Tensor, ignore_index: int, loss: Tensor, lse: Tensor) -> None:
+    rows, vocab = logits2.shape
+    _lib.call(
+        "nmb_ce_fwd", logits2.data_ptr(), logits2.stride(0), targets.data_ptr(), rows, vocab,
+        int(ignore_index), loss.data_ptr(), lse.data_ptr(), _lib.dtype_code(logits2.dtype),
+        _lib.stream_of(logits2),
+    )
+
+
+def ce_bwd_(logits2: Tensor, targets: Tensor, ignore_index: int, lse: Tensor, grad: Tensor) -> None:
+    rows, vocab = logits2.shape
+    _lib.call(
+        "nmb_ce_bwd", logits2.data_ptr(), logits2.stride(0), targets.data_ptr(), rows, vocab,
+        int(ignore_index), lse.data_ptr(), grad.data_ptr(), _lib.dtype_code(logits2.dtype),
+        _lib.stream_of(logits2),
+    )
+
+
+def _chunks(rows: int, chunk: int):
+    for start in range(0, rows, chunk):
+        yield start, min(rows, start + chunk)
+
+
+class LMHeadCrossEntropyFunction(torch.autograd.Function):
+    """Tied LM head + token cross entropy without full logits.
+
+    Forward, per token chunk: logits = x_c E^T (one GEMM into a [chunk, V]
+    buffer), then ``nmb_ce_fwd`` -> per-token loss and lse.  Only lse is kept.
+    Backward, per chunk: recompute the chunk's logits, ``nmb_ce_bwd`` turns them
+    in place into G = (softmax - onehot) * grad, then dx_c = G E and
+    dE += G^T x_c (fixed chunk order: deterministic).  Matches
+    VocabParallelLinear + _VocabParallelCrossEntropy at TP=1
+    (tensor_parallel/layers.py:207-214, cross_entropy.py:30-86).
+    """
+
+    @staticmethod
+    def forward(ctx: Any, x2: Tensor, weight: Tensor, targets: Tensor, ignore_index: int,
+                chunk: int) -> Tensor:
+        _require_gpu(x2, weight, targets)
+        rows = x2.shape[0]
+        loss = torch.empty(rows, dtype=torch.float32, device=x2.device)
+        lse = torch.empty_like(loss)
+        buf = torch.empty(min(chunk, max(rows, 1)), weight.shape[0], dtype=x2.dtype, device=x2.device)
+        for s, e in _chunks(rows, chunk):
+            logits = buf[: e - s]
+            torch.mm(x2[s:e], weight.t(), out=logits)
+            ce_fwd(logits, targets[s:e], ignore_index, loss[s:e], lse[s:e])
+        ctx.save_for_backward(x2, weight, targets, lse)
+        ctx.ignore_index = ignore_index
+        ctx.chunk = chunk
+        return loss
+
+    @staticmethod
+    def backward(ctx: Any, grad_loss: Tensor):
+        x2, weight, targets, lse = ctx.saved_tensors
+        grad_loss = grad_loss.float().contiguous()
+        rows = x2.shape[0]
+        dx = torch.empty_like(x2)
+        dw = torch.zeros_like(weight)
+        buf = torch.empty(min(ctx.chunk, max(rows, 1)), weight.shape[0], dtype=x2.dtype,
+                          device=x2.device)
+        for s, e in _chunks(rows, ctx.chunk):
+            g = buf[: e - s]
+            torch.mm(x2[s:e], weight.t(), out=g)
+            ce_bwd_(g, targets[s:e], ctx.ignore_index, lse[s:e], grad_loss[s:e])
+            torch.mm(g, weight, out=dx[s:e])
+            dw.addmm_(g.t(), x2[s:e])
+        return dx, dw, None, None, None
+
+
+def lm_head_cross_entropy(
+    hidden: Tensor,
+    weight: Tensor,
+    targets: Tensor,
+    *,
+    ignore_index: int = IGNORE_INDEX,
+    reduction: str = "mean",
+    chunk: int = 2048,
+    validate: bool = True,
+) -> Tensor:
+    """Loss of ``F.linear(hidden, weight)`` under VocabParallelCrossEntropy
+    (tensor_parallel/cross_entropy.py:89-123) without materialising logits."""
+    if reduction not in ("none", "mean", "sum"):
+        raise ValueError(f"unsupported reduction: {reduction}")
+    if hidden.shape[:-1] != targets.shape:
+        raise ValueError(
+            "targets must match all non-vocabulary logits dimensions: "
+            f"hidden={tuple(hidden.shape)}, targets={tuple(targets.shape)}"
+        )
+    vocab = weight.shape[0]
+    if validate:
+        invalid = (targets != ignore_index) & ((targets < 0) | (targets >= vocab))
+        if torch.any(invalid):
+            raise ValueError("targets contain ids outside the original (unpadded) vocabulary")
+    x2 = hidden.reshape(-1, hidden.shape[-1]).contiguous()
+    t1 = targets.reshape(-1).to(torch.int64).contiguous()
+    loss = LMHeadCrossEntropyFunction.apply(x2, weight, t1, int(ignore_index), int(chunk))
+    if reduction == "none":
+        return loss.view(targets.shape)
+    if reduction == "sum":
+        return loss.sum()
+    valid = (t1 != ignore_index).sum().clamp_min(1)
+    return loss.sum() / valid

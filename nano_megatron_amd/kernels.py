@@ -1,0 +1,81 @@
+"""The kernel-backend seam with the MI355X backend behind it.
+
+Mirrors nn/kernels/interface.py:10-25 (the ``KernelBackend`` protocol) and
+nn/kernels/__init__.py:11-22 (``build_kernel_backend``).  ``HipKernelBackend``
+is the drop-in for ``TorchKernelBackend`` (nn/kernels/torch_backend.py:14-76):
+same members, argument meanings and exceptions.
+"""
+
+from __future__ import annotations
+
+from typing import Any, Protocol
+
+from torch import Tensor, nn
+
+from nano_megatron_amd import functional as Fn
+from nano_megatron_amd.nn import RMSNorm
+
+
+class KernelBackend(Protocol):
+    name: str
+
+    def linear(self, in_features: int, out_features: int, **kwargs: Any) -> nn.Module: ...
+
+    def rms_norm(self, hidden_size: int, eps: float, **kwargs: Any) -> nn.Module: ...
+
+    def local_attention(self, q: Tensor, k: Tensor, v: Tensor, **kwargs: Any) -> Tensor: ...
+
+
+class HipKernelBackend:
+    """gfx950 kernels: fused RMSNorm, MFMA attention; library GEMMs for ``linear``."""
+
+    name = "hip"
+
+    def linear(self, in_features: int, out_features: int, **kwargs: Any) -> nn.Module:
+        # A plain dense projection: the module (and its kaiming-uniform init, so
+        # seeded weights equal the reference's) is nn.Linear, whose GEMM runs on
+        # MFMA through hipBLASLt.
+        return nn.Linear(in_features, out_features, **kwargs)
+
+    def rms_norm(self, hidden_size: int, eps: float, **kwargs: Any) -> nn.Module:
+        return RMSNorm(hidden_size, eps, **kwargs)
+
+    def local_attention(
+        self,
+        q: Tensor,
+        k: Tensor,
+        v: Tensor,
+        *,
+        causal: bool = True,
+        sequence_offset: int = 0,
+        dropout_p: float = 0.0,
+        scale: float | None = None,
+        attention_mask: Tensor | None = None,
+        **_: Any,
+    ) -> Tensor:
+        """Attention for [B,H,S,D] tensors; GQA reads KV heads in place (no repeat)."""
+        if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+            raise ValueError("q, k and v must have [batch, heads, sequence, head_dim] shape")
+        if k.shape != v.shape:
+            raise ValueError("k and v must have identical shapes")
+        if q.shape[0] != k.shape[0] or q.shape[-1] != k.shape[-1]:
+            raise ValueError("q and k/v must agree on batch size and head_dim")
+        if q.shape[1] % k.shape[1]:
+            raise ValueError(
+                f"query heads ({q.shape[1]}) must be divisible by KV heads ({k.shape[1]})"
+            )
+        if dropout_p:
+            raise ValueError("the hip backend implements attention dropout_p = 0 only")
+        if attention_mask is not None:
+            raise ValueError("the hip backend implements the causal/offset mask, not arbitrary masks")
+        return Fn.attention(q, k, v, causal=causal, sequence_offset=sequence_offset, scale=scale)
+
+
+def build_kernel_backend(config: Any, parallel: Any = None) -> KernelBackend:
+    """nn/kernels/__init__.py:11-22 with the "hip" value."""
+    del parallel
+    backend = getattr(config, "backend", config)
+    value = getattr(backend, "value", backend)
+    if value == "hip":
+        return HipKernelBackend()
+    raise ValueError(f"unknown kernel backend: {value!r}")

@@ -1,0 +1,99 @@
+"""The C ABI (include/nmb.h) on the CPU: the library loads, exports every
+declared symbol, and rejects bad arguments with a status and a message before
+any device work (no kernel is launched by these tests)."""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import re
+
+import pytest
+import torch
+
+from nano_megatron_amd import _lib
+
+HEADER = pathlib.Path(__file__).resolve().parents[1] / "include" / "nmb.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    return re.findall(r"^\s*(?:const\s+char\s*\*|int)\s+(nmb_\w+)\s*\(", text, flags=re.M)
+
+
+def test_header_declares_the_boundary() -> None:
+    names = declared_functions()
+    for expected in ("nmb_rmsnorm_fwd", "nmb_rmsnorm_bwd", "nmb_rope_apply", "nmb_swiglu_fwd",
+                     "nmb_swiglu_bwd", "nmb_attn_fwd", "nmb_attn_bwd", "nmb_ce_fwd", "nmb_ce_bwd",
+                     "nmb_last_error"):
+        assert expected in names
+
+
+def test_library_exports_every_declared_symbol() -> None:
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert lib.nmb_abi_version() == 1
+
+
+FAKE = 256  # a non-null, 16-byte aligned address that is never dereferenced
+
+
+def test_rmsnorm_rejects_bad_arguments_without_launch() -> None:
+    lib = _lib.load()
+    st = lib.nmb_rmsnorm_fwd(FAKE, FAKE, FAKE, None, 4, 12, 1e-5, _lib.NMB_BF16, None)
+    assert st == _lib.NMB_EUNSUPPORTED
+    assert b"multiple of 8" in lib.nmb_last_error()
+    st = lib.nmb_rmsnorm_fwd(FAKE, FAKE, FAKE, None, 4, 64, 0.0, _lib.NMB_BF16, None)
+    assert st == _lib.NMB_EINVAL and b"eps" in lib.nmb_last_error()
+    st = lib.nmb_rmsnorm_fwd(None, FAKE, FAKE, None, 4, 64, 1e-5, _lib.NMB_BF16, None)
+    assert st == _lib.NMB_EINVAL
+    st = lib.nmb_rmsnorm_fwd(FAKE, FAKE, FAKE, None, 4, 64, 1e-5, 7, None)
+    assert st == _lib.NMB_EUNSUPPORTED
+    nbytes = ctypes.c_size_t(0)
+    assert lib.nmb_rmsnorm_bwd_workspace_bytes(8192, 1024, ctypes.byref(nbytes)) == 0
+    assert nbytes.value > 0 and nbytes.value % 4 == 0
+    st = lib.nmb_rmsnorm_bwd(FAKE, FAKE, FAKE, None, FAKE, FAKE, FAKE, 4, 8192, 1024, 1e-5,
+                             _lib.NMB_BF16, None)
+    assert st == _lib.NMB_EINVAL and b"workspace" in lib.nmb_last_error()
+
+
+def test_attention_rejects_bad_arguments_without_launch() -> None:
+    lib = _lib.load()
+    strides = _lib.i64x3((1024, 64, 64))
+    ptrs = _lib.ptr_array([FAKE])
+    offs = _lib.i64_array([0])
+    st = lib.nmb_attn_fwd(FAKE, ptrs, ptrs, offs, 1, FAKE, FAKE, 1, 6, 4, 16, 16, 64,
+                          strides, strides, strides, 1, 0, 0.0, _lib.NMB_BF16, None)
+    assert st == _lib.NMB_EINVAL
+    assert b"must be divisible by KV heads" in lib.nmb_last_error()
+    st = lib.nmb_attn_fwd(FAKE, ptrs, ptrs, offs, 1, FAKE, FAKE, 1, 4, 4, 16, 16, 96,
+                          strides, strides, strides, 1, 0, 0.0, _lib.NMB_BF16, None)
+    assert st == _lib.NMB_EUNSUPPORTED and b"head_dim" in lib.nmb_last_error()
+    st = lib.nmb_attn_fwd(FAKE, ptrs, ptrs, offs, 9, FAKE, FAKE, 1, 4, 4, 16, 16, 64,
+                          strides, strides, strides, 1, 0, 0.0, _lib.NMB_BF16, None)
+    assert st == _lib.NMB_EINVAL and b"n_blocks" in lib.nmb_last_error()
+
+
+def test_rope_and_swiglu_and_ce_reject_bad_arguments() -> None:
+    lib = _lib.load()
+    s = _lib.i64x3((0, 0, 0))
+    st = lib.nmb_rope_apply(FAKE, FAKE, FAKE, FAKE, 16, None, 0, 0, 1, 4, 1, 7, s, s, 0,
+                            _lib.NMB_F32, None)
+    assert st == _lib.NMB_EINVAL and b"even" in lib.nmb_last_error()
+    st = lib.nmb_rope_apply(FAKE, FAKE, FAKE, FAKE, 16, None, 0, 10, 1, 8, 1, 64,
+                            _lib.i64x3((512, 64, 64)), _lib.i64x3((512, 64, 64)), 0,
+                            _lib.NMB_BF16, None)
+    assert st == _lib.NMB_EINVAL and b"exceed" in lib.nmb_last_error()
+    st = lib.nmb_swiglu_fwd(FAKE, 10, FAKE, 10, FAKE, 10, 4, 10, _lib.NMB_BF16, None)
+    assert st == _lib.NMB_EUNSUPPORTED
+    st = lib.nmb_ce_fwd(FAKE, 4, FAKE, 2, 8, -100, FAKE, FAKE, _lib.NMB_F32, None)
+    assert st == _lib.NMB_EINVAL
+
+
+def test_python_wrapper_maps_status_to_exceptions() -> None:
+    with pytest.raises(ValueError, match="multiple of 8"):
+        _lib.call("nmb_rmsnorm_fwd", FAKE, FAKE, FAKE, None, 4, 12, 1e-5, _lib.NMB_BF16, None)
+    with pytest.raises(ValueError):
+        _lib.dtype_code(torch.float16)

@@ -1,0 +1,248 @@
+"""Kernel parity on the GPU: each HIP op against the CPU oracle on the same
+seeded inputs (fp32: rtol 1e-5; bf16: rtol 2e-2 / atol 1e-2), edge cases
+(ragged sizes, GQA, offsets, masks, ignored targets) and determinism."""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+import nano_megatron_amd as nm
+from nano_megatron_amd import functional as Fn
+from oracle import reference as R
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = dict(rtol=1e-5, atol=1e-5)
+BF16_TOL = dict(rtol=2e-2, atol=1e-2)
+
+
+def tol(dtype):
+    return F32_TOL if dtype == torch.float32 else BF16_TOL
+
+
+def close(got, exp, dtype, scale_atol=False, msg=""):
+    t = dict(tol(dtype))
+    if scale_atol:  # gradients: atol relative to the tensor's magnitude
+        t["atol"] = t["atol"] * max(1.0, float(exp.abs().max()))
+    torch.testing.assert_close(got.detach().float().cpu(), exp.detach().float(), msg=msg, **t)
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# ---------------------------------------------------------------- RMSNorm
+@pytest.mark.parametrize("rows,cols,dtype", [
+    (8192, 1024, torch.bfloat16), (512, 256, torch.float32), (37, 2048, torch.bfloat16),
+    (3, 64, torch.float32), (1, 4096, torch.bfloat16),
+])
+def test_rmsnorm_matches_oracle(device, rows, cols, dtype) -> None:
+    g = gen(1)
+    x = torch.randn(rows, cols, generator=g).to(dtype)
+    w = (1 + 0.02 * torch.randn(cols, generator=g)).to(dtype)
+    dy = torch.randn(rows, cols, generator=g).to(dtype)
+    xr, wr = x.clone().requires_grad_(True), w.clone().requires_grad_(True)
+    yr = R.rms_norm(xr, wr, 1e-5)
+    yr.backward(dy)
+    xd, wd = x.to(device).requires_grad_(True), w.to(device).requires_grad_(True)
+    yd = nm.rms_norm(xd, wd, 1e-5)
+    yd.backward(dy.to(device))
+    close(yd, yr, dtype)
+    close(xd.grad, xr.grad, dtype, scale_atol=True)
+    close(wd.grad, wr.grad, dtype, scale_atol=True)
+    if dtype == torch.bfloat16:
+        # forward rounding points replicated: nearly every element bit-equal
+        eq = (yd.cpu() == yr).float().mean().item()
+        assert eq > 0.99, eq
+
+
+# ---------------------------------------------------------------- RoPE
+@pytest.mark.parametrize("shape,dtype", [
+    ((16, 16, 512, 64), torch.bfloat16), ((2, 4, 128, 64), torch.float32),
+    ((1, 3, 33, 128), torch.bfloat16),
+])
+def test_rope_matches_oracle(device, shape, dtype) -> None:
+    g = gen(1)
+    b, h, s, d = shape
+    q = torch.randn(b, s, h, d, generator=g).to(dtype).transpose(1, 2)
+    k = torch.randn(b, s, max(1, h // 2), d, generator=g).to(dtype).transpose(1, 2)
+    cos, sin = R.rope_cos_sin(torch.arange(s), d, 1e4, dtype)
+    qr, kr = q.clone().requires_grad_(True), k.clone().requires_grad_(True)
+    oq, ok = R.apply_rotary_pos_emb(qr, kr, cos, sin)
+    gq, gk = torch.randn_like(oq), torch.randn_like(ok)
+    (oq * gq).sum().backward(retain_graph=True)
+    (ok * gk).sum().backward()
+    rope = nm.RotaryEmbedding(d)
+    dcos, dsin = rope(torch.arange(s, device=device), dtype=dtype)
+    close(dcos, cos, dtype)
+    qd, kd = q.to(device).requires_grad_(True), k.to(device).requires_grad_(True)
+    pq, pk = nm.apply_rotary_pos_emb(qd, kd, dcos, dsin)
+    (pq * gq.to(device)).sum().backward(retain_graph=True)
+    (pk * gk.to(device)).sum().backward()
+    close(pq, oq, dtype)
+    close(pk, ok, dtype)
+    close(qd.grad, qr.grad, dtype)
+    close(kd.grad, kr.grad, dtype)
+
+
+def test_rope_offset_positions_and_inverse(device) -> None:
+    """Offset form (positions offset + s) equals explicit ids; inverse undoes forward."""
+    g = gen(2)
+    x = torch.randn(2, 40, 3, 64, generator=g).to(device)
+    tab = Fn.RopeTables.get(device, 64, 1e4, 200)
+    a = torch.empty_like(x)
+    Fn.rope_apply(x, a, tab.cos, tab.sin, pos_offset=100)
+    pos = torch.arange(100, 140, dtype=torch.int32, device=device)
+    b = torch.empty_like(x)
+    Fn.rope_apply(x, b, tab.cos, tab.sin, positions=pos)
+    assert torch.equal(a, b)
+    back = torch.empty_like(x)
+    Fn.rope_apply(a, back, tab.cos, tab.sin, pos_offset=100, inverse=True)
+    torch.testing.assert_close(back, x, rtol=1e-5, atol=1e-5)
+
+
+# ---------------------------------------------------------------- SwiGLU
+@pytest.mark.parametrize("rows,cols,dtype", [
+    (8192, 2736, torch.bfloat16), (512, 688, torch.float32), (13, 5632, torch.bfloat16),
+])
+def test_swiglu_matches_oracle(device, rows, cols, dtype) -> None:
+    g0 = gen(1)
+    gate = torch.randn(rows, cols, generator=g0).to(dtype)
+    up = torch.randn(rows, cols, generator=g0).to(dtype)
+    dh = torch.randn(rows, cols, generator=g0).to(dtype)
+    gr, ur = gate.clone().requires_grad_(True), up.clone().requires_grad_(True)
+    hr = R.swiglu(gr, ur)
+    hr.backward(dh)
+    gd, ud = gate.to(device).requires_grad_(True), up.to(device).requires_grad_(True)
+    hd = nm.swiglu(gd, ud)
+    hd.backward(dh.to(device))
+    close(hd, hr, dtype)
+    close(gd.grad, gr.grad, dtype, scale_atol=True)
+    close(ud.grad, ur.grad, dtype, scale_atol=True)
+    # fused recompute-backward re-emits h bit-identically to the forward
+    dg, du, h2 = (torch.empty_like(gd) for _ in range(3))
+    Fn.swiglu_bwd(gd.detach(), ud.detach(), dh.to(device), dg, du, h2)
+    assert torch.equal(h2, hd.detach())
+
+
+# ---------------------------------------------------------------- attention
+ATTN_CASES = [
+    # b, hq, hkv, sq, sk, d, dtype, offset, causal
+    (2, 4, 4, 128, 128, 64, torch.bfloat16, 0, True),
+    (1, 4, 2, 200, 200, 64, torch.bfloat16, 0, True),
+    (1, 2, 2, 96, 96, 128, torch.bfloat16, 0, True),
+    (1, 4, 4, 64, 80, 64, torch.bfloat16, 0, False),
+    (1, 2, 1, 64, 128, 64, torch.bfloat16, 64, True),
+    (2, 4, 2, 100, 100, 64, torch.float32, 0, True),
+    (1, 2, 2, 48, 112, 64, torch.float32, 64, True),
+    (1, 8, 2, 256, 256, 128, torch.bfloat16, 0, True),
+]
+
+
+@pytest.mark.parametrize("b,hq,hkv,sq,sk,d,dtype,offset,causal", ATTN_CASES)
+def test_attention_matches_oracle(device, b, hq, hkv, sq, sk, d, dtype, offset, causal) -> None:
+    g = gen(1)
+    q = torch.randn(b, hq, sq, d, generator=g).to(dtype)
+    k = torch.randn(b, hkv, sk, d, generator=g).to(dtype)
+    v = torch.randn(b, hkv, sk, d, generator=g).to(dtype)
+    do = torch.randn(b, hq, sq, d, generator=g).to(dtype)
+    qr, kr, vr = (t.clone().requires_grad_(True) for t in (q, k, v))
+    if causal:
+        # SDPA's offset mask uses key positions 0..Sk-1 and query positions offset + i
+        o_ref = R.local_attention(qr, kr, vr, causal=True, sequence_offset=offset)
+    else:
+        o_ref = R.local_attention(qr, kr, vr, causal=False)
+    o_ref.backward(do)
+    qd, kd, vd = (t.to(device).requires_grad_(True) for t in (q, k, v))
+    o = nm.attention(qd, kd, vd, causal=causal, sequence_offset=offset)
+    o.backward(do.to(device))
+    close(o, o_ref, dtype)
+    close(qd.grad, qr.grad, dtype, scale_atol=True, msg="dq")
+    close(kd.grad, kr.grad, dtype, scale_atol=True, msg="dk")
+    close(vd.grad, vr.grad, dtype, scale_atol=True, msg="dv")
+
+
+def test_attention_c3_shape_and_lse(device) -> None:
+    """Config 3 attention shape [16,16,512,64] bf16; lse == logsumexp of masked scores."""
+    g = gen(1)
+    b, h, s, d = 16, 16, 512, 64
+    q = torch.randn(b, s, h, d, generator=g).bfloat16()
+    k = torch.randn(b, s, h, d, generator=g).bfloat16()
+    v = torch.randn(b, s, h, d, generator=g).bfloat16()
+    o, lse = Fn.attn_fwd_bshd(q.to(device), [k.to(device)], [v.to(device)], (0,), causal=True,
+                              q_offset=0, scale=None)
+    ref = R.local_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2))
+    close(o.transpose(1, 2), ref, torch.bfloat16)
+    qf, kf = q[:2].float().transpose(1, 2), k[:2].float().transpose(1, 2)
+    scores = qf @ kf.transpose(-1, -2) / math.sqrt(d)
+    mask = torch.ones(s, s, dtype=torch.bool).tril()
+    ref_lse = scores.masked_fill(~mask, -math.inf).logsumexp(-1)
+    torch.testing.assert_close(lse[:2].cpu(), ref_lse, rtol=1e-3, atol=2e-3)
+
+
+def test_attention_is_deterministic(device) -> None:
+    g = gen(3)
+    q, k, v, do = (torch.randn(2, 8, 256, 64, generator=g).bfloat16().to(device) for _ in range(4))
+    outs = []
+    for _ in range(2):
+        qd, kd, vd = (t.clone().requires_grad_(True) for t in (q, k, v))
+        o = nm.attention(qd, kd, vd)
+        o.backward(do)
+        outs.append((o.detach(), qd.grad, kd.grad, vd.grad))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("d,dtype", [(128, torch.bfloat16), (64, torch.float32)])
+def test_ring_share_matches_oracle(device, d, dtype) -> None:
+    """One rank (r=3 of 4) of the ring: blocks visited (3 - s) % 4, block-causal."""
+    g = gen(1)
+    s, h, hkv, rank = 192, 4, 2, 3
+    q = torch.randn(1, h, s, d, generator=g).to(dtype)
+    blocks = [(torch.randn(1, hkv, s, d, generator=g).to(dtype), torch.randn(1, hkv, s, d, generator=g).to(dtype))
+              for _ in range(4)]
+    order = [(rank - step) % 4 for step in range(4)]
+    offsets = [r * s for r in order]
+    kvs = [blocks[r] for r in order]
+    out_ref, lse_ref = R.ring_attention_forward(q, kvs, offsets, causal=True, query_offset=rank * s)
+    do = torch.randn(1, h, s, d, generator=g).to(dtype)
+    dq_ref, dk_ref, dv_ref = R.ring_attention_backward(do, q, kvs, offsets, out_ref, lse_ref,
+                                                       causal=True, query_offset=rank * s)
+    qd = q.to(device).requires_grad_(True)
+    kd = [(k.to(device).requires_grad_(True), v.to(device).requires_grad_(True)) for k, v in kvs]
+    o = nm.ring_attention(qd, kd, offsets, causal=True, query_offset=rank * s)
+    o.backward(do.to(device))
+    close(o, out_ref, dtype)
+    close(qd.grad, dq_ref, dtype, scale_atol=True)
+    for (k, v), dk, dv in zip(kd, dk_ref, dv_ref):
+        close(k.grad, dk, dtype, scale_atol=True)
+        close(v.grad, dv, dtype, scale_atol=True)
+
+
+# ---------------------------------------------------------------- LM head + CE
+@pytest.mark.parametrize("rows,hidden,vocab,dtype,chunk", [
+    (512, 256, 8192, torch.float32, 200), (1024, 1024, 8192, torch.bfloat16, 384),
+    (64, 128, 1000, torch.float32, 64),
+])
+def test_lm_head_cross_entropy_matches_oracle(device, rows, hidden, vocab, dtype, chunk) -> None:
+    g = gen(1)
+    x = torch.randn(rows, hidden, generator=g).to(dtype)
+    e = (0.02 * torch.randn(vocab, hidden, generator=g)).to(dtype)
+    t = torch.randint(0, vocab, (rows,), generator=g)
+    t[::7] = -100
+    xr, er = x.clone().requires_grad_(True), e.clone().requires_grad_(True)
+    lr = R.cross_entropy_tokens(torch.nn.functional.linear(xr, er), t, reduction="mean")
+    lr.backward()
+    xd, ed = x.to(device).requires_grad_(True), e.to(device).requires_grad_(True)
+    ld = nm.lm_head_cross_entropy(xd, ed, t.to(device), chunk=chunk)
+    ld.backward()
+    close(ld, lr, dtype)
+    close(xd.grad, xr.grad, dtype, scale_atol=True)
+    close(ed.grad, er.grad, dtype, scale_atol=True)
+    per_tok = nm.lm_head_cross_entropy(xd.detach(), ed.detach(), t.to(device), reduction="none", chunk=chunk)
+    assert torch.all(per_tok.cpu()[t == -100] == 0)
+    with pytest.raises(ValueError, match="outside"):
+        nm.lm_head_cross_entropy(xd.detach(), ed.detach(), torch.full_like(t, vocab).to(device))
