@@ -104,18 +104,23 @@ def run_steps(mode: str, steps: int, warmup: int, device) -> dict:
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    # memory: activations = peak during a step minus what is resident at its start
+    # Activation memory (training/trainer.py:583-585, 752-776 definitions): with
+    # the gradients of the previous step kept allocated (zeroed in place), the
+    # peak during forward+backward minus what was resident at its start, and the
+    # memory the forward leaves saved for the backward.
+    for p in opt.params:
+        p.grad = torch.zeros_like(p)
+    torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
     start_alloc = torch.cuda.memory_allocated()
-    opt.zero_grad()
     out = model(x, labels=y)
     torch.cuda.synchronize()
     saved_after_fwd = torch.cuda.memory_allocated() - start_alloc
     out.loss.backward()
-    opt.step()
     torch.cuda.synchronize()
     peak = torch.cuda.max_memory_allocated() - start_alloc
     del out
+    opt.step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -196,18 +201,32 @@ def kernel_rooflines(device) -> list[dict]:
         ("ce_bwd", lambda: Fn.ce_bwd_(logits, targets, -100, lse_c, grad_c), 2 * chunk * V * E + chunk * 16, 0, "hbm", T // chunk),
     ]
     out = []
-    stream = torch.cuda.current_stream(device)
+    side = torch.cuda.Stream(device)
     for name, fn, nbytes, flops, bound, per_step in cases:
-        for _ in range(3):
-            fn()
-        n = 50
+        # n launches captured in a HIP graph and replayed: the events then time
+        # GPU work only, not the host cost of issuing each launch.
+        n = 20
+        side.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                fn()
+        torch.cuda.current_stream(device).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(n):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream(device)
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 5
         start.record(stream)
-        for _ in range(n):
-            fn()
+        for _ in range(reps):
+            graph.replay()
         end.record(stream)
         end.synchronize()
-        us = start.elapsed_time(end) * 1e3 / n
+        us = start.elapsed_time(end) * 1e3 / (n * reps)
+        del graph
         gbs = nbytes / us / 1e3
         entry = dict(kernel=name, us=round(us, 2), bytes=int(nbytes), gbs=round(gbs, 1),
                      hbm_frac=round(gbs / HBM_PEAK_GBS, 3), bound=bound,

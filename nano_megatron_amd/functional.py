@@ -188,11 +188,17 @@ def _new_bhsd(shape_bhsd: Sequence[int], like: Tensor) -> Tensor:
     return torch.empty(b, s, h, d, dtype=like.dtype, device=like.device).transpose(1, 2)
 
 
+def _eff_strides(t: Tensor, dims=(0, 1, 2)) -> tuple[int, ...]:
+    """Strides of the given dims with size-1 dims reported as 0 (never multiplied
+    by a non-zero index, so any stride is equivalent there)."""
+    return tuple(t.stride(i) if t.shape[i] > 1 else 0 for i in dims)
+
+
 def _canonical_bhsd(t: Tensor) -> Tensor:
     """Return t ([B,H,S,D]) with [B,S,H,D]-contiguous memory, copying only if needed."""
     b, h, s, d = t.shape
-    want = (s * h * d, d, h * d, 1)
-    if tuple(t.stride()) == want or t.numel() == 0:
+    want = tuple(st if n > 1 else 0 for st, n in zip((s * h * d, d, h * d, 1), (b, h, s, d)))
+    if t.numel() == 0 or _eff_strides(t, (0, 1, 2, 3)) == want:
         return t
     return t.transpose(1, 2).contiguous().transpose(1, 2)
 
@@ -334,9 +340,9 @@ def attn_fwd_bshd(
         out = torch.empty(b, sq, hq, d, dtype=q.dtype, device=q.device)
     if lse is None:
         lse = torch.empty(b, hq, sq, dtype=torch.float32, device=q.device)
-    kv_strides = (ks[0].stride(0), ks[0].stride(1), ks[0].stride(2))
+    kv_strides = _eff_strides(ks[0])
     for t in (*ks, *vs):
-        if (t.stride(0), t.stride(1), t.stride(2)) != kv_strides or t.stride(3) != 1:
+        if _eff_strides(t) != kv_strides or t.stride(3) != 1:
             raise ValueError("attention: all K/V blocks must share one [B,S,H,D] stride layout")
     if q.stride(3) != 1 or out.stride(3) != 1:
         raise ValueError("attention: head_dim must be the contiguous dimension")
@@ -344,7 +350,7 @@ def attn_fwd_bshd(
         "nmb_attn_fwd", q.data_ptr(), _lib.ptr_array(k.data_ptr() for k in ks),
         _lib.ptr_array(v.data_ptr() for v in vs), _lib.i64_array(k_offsets), len(ks),
         out.data_ptr(), lse.data_ptr(), b, hq, hkv, sq, sk, d,
-        _lib.i64x3(q.stride()[:3]), _lib.i64x3(kv_strides), _lib.i64x3(out.stride()[:3]),
+        _lib.i64x3(_eff_strides(q)), _lib.i64x3(kv_strides), _lib.i64x3(_eff_strides(out)),
         1 if causal else 0, int(q_offset), float(scale) if scale else 0.0,
         _lib.dtype_code(q.dtype), _lib.stream_of(q),
     )
@@ -371,11 +377,11 @@ def attn_bwd_bshd(
     _require_gpu(q, o, do, lse, dq)
     b, sq, hq, d = q.shape
     _, sk, hkv, _ = ks[0].shape
-    kv_strides = (ks[0].stride(0), ks[0].stride(1), ks[0].stride(2))
+    kv_strides = _eff_strides(ks[0])
     for t in (*ks, *vs, *dks, *dvs):
-        if (t.stride(0), t.stride(1), t.stride(2)) != kv_strides:
+        if _eff_strides(t) != kv_strides or t.stride(3) != 1:
             raise ValueError("attention backward: K, V, dK, dV must share one stride layout")
-    if tuple(dq.stride()) != tuple(q.stride()) or tuple(do.stride()) != tuple(o.stride()):
+    if _eff_strides(dq) != _eff_strides(q) or _eff_strides(do) != _eff_strides(o):
         raise ValueError("attention backward: dq must match q's strides and dO must match O's")
     nbytes = _lib.ctypes.c_size_t(0)
     _lib.call("nmb_attn_bwd_workspace_bytes", b, hq, sq, _lib.ctypes.byref(nbytes))
@@ -386,7 +392,7 @@ def attn_bwd_bshd(
         o.data_ptr(), do.data_ptr(), lse.data_ptr(), dq.data_ptr(),
         _lib.ptr_array(t.data_ptr() for t in dks), _lib.ptr_array(t.data_ptr() for t in dvs),
         ws.data_ptr(), ws.numel(), b, hq, hkv, sq, sk, d,
-        _lib.i64x3(q.stride()[:3]), _lib.i64x3(kv_strides), _lib.i64x3(o.stride()[:3]),
+        _lib.i64x3(_eff_strides(q)), _lib.i64x3(kv_strides), _lib.i64x3(_eff_strides(o)),
         1 if causal else 0, int(q_offset), float(scale) if scale else 0.0,
         _lib.dtype_code(q.dtype), _lib.stream_of(q),
     )
