@@ -50,36 +50,6 @@ def parse() -> argparse.Namespace:
     return p.parse_args()
 
 
-class MasterAdamW:
-    """fp32-master AdamW over bf16 parameters (data_parallel/_zero.py:166-199 at DP=1)
-    with global grad-norm clipping (data_parallel/_zero.py:130-164)."""
-
-    def __init__(self, params, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, clip=1.0):
-        import torch
-
-        self.params = [p for p in params if p.requires_grad]
-        self.master = [p.detach().float().clone().requires_grad_(True) for p in self.params]
-        self.opt = torch.optim.AdamW(self.master, lr=lr, betas=betas, eps=eps,
-                                     weight_decay=weight_decay, fused=True)
-        self.clip = clip
-
-    def step(self) -> None:
-        import torch
-
-        for p, m in zip(self.params, self.master):
-            m.grad = p.grad.float()
-        torch.nn.utils.clip_grad_norm_(self.master, self.clip, foreach=True)
-        self.opt.step()
-        with torch.no_grad():
-            torch._foreach_copy_([p.data for p in self.params], [m.data for m in self.master])
-
-    def zero_grad(self) -> None:
-        for p in self.params:
-            p.grad = None
-        for m in self.master:
-            m.grad = None
-
-
 def run_steps(mode: str, steps: int, warmup: int, device) -> dict:
     import torch
 
@@ -89,7 +59,10 @@ def run_steps(mode: str, steps: int, warmup: int, device) -> dict:
     cfg = nm.GPTConfig(**C3)
     model = nm.GPTModel(cfg, activation_checkpoint_config=nm.ActivationCheckpointConfig(mode=mode))
     model = model.to(device=device, dtype=torch.bfloat16).train()
-    opt = MasterAdamW(model.parameters())
+    from nano_megatron_amd.optim import MasterAdamW
+
+    opt = MasterAdamW(model.parameters(), lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1,
+                      clip_grad_norm=1.0)
     g = torch.Generator(device=device).manual_seed(1234)
     ids = torch.randint(0, cfg.vocab_size, (BATCH, SEQ + 1), device=device, generator=g)
     x, y = ids[:, :SEQ].contiguous(), ids[:, 1:].contiguous()

@@ -150,6 +150,25 @@ int nmb_ce_bwd(void* logits, int64_t ld, const int64_t* targets, int64_t rows, i
                int64_t ignore_index, const float* lse, const float* grad, int dtype,
                hipStream_t stream);
 
+/* ------------------------------------------------------------ optimizer
+ * replaces FlatShardZeROStrategy.clip_grad_norm + optimizer_step at DP=1
+ * (data_parallel/_zero.py:130-199; defaults config/schema.py:439-445):
+ * global grad-norm clip (max_norm <= 0: no clip) and fp32-master AdamW with
+ * decoupled weight decay, writing the master, both moments and the
+ * parameter (cast to param_dtype) in one pass.
+ * params / grads: DEVICE arrays of n_tensors device pointers; offsets: DEVICE
+ * array of n_tensors + 1 element prefix sums (offsets[n] = total_elements);
+ * master / exp_avg / exp_avg_sq: flat fp32 [total_elements] in that order.
+ * norm_out (nullable, device, 2 floats): receives the pre-clip norm and the
+ * clip coefficient.  Deterministic (fixed-order reductions). */
+int nmb_adamw_workspace_bytes(int64_t total_elements, size_t* bytes);
+
+int nmb_adamw_step(const uint64_t* params, const uint64_t* grads, const int64_t* offsets,
+                   int n_tensors, int64_t total_elements, float* master, float* exp_avg,
+                   float* exp_avg_sq, int param_dtype, int grad_dtype, float lr, float beta1,
+                   float beta2, float eps, float weight_decay, int64_t step, float max_norm,
+                   float* norm_out, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -47,6 +47,44 @@ class BlockMeta:
     positions: Tensor | None  # int32 [S] or [B,S], or None for offset + arange
 
 
+def _adjacent(ws: tuple[Tensor, ...]) -> bool:
+    """True if the row blocks ws[0], ws[1], ... lie back to back in one storage."""
+    w0 = ws[0]
+    ptr = w0.data_ptr()
+    for w in ws:
+        if (not w.is_contiguous() or w.dtype != w0.dtype or w.device != w0.device
+                or w.shape[1:] != w0.shape[1:] or w.data_ptr() != ptr
+                or w.untyped_storage().data_ptr() != w0.untyped_storage().data_ptr()):
+            return False
+        ptr += w.numel() * w.element_size()
+    return True
+
+
+def joined(ws: tuple[Tensor, ...]) -> Tensor:
+    """The row-concatenation of ws: an alias when they are adjacent, else a copy."""
+    if _adjacent(ws):
+        rows = sum(w.shape[0] for w in ws)
+        return ws[0].as_strided((rows, *ws[0].shape[1:]), ws[0].stride())
+    return torch.cat(ws)
+
+
+def pack_adjacent(params) -> None:
+    """Re-home parameters as adjacent row blocks of one buffer (values and
+    Parameter objects unchanged), so ``joined`` needs no copy."""
+    ws = tuple(p.data for p in params)
+    if _adjacent(ws):
+        return
+    buf = torch.empty(sum(w.shape[0] for w in ws), *ws[0].shape[1:], dtype=ws[0].dtype,
+                      device=ws[0].device)
+    off = 0
+    with torch.no_grad():
+        for p in params:
+            n = p.shape[0]
+            buf[off:off + n].copy_(p.data)
+            p.data = buf[off:off + n]
+            off += n
+
+
 def _qkv_views(qkv: Tensor, b: int, s: int, m: BlockMeta) -> tuple[Tensor, Tensor, Tensor]:
     """[B*S, (Hq+2Hkv)*D] -> q [B,S,Hq,D], k, v [B,S,Hkv,D] strided views."""
     qd = m.heads * m.head_dim
@@ -64,7 +102,7 @@ def block_forward(x: Tensor, w: tuple[Tensor, ...], m: BlockMeta, *, recompute: 
     b, s, hdim = x.shape
     x2 = x.reshape(b * s, hdim)
     n1 = Fn.rmsnorm_fwd(x2, w_in, m.eps)
-    qkv = torch.mm(n1, torch.cat((wq, wk, wv)).t())
+    qkv = torch.mm(n1, joined((wq, wk, wv)).t())
     q, k, v = _qkv_views(qkv, b, s, m)
     Fn.rope_apply(q, q, m.cos, m.sin, pos_offset=m.sequence_offset, positions=m.positions)
     Fn.rope_apply(k, k, m.cos, m.sin, pos_offset=m.sequence_offset, positions=m.positions)
@@ -72,7 +110,7 @@ def block_forward(x: Tensor, w: tuple[Tensor, ...], m: BlockMeta, *, recompute: 
     o2 = o.view(b * s, m.heads * m.head_dim)
     h = torch.addmm(x2, o2, wo.t())
     n2 = Fn.rmsnorm_fwd(h, w_post, m.eps)
-    gu = torch.mm(n2, torch.cat((wg, wu)).t())
+    gu = torch.mm(n2, joined((wg, wu)).t())
     acts = dict(x2=x2, n1=n1, qkv=qkv, o2=o2, lse=lse, h=h, n2=n2, gu=gu)
     if recompute:
         return acts
@@ -99,7 +137,7 @@ def block_backward(acts: dict, dy: Tensor, w: tuple[Tensor, ...], m: BlockMeta, 
     act = torch.empty(b * s, f, dtype=gu.dtype, device=gu.device)
     Fn.swiglu_bwd(gu[:, :f], gu[:, f:], ds, dgu[:, :f], dgu[:, f:], act)
     dwd = torch.mm(dy2.t(), act)
-    dn2 = torch.mm(dgu, torch.cat((wg, wu)))
+    dn2 = torch.mm(dgu, joined((wg, wu)))
     dwgu = torch.mm(dgu.t(), n2)
     dh, dw_post = Fn.rmsnorm_bwd(h, w_post, dn2, m.eps, residual_grad=dy2)
 
@@ -115,7 +153,7 @@ def block_backward(acts: dict, dy: Tensor, w: tuple[Tensor, ...], m: BlockMeta, 
                      causal=True, q_offset=m.sequence_offset, scale=None)
     Fn.rope_apply(dq, dq, m.cos, m.sin, pos_offset=m.sequence_offset, positions=m.positions, inverse=True)
     Fn.rope_apply(dk, dk, m.cos, m.sin, pos_offset=m.sequence_offset, positions=m.positions, inverse=True)
-    dn1 = torch.mm(dqkv, torch.cat((wq, wk, wv)))
+    dn1 = torch.mm(dqkv, joined((wq, wk, wv)))
     dwqkv = torch.mm(dqkv.t(), n1)
     dx, dw_in = Fn.rmsnorm_bwd(x2, w_in, dn1, m.eps, residual_grad=dh)
 

@@ -1,0 +1,175 @@
+// Fused fp32-master AdamW with global gradient-norm clipping for gfx950.
+//
+// Follows FlatShardZeROStrategy.clip_grad_norm + optimizer_step at DP=1
+// (reference data_parallel/_zero.py:130-199):
+//   norm = sqrt(sum g^2) over all parameters; coef = min(max_norm / (norm + 1e-6), 1)
+//   g' = coef * g (fp32)
+//   m = b1 m + (1 - b1) g';  v = b2 v + (1 - b2) g'^2
+//   p = p * (1 - lr wd);  p -= (lr / bc1) * m / (sqrt(v) / sqrt(bc2) + eps)
+//   param = cast(p)
+// The parameters are many tensors; their gradients and working copies are
+// reached through device tables (pointers per tensor, element prefix sums),
+// while the fp32 master / moments are flat arrays indexed by the same prefix
+// sums.  The element range is cut into fixed chunks; each block owns one
+// chunk, so every reduction has a fixed order (deterministic), and the clip
+// coefficient stays on the device (no host synchronisation).
+#include <math.h>
+
+#include "common.h"
+
+namespace nmb {
+namespace {
+
+constexpr int64_t kChunk = 32768;
+
+// Index of the tensor holding flat element i: largest t with offsets[t] <= i.
+__device__ __forceinline__ int find_tensor(const int64_t* __restrict__ offsets, int n, int64_t i) {
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (offsets[mid] <= i) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+template <typename G>
+__global__ __launch_bounds__(256) void sumsq_kernel(const uint64_t* __restrict__ grads,
+                                                    const int64_t* __restrict__ offsets, int n,
+                                                    int64_t total, float* __restrict__ partial) {
+  __shared__ float sh[4];
+  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kChunk;
+  const int64_t c1 = min(total, c0 + kChunk);
+  float acc = 0.f;
+  for (int t = find_tensor(offsets, n, c0); t < n && offsets[t] < c1; ++t) {
+    const int64_t lo = max(c0, offsets[t]), hi = min(c1, offsets[t + 1]);
+    const G* g = reinterpret_cast<const G*>(grads[t]) - offsets[t];
+    for (int64_t i = lo + threadIdx.x; i < hi; i += 256) {
+      const float v = to_f32(g[i]);
+      acc += v * v;
+    }
+  }
+  acc = wave_sum(acc);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) partial[blockIdx.x] = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+}
+
+// One block: norm and clip coefficient from the partial sums (fixed order).
+__global__ __launch_bounds__(256) void clip_coef_kernel(const float* __restrict__ partial,
+                                                        int nparts, float max_norm,
+                                                        float* __restrict__ scalars) {
+  __shared__ float sh[4];
+  float acc = 0.f;
+  for (int i = threadIdx.x; i < nparts; i += 256) acc += partial[i];
+  acc = wave_sum(acc);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const float norm = sqrtf((sh[0] + sh[1]) + (sh[2] + sh[3]));
+    float coef = 1.f;
+    if (max_norm > 0.f) coef = fminf(max_norm / (norm + 1.0e-6f), 1.f);
+    scalars[0] = norm;
+    scalars[1] = coef;
+  }
+}
+
+struct AdamArgs {
+  float lr, beta1, beta2, eps, weight_decay, step_size, inv_sqrt_bc2;
+};
+
+template <typename P, typename G>
+__global__ __launch_bounds__(256) void adamw_kernel(const uint64_t* __restrict__ params,
+                                                    const uint64_t* __restrict__ grads,
+                                                    const int64_t* __restrict__ offsets, int n,
+                                                    int64_t total, float* __restrict__ master,
+                                                    float* __restrict__ exp_avg,
+                                                    float* __restrict__ exp_avg_sq,
+                                                    const float* __restrict__ scalars,
+                                                    AdamArgs a) {
+  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kChunk;
+  const int64_t c1 = min(total, c0 + kChunk);
+  const float coef = scalars[1];
+  const float decay = 1.f - a.lr * a.weight_decay;
+  for (int t = find_tensor(offsets, n, c0); t < n && offsets[t] < c1; ++t) {
+    const int64_t lo = max(c0, offsets[t]), hi = min(c1, offsets[t + 1]);
+    const G* g = reinterpret_cast<const G*>(grads[t]) - offsets[t];
+    P* p = reinterpret_cast<P*>(params[t]) - offsets[t];
+    for (int64_t i = lo + threadIdx.x; i < hi; i += 256) {
+      const float gv = to_f32(g[i]) * coef;
+      const float m = a.beta1 * exp_avg[i] + (1.f - a.beta1) * gv;
+      const float v = a.beta2 * exp_avg_sq[i] + (1.f - a.beta2) * gv * gv;
+      float w = master[i];
+      if (a.weight_decay != 0.f) w *= decay;
+      w -= a.step_size * m / (sqrtf(v) * a.inv_sqrt_bc2 + a.eps);
+      exp_avg[i] = m;
+      exp_avg_sq[i] = v;
+      master[i] = w;
+      p[i] = from_f32<P>(w);
+    }
+  }
+}
+
+}  // namespace
+}  // namespace nmb
+
+extern "C" int nmb_adamw_workspace_bytes(int64_t total_elements, size_t* bytes) {
+  NMB_REQUIRE(bytes != nullptr && total_elements >= 0, "adamw_workspace_bytes: bad args");
+  const int64_t nblocks = (total_elements + nmb::kChunk - 1) / nmb::kChunk;
+  *bytes = static_cast<size_t>(nblocks + 4) * sizeof(float);
+  return NMB_OK;
+}
+
+extern "C" int nmb_adamw_step(const uint64_t* params, const uint64_t* grads,
+                              const int64_t* offsets, int n_tensors, int64_t total_elements,
+                              float* master, float* exp_avg, float* exp_avg_sq, int param_dtype,
+                              int grad_dtype, float lr, float beta1, float beta2, float eps,
+                              float weight_decay, int64_t step, float max_norm, float* norm_out,
+                              void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  NMB_REQUIRE(params && grads && offsets && master && exp_avg && exp_avg_sq,
+              "adamw_step: null argument");
+  NMB_REQUIRE(n_tensors > 0 && total_elements > 0, "adamw_step: empty parameter set");
+  NMB_REQUIRE(step >= 1, "adamw_step: step must be >= 1, got %lld", (long long)step);
+  NMB_REQUIRE(lr > 0.f && eps > 0.f && beta1 >= 0.f && beta1 < 1.f && beta2 >= 0.f && beta2 < 1.f,
+              "adamw_step: invalid hyper-parameters");
+  const int64_t nblocks = (total_elements + nmb::kChunk - 1) / nmb::kChunk;
+  NMB_REQUIRE(nblocks < (int64_t{1} << 30), "adamw_step: too many elements");
+  const size_t need = static_cast<size_t>(nblocks + 4) * sizeof(float);
+  NMB_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+              "adamw_step: workspace of %zu bytes is smaller than the %zu required",
+              workspace_bytes, need);
+  float* partial = static_cast<float*>(workspace);
+  float* scalars = norm_out != nullptr ? norm_out : partial + nblocks;
+  const unsigned grid = static_cast<unsigned>(nblocks);
+  if (grad_dtype == NMB_BF16)
+    hipLaunchKernelGGL(nmb::sumsq_kernel<nmb::bf16>, dim3(grid), dim3(256), 0, stream, grads,
+                       offsets, n_tensors, total_elements, partial);
+  else if (grad_dtype == NMB_F32)
+    hipLaunchKernelGGL(nmb::sumsq_kernel<float>, dim3(grid), dim3(256), 0, stream, grads, offsets,
+                       n_tensors, total_elements, partial);
+  else
+    NMB_REQUIRE_SUPPORTED(false, "adamw_step: unsupported grad dtype %d", grad_dtype);
+  NMB_CHECK_LAUNCH("adamw_step(sumsq)");
+  hipLaunchKernelGGL(nmb::clip_coef_kernel, dim3(1), dim3(256), 0, stream, partial,
+                     static_cast<int>(nblocks), max_norm, scalars);
+  NMB_CHECK_LAUNCH("adamw_step(clip)");
+  nmb::AdamArgs a;
+  a.lr = lr;
+  a.beta1 = beta1;
+  a.beta2 = beta2;
+  a.eps = eps;
+  a.weight_decay = weight_decay;
+  const double bc1 = 1.0 - pow(static_cast<double>(beta1), static_cast<double>(step));
+  const double bc2 = 1.0 - pow(static_cast<double>(beta2), static_cast<double>(step));
+  a.step_size = static_cast<float>(lr / bc1);
+  a.inv_sqrt_bc2 = static_cast<float>(1.0 / sqrt(bc2));
+#define NMB_ADAM(P, G)                                                                        \
+  hipLaunchKernelGGL((nmb::adamw_kernel<P, G>), dim3(grid), dim3(256), 0, stream, params, grads, \
+                     offsets, n_tensors, total_elements, master, exp_avg, exp_avg_sq, scalars, a)
+  if (param_dtype == NMB_BF16 && grad_dtype == NMB_BF16) NMB_ADAM(nmb::bf16, nmb::bf16);
+  else if (param_dtype == NMB_F32 && grad_dtype == NMB_F32) NMB_ADAM(float, float);
+  else if (param_dtype == NMB_BF16 && grad_dtype == NMB_F32) NMB_ADAM(nmb::bf16, float);
+  else NMB_REQUIRE_SUPPORTED(false, "adamw_step: unsupported dtype pair %d/%d", param_dtype, grad_dtype);
+#undef NMB_ADAM
+  NMB_CHECK_LAUNCH("adamw_step(update)");
+  return NMB_OK;
+}

@@ -78,39 +78,71 @@ __device__ __forceinline__ bf16x8 ld4x2(const bf16* p) {
   return r;
 }
 
-// Stage rows [r0, r0 + R) x D of a strided bf16 matrix into LDS, row-major with
-// row stride LD; rows at or beyond nrows are zero.
-template <int R, int D, int LD>
-__device__ __forceinline__ void stage_rows(bf16* __restrict__ dst, const bf16* __restrict__ src,
-                                           int64_t row_stride, int r0, int nrows) {
-  for (int c = threadIdx.x; c < R * D / 8; c += 256) {
-    const int r = c / (D / 8), dc = c % (D / 8);
-    bf16x8 val = zero8();
-    if (r0 + r < nrows) val = ld8(src + static_cast<int64_t>(r0 + r) * row_stride + dc * 8);
-    *reinterpret_cast<bf16x8*>(dst + r * LD + dc * 8) = val;
-  }
-}
+// exp2 as the raw v_exp_f32: results below 2^-126 flush to 0, which is
+// immaterial for softmax weights (the library exp2 adds a 5-instruction
+// denormal range fix-up around every exponential).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Stage the transpose: dst[d][r] (row stride LD) for rows [r0, r0 + R).  Each
-// thread moves a pair of rows so that LDS writes are 32-bit words.
-template <int R, int D, int LD>
-__device__ __forceinline__ void stage_rows_t(bf16* __restrict__ dst, const bf16* __restrict__ src,
-                                             int64_t row_stride, int r0, int nrows) {
-  for (int c = threadIdx.x; c < (R / 2) * (D / 8); c += 256) {
-    const int rp = c % (R / 2), dc = c / (R / 2);
-    const int ra = r0 + 2 * rp;
-    bf16x8 v0 = zero8(), v1 = zero8();
-    if (ra < nrows) v0 = ld8(src + static_cast<int64_t>(ra) * row_stride + dc * 8);
-    if (ra + 1 < nrows) v1 = ld8(src + static_cast<int64_t>(ra + 1) * row_stride + dc * 8);
+// A thread's share of an R x D bf16 tile, read from global memory as pairs of
+// rows (16 bytes of each row per item, consecutive lanes on consecutive
+// 16-byte chunks of a row, so the reads are coalesced).  One read feeds both
+// the row-major LDS copy and the transposed copy (written as 32-bit words
+// holding the two rows' values).  Loading into registers ahead of use lets a
+// tile's global reads overlap the MFMA work on the previous tile.
+template <int R, int D>
+struct PairTile {
+  static constexpr int kChunks = D / 8;
+  static constexpr int kItems = (R / 2) * kChunks;
+  static constexpr int kPer = (kItems + 255) / 256;
+  bf16x8 a[kPer], b[kPer];
+
+  __device__ __forceinline__ void load(const bf16* __restrict__ src, int64_t row_stride, int r0,
+                                       int nrows) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      bf16 pr[2] = {v0[i], v1[i]};
-      uint32_t w;
-      __builtin_memcpy(&w, pr, 4);
-      *reinterpret_cast<uint32_t*>(dst + (dc * 8 + i) * LD + 2 * rp) = w;
+    for (int i = 0; i < kPer; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const int dc = c % kChunks, rp = c / kChunks;
+      const int ra = r0 + 2 * rp;
+      a[i] = zero8();
+      b[i] = zero8();
+      if (c < kItems) {
+        if (ra < nrows) a[i] = ld8(src + static_cast<int64_t>(ra) * row_stride + dc * 8);
+        if (ra + 1 < nrows) b[i] = ld8(src + static_cast<int64_t>(ra + 1) * row_stride + dc * 8);
+      }
     }
   }
-}
+
+  template <int LD>
+  __device__ __forceinline__ void store_rows(bf16* __restrict__ dst) const {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const int dc = c % kChunks, rp = c / kChunks;
+      if (c < kItems) {
+        *reinterpret_cast<bf16x8*>(dst + (2 * rp) * LD + dc * 8) = a[i];
+        *reinterpret_cast<bf16x8*>(dst + (2 * rp + 1) * LD + dc * 8) = b[i];
+      }
+    }
+  }
+
+  template <int LD>
+  __device__ __forceinline__ void store_cols(bf16* __restrict__ dst) const {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const int dc = c % kChunks, rp = c / kChunks;
+      if (c < kItems) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          bf16 pr[2] = {a[i][e], b[i][e]};
+          uint32_t w;
+          __builtin_memcpy(&w, pr, 4);
+          *reinterpret_cast<uint32_t*>(dst + (dc * 8 + e) * LD + 2 * rp) = w;
+        }
+      }
+    }
+  }
+};
 
 // Number of 64-key tiles of a block that any query up to absolute position
 // q_last can see.
@@ -125,23 +157,72 @@ __device__ __forceinline__ int visible_key_tiles(const AttnShape& p, int64_t kof
   return n;
 }
 
+// Blocks are dispatched round-robin over the 8 XCDs (block L runs on XCD L % 8,
+// each XCD with its own L2).  Work item w = (L % 8) * per_xcd + L / 8 puts
+// consecutive items -- the q-tiles of one head, which read the same K/V -- on
+// the same XCD.  Returns -1 for the padding blocks of the last round.
+__device__ __forceinline__ int xcd_item(int items, int per_xcd) {
+  const int L = static_cast<int>(blockIdx.x);
+  const int w = (L % 8) * per_xcd + L / 8;
+  return w < items ? w : -1;
+}
+
+// Advance (blk, kt) to the next visible K/V tile of the concatenated blocks.
+__device__ __forceinline__ void next_tile(const AttnShape& p, const KVBlocks& kv, int64_t q_last,
+                                          int& blk, int& kt) {
+  ++kt;
+  if (kt < visible_key_tiles(p, kv.koff[blk], q_last)) return;
+  kt = 0;
+  for (++blk; blk < p.nblk; ++blk)
+    if (visible_key_tiles(p, kv.koff[blk], q_last) > 0) return;
+}
+
+__device__ __forceinline__ int first_block(const AttnShape& p, const KVBlocks& kv, int64_t q_last) {
+  int blk = 0;
+  while (blk < p.nblk && visible_key_tiles(p, kv.koff[blk], q_last) == 0) ++blk;
+  return blk;
+}
+
+// Largest tile-relative key index (key = k0 + index) visible to a query at
+// absolute position qa: keys beyond Sk are never visible, and with causal
+// masking key position koff + k0 + index must not exceed qa.
+__device__ __forceinline__ int mask_limit(const AttnShape& p, int64_t koff, int k0, int64_t qa) {
+  int64_t lim = static_cast<int64_t>(p.Sk) - 1 - k0;
+  if (p.causal) {
+    const int64_t c = qa - koff - k0;
+    if (c < lim) lim = c;
+  }
+  if (lim < -1) lim = -1;
+  if (lim > 1 << 20) lim = 1 << 20;
+  return static_cast<int>(lim);
+}
+
 // ---------------------------------------------------------------- forward
+// Workgroup = 128 queries of one (batch, head): wave w owns queries
+// 32w..32w+31 as two 16-query MFMA column tiles.  K/V stream through LDS in
+// 64-key tiles; the next tile's global reads are issued before the current
+// tile's MFMA work.  Scores stay raw; exp2(s * c - m * c) folds the softmax
+// scale into one FMA per score.
 template <int D>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16* __restrict__ q, KVBlocks kv,
-                                                       bf16* __restrict__ o,
-                                                       float* __restrict__ lse, AttnShape p) {
+__global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_fwd_kernel(const bf16* __restrict__ q, KVBlocks kv,
+                                                          bf16* __restrict__ o,
+                                                          float* __restrict__ lse, AttnShape p,
+                                                          int n_qt, int items, int per_xcd) {
   constexpr int BQ = 128, BK = 64, KS = D / 32, DT = D / 16;
   constexpr int LDK = D + 8, LDV = BK + 8;
   __shared__ __attribute__((aligned(16))) bf16 sK[BK * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sVt[D * LDV];
 
+  const int w = xcd_item(items, per_xcd);
+  if (w < 0) return;
+  const int bh = w / n_qt;
+  const int qt = n_qt - 1 - (w % n_qt);  // heavy causal tiles first within a head
+  const int b = bh / p.Hq, h = bh % p.Hq;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g = lane >> 4;
-  const int n_qt = (p.Sq + BQ - 1) / BQ;
-  const int qt = n_qt - 1 - static_cast<int>(blockIdx.x);  // heavy causal tiles first
-  const int h = blockIdx.y, b = blockIdx.z;
   const int hk = h / (p.Hq / p.Hkv);
   const int q0 = qt * BQ + wave * 32;
+  const float c = p.scale_log2;
 
   const bf16* qb = q + b * p.q_sb + h * p.q_sh;
   bf16x8 qf[2][KS];
@@ -163,88 +244,101 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16* __restrict__ 
   const int64_t qa_wave_first = p.q_offset + q0;
   const int64_t qa_wave_last = p.q_offset + min(q0 + 31, p.Sq - 1);
   const int64_t qa_wg_last = p.q_offset + min(qt * BQ + BQ - 1, p.Sq - 1);
+  const int64_t kv_off = b * p.kv_sb + hk * p.kv_sh;
 
-  for (int blk = 0; blk < p.nblk; ++blk) {
-    const bf16* kb = static_cast<const bf16*>(kv.k[blk]) + b * p.kv_sb + hk * p.kv_sh;
-    const bf16* vb = static_cast<const bf16*>(kv.v[blk]) + b * p.kv_sb + hk * p.kv_sh;
+  PairTile<BK, D> kr, vr;
+  int blk = first_block(p, kv, qa_wg_last), kt = 0;
+  if (blk < p.nblk) {
+    kr.load(static_cast<const bf16*>(kv.k[blk]) + kv_off, p.kv_ss, 0, p.Sk);
+    vr.load(static_cast<const bf16*>(kv.v[blk]) + kv_off, p.kv_ss, 0, p.Sk);
+  }
+  while (blk < p.nblk) {
+    __syncthreads();
+    kr.template store_rows<LDK>(sK);
+    vr.template store_cols<LDV>(sVt);
+    __syncthreads();
     const int64_t koff = kv.koff[blk];
-    const int n_kt = visible_key_tiles(p, koff, qa_wg_last);
-    for (int kt = 0; kt < n_kt; ++kt) {
-      const int k0 = kt * BK;
-      __syncthreads();
-      stage_rows<BK, D, LDK>(sK, kb, p.kv_ss, k0, p.Sk);
-      stage_rows_t<BK, D, LDV>(sVt, vb, p.kv_ss, k0, p.Sk);
-      __syncthreads();
-      if (p.causal && koff + k0 > qa_wave_last) continue;  // wave-uniform: nothing visible
-      const bool need_mask =
-          (k0 + BK > p.Sk) || (p.causal && koff + k0 + BK - 1 > qa_wave_first);
+    const int k0 = kt * BK;
+    int nb = blk, nk = kt;
+    next_tile(p, kv, qa_wg_last, nb, nk);
+    if (nb < p.nblk) {
+      kr.load(static_cast<const bf16*>(kv.k[nb]) + kv_off, p.kv_ss, nk * BK, p.Sk);
+      vr.load(static_cast<const bf16*>(kv.v[nb]) + kv_off, p.kv_ss, nk * BK, p.Sk);
+    }
+    blk = nb;
+    kt = nk;
+    if (p.causal && koff + k0 > qa_wave_last) continue;  // wave-uniform: nothing visible
+    const bool need_mask = (k0 + BK > p.Sk) || (p.causal && koff + k0 + BK - 1 > qa_wave_first);
 
-      f32x4 s[4][2];
+    f32x4 s[4][2];
 #pragma unroll
-      for (int mk = 0; mk < 4; ++mk) {
+    for (int mk = 0; mk < 4; ++mk) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) s[mk][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int t = 0; t < 2; ++t) s[mk][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const bf16x8 a = ld8(sK + (mk * 16 + l16) * LDK + ks * 32 + g * 8);
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8 a = ld8(sK + (mk * 16 + l16) * LDK + ks * 32 + g * 8);
 #pragma unroll
-          for (int t = 0; t < 2; ++t) s[mk][t] = mfma16(a, qf[t][ks], s[mk][t]);
-        }
+        for (int t = 0; t < 2; ++t) s[mk][t] = mfma16(a, qf[t][ks], s[mk][t]);
       }
-      bf16x8 pf[2][2];
+    }
+    bf16x8 pf[2][2];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int64_t qa = p.q_offset + q0 + 16 * t + l16;
-        float tmax = -__builtin_inff();
+    for (int t = 0; t < 2; ++t) {
+      float tmax = -__builtin_inff();
+      if (need_mask) {
+        // last visible tile-relative key index of this lane's query
+        const int lim = mask_limit(p, koff, k0, p.q_offset + q0 + 16 * t + l16);
 #pragma unroll
         for (int mk = 0; mk < 4; ++mk)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            float val = s[mk][t][e] * p.scale_log2;
-            if (need_mask) {
-              const int kl = k0 + mk * 16 + g * 4 + e;
-              if (kl >= p.Sk || (p.causal && koff + kl > qa)) val = -__builtin_inff();
-            }
-            s[mk][t][e] = val;
-            tmax = fmaxf(tmax, val);
-          }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float mnew = fmaxf(m[t], tmax);
-        const bool dead = mnew == -__builtin_inff();
-        const float alpha = dead ? 1.f : exp2f(m[t] - mnew);
-        const float msub = dead ? 0.f : mnew;
-        float rs = 0.f;
-#pragma unroll
-        for (int mk = 0; mk < 4; ++mk)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float pv = exp2f(s[mk][t][e] - msub);
-            s[mk][t][e] = pv;
-            rs += pv;
-          }
-        rs += __shfl_xor(rs, 16, 64);
-        rs += __shfl_xor(rs, 32, 64);
-        l[t] = l[t] * alpha + rs;
-        m[t] = mnew;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[t][dt] *= alpha;
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            pf[s2][t][e] = static_cast<bf16>(s[2 * s2][t][e]);
-            pf[s2][t][4 + e] = static_cast<bf16>(s[2 * s2 + 1][t][e]);
+            // branch-free select: a conditional store into the vector element
+            // under short-circuit control flow is not reliably kept
+            const float sv = s[mk][t][e];
+            s[mk][t][e] = (mk * 16 + g * 4 + e > lim) ? -__builtin_inff() : sv;
           }
       }
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
+      for (int mk = 0; mk < 4; ++mk)
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          const bf16x8 a = ld4x2(sVt + (dt * 16 + l16) * LDV + 32 * s2 + g * 4);
+        for (int e = 0; e < 4; ++e) tmax = fmaxf(tmax, s[mk][t][e]);
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float mnew = fmaxf(m[t], tmax);
+      const bool dead = mnew == -__builtin_inff();
+      const float alpha = dead ? 1.f : fast_exp2((m[t] - mnew) * c);
+      const float mc = dead ? 0.f : mnew * c;
+      float rs = 0.f;
 #pragma unroll
-          for (int t = 0; t < 2; ++t) acc[t][dt] = mfma16(a, pf[s2][t], acc[t][dt]);
+      for (int mk = 0; mk < 4; ++mk)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float pv = fast_exp2(fmaf(s[mk][t][e], c, -mc));
+          s[mk][t][e] = pv;
+          rs += pv;
         }
+      rs += __shfl_xor(rs, 16, 64);
+      rs += __shfl_xor(rs, 32, 64);
+      l[t] = l[t] * alpha + rs;
+      m[t] = mnew;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) acc[t][dt] *= alpha;
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pf[s2][t][e] = static_cast<bf16>(s[2 * s2][t][e]);
+          pf[s2][t][4 + e] = static_cast<bf16>(s[2 * s2 + 1][t][e]);
+        }
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const bf16x8 a = ld4x2(sVt + (dt * 16 + l16) * LDV + 32 * s2 + g * 4);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) acc[t][dt] = mfma16(a, pf[s2][t], acc[t][dt]);
       }
     }
   }
@@ -257,16 +351,22 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16* __restrict__ 
     const float inv = l[t] > 0.f ? 1.f / l[t] : 0.f;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      bf16x4 w;
+      bf16x4 wv;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) w[e] = static_cast<bf16>(acc[t][dt][e] * inv);
-      *reinterpret_cast<bf16x4*>(ob + static_cast<int64_t>(qi) * p.o_ss + dt * 16 + g * 4) = w;
+      for (int e = 0; e < 4; ++e) wv[e] = static_cast<bf16>(acc[t][dt][e] * inv);
+      *reinterpret_cast<bf16x4*>(ob + static_cast<int64_t>(qi) * p.o_ss + dt * 16 + g * 4) = wv;
     }
-    if (g == 0) lb[qi] = l[t] > 0.f ? (m[t] + log2f(l[t])) * kLn2 : -__builtin_inff();
+    if (g == 0) lb[qi] = l[t] > 0.f ? (m[t] * c + log2f(l[t])) * kLn2 : -__builtin_inff();
   }
 }
 
-// ---------------------------------------------------------------- delta
+// log2-domain lse for P = exp2(S * scale_log2 - lse2); a query with no visible
+// key (lse = -inf) maps to +inf so that every P of its row is 0.
+__device__ __forceinline__ float lse_to_log2(float v) {
+  return v == -__builtin_inff() ? __builtin_inff() : v * kLog2e;
+}
+
+// ---------------------------------------------------------------- delta (fp32 path)
 // delta[b, h, i] = sum_d dO[b, i, h, d] * O[b, i, h, d] (fp32).
 template <typename T>
 __global__ __launch_bounds__(256) void attn_delta_kernel(const T* __restrict__ o,
@@ -287,50 +387,57 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(const T* __restrict__ o
   }
 }
 
-// log2-domain lse for P = exp2(S * scale_log2 - lse2); a query with no visible
-// key (lse = -inf) maps to +inf so that every P of its row is 0.
-__device__ __forceinline__ float lse_to_log2(float v) {
-  return v == -__builtin_inff() ? __builtin_inff() : v * kLog2e;
-}
-
 // ---------------------------------------------------------------- dQ
+// Same tiling as the forward (S^T = K Q^T per wave).  The prologue computes
+// delta = rowsum(dO * O) for the workgroup's queries from the registers that
+// hold dO and writes it for the dK/dV kernel, which runs next on the stream.
 template <int D>
-__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const bf16* __restrict__ q, KVBlocks kv,
-                                                          const bf16* __restrict__ dout,
-                                                          const float* __restrict__ lse,
-                                                          const float* __restrict__ delta,
-                                                          bf16* __restrict__ dq, AttnShape p) {
+__global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
+    const bf16* __restrict__ q, KVBlocks kv, const bf16* __restrict__ o,
+    const bf16* __restrict__ dout, const float* __restrict__ lse, float* __restrict__ delta,
+    bf16* __restrict__ dq, AttnShape p, int n_qt, int items, int per_xcd) {
   constexpr int BQ = 128, BK = 64, KS = D / 32, DT = D / 16;
   constexpr int LDK = D + 8, LDT = BK + 8;
   __shared__ __attribute__((aligned(16))) bf16 sK[BK * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sKt[D * LDT];
   __shared__ __attribute__((aligned(16))) bf16 sV[BK * LDK];
 
+  const int w = xcd_item(items, per_xcd);
+  if (w < 0) return;
+  const int bh = w / n_qt;
+  const int qt = n_qt - 1 - (w % n_qt);
+  const int b = bh / p.Hq, h = bh % p.Hq;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g = lane >> 4;
-  const int n_qt = (p.Sq + BQ - 1) / BQ;
-  const int qt = n_qt - 1 - static_cast<int>(blockIdx.x);
-  const int h = blockIdx.y, b = blockIdx.z;
   const int hk = h / (p.Hq / p.Hkv);
   const int q0 = qt * BQ + wave * 32;
+  const float c = p.scale_log2;
 
   const bf16* qb = q + b * p.q_sb + h * p.q_sh;
+  const bf16* ob = o + b * p.o_sb + h * p.o_sh;
   const bf16* db = dout + b * p.o_sb + h * p.o_sh;
   const float* lb = lse + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
-  const float* deb = delta + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
+  float* deb = delta + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
   bf16x8 qf[2][KS], df[2][KS];
   float lse2[2], dl[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int qi = q0 + 16 * t + l16;
     const bool ok = qi < p.Sq;
+    float part = 0.f;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       qf[t][ks] = ok ? ld8(qb + static_cast<int64_t>(qi) * p.q_ss + ks * 32 + g * 8) : zero8();
       df[t][ks] = ok ? ld8(db + static_cast<int64_t>(qi) * p.o_ss + ks * 32 + g * 8) : zero8();
+      const bf16x8 of = ok ? ld8(ob + static_cast<int64_t>(qi) * p.o_ss + ks * 32 + g * 8) : zero8();
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part += static_cast<float>(df[t][ks][e]) * static_cast<float>(of[e]);
     }
+    part += __shfl_xor(part, 16, 64);
+    part += __shfl_xor(part, 32, 64);
+    dl[t] = part;
+    if (ok && g == 0) deb[qi] = part;
     lse2[t] = ok ? lse_to_log2(lb[qi]) : __builtin_inff();
-    dl[t] = ok ? deb[qi] : 0.f;
   }
   f32x4 acc[2][DT];
 #pragma unroll
@@ -341,73 +448,79 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const bf16* __restrict
   const int64_t qa_wave_first = p.q_offset + q0;
   const int64_t qa_wave_last = p.q_offset + min(q0 + 31, p.Sq - 1);
   const int64_t qa_wg_last = p.q_offset + min(qt * BQ + BQ - 1, p.Sq - 1);
+  const int64_t kv_off = b * p.kv_sb + hk * p.kv_sh;
 
-  for (int blk = 0; blk < p.nblk; ++blk) {
-    const bf16* kb = static_cast<const bf16*>(kv.k[blk]) + b * p.kv_sb + hk * p.kv_sh;
-    const bf16* vb = static_cast<const bf16*>(kv.v[blk]) + b * p.kv_sb + hk * p.kv_sh;
+  PairTile<BK, D> kr, vr;
+  int blk = first_block(p, kv, qa_wg_last), kt = 0;
+  if (blk < p.nblk) {
+    kr.load(static_cast<const bf16*>(kv.k[blk]) + kv_off, p.kv_ss, 0, p.Sk);
+    vr.load(static_cast<const bf16*>(kv.v[blk]) + kv_off, p.kv_ss, 0, p.Sk);
+  }
+  while (blk < p.nblk) {
+    __syncthreads();
+    kr.template store_rows<LDK>(sK);
+    kr.template store_cols<LDT>(sKt);
+    vr.template store_rows<LDK>(sV);
+    __syncthreads();
     const int64_t koff = kv.koff[blk];
-    const int n_kt = visible_key_tiles(p, koff, qa_wg_last);
-    for (int kt = 0; kt < n_kt; ++kt) {
-      const int k0 = kt * BK;
-      __syncthreads();
-      stage_rows<BK, D, LDK>(sK, kb, p.kv_ss, k0, p.Sk);
-      stage_rows_t<BK, D, LDT>(sKt, kb, p.kv_ss, k0, p.Sk);
-      stage_rows<BK, D, LDK>(sV, vb, p.kv_ss, k0, p.Sk);
-      __syncthreads();
-      if (p.causal && koff + k0 > qa_wave_last) continue;
-      const bool need_mask =
-          (k0 + BK > p.Sk) || (p.causal && koff + k0 + BK - 1 > qa_wave_first);
+    const int k0 = kt * BK;
+    int nb = blk, nk = kt;
+    next_tile(p, kv, qa_wg_last, nb, nk);
+    if (nb < p.nblk) {
+      kr.load(static_cast<const bf16*>(kv.k[nb]) + kv_off, p.kv_ss, nk * BK, p.Sk);
+      vr.load(static_cast<const bf16*>(kv.v[nb]) + kv_off, p.kv_ss, nk * BK, p.Sk);
+    }
+    blk = nb;
+    kt = nk;
+    if (p.causal && koff + k0 > qa_wave_last) continue;
+    const bool need_mask = (k0 + BK > p.Sk) || (p.causal && koff + k0 + BK - 1 > qa_wave_first);
 
-      f32x4 s[4][2], dp[4][2];
+    f32x4 s[4][2], dp[4][2];
 #pragma unroll
-      for (int mk = 0; mk < 4; ++mk) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          s[mk][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-          dp[mk][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const bf16x8 ak = ld8(sK + (mk * 16 + l16) * LDK + ks * 32 + g * 8);
-          const bf16x8 av = ld8(sV + (mk * 16 + l16) * LDK + ks * 32 + g * 8);
-#pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            s[mk][t] = mfma16(ak, qf[t][ks], s[mk][t]);
-            dp[mk][t] = mfma16(av, df[t][ks], dp[mk][t]);
-          }
-        }
-      }
-      bf16x8 dsf[2][2];
+    for (int mk = 0; mk < 4; ++mk) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const int64_t qa = p.q_offset + q0 + 16 * t + l16;
-#pragma unroll
-        for (int mk = 0; mk < 4; ++mk)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float pv = exp2f(s[mk][t][e] * p.scale_log2 - lse2[t]);
-            if (need_mask) {
-              const int kl = k0 + mk * 16 + g * 4 + e;
-              if (kl >= p.Sk || (p.causal && koff + kl > qa)) pv = 0.f;
-            }
-            s[mk][t][e] = pv * (dp[mk][t][e] - dl[t]);
-          }
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            dsf[s2][t][e] = static_cast<bf16>(s[2 * s2][t][e]);
-            dsf[s2][t][4 + e] = static_cast<bf16>(s[2 * s2 + 1][t][e]);
-          }
+        s[mk][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        dp[mk][t] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8 ak = ld8(sK + (mk * 16 + l16) * LDK + ks * 32 + g * 8);
+        const bf16x8 av = ld8(sV + (mk * 16 + l16) * LDK + ks * 32 + g * 8);
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          const bf16x8 a = ld4x2(sKt + (dt * 16 + l16) * LDT + 32 * s2 + g * 4);
-#pragma unroll
-          for (int t = 0; t < 2; ++t) acc[t][dt] = mfma16(a, dsf[s2][t], acc[t][dt]);
+        for (int t = 0; t < 2; ++t) {
+          s[mk][t] = mfma16(ak, qf[t][ks], s[mk][t]);
+          dp[mk][t] = mfma16(av, df[t][ks], dp[mk][t]);
         }
+      }
+    }
+    bf16x8 dsf[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int lim = need_mask ? mask_limit(p, koff, k0, p.q_offset + q0 + 16 * t + l16) : BK;
+#pragma unroll
+      for (int mk = 0; mk < 4; ++mk)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float pv = fast_exp2(fmaf(s[mk][t][e], c, -lse2[t]));
+          pv = (mk * 16 + g * 4 + e > lim) ? 0.f : pv;
+          s[mk][t][e] = pv * (dp[mk][t][e] - dl[t]);
+        }
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          dsf[s2][t][e] = static_cast<bf16>(s[2 * s2][t][e]);
+          dsf[s2][t][4 + e] = static_cast<bf16>(s[2 * s2 + 1][t][e]);
+        }
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const bf16x8 a = ld4x2(sKt + (dt * 16 + l16) * LDT + 32 * s2 + g * 4);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) acc[t][dt] = mfma16(a, dsf[s2][t], acc[t][dt]);
       }
     }
   }
@@ -418,10 +531,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const bf16* __restrict
     if (qi >= p.Sq) continue;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      bf16x4 w;
+      bf16x4 wv;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) w[e] = static_cast<bf16>(acc[t][dt][e] * p.scale);
-      *reinterpret_cast<bf16x4*>(dqb + static_cast<int64_t>(qi) * p.q_ss + dt * 16 + g * 4) = w;
+      for (int e = 0; e < 4; ++e) wv[e] = static_cast<bf16>(acc[t][dt][e] * p.scale);
+      *reinterpret_cast<bf16x4*>(dqb + static_cast<int64_t>(qi) * p.q_ss + dt * 16 + g * 4) = wv;
     }
   }
 }
@@ -429,14 +542,13 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const bf16* __restrict
 // ---------------------------------------------------------------- dK, dV
 // Workgroup = 64 keys of one (batch, KV head, block); wave w owns keys
 // 16w..16w+15.  Loops over the query heads of the GQA group and over the
-// 64-query tiles that can see these keys.
+// 64-query tiles that can see these keys, with the next Q/dO tile's global
+// reads in flight during the current tile's MFMA work.
 template <int D>
-__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const bf16* __restrict__ q,
-                                                            KVBlocks kv,
-                                                            const bf16* __restrict__ dout,
-                                                            const float* __restrict__ lse,
-                                                            const float* __restrict__ delta,
-                                                            AttnShape p) {
+__global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
+    const bf16* __restrict__ q, KVBlocks kv, const bf16* __restrict__ dout,
+    const float* __restrict__ lse, const float* __restrict__ delta, AttnShape p, int n_kt,
+    int items, int per_xcd) {
   constexpr int BQ = 64, BK = 64, KS = D / 32, DT = D / 16;
   constexpr int LDQ = D + 8, LDT = BQ + 8;
   __shared__ __attribute__((aligned(16))) bf16 sQ[BQ * LDQ];
@@ -445,18 +557,26 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const bf16* __restri
   __shared__ __attribute__((aligned(16))) bf16 sDt[D * LDT];
   __shared__ float sL[BQ], sDl[BQ];
 
+  const int w = xcd_item(items, per_xcd);
+  if (w < 0) return;
+  // item = ((b * nblk + blk) * Hkv + hk) * n_kt + key tile
+  const int ktile = w % n_kt;
+  const int rest = w / n_kt;
+  const int hk = rest % p.Hkv;
+  const int bb = rest / p.Hkv;
+  const int blk = bb % p.nblk;
+  const int b = bb / p.nblk;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g = lane >> 4;
-  const int blk = static_cast<int>(blockIdx.z) % p.nblk;
-  const int b = static_cast<int>(blockIdx.z) / p.nblk;
-  const int hk = blockIdx.y;
-  const int k0 = static_cast<int>(blockIdx.x) * BK;
+  const int k0 = ktile * BK;
   const int kw0 = k0 + wave * 16;
   const int64_t koff = kv.koff[blk];
   const int group = p.Hq / p.Hkv;
+  const float c = p.scale_log2;
 
-  const bf16* kb = static_cast<const bf16*>(kv.k[blk]) + b * p.kv_sb + hk * p.kv_sh;
-  const bf16* vb = static_cast<const bf16*>(kv.v[blk]) + b * p.kv_sb + hk * p.kv_sh;
+  const int64_t kv_off = b * p.kv_sb + hk * p.kv_sh;
+  const bf16* kb = static_cast<const bf16*>(kv.k[blk]) + kv_off;
+  const bf16* vb = static_cast<const bf16*>(kv.v[blk]) + kv_off;
   bf16x8 kf[KS], vf[KS];
   {
     const int key = kw0 + l16;
@@ -473,7 +593,6 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const bf16* __restri
     dka[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     dva[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  // first query (local index) that can see key k0 of this tile
   int first_q = 0;
   if (p.causal) {
     const int64_t fq = koff + k0 - p.q_offset;
@@ -481,95 +600,107 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const bf16* __restri
   }
   const int qt_begin = first_q / BQ;
   const int n_qt = (p.Sq + BQ - 1) / BQ;
+  const int per_head = n_qt - qt_begin;
+  const int n_iter = per_head > 0 ? group * per_head : 0;
   const int64_t ka_wave_first = koff + kw0;
   const int64_t ka_wave_last = koff + kw0 + 15;
 
-  for (int hi = 0; hi < group; ++hi) {
-    const int h = hk * group + hi;
-    const bf16* qb = q + b * p.q_sb + h * p.q_sh;
-    const bf16* db = dout + b * p.o_sb + h * p.o_sh;
-    const float* lb = lse + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
-    const float* deb = delta + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
-    for (int qt = qt_begin; qt < n_qt; ++qt) {
-      const int q0 = qt * BQ;
-      __syncthreads();
-      stage_rows<BQ, D, LDQ>(sQ, qb, p.q_ss, q0, p.Sq);
-      stage_rows_t<BQ, D, LDT>(sQt, qb, p.q_ss, q0, p.Sq);
-      stage_rows<BQ, D, LDQ>(sD, db, p.o_ss, q0, p.Sq);
-      stage_rows_t<BQ, D, LDT>(sDt, db, p.o_ss, q0, p.Sq);
-      if (threadIdx.x < BQ) {
-        const int qi = q0 + threadIdx.x;
-        sL[threadIdx.x] = qi < p.Sq ? lse_to_log2(lb[qi]) : __builtin_inff();
-        sDl[threadIdx.x] = qi < p.Sq ? deb[qi] : 0.f;
-      }
-      __syncthreads();
-      const int64_t qa_last = p.q_offset + min(q0 + BQ - 1, p.Sq - 1);
-      if (kw0 >= p.Sk) continue;
-      if (p.causal && ka_wave_first > qa_last) continue;
-      const bool need_mask =
-          (kw0 + 16 > p.Sk) || (p.causal && ka_wave_last > p.q_offset + q0);
+  PairTile<BQ, D> qr, dr;
+  float lv = 0.f, dv = 0.f;
+  auto load = [&](int it) {
+    const int h = hk * group + it / per_head;
+    const int q0 = (qt_begin + it % per_head) * BQ;
+    qr.load(q + b * p.q_sb + h * p.q_sh, p.q_ss, q0, p.Sq);
+    dr.load(dout + b * p.o_sb + h * p.o_sh, p.o_ss, q0, p.Sq);
+    if (threadIdx.x < BQ) {
+      const int qi = q0 + threadIdx.x;
+      const int64_t row = (static_cast<int64_t>(b) * p.Hq + h) * p.Sq + qi;
+      lv = qi < p.Sq ? lse_to_log2(lse[row]) : __builtin_inff();
+      dv = qi < p.Sq ? delta[row] : 0.f;
+    }
+  };
+  if (n_iter > 0) load(0);
+  for (int it = 0; it < n_iter; ++it) {
+    __syncthreads();
+    qr.template store_rows<LDQ>(sQ);
+    qr.template store_cols<LDT>(sQt);
+    dr.template store_rows<LDQ>(sD);
+    dr.template store_cols<LDT>(sDt);
+    if (threadIdx.x < BQ) {
+      sL[threadIdx.x] = lv;
+      sDl[threadIdx.x] = dv;
+    }
+    __syncthreads();
+    const int q0 = (qt_begin + it % per_head) * BQ;
+    if (it + 1 < n_iter) load(it + 1);
+    const int64_t qa_last = p.q_offset + min(q0 + BQ - 1, p.Sq - 1);
+    if (kw0 >= p.Sk) continue;
+    if (p.causal && ka_wave_first > qa_last) continue;
+    const bool need_mask = (kw0 + 16 > p.Sk) || (p.causal && ka_wave_last > p.q_offset + q0);
 
-      // S = Q K^T and dP = dO V^T for this wave's 16 keys: lane holds
-      // S[q = 16 mq + 4 g + e][key = kw0 + l16].
-      f32x4 s[4], dp[4];
+    // S = Q K^T and dP = dO V^T for this wave's 16 keys: lane holds
+    // S[q = 16 mq + 4 g + e][key = kw0 + l16].
+    f32x4 s[4], dp[4];
 #pragma unroll
-      for (int mq = 0; mq < 4; ++mq) {
-        s[mq] = f32x4{0.f, 0.f, 0.f, 0.f};
-        dp[mq] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int mq = 0; mq < 4; ++mq) {
+      s[mq] = f32x4{0.f, 0.f, 0.f, 0.f};
+      dp[mq] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const bf16x8 aq = ld8(sQ + (mq * 16 + l16) * LDQ + ks * 32 + g * 8);
-          const bf16x8 ad = ld8(sD + (mq * 16 + l16) * LDQ + ks * 32 + g * 8);
-          s[mq] = mfma16(aq, kf[ks], s[mq]);
-          dp[mq] = mfma16(ad, vf[ks], dp[mq]);
-        }
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8 aq = ld8(sQ + (mq * 16 + l16) * LDQ + ks * 32 + g * 8);
+        const bf16x8 ad = ld8(sD + (mq * 16 + l16) * LDQ + ks * 32 + g * 8);
+        s[mq] = mfma16(aq, kf[ks], s[mq]);
+        dp[mq] = mfma16(ad, vf[ks], dp[mq]);
       }
-      const int64_t ka = koff + kw0 + l16;
+    }
+    // smallest tile-relative query index that sees this lane's key (BQ: none)
+    int qmin = 0;
+    if (need_mask) {
+      int64_t f = p.causal ? koff + kw0 + l16 - p.q_offset - q0 : 0;
+      if (kw0 + l16 >= p.Sk) f = BQ;
+      qmin = f < 0 ? 0 : (f > BQ ? BQ : static_cast<int>(f));
+    }
 #pragma unroll
-      for (int mq = 0; mq < 4; ++mq)
+    for (int mq = 0; mq < 4; ++mq)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int ql = mq * 16 + g * 4 + e;
-          float pv = exp2f(s[mq][e] * p.scale_log2 - sL[ql]);
-          if (need_mask) {
-            if (kw0 + l16 >= p.Sk || (p.causal && ka > p.q_offset + q0 + ql)) pv = 0.f;
-          }
-          s[mq][e] = pv;
-          dp[mq][e] = pv * (dp[mq][e] - sDl[ql]);
-        }
-      bf16x8 pa[2], da[2];
+      for (int e = 0; e < 4; ++e) {
+        const int ql = mq * 16 + g * 4 + e;
+        float pv = fast_exp2(fmaf(s[mq][e], c, -sL[ql]));
+        pv = ql < qmin ? 0.f : pv;
+        s[mq][e] = pv;
+        dp[mq][e] = pv * (dp[mq][e] - sDl[ql]);
+      }
+    bf16x8 pa[2], da[2];
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
+    for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          pa[s2][e] = static_cast<bf16>(s[2 * s2][e]);
-          pa[s2][4 + e] = static_cast<bf16>(s[2 * s2 + 1][e]);
-          da[s2][e] = static_cast<bf16>(dp[2 * s2][e]);
-          da[s2][4 + e] = static_cast<bf16>(dp[2 * s2 + 1][e]);
-        }
+      for (int e = 0; e < 4; ++e) {
+        pa[s2][e] = static_cast<bf16>(s[2 * s2][e]);
+        pa[s2][4 + e] = static_cast<bf16>(s[2 * s2 + 1][e]);
+        da[s2][e] = static_cast<bf16>(dp[2 * s2][e]);
+        da[s2][4 + e] = static_cast<bf16>(dp[2 * s2 + 1][e]);
+      }
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
+    for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          const bf16x8 bd = ld4x2(sDt + (dt * 16 + l16) * LDT + 32 * s2 + g * 4);
-          const bf16x8 bq = ld4x2(sQt + (dt * 16 + l16) * LDT + 32 * s2 + g * 4);
-          dva[dt] = mfma16(pa[s2], bd, dva[dt]);
-          dka[dt] = mfma16(da[s2], bq, dka[dt]);
-        }
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const bf16x8 bd = ld4x2(sDt + (dt * 16 + l16) * LDT + 32 * s2 + g * 4);
+        const bf16x8 bq = ld4x2(sQt + (dt * 16 + l16) * LDT + 32 * s2 + g * 4);
+        dva[dt] = mfma16(pa[s2], bd, dva[dt]);
+        dka[dt] = mfma16(da[s2], bq, dka[dt]);
       }
     }
   }
   // lane holds dK[key = kw0 + 4 g + e][d = 16 dt + l16]
-  bf16* dkb = static_cast<bf16*>(kv.dk[blk]) + b * p.kv_sb + hk * p.kv_sh;
-  bf16* dvb = static_cast<bf16*>(kv.dv[blk]) + b * p.kv_sb + hk * p.kv_sh;
+  bf16* dkb = static_cast<bf16*>(kv.dk[blk]) + kv_off;
+  bf16* dvb = static_cast<bf16*>(kv.dv[blk]) + kv_off;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int key = kw0 + g * 4 + e;
     if (key >= p.Sk) continue;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      dkb[static_cast<int64_t>(key) * p.kv_ss + dt * 16 + l16] =
-          static_cast<bf16>(dka[dt][e] * p.scale);
+      dkb[static_cast<int64_t>(key) * p.kv_ss + dt * 16 + l16] = static_cast<bf16>(dka[dt][e] * p.scale);
       dvb[static_cast<int64_t>(key) * p.kv_ss + dt * 16 + l16] = static_cast<bf16>(dva[dt][e]);
     }
   }
@@ -784,6 +915,15 @@ int fill_shape(AttnShape* p, KVBlocks* kv, const void* q, const void* const* kb,
 using nmb::AttnShape;
 using nmb::KVBlocks;
 
+namespace {
+// Launch geometry of the XCD-mapped kernels: a 1-D grid of 8 * per_xcd blocks.
+void xcd_grid(int64_t items, int* per_xcd, unsigned* blocks) {
+  const int64_t per = (items + 7) / 8;
+  *per_xcd = static_cast<int>(per);
+  *blocks = static_cast<unsigned>(per * 8);
+}
+}  // namespace
+
 extern "C" int nmb_attn_fwd(const void* q, const void* const* k_blocks,
                             const void* const* v_blocks, const int64_t* k_offsets, int n_blocks,
                             void* o, float* lse, int64_t batch, int64_t q_heads, int64_t kv_heads,
@@ -801,14 +941,20 @@ extern "C" int nmb_attn_fwd(const void* q, const void* const* k_blocks,
   if (batch == 0 || seq_q == 0) return NMB_OK;
   if (dtype == NMB_BF16) {
     NMB_REQUIRE(nmb::aligned16(o), "attn_fwd: o must be 16-byte aligned");
-    const dim3 grid(static_cast<unsigned>((seq_q + 127) / 128), static_cast<unsigned>(q_heads),
-                    static_cast<unsigned>(batch));
+    const int n_qt = static_cast<int>((seq_q + 127) / 128);
+    const int64_t items = static_cast<int64_t>(n_qt) * q_heads * batch;
+    NMB_REQUIRE(items < (int64_t{1} << 30), "attn_fwd: problem too large for one launch");
+    int per_xcd;
+    unsigned blocks;
+    xcd_grid(items, &per_xcd, &blocks);
     const nmb::bf16* qp = static_cast<const nmb::bf16*>(q);
     nmb::bf16* op = static_cast<nmb::bf16*>(o);
     if (head_dim == 64)
-      hipLaunchKernelGGL(nmb::attn_fwd_kernel<64>, grid, dim3(256), 0, stream, qp, kv, op, lse, p);
+      hipLaunchKernelGGL(nmb::attn_fwd_kernel<64>, dim3(blocks), dim3(256), 0, stream, qp, kv, op,
+                         lse, p, n_qt, static_cast<int>(items), per_xcd);
     else
-      hipLaunchKernelGGL(nmb::attn_fwd_kernel<128>, grid, dim3(256), 0, stream, qp, kv, op, lse, p);
+      hipLaunchKernelGGL(nmb::attn_fwd_kernel<128>, dim3(blocks), dim3(256), 0, stream, qp, kv, op,
+                         lse, p, n_qt, static_cast<int>(items), per_xcd);
   } else {
     const dim3 grid(static_cast<unsigned>(seq_q), static_cast<unsigned>(q_heads),
                     static_cast<unsigned>(batch));
@@ -858,48 +1004,54 @@ extern "C" int nmb_attn_bwd(const void* q, const void* const* k_blocks,
   if (batch == 0) return NMB_OK;
   float* delta = static_cast<float*>(workspace);
   const int D = static_cast<int>(head_dim);
-  if (seq_q > 0) {
-    int64_t rows = batch * q_heads * seq_q;
-    int64_t blocks = (rows + 255) / 256;
-    if (blocks > 8192) blocks = 8192;
-    if (dtype == NMB_BF16)
-      hipLaunchKernelGGL(nmb::attn_delta_kernel<nmb::bf16>, dim3(static_cast<unsigned>(blocks)),
-                         dim3(256), 0, stream, static_cast<const nmb::bf16*>(o),
-                         static_cast<const nmb::bf16*>(dout), delta, p, D);
-    else
-      hipLaunchKernelGGL(nmb::attn_delta_kernel<float>, dim3(static_cast<unsigned>(blocks)),
-                         dim3(256), 0, stream, static_cast<const float*>(o),
-                         static_cast<const float*>(dout), delta, p, D);
-    NMB_CHECK_LAUNCH("attn_bwd(delta)");
-  }
   if (dtype == NMB_BF16) {
-    NMB_REQUIRE(nmb::aligned16(dq) && nmb::aligned16(dout), "attn_bwd: dq/dout must be aligned");
+    NMB_REQUIRE(nmb::aligned16(dq) && nmb::aligned16(dout) && nmb::aligned16(o),
+                "attn_bwd: dq/dout/o must be 16-byte aligned");
     const nmb::bf16* qp = static_cast<const nmb::bf16*>(q);
+    const nmb::bf16* opp = static_cast<const nmb::bf16*>(o);
     const nmb::bf16* dp = static_cast<const nmb::bf16*>(dout);
     nmb::bf16* dqp = static_cast<nmb::bf16*>(dq);
+    // the dQ kernel also writes delta, which the dK/dV kernel reads: keep this order
     if (seq_q > 0) {
-      const dim3 grid(static_cast<unsigned>((seq_q + 127) / 128), static_cast<unsigned>(q_heads),
-                      static_cast<unsigned>(batch));
+      const int n_qt = static_cast<int>((seq_q + 127) / 128);
+      const int64_t items = static_cast<int64_t>(n_qt) * q_heads * batch;
+      NMB_REQUIRE(items < (int64_t{1} << 30), "attn_bwd: problem too large for one launch");
+      int per_xcd;
+      unsigned blocks;
+      xcd_grid(items, &per_xcd, &blocks);
       if (D == 64)
-        hipLaunchKernelGGL(nmb::attn_bwd_dq_kernel<64>, grid, dim3(256), 0, stream, qp, kv, dp,
-                           lse, delta, dqp, p);
+        hipLaunchKernelGGL(nmb::attn_bwd_dq_kernel<64>, dim3(blocks), dim3(256), 0, stream, qp, kv,
+                           opp, dp, lse, delta, dqp, p, n_qt, static_cast<int>(items), per_xcd);
       else
-        hipLaunchKernelGGL(nmb::attn_bwd_dq_kernel<128>, grid, dim3(256), 0, stream, qp, kv, dp,
-                           lse, delta, dqp, p);
+        hipLaunchKernelGGL(nmb::attn_bwd_dq_kernel<128>, dim3(blocks), dim3(256), 0, stream, qp,
+                           kv, opp, dp, lse, delta, dqp, p, n_qt, static_cast<int>(items), per_xcd);
       NMB_CHECK_LAUNCH("attn_bwd(dq)");
     }
     if (seq_k > 0) {
-      const dim3 grid(static_cast<unsigned>((seq_k + 63) / 64), static_cast<unsigned>(kv_heads),
-                      static_cast<unsigned>(batch * n_blocks));
+      const int n_kt = static_cast<int>((seq_k + 63) / 64);
+      const int64_t items = static_cast<int64_t>(n_kt) * kv_heads * batch * n_blocks;
+      NMB_REQUIRE(items < (int64_t{1} << 30), "attn_bwd: problem too large for one launch");
+      int per_xcd;
+      unsigned blocks;
+      xcd_grid(items, &per_xcd, &blocks);
       if (D == 64)
-        hipLaunchKernelGGL(nmb::attn_bwd_dkdv_kernel<64>, grid, dim3(256), 0, stream, qp, kv, dp,
-                           lse, delta, p);
+        hipLaunchKernelGGL(nmb::attn_bwd_dkdv_kernel<64>, dim3(blocks), dim3(256), 0, stream, qp,
+                           kv, dp, lse, delta, p, n_kt, static_cast<int>(items), per_xcd);
       else
-        hipLaunchKernelGGL(nmb::attn_bwd_dkdv_kernel<128>, grid, dim3(256), 0, stream, qp, kv, dp,
-                           lse, delta, p);
+        hipLaunchKernelGGL(nmb::attn_bwd_dkdv_kernel<128>, dim3(blocks), dim3(256), 0, stream, qp,
+                           kv, dp, lse, delta, p, n_kt, static_cast<int>(items), per_xcd);
       NMB_CHECK_LAUNCH("attn_bwd(dkdv)");
     }
   } else {
+    if (seq_q > 0) {
+      int64_t rows = batch * q_heads * seq_q;
+      int64_t blocks = (rows + 255) / 256;
+      if (blocks > 8192) blocks = 8192;
+      hipLaunchKernelGGL(nmb::attn_delta_kernel<float>, dim3(static_cast<unsigned>(blocks)),
+                         dim3(256), 0, stream, static_cast<const float*>(o),
+                         static_cast<const float*>(dout), delta, p, D);
+      NMB_CHECK_LAUNCH("attn_bwd(delta)");
+    }
     const float* qp = static_cast<const float*>(q);
     const float* dp = static_cast<const float*>(dout);
     if (seq_q > 0) {

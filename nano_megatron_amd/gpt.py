@@ -34,7 +34,12 @@ import torch.nn.functional as F
 from torch import Tensor, nn
 
 from nano_megatron_amd import functional as Fn
-from nano_megatron_amd.block import BlockMeta, CheckpointedBlockFunction, EagerBlockFunction
+from nano_megatron_amd.block import (
+    BlockMeta,
+    CheckpointedBlockFunction,
+    EagerBlockFunction,
+    pack_adjacent,
+)
 from nano_megatron_amd.kernels import HipKernelBackend, KernelBackend
 from nano_megatron_amd.nn import RotaryEmbedding, _offload_context, activation_checkpoint
 
@@ -507,6 +512,15 @@ class GPTModel(nn.Module):
             if owns_lm_head else None
         )
 
+    def _pack_block_weights(self) -> None:
+        """Keep each layer's [Wq; Wk; Wv] and [Wg; Wu] adjacent in memory so the
+        fused projections read them in place (a no-op once packed)."""
+        for layer in self.layers:
+            if layer.fusable():
+                a, m = layer.attention, layer.mlp
+                pack_adjacent((a.q_proj.weight, a.k_proj.weight, a.v_proj.weight))
+                pack_adjacent((m.gate_proj.weight, m.up_proj.weight))
+
     def _checkpoint_layer(self, layer: GPTLayer) -> bool:
         """models/gpt/model.py:162-170."""
         config = self.activation_checkpoint_config
@@ -535,6 +549,7 @@ class GPTModel(nn.Module):
                            torch.arange(offset, offset + sequence)) and position_ids.ndim == 1:
                 position_ids = None  # the default arange: offset form, no position tensor
 
+        self._pack_block_weights()
         mode = getattr(self.activation_checkpoint_config, "mode", "none")
         offload = bool(getattr(self.activation_checkpoint_config, "offload_saved_tensors", False))
         for layer in self.layers:
