@@ -147,11 +147,11 @@ struct PairTile {
 // Number of 64-key tiles of a block that any query up to absolute position
 // q_last can see.
 __device__ __forceinline__ int visible_key_tiles(const AttnShape& p, int64_t koff, int64_t q_last) {
-  int n = (p.Sk + 63) / 64;
+  int n = (p.Sk + 63) >> 6;
   if (p.causal) {
     const int64_t lim = q_last - koff;
     if (lim < 0) return 0;
-    const int64_t t = lim / 64 + 1;
+    const int64_t t = (lim >> 6) + 1;
     if (t < n) n = static_cast<int>(t);
   }
   return n;
@@ -167,19 +167,27 @@ __device__ __forceinline__ int xcd_item(int items, int per_xcd) {
   return w < items ? w : -1;
 }
 
-// Advance (blk, kt) to the next visible K/V tile of the concatenated blocks.
+// Advance (blk, kt) to the next visible K/V tile of the concatenated blocks;
+// nt holds the visible tile count of block blk (recomputed only when the
+// block changes).
 __device__ __forceinline__ void next_tile(const AttnShape& p, const KVBlocks& kv, int64_t q_last,
-                                          int& blk, int& kt) {
-  ++kt;
-  if (kt < visible_key_tiles(p, kv.koff[blk], q_last)) return;
+                                          int& blk, int& kt, int& nt) {
+  if (++kt < nt) return;
   kt = 0;
-  for (++blk; blk < p.nblk; ++blk)
-    if (visible_key_tiles(p, kv.koff[blk], q_last) > 0) return;
+  for (++blk; blk < p.nblk; ++blk) {
+    nt = visible_key_tiles(p, kv.koff[blk], q_last);
+    if (nt > 0) return;
+  }
 }
 
-__device__ __forceinline__ int first_block(const AttnShape& p, const KVBlocks& kv, int64_t q_last) {
+__device__ __forceinline__ int first_block(const AttnShape& p, const KVBlocks& kv, int64_t q_last,
+                                           int& nt) {
   int blk = 0;
-  while (blk < p.nblk && visible_key_tiles(p, kv.koff[blk], q_last) == 0) ++blk;
+  nt = 0;
+  for (; blk < p.nblk; ++blk) {
+    nt = visible_key_tiles(p, kv.koff[blk], q_last);
+    if (nt > 0) break;
+  }
   return blk;
 }
 
@@ -209,7 +217,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_fwd_kernel(const bf
                                                           float* __restrict__ lse, AttnShape p,
                                                           int n_qt, int items, int per_xcd) {
   constexpr int BQ = 128, BK = 64, KS = D / 32, DT = D / 16;
-  constexpr int LDK = D + 8, LDV = BK + 8;
+  constexpr int LDK = D + 8, LDV = BK + 4;
   __shared__ __attribute__((aligned(16))) bf16 sK[BK * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sVt[D * LDV];
 
@@ -247,7 +255,8 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_fwd_kernel(const bf
   const int64_t kv_off = b * p.kv_sb + hk * p.kv_sh;
 
   PairTile<BK, D> kr, vr;
-  int blk = first_block(p, kv, qa_wg_last), kt = 0;
+  int nt = 0;
+  int blk = first_block(p, kv, qa_wg_last, nt), kt = 0;
   if (blk < p.nblk) {
     kr.load(static_cast<const bf16*>(kv.k[blk]) + kv_off, p.kv_ss, 0, p.Sk);
     vr.load(static_cast<const bf16*>(kv.v[blk]) + kv_off, p.kv_ss, 0, p.Sk);
@@ -260,7 +269,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_fwd_kernel(const bf
     const int64_t koff = kv.koff[blk];
     const int k0 = kt * BK;
     int nb = blk, nk = kt;
-    next_tile(p, kv, qa_wg_last, nb, nk);
+    next_tile(p, kv, qa_wg_last, nb, nk, nt);
     if (nb < p.nblk) {
       kr.load(static_cast<const bf16*>(kv.k[nb]) + kv_off, p.kv_ss, nk * BK, p.Sk);
       vr.load(static_cast<const bf16*>(kv.v[nb]) + kv_off, p.kv_ss, nk * BK, p.Sk);
@@ -397,7 +406,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
     const bf16* __restrict__ dout, const float* __restrict__ lse, float* __restrict__ delta,
     bf16* __restrict__ dq, AttnShape p, int n_qt, int items, int per_xcd) {
   constexpr int BQ = 128, BK = 64, KS = D / 32, DT = D / 16;
-  constexpr int LDK = D + 8, LDT = BK + 8;
+  constexpr int LDK = D + 8, LDT = BK + 4;
   __shared__ __attribute__((aligned(16))) bf16 sK[BK * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sKt[D * LDT];
   __shared__ __attribute__((aligned(16))) bf16 sV[BK * LDK];
@@ -451,7 +460,8 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
   const int64_t kv_off = b * p.kv_sb + hk * p.kv_sh;
 
   PairTile<BK, D> kr, vr;
-  int blk = first_block(p, kv, qa_wg_last), kt = 0;
+  int nt = 0;
+  int blk = first_block(p, kv, qa_wg_last, nt), kt = 0;
   if (blk < p.nblk) {
     kr.load(static_cast<const bf16*>(kv.k[blk]) + kv_off, p.kv_ss, 0, p.Sk);
     vr.load(static_cast<const bf16*>(kv.v[blk]) + kv_off, p.kv_ss, 0, p.Sk);
@@ -465,7 +475,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
     const int64_t koff = kv.koff[blk];
     const int k0 = kt * BK;
     int nb = blk, nk = kt;
-    next_tile(p, kv, qa_wg_last, nb, nk);
+    next_tile(p, kv, qa_wg_last, nb, nk, nt);
     if (nb < p.nblk) {
       kr.load(static_cast<const bf16*>(kv.k[nb]) + kv_off, p.kv_ss, nk * BK, p.Sk);
       vr.load(static_cast<const bf16*>(kv.v[nb]) + kv_off, p.kv_ss, nk * BK, p.Sk);
@@ -550,7 +560,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
     const float* __restrict__ lse, const float* __restrict__ delta, AttnShape p, int n_kt,
     int items, int per_xcd) {
   constexpr int BQ = 64, BK = 64, KS = D / 32, DT = D / 16;
-  constexpr int LDQ = D + 8, LDT = BQ + 8;
+  constexpr int LDQ = D + 8, LDT = BQ + 4;
   __shared__ __attribute__((aligned(16))) bf16 sQ[BQ * LDQ];
   __shared__ __attribute__((aligned(16))) bf16 sQt[D * LDT];
   __shared__ __attribute__((aligned(16))) bf16 sD[BQ * LDQ];

@@ -17,7 +17,7 @@ namespace nmb {
 namespace {
 
 constexpr int kWaves = 4;
-constexpr int kBwdBlocks = 512;
+constexpr int kBwdBlocks = 256;
 
 template <typename T>
 __device__ __forceinline__ float inv_rms(float sum_sq, int cols, float eps) {
@@ -67,105 +67,148 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const T* __restrict__ 
   if (rstd != nullptr && lane == 0) rstd[row] = r;
 }
 
+// Backward: 8 wavefronts per workgroup, each owning rows r0 + wave, r0 + wave
+// + 8, ...; two rows are processed per iteration so their loads overlap.
+constexpr int kBwdWaves = 8;
+
 template <typename T, int ITERS>
-__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
+__device__ __forceinline__ void bwd_row(const T* __restrict__ xr, const T* __restrict__ dyr,
+                                        const T* __restrict__ dresr, T* __restrict__ dxr,
+                                        const float (&wv)[ITERS][VecTraits<T>::N],
+                                        float (&acc)[ITERS][VecTraits<T>::N],
+                                        float (&xv)[ITERS][VecTraits<T>::N],
+                                        float (&dv)[ITERS][VecTraits<T>::N], int lane, int cols,
+                                        float eps) {
+  constexpr int V = VecTraits<T>::N;
+  float ss = 0.f;
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it)
+#pragma unroll
+    for (int i = 0; i < V; ++i) ss += xv[it][i] * xv[it][i];
+  ss = wave_sum(ss);
+  const float r = inv_rms<T>(ss, cols, eps);
+  float dot = 0.f;
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float n = mul_rn(xv[it][i], r);
+      const float g = round_as<T>(mul_rn(dv[it][i], wv[it][i]));
+      dot += g * n;
+      // weight gradient of y = cast(n) * w: dy * cast(n), rounded as the
+      // reference's per-element product tensor is.
+      acc[it][i] += round_as<T>(mul_rn(dv[it][i], round_as<T>(n)));
+      xv[it][i] = n;
+      dv[it][i] = g;
+    }
+  }
+  dot = wave_sum(dot);
+  const float mean_dot = __fdiv_rn(dot, static_cast<float>(cols));
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const int c = (it * 64 + lane) * V;
+    if (c < cols) {
+      float o[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) o[i] = r * (dv[it][i] - xv[it][i] * mean_dot);
+      if (dresr != nullptr) {
+        float rv[V];
+        load_vec<T>(dresr + c, rv);
+#pragma unroll
+        for (int i = 0; i < V; ++i) o[i] += rv[i];
+      }
+      store_vec<T>(dxr + c, o);
+    }
+  }
+}
+
+template <typename T, int ITERS>
+__device__ __forceinline__ void load_row(const T* __restrict__ p, float (&v)[ITERS][VecTraits<T>::N],
+                                         int lane, int cols) {
+  constexpr int V = VecTraits<T>::N;
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const int c = (it * 64 + lane) * V;
+    if (c < cols) {
+      load_vec<T>(p + c, v[it]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < V; ++i) v[it][i] = 0.f;
+    }
+  }
+}
+
+template <typename T, int ITERS>
+__global__ __launch_bounds__(512) void rmsnorm_bwd_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ dy,
     const T* __restrict__ dres, T* __restrict__ dx, float* __restrict__ partial, int64_t rows,
     int cols, float eps, int64_t rows_per_block) {
   constexpr int V = VecTraits<T>::N;
-  extern __shared__ float s_dw[];  // [kWaves][cols]
+  extern __shared__ float s_dw[];  // [4][cols]
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   float wv[ITERS][V];
   float acc[ITERS][V];
+  load_row<T, ITERS>(w, wv, lane, cols);
 #pragma unroll
-  for (int it = 0; it < ITERS; ++it) {
-    const int c = (it * 64 + lane) * V;
-    if (c < cols) {
-      load_vec<T>(w + c, wv[it]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < V; ++i) wv[it][i] = 0.f;
-    }
+  for (int it = 0; it < ITERS; ++it)
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[it][i] = 0.f;
-  }
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rows_per_block;
   const int64_t r1 = min(rows, r0 + rows_per_block);
-  for (int64_t row = r0 + wave; row < r1; row += kWaves) {
-    const T* xr = x + row * cols;
-    const T* dyr = dy + row * cols;
-    float xv[ITERS][V], dv[ITERS][V];
-    float ss = 0.f;
-#pragma unroll
-    for (int it = 0; it < ITERS; ++it) {
-      const int c = (it * 64 + lane) * V;
-      if (c < cols) {
-        load_vec<T>(xr + c, xv[it]);
-        load_vec<T>(dyr + c, dv[it]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < V; ++i) xv[it][i] = dv[it][i] = 0.f;
-      }
-#pragma unroll
-      for (int i = 0; i < V; ++i) ss += xv[it][i] * xv[it][i];
-    }
-    ss = wave_sum(ss);
-    const float r = inv_rms<T>(ss, cols, eps);
-    float dot = 0.f;
-#pragma unroll
-    for (int it = 0; it < ITERS; ++it) {
-#pragma unroll
-      for (int i = 0; i < V; ++i) {
-        const float n = mul_rn(xv[it][i], r);
-        const float g = round_as<T>(mul_rn(dv[it][i], wv[it][i]));
-        dot += g * n;
-        // weight gradient of y = cast(n) * w: dy * cast(n), rounded as the
-        // reference's per-element product tensor is.
-        acc[it][i] += round_as<T>(mul_rn(dv[it][i], round_as<T>(n)));
-        xv[it][i] = n;   // keep n
-        dv[it][i] = g;   // keep g
-      }
-    }
-    dot = wave_sum(dot);
-    const float mean_dot = __fdiv_rn(dot, static_cast<float>(cols));
-    T* dxr = dx + row * cols;
-#pragma unroll
-    for (int it = 0; it < ITERS; ++it) {
-      const int c = (it * 64 + lane) * V;
-      if (c < cols) {
-        float o[V];
-#pragma unroll
-        for (int i = 0; i < V; ++i) o[i] = r * (dv[it][i] - xv[it][i] * mean_dot);
-        if (dres != nullptr) {
-          float rv[V];
-          load_vec<T>(dres + row * cols + c, rv);
-#pragma unroll
-          for (int i = 0; i < V; ++i) o[i] += rv[i];
-        }
-        store_vec<T>(dxr + c, o);
-      }
-    }
+  int64_t row = r0 + wave;
+  for (; row + kBwdWaves < r1; row += 2 * kBwdWaves) {
+    const int64_t rb = row + kBwdWaves;
+    float xa[ITERS][V], da[ITERS][V], xb[ITERS][V], db[ITERS][V];
+    load_row<T, ITERS>(x + row * cols, xa, lane, cols);
+    load_row<T, ITERS>(dy + row * cols, da, lane, cols);
+    load_row<T, ITERS>(x + rb * cols, xb, lane, cols);
+    load_row<T, ITERS>(dy + rb * cols, db, lane, cols);
+    bwd_row<T, ITERS>(x + row * cols, dy + row * cols, dres ? dres + row * cols : nullptr,
+                      dx + row * cols, wv, acc, xa, da, lane, cols, eps);
+    bwd_row<T, ITERS>(x + rb * cols, dy + rb * cols, dres ? dres + rb * cols : nullptr,
+                      dx + rb * cols, wv, acc, xb, db, lane, cols, eps);
   }
+  if (row < r1) {
+    float xa[ITERS][V], da[ITERS][V];
+    load_row<T, ITERS>(x + row * cols, xa, lane, cols);
+    load_row<T, ITERS>(dy + row * cols, da, lane, cols);
+    bwd_row<T, ITERS>(x + row * cols, dy + row * cols, dres ? dres + row * cols : nullptr,
+                      dx + row * cols, wv, acc, xa, da, lane, cols, eps);
+  }
+  // fold the 8 wave partials in two rounds through 4 LDS rows (<= 64 KiB)
+  const int slot = wave & 3;
+  if (wave >= 4) {
 #pragma unroll
-  for (int it = 0; it < ITERS; ++it) {
-    const int c = (it * 64 + lane) * V;
-    if (c < cols) {
+    for (int it = 0; it < ITERS; ++it) {
+      const int c = (it * 64 + lane) * V;
+      if (c < cols) {
 #pragma unroll
-      for (int i = 0; i < V; ++i) s_dw[wave * cols + c + i] = acc[it][i];
+        for (int i = 0; i < V; ++i) s_dw[slot * cols + c + i] = acc[it][i];
+      }
     }
   }
   __syncthreads();
-  for (int c = threadIdx.x; c < cols; c += 256) {
-    float s = 0.f;
+  if (wave < 4) {
 #pragma unroll
-    for (int k = 0; k < kWaves; ++k) s += s_dw[k * cols + c];
-    partial[static_cast<int64_t>(blockIdx.x) * cols + c] = s;
+    for (int it = 0; it < ITERS; ++it) {
+      const int c = (it * 64 + lane) * V;
+      if (c < cols) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) s_dw[slot * cols + c + i] += acc[it][i];
+      }
+    }
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < cols; c += 512) {
+    const float t = (s_dw[c] + s_dw[cols + c]) + (s_dw[2 * cols + c] + s_dw[3 * cols + c]);
+    partial[static_cast<int64_t>(blockIdx.x) * cols + c] = t;
   }
 }
 
-// dw[c] = sum_b partial[b][c] in a fixed order.  Block: 16 column groups of 16
-// columns each (64-byte segments); the 16 row groups are combined in LDS.
+// dw[c] = sum_b partial[b][c] in a fixed order.  Block: 16 row groups x 16
+// columns (64-byte segments); each thread issues its (at most 16) loads
+// back to back, then the row groups are combined in LDS.
 template <typename T>
 __global__ __launch_bounds__(256) void column_sum_kernel(const float* __restrict__ partial,
                                                          int nblocks, int cols,
@@ -176,7 +219,14 @@ __global__ __launch_bounds__(256) void column_sum_kernel(const float* __restrict
   const int c = blockIdx.x * 16 + cl;
   float acc = 0.f;
   if (c < cols) {
-    for (int b = rg; b < nblocks; b += 16) acc += partial[static_cast<int64_t>(b) * cols + c];
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int b = rg + 16 * j;
+      v[j] = b < nblocks ? partial[static_cast<int64_t>(b) * cols + c] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc += v[j];
   }
   s[rg][cl] = acc;
   __syncthreads();
@@ -191,11 +241,11 @@ __global__ __launch_bounds__(256) void column_sum_kernel(const float* __restrict
 int iters_for(int cols, int vec) { return (cols + 64 * vec - 1) / (64 * vec); }
 
 void bwd_grid(int64_t rows, int* nblocks, int64_t* rows_per_block) {
-  int64_t nb = (rows + kWaves - 1) / kWaves;
+  int64_t nb = (rows + kBwdWaves - 1) / kBwdWaves;
   if (nb > kBwdBlocks) nb = kBwdBlocks;
   if (nb < 1) nb = 1;
   int64_t rpb = (rows + nb - 1) / nb;
-  rpb = (rpb + kWaves - 1) / kWaves * kWaves;
+  rpb = (rpb + kBwdWaves - 1) / kBwdWaves * kBwdWaves;
   nb = (rows + rpb - 1) / rpb;
   if (nb < 1) nb = 1;
   *nblocks = static_cast<int>(nb);
@@ -258,6 +308,7 @@ int bwd_impl(const void* x, const void* w, const void* dy, const void* dres, voi
   int64_t rpb;
   bwd_grid(rows, &nblocks, &rpb);
   const size_t need = static_cast<size_t>(nblocks) * static_cast<size_t>(cols) * sizeof(float);
+  NMB_REQUIRE(nblocks <= 256, "rmsnorm_bwd: internal grid exceeds the column-sum capacity");
   NMB_REQUIRE(ws != nullptr && ws_bytes >= need,
               "rmsnorm_bwd: workspace of %zu bytes is smaller than the %zu required", ws_bytes,
               need);
@@ -268,11 +319,11 @@ int bwd_impl(const void* x, const void* w, const void* dy, const void* dres, voi
   const T* drp = static_cast<const T*>(dres);
   T* dxp = static_cast<T*>(dx);
   float* part = static_cast<float*>(ws);
-  const size_t lds = static_cast<size_t>(kWaves) * cols * sizeof(float);
+  const size_t lds = static_cast<size_t>(4) * cols * sizeof(float);
   switch (iters_for(c, VecTraits<T>::N)) {
 #define NMB_CASE(I)                                                                       \
   case I:                                                                                 \
-    hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, I>), dim3(nblocks), dim3(256), lds, stream, \
+    hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, I>), dim3(nblocks), dim3(512), lds, stream, \
                        xp, wp, dyp, drp, dxp, part, rows, c, eps, rpb);                   \
     break;
     NMB_CASE(1) NMB_CASE(2) NMB_CASE(3) NMB_CASE(4) NMB_CASE(5) NMB_CASE(6) NMB_CASE(7)
