@@ -150,6 +150,18 @@ int nmb_ce_bwd(void* logits, int64_t ld, const int64_t* targets, int64_t rows, i
                int64_t ignore_index, const float* lse, const float* grad, int dtype,
                hipStream_t stream);
 
+/* ------------------------------------------------------------ GEMM
+ * replaces the dense projections nn.Linear / F.linear (nn/kernels/
+ * torch_backend.py:19-20, tensor_parallel/layers.py:214) and their autograd
+ * products, bf16 in / bf16 out with fp32 accumulation:
+ *   D[M, N] = alpha * op(A)[M, K] * op(B)[K, N] + beta * C[M, N]   (row-major)
+ * a_layout 0: A stored [M, K] (row stride lda); 1: A stored [K, M].
+ * b_layout 0: B stored [N, K] (a weight used as W^T); 1: B stored [K, N].
+ * C may alias D.  The contiguous extents and lda/ldb must be multiples of 8. */
+int nmb_gemm_bf16(int a_layout, int b_layout, int64_t m, int64_t n, int64_t k, float alpha,
+                  const void* a, int64_t lda, const void* b, int64_t ldb, float beta,
+                  const void* c, int64_t ldc, void* d, int64_t ldd, hipStream_t stream);
+
 /* ------------------------------------------------------------ optimizer
  * replaces FlatShardZeROStrategy.clip_grad_norm + optimizer_step at DP=1
  * (data_parallel/_zero.py:130-199; defaults config/schema.py:439-445):

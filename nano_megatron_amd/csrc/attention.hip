@@ -206,17 +206,19 @@ __device__ __forceinline__ int mask_limit(const AttnShape& p, int64_t koff, int 
 }
 
 // ---------------------------------------------------------------- forward
-// Workgroup = 128 queries of one (batch, head): wave w owns queries
-// 32w..32w+31 as two 16-query MFMA column tiles.  K/V stream through LDS in
-// 64-key tiles; the next tile's global reads are issued before the current
-// tile's MFMA work.  Scores stay raw; exp2(s * c - m * c) folds the softmax
-// scale into one FMA per score.
-template <int D>
-__global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_fwd_kernel(const bf16* __restrict__ q, KVBlocks kv,
-                                                          bf16* __restrict__ o,
-                                                          float* __restrict__ lse, AttnShape p,
-                                                          int n_qt, int items, int per_xcd) {
-  constexpr int BQ = 128, BK = 64, KS = D / 32, DT = D / 16;
+// Workgroup = 4 wavefronts x TQ column tiles of 16 queries of one (batch,
+// head): column tile t of wave w holds queries 64 t + 16 w .. +15 of the
+// workgroup's 64 TQ queries, so under causal masking every wave sees about the
+// same keys (balanced), and a tile whose first key lies beyond all queries of
+// a column tile is skipped for that column tile (wave-uniform).  K/V stream
+// through LDS in 64-key tiles; the next tile's global reads are issued before
+// the current tile's MFMA work.  Scores stay raw; exp2(s * c - m * c) folds
+// the softmax scale into one FMA per score.
+template <int D, int TQ>
+__global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_kernel(
+    const bf16* __restrict__ q, KVBlocks kv, bf16* __restrict__ o, float* __restrict__ lse,
+    AttnShape p, int n_qt, int items, int per_xcd) {
+  constexpr int BQ = 64 * TQ, BK = 64, KS = D / 32, DT = D / 16;
   constexpr int LDK = D + 8, LDV = BK + 4;
   __shared__ __attribute__((aligned(16))) bf16 sK[BK * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sVt[D * LDV];
@@ -229,28 +231,27 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_fwd_kernel(const bf
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g = lane >> 4;
   const int hk = h / (p.Hq / p.Hkv);
-  const int q0 = qt * BQ + wave * 32;
+  const int qbase = qt * BQ + 16 * wave;  // column tile t: qbase + 64 t + l16
   const float c = p.scale_log2;
 
   const bf16* qb = q + b * p.q_sb + h * p.q_sh;
-  bf16x8 qf[2][KS];
+  bf16x8 qf[TQ][KS];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int qi = q0 + 16 * t + l16;
+  for (int t = 0; t < TQ; ++t) {
+    const int qi = qbase + 64 * t + l16;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
       qf[t][ks] = qi < p.Sq ? ld8(qb + static_cast<int64_t>(qi) * p.q_ss + ks * 32 + g * 8) : zero8();
   }
-  float m[2] = {-__builtin_inff(), -__builtin_inff()};
-  float l[2] = {0.f, 0.f};
-  f32x4 acc[2][DT];
+  float m[TQ], l[TQ];
+  f32x4 acc[TQ][DT];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int t = 0; t < TQ; ++t) {
+    m[t] = -__builtin_inff();
+    l[t] = 0.f;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int64_t qa_wave_first = p.q_offset + q0;
-  const int64_t qa_wave_last = p.q_offset + min(q0 + 31, p.Sq - 1);
+  }
   const int64_t qa_wg_last = p.q_offset + min(qt * BQ + BQ - 1, p.Sq - 1);
   const int64_t kv_off = b * p.kv_sb + hk * p.kv_sh;
 
@@ -276,42 +277,55 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_fwd_kernel(const bf
     }
     blk = nb;
     kt = nk;
-    if (p.causal && koff + k0 > qa_wave_last) continue;  // wave-uniform: nothing visible
-    const bool need_mask = (k0 + BK > p.Sk) || (p.causal && koff + k0 + BK - 1 > qa_wave_first);
-
-    f32x4 s[4][2];
+    // per column tile: is any key of this tile visible, is masking needed?
+    bool live[TQ], need_mask[TQ];
 #pragma unroll
-    for (int mk = 0; mk < 4; ++mk) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t) s[mk][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 a = ld8(sK + (mk * 16 + l16) * LDK + ks * 32 + g * 8);
-#pragma unroll
-        for (int t = 0; t < 2; ++t) s[mk][t] = mfma16(a, qf[t][ks], s[mk][t]);
-      }
+    for (int t = 0; t < TQ; ++t) {
+      const int64_t qfirst = p.q_offset + qbase + 64 * t;
+      const int64_t qlast = p.q_offset + min(qbase + 64 * t + 15, p.Sq - 1);
+      live[t] = !(p.causal && koff + k0 > qlast) && (qbase + 64 * t < p.Sq);
+      need_mask[t] = (k0 + BK > p.Sk) || (p.causal && koff + k0 + BK - 1 > qfirst);
     }
-    bf16x8 pf[2][2];
+
+    // K and V^T fragments of this tile, read from LDS once and reused by every
+    // column tile of the wave
+    bf16x8 kfr[KS][4], vfr[DT][2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int mk = 0; mk < 4; ++mk) kfr[ks][mk] = ld8(sK + (mk * 16 + l16) * LDK + ks * 32 + g * 8);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) vfr[dt][s2] = ld4x2(sVt + (dt * 16 + l16) * LDV + 32 * s2 + g * 4);
+#pragma unroll
+    for (int t = 0; t < TQ; ++t) {
+      if (!live[t]) continue;
+      f32x4 s[4];
+#pragma unroll
+      for (int mk = 0; mk < 4; ++mk) s[mk] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int mk = 0; mk < 4; ++mk) s[mk] = mfma16(kfr[ks][mk], qf[t][ks], s[mk]);
       float tmax = -__builtin_inff();
-      if (need_mask) {
+      if (need_mask[t]) {
         // last visible tile-relative key index of this lane's query
-        const int lim = mask_limit(p, koff, k0, p.q_offset + q0 + 16 * t + l16);
+        const int lim = mask_limit(p, koff, k0, p.q_offset + qbase + 64 * t + l16);
 #pragma unroll
         for (int mk = 0; mk < 4; ++mk)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             // branch-free select: a conditional store into the vector element
             // under short-circuit control flow is not reliably kept
-            const float sv = s[mk][t][e];
-            s[mk][t][e] = (mk * 16 + g * 4 + e > lim) ? -__builtin_inff() : sv;
+            const float sv = s[mk][e];
+            s[mk][e] = (mk * 16 + g * 4 + e > lim) ? -__builtin_inff() : sv;
           }
       }
 #pragma unroll
       for (int mk = 0; mk < 4; ++mk)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) tmax = fmaxf(tmax, s[mk][t][e]);
+        for (int e = 0; e < 4; ++e) tmax = fmaxf(tmax, s[mk][e]);
       tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
       tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
       const float mnew = fmaxf(m[t], tmax);
@@ -323,39 +337,37 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_fwd_kernel(const bf
       for (int mk = 0; mk < 4; ++mk)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float pv = fast_exp2(fmaf(s[mk][t][e], c, -mc));
-          s[mk][t][e] = pv;
+          const float pv = fast_exp2(fmaf(s[mk][e], c, -mc));
+          s[mk][e] = pv;
           rs += pv;
         }
       rs += __shfl_xor(rs, 16, 64);
       rs += __shfl_xor(rs, 32, 64);
       l[t] = l[t] * alpha + rs;
       m[t] = mnew;
+      if (__any(alpha != 1.f)) {  // wave-uniform: skip the rescale when no max moved
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) acc[t][dt] *= alpha;
+        for (int dt = 0; dt < DT; ++dt) acc[t][dt] *= alpha;
+      }
+      bf16x8 pf[2];
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          pf[s2][t][e] = static_cast<bf16>(s[2 * s2][t][e]);
-          pf[s2][t][4 + e] = static_cast<bf16>(s[2 * s2 + 1][t][e]);
+          pf[s2][e] = static_cast<bf16>(s[2 * s2][e]);
+          pf[s2][4 + e] = static_cast<bf16>(s[2 * s2 + 1][e]);
         }
-    }
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const bf16x8 a = ld4x2(sVt + (dt * 16 + l16) * LDV + 32 * s2 + g * 4);
-#pragma unroll
-        for (int t = 0; t < 2; ++t) acc[t][dt] = mfma16(a, pf[s2][t], acc[t][dt]);
-      }
+        for (int s2 = 0; s2 < 2; ++s2) acc[t][dt] = mfma16(vfr[dt][s2], pf[s2], acc[t][dt]);
     }
   }
   bf16* ob = o + b * p.o_sb + h * p.o_sh;
   float* lb = lse + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int qi = q0 + 16 * t + l16;
+  for (int t = 0; t < TQ; ++t) {
+    const int qi = qbase + 64 * t + l16;
     if (qi >= p.Sq) continue;
     const float inv = l[t] > 0.f ? 1.f / l[t] : 0.f;
 #pragma unroll
@@ -951,7 +963,9 @@ extern "C" int nmb_attn_fwd(const void* q, const void* const* k_blocks,
   if (batch == 0 || seq_q == 0) return NMB_OK;
   if (dtype == NMB_BF16) {
     NMB_REQUIRE(nmb::aligned16(o), "attn_fwd: o must be 16-byte aligned");
-    const int n_qt = static_cast<int>((seq_q + 127) / 128);
+    // queries per workgroup: 4 waves x TQ column tiles of 16 (TQ = 4 at D 64, 2 at D 128)
+    const int bq = head_dim == 64 ? 256 : 128;
+    const int n_qt = static_cast<int>((seq_q + bq - 1) / bq);
     const int64_t items = static_cast<int64_t>(n_qt) * q_heads * batch;
     NMB_REQUIRE(items < (int64_t{1} << 30), "attn_fwd: problem too large for one launch");
     int per_xcd;
@@ -960,11 +974,11 @@ extern "C" int nmb_attn_fwd(const void* q, const void* const* k_blocks,
     const nmb::bf16* qp = static_cast<const nmb::bf16*>(q);
     nmb::bf16* op = static_cast<nmb::bf16*>(o);
     if (head_dim == 64)
-      hipLaunchKernelGGL(nmb::attn_fwd_kernel<64>, dim3(blocks), dim3(256), 0, stream, qp, kv, op,
-                         lse, p, n_qt, static_cast<int>(items), per_xcd);
+      hipLaunchKernelGGL((nmb::attn_fwd_kernel<64, 4>), dim3(blocks), dim3(256), 0, stream, qp, kv,
+                         op, lse, p, n_qt, static_cast<int>(items), per_xcd);
     else
-      hipLaunchKernelGGL(nmb::attn_fwd_kernel<128>, dim3(blocks), dim3(256), 0, stream, qp, kv, op,
-                         lse, p, n_qt, static_cast<int>(items), per_xcd);
+      hipLaunchKernelGGL((nmb::attn_fwd_kernel<128, 2>), dim3(blocks), dim3(256), 0, stream, qp, kv,
+                         op, lse, p, n_qt, static_cast<int>(items), per_xcd);
   } else {
     const dim3 grid(static_cast<unsigned>(seq_q), static_cast<unsigned>(q_heads),
                     static_cast<unsigned>(batch));

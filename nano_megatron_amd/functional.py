@@ -39,6 +39,53 @@ def _workspace(nbytes: int, device: torch.device) -> Tensor:
     return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
 
 
+# ---------------------------------------------------------------- GEMM
+def _operand_layout(t: Tensor, rows_dim: int) -> tuple[int, int]:
+    """(layout, ld) of a 2-D operand: 0 if dim 1 is contiguous (ld = stride(0)),
+    1 if dim 0 is contiguous (ld = stride(1))."""
+    if t.stride(1) == 1 and (t.shape[0] == 1 or t.stride(0) >= t.shape[1]):
+        return 0, max(t.stride(0), t.shape[1])
+    if t.stride(0) == 1 and (t.shape[1] == 1 or t.stride(1) >= t.shape[0]):
+        return 1, max(t.stride(1), t.shape[0])
+    raise ValueError("gemm operands need one contiguous dimension")
+
+
+def mm(a: Tensor, b: Tensor, *, out: Tensor | None = None, c: Tensor | None = None,
+       alpha: float = 1.0, beta: float = 0.0) -> Tensor:
+    """``out = alpha * a @ b + beta * c`` for 2-D tensors.
+
+    bf16 runs the gfx950 MFMA kernel ``nmb_gemm_bf16`` (any mix of row/column
+    major operands); fp32 (the parity configuration) uses the library GEMM.
+    """
+    m, k = a.shape
+    k2, n = b.shape
+    if k != k2:
+        raise ValueError(f"gemm: inner dimensions differ ({k} vs {k2})")
+    if out is None:
+        out = torch.empty(m, n, dtype=a.dtype, device=a.device)
+    if a.dtype != torch.bfloat16:
+        if beta != 0.0:
+            torch.addmm(c, a, b, beta=beta, alpha=alpha, out=out)
+        else:
+            torch.mm(a, b, out=out) if alpha == 1.0 else torch.mm(a, b, out=out).mul_(alpha)
+        return out
+    _require_gpu(a, b, out)
+    la, lda = _operand_layout(a, 0)
+    # B is [K, N]: layout 0 means stored [N, K] (dim 0 = K contiguous)
+    lb_rowmajor, ldb = _operand_layout(b, 0)
+    lb = 1 - lb_rowmajor
+    if out.stride(1) != 1:
+        raise ValueError("gemm: the output must be row-major")
+    if beta != 0.0 and (c is None or c.stride(1) != 1):
+        raise ValueError("gemm: beta != 0 needs a row-major C")
+    _lib.call(
+        "nmb_gemm_bf16", la, lb, m, n, k, float(alpha), a.data_ptr(), lda, b.data_ptr(), ldb,
+        float(beta), _lib.ptr(c), c.stride(0) if c is not None else n, out.data_ptr(),
+        out.stride(0), _lib.stream_of(a),
+    )
+    return out
+
+
 # ---------------------------------------------------------------- RMSNorm
 def rmsnorm_fwd(x2: Tensor, weight: Tensor, eps: float) -> Tensor:
     """y = RMSNorm(x2) for a contiguous [rows, hidden] tensor (nn/norms.py:38-41)."""

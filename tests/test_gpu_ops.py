@@ -246,3 +246,27 @@ def test_lm_head_cross_entropy_matches_oracle(device, rows, hidden, vocab, dtype
     assert torch.all(per_tok.cpu()[t == -100] == 0)
     with pytest.raises(ValueError, match="outside"):
         nm.lm_head_cross_entropy(xd.detach(), ed.detach(), torch.full_like(t, vocab).to(device))
+
+
+# ---------------------------------------------------------------- GEMM
+@pytest.mark.parametrize("m,n,k,layout", [
+    (512, 384, 256, "NT"), (1000, 264, 200, "NT"), (333, 520, 136, "NN"),
+    (520, 88, 72, "TN"), (256, 1024, 4096, "TN"), (300, 256, 64, "NN"),
+])
+def test_gemm_bf16_matches_fp32_product(device, m, n, k, layout) -> None:
+    """nmb_gemm_bf16 for row/column-major operand mixes, ragged tiles, alpha/beta."""
+    g = torch.Generator(device=device).manual_seed(m + n + k)
+    bf = torch.bfloat16
+    if layout == "NT":
+        a, b = torch.randn(m, k, device=device, generator=g).to(bf), torch.randn(n, k, device=device, generator=g).to(bf).t()
+    elif layout == "NN":
+        a, b = torch.randn(m, k, device=device, generator=g).to(bf), torch.randn(k, n, device=device, generator=g).to(bf)
+    else:
+        a, b = torch.randn(k, m, device=device, generator=g).to(bf).t(), torch.randn(k, n, device=device, generator=g).to(bf)
+    c = torch.randn(m, n, device=device, generator=g).to(bf)
+    ref = 0.5 * (a.float() @ b.float()) + 2.0 * c.float()
+    out = Fn.mm(a, b, c=c, alpha=0.5, beta=2.0)
+    torch.testing.assert_close(out.float(), ref, rtol=2e-2, atol=2e-2 * float(ref.abs().max()))
+    out2 = Fn.mm(a, b)
+    torch.testing.assert_close(out2.float(), a.float() @ b.float(), rtol=2e-2,
+                               atol=2e-2 * float((a.float() @ b.float()).abs().max()))
