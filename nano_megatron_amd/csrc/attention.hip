@@ -562,16 +562,18 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
 }
 
 // ---------------------------------------------------------------- dK, dV
-// Workgroup = 64 keys of one (batch, KV head, block); wave w owns keys
-// 16w..16w+15.  Loops over the query heads of the GQA group and over the
-// 64-query tiles that can see these keys, with the next Q/dO tile's global
-// reads in flight during the current tile's MFMA work.
+// Workgroup = 128 keys of one (batch, KV head, block): key tile j (16 keys) of
+// wave w holds keys 64 j + 16 w .. +15 of the workgroup's range (interleaved,
+// so causal work is balanced across waves), so each Q/dO fragment read from
+// LDS feeds two MFMA tiles.  Loops over the query heads of the GQA group and
+// over the 64-query tiles that can see these keys, with the next Q/dO tile's
+// global reads in flight during the current tile's MFMA work.
 template <int D>
 __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
     const bf16* __restrict__ q, KVBlocks kv, const bf16* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, AttnShape p, int n_kt,
     int items, int per_xcd) {
-  constexpr int BQ = 64, BK = 64, KS = D / 32, DT = D / 16;
+  constexpr int BQ = 64, KT = 2, BKW = 64 * KT, KS = D / 32, DT = D / 16;
   constexpr int LDQ = D + 8, LDT = BQ + 4;
   __shared__ __attribute__((aligned(16))) bf16 sQ[BQ * LDQ];
   __shared__ __attribute__((aligned(16))) bf16 sQt[D * LDT];
@@ -590,8 +592,8 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
   const int b = bb / p.nblk;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g = lane >> 4;
-  const int k0 = ktile * BK;
-  const int kw0 = k0 + wave * 16;
+  const int k0 = ktile * BKW;
+  const int kbase = k0 + 16 * wave;  // key tile j: kbase + 64 j + l16
   const int64_t koff = kv.koff[blk];
   const int group = p.Hq / p.Hkv;
   const float c = p.scale_log2;
@@ -599,22 +601,25 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
   const int64_t kv_off = b * p.kv_sb + hk * p.kv_sh;
   const bf16* kb = static_cast<const bf16*>(kv.k[blk]) + kv_off;
   const bf16* vb = static_cast<const bf16*>(kv.v[blk]) + kv_off;
-  bf16x8 kf[KS], vf[KS];
-  {
-    const int key = kw0 + l16;
+  bf16x8 kf[KT][KS], vf[KT][KS];
+#pragma unroll
+  for (int j = 0; j < KT; ++j) {
+    const int key = kbase + 64 * j + l16;
     const bool ok = key < p.Sk;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      kf[ks] = ok ? ld8(kb + static_cast<int64_t>(key) * p.kv_ss + ks * 32 + g * 8) : zero8();
-      vf[ks] = ok ? ld8(vb + static_cast<int64_t>(key) * p.kv_ss + ks * 32 + g * 8) : zero8();
+      kf[j][ks] = ok ? ld8(kb + static_cast<int64_t>(key) * p.kv_ss + ks * 32 + g * 8) : zero8();
+      vf[j][ks] = ok ? ld8(vb + static_cast<int64_t>(key) * p.kv_ss + ks * 32 + g * 8) : zero8();
     }
   }
-  f32x4 dka[DT], dva[DT];
+  f32x4 dka[KT][DT], dva[KT][DT];
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
-    dka[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    dva[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
+  for (int j = 0; j < KT; ++j)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      dka[j][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      dva[j][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
   int first_q = 0;
   if (p.causal) {
     const int64_t fq = koff + k0 - p.q_offset;
@@ -624,8 +629,6 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
   const int n_qt = (p.Sq + BQ - 1) / BQ;
   const int per_head = n_qt - qt_begin;
   const int n_iter = per_head > 0 ? group * per_head : 0;
-  const int64_t ka_wave_first = koff + kw0;
-  const int64_t ka_wave_last = koff + kw0 + 15;
 
   PairTile<BQ, D> qr, dr;
   float lv = 0.f, dv = 0.f;
@@ -656,76 +659,102 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
     const int q0 = (qt_begin + it % per_head) * BQ;
     if (it + 1 < n_iter) load(it + 1);
     const int64_t qa_last = p.q_offset + min(q0 + BQ - 1, p.Sq - 1);
-    if (kw0 >= p.Sk) continue;
-    if (p.causal && ka_wave_first > qa_last) continue;
-    const bool need_mask = (kw0 + 16 > p.Sk) || (p.causal && ka_wave_last > p.q_offset + q0);
+    bool live[KT], need_mask[KT];
+    bool any = false;
+#pragma unroll
+    for (int j = 0; j < KT; ++j) {
+      const int kt0 = kbase + 64 * j;
+      live[j] = kt0 < p.Sk && !(p.causal && koff + kt0 > qa_last);
+      need_mask[j] = (kt0 + 16 > p.Sk) || (p.causal && koff + kt0 + 15 > p.q_offset + q0);
+      any = any || live[j];
+    }
+    if (!any) continue;
 
-    // S = Q K^T and dP = dO V^T for this wave's 16 keys: lane holds
-    // S[q = 16 mq + 4 g + e][key = kw0 + l16].
-    f32x4 s[4], dp[4];
+    // S = Q K^T and dP = dO V^T: lane holds S[q = 16 mq + 4 g + e][key = kbase + 64 j + l16]
+    f32x4 s[4][KT], dp[4][KT];
+#pragma unroll
+    for (int mq = 0; mq < 4; ++mq)
+#pragma unroll
+      for (int j = 0; j < KT; ++j) {
+        s[mq][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        dp[mq][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
 #pragma unroll
     for (int mq = 0; mq < 4; ++mq) {
-      s[mq] = f32x4{0.f, 0.f, 0.f, 0.f};
-      dp[mq] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const bf16x8 aq = ld8(sQ + (mq * 16 + l16) * LDQ + ks * 32 + g * 8);
         const bf16x8 ad = ld8(sD + (mq * 16 + l16) * LDQ + ks * 32 + g * 8);
-        s[mq] = mfma16(aq, kf[ks], s[mq]);
-        dp[mq] = mfma16(ad, vf[ks], dp[mq]);
+#pragma unroll
+        for (int j = 0; j < KT; ++j)
+          if (live[j]) {
+            s[mq][j] = mfma16(aq, kf[j][ks], s[mq][j]);
+            dp[mq][j] = mfma16(ad, vf[j][ks], dp[mq][j]);
+          }
       }
     }
-    // smallest tile-relative query index that sees this lane's key (BQ: none)
-    int qmin = 0;
-    if (need_mask) {
-      int64_t f = p.causal ? koff + kw0 + l16 - p.q_offset - q0 : 0;
-      if (kw0 + l16 >= p.Sk) f = BQ;
-      qmin = f < 0 ? 0 : (f > BQ ? BQ : static_cast<int>(f));
+    bf16x8 pa[2][KT], da[2][KT];
+#pragma unroll
+    for (int j = 0; j < KT; ++j) {
+      if (!live[j]) continue;
+      // smallest tile-relative query index that sees this lane's key (BQ: none)
+      int qmin = 0;
+      if (need_mask[j]) {
+        const int key = kbase + 64 * j + l16;
+        int64_t f = p.causal ? koff + key - p.q_offset - q0 : 0;
+        if (key >= p.Sk) f = BQ;
+        qmin = f < 0 ? 0 : (f > BQ ? BQ : static_cast<int>(f));
+      }
+#pragma unroll
+      for (int mq = 0; mq < 4; ++mq)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int ql = mq * 16 + g * 4 + e;
+          float pv = fast_exp2(fmaf(s[mq][j][e], c, -sL[ql]));
+          pv = ql < qmin ? 0.f : pv;
+          s[mq][j][e] = pv;
+          dp[mq][j][e] = pv * (dp[mq][j][e] - sDl[ql]);
+        }
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pa[s2][j][e] = static_cast<bf16>(s[2 * s2][j][e]);
+          pa[s2][j][4 + e] = static_cast<bf16>(s[2 * s2 + 1][j][e]);
+          da[s2][j][e] = static_cast<bf16>(dp[2 * s2][j][e]);
+          da[s2][j][4 + e] = static_cast<bf16>(dp[2 * s2 + 1][j][e]);
+        }
     }
-#pragma unroll
-    for (int mq = 0; mq < 4; ++mq)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int ql = mq * 16 + g * 4 + e;
-        float pv = fast_exp2(fmaf(s[mq][e], c, -sL[ql]));
-        pv = ql < qmin ? 0.f : pv;
-        s[mq][e] = pv;
-        dp[mq][e] = pv * (dp[mq][e] - sDl[ql]);
-      }
-    bf16x8 pa[2], da[2];
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        pa[s2][e] = static_cast<bf16>(s[2 * s2][e]);
-        pa[s2][4 + e] = static_cast<bf16>(s[2 * s2 + 1][e]);
-        da[s2][e] = static_cast<bf16>(dp[2 * s2][e]);
-        da[s2][4 + e] = static_cast<bf16>(dp[2 * s2 + 1][e]);
-      }
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
         const bf16x8 bd = ld4x2(sDt + (dt * 16 + l16) * LDT + 32 * s2 + g * 4);
         const bf16x8 bq = ld4x2(sQt + (dt * 16 + l16) * LDT + 32 * s2 + g * 4);
-        dva[dt] = mfma16(pa[s2], bd, dva[dt]);
-        dka[dt] = mfma16(da[s2], bq, dka[dt]);
+#pragma unroll
+        for (int j = 0; j < KT; ++j)
+          if (live[j]) {
+            dva[j][dt] = mfma16(pa[s2][j], bd, dva[j][dt]);
+            dka[j][dt] = mfma16(da[s2][j], bq, dka[j][dt]);
+          }
       }
     }
   }
-  // lane holds dK[key = kw0 + 4 g + e][d = 16 dt + l16]
+  // lane holds dK[key = kbase + 64 j + 4 g + e][d = 16 dt + l16]
   bf16* dkb = static_cast<bf16*>(kv.dk[blk]) + kv_off;
   bf16* dvb = static_cast<bf16*>(kv.dv[blk]) + kv_off;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int key = kw0 + g * 4 + e;
-    if (key >= p.Sk) continue;
+  for (int j = 0; j < KT; ++j)
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      dkb[static_cast<int64_t>(key) * p.kv_ss + dt * 16 + l16] = static_cast<bf16>(dka[dt][e] * p.scale);
-      dvb[static_cast<int64_t>(key) * p.kv_ss + dt * 16 + l16] = static_cast<bf16>(dva[dt][e]);
+    for (int e = 0; e < 4; ++e) {
+      const int key = kbase + 64 * j + g * 4 + e;
+      if (key >= p.Sk) continue;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        dkb[static_cast<int64_t>(key) * p.kv_ss + dt * 16 + l16] = static_cast<bf16>(dka[j][dt][e] * p.scale);
+        dvb[static_cast<int64_t>(key) * p.kv_ss + dt * 16 + l16] = static_cast<bf16>(dva[j][dt][e]);
+      }
     }
-  }
 }
 
 // ---------------------------------------------------------------- fp32 path
@@ -1052,7 +1081,7 @@ extern "C" int nmb_attn_bwd(const void* q, const void* const* k_blocks,
       NMB_CHECK_LAUNCH("attn_bwd(dq)");
     }
     if (seq_k > 0) {
-      const int n_kt = static_cast<int>((seq_k + 63) / 64);
+      const int n_kt = static_cast<int>((seq_k + 127) / 128);  // 128 keys per workgroup
       const int64_t items = static_cast<int64_t>(n_kt) * kv_heads * batch * n_blocks;
       NMB_REQUIRE(items < (int64_t{1} << 30), "attn_bwd: problem too large for one launch");
       int per_xcd;
