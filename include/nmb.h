@@ -157,10 +157,17 @@ int nmb_ce_bwd(void* logits, int64_t ld, const int64_t* targets, int64_t rows, i
  *   D[M, N] = alpha * op(A)[M, K] * op(B)[K, N] + beta * C[M, N]   (row-major)
  * a_layout 0: A stored [M, K] (row stride lda); 1: A stored [K, M].
  * b_layout 0: B stored [N, K] (a weight used as W^T); 1: B stored [K, N].
- * C may alias D.  The contiguous extents and lda/ldb must be multiples of 8. */
+ * C may alias D.  N, the contiguous extents and lda/ldb/ldc/ldd must be
+ * multiples of 8; all pointers 16-byte aligned.  Small M x N with long K is
+ * split along K: fp32 partials go to the caller's workspace (size from
+ * nmb_gemm_bf16_workspace_bytes, 0 when unsplit) and are summed in a fixed
+ * order (deterministic). */
+int nmb_gemm_bf16_workspace_bytes(int a_layout, int b_layout, int64_t m, int64_t n, int64_t k,
+                                  int64_t* bytes);
 int nmb_gemm_bf16(int a_layout, int b_layout, int64_t m, int64_t n, int64_t k, float alpha,
                   const void* a, int64_t lda, const void* b, int64_t ldb, float beta,
-                  const void* c, int64_t ldc, void* d, int64_t ldd, hipStream_t stream);
+                  const void* c, int64_t ldc, void* d, int64_t ldd, void* workspace,
+                  int64_t workspace_bytes, hipStream_t stream);
 
 /* ------------------------------------------------------------ optimizer
  * replaces FlatShardZeROStrategy.clip_grad_norm + optimizer_step at DP=1

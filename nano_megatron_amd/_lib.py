@@ -58,8 +58,10 @@ SIGNATURES: dict[str, list] = {
     ],
     "nmb_ce_fwd": [_p, _i64, _p, _i64, _i64, _i64, _p, _p, _i32, _p],
     "nmb_ce_bwd": [_p, _i64, _p, _i64, _i64, _i64, _p, _p, _i32, _p],
+    "nmb_gemm_bf16_workspace_bytes": [_i32, _i32, _i64, _i64, _i64, _pi64],
     "nmb_gemm_bf16": [
         _i32, _i32, _i64, _i64, _i64, _f32, _p, _i64, _p, _i64, _f32, _p, _i64, _p, _i64, _p,
+        _i64, _p,
     ],
     "nmb_adamw_workspace_bytes": [_i64, _psz],
     "nmb_adamw_step": [

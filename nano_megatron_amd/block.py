@@ -102,22 +102,22 @@ def block_forward(x: Tensor, w: tuple[Tensor, ...], m: BlockMeta, *, recompute: 
     b, s, hdim = x.shape
     x2 = x.reshape(b * s, hdim)
     n1 = Fn.rmsnorm_fwd(x2, w_in, m.eps)
-    qkv = torch.mm(n1, joined((wq, wk, wv)).t())
+    qkv = Fn.mm(n1, joined((wq, wk, wv)).t())
     q, k, v = _qkv_views(qkv, b, s, m)
     Fn.rope_apply(q, q, m.cos, m.sin, pos_offset=m.sequence_offset, positions=m.positions)
     Fn.rope_apply(k, k, m.cos, m.sin, pos_offset=m.sequence_offset, positions=m.positions)
     o, lse = Fn.attn_fwd_bshd(q, [k], [v], (0,), causal=True, q_offset=m.sequence_offset, scale=None)
     o2 = o.view(b * s, m.heads * m.head_dim)
-    h = torch.addmm(x2, o2, wo.t())
+    h = Fn.mm(o2, wo.t(), c=x2, beta=1.0)
     n2 = Fn.rmsnorm_fwd(h, w_post, m.eps)
-    gu = torch.mm(n2, joined((wg, wu)).t())
+    gu = Fn.mm(n2, joined((wg, wu)).t())
     acts = dict(x2=x2, n1=n1, qkv=qkv, o2=o2, lse=lse, h=h, n2=n2, gu=gu)
     if recompute:
         return acts
     f = wg.shape[0]
     act = Fn.swiglu_fwd(gu[:, :f], gu[:, f:])
     acts["s"] = act
-    acts["y"] = torch.addmm(h, act, wd.t()).view(b, s, hdim)
+    acts["y"] = Fn.mm(act, wd.t(), c=h, beta=1.0).view(b, s, hdim)
     return acts
 
 
@@ -132,18 +132,18 @@ def block_backward(acts: dict, dy: Tensor, w: tuple[Tensor, ...], m: BlockMeta, 
     x2, n1, qkv, o2, lse, h, n2, gu = (acts[k] for k in ("x2", "n1", "qkv", "o2", "lse", "h", "n2", "gu"))
 
     # MLP: y = h + s Wd^T, s = silu(g) * u, [g|u] = n2 [Wg;Wu]^T
-    ds = torch.mm(dy2, wd)
+    ds = Fn.mm(dy2, wd)
     dgu = torch.empty_like(gu)
     act = torch.empty(b * s, f, dtype=gu.dtype, device=gu.device)
     Fn.swiglu_bwd(gu[:, :f], gu[:, f:], ds, dgu[:, :f], dgu[:, f:], act)
-    dwd = torch.mm(dy2.t(), act)
-    dn2 = torch.mm(dgu, joined((wg, wu)))
-    dwgu = torch.mm(dgu.t(), n2)
+    dwd = Fn.mm(dy2.t(), act)
+    dn2 = Fn.mm(dgu, joined((wg, wu)))
+    dwgu = Fn.mm(dgu.t(), n2)
     dh, dw_post = Fn.rmsnorm_bwd(h, w_post, dn2, m.eps, residual_grad=dy2)
 
     # attention: h = x + o Wo^T
-    do2 = torch.mm(dh, wo)
-    dwo = torch.mm(dh.t(), o2)
+    do2 = Fn.mm(dh, wo)
+    dwo = Fn.mm(dh.t(), o2)
     q, k, v = _qkv_views(qkv, b, s, m)
     dqkv = torch.empty_like(qkv)
     dq, dk, dv = _qkv_views(dqkv, b, s, m)
@@ -153,8 +153,8 @@ def block_backward(acts: dict, dy: Tensor, w: tuple[Tensor, ...], m: BlockMeta, 
                      causal=True, q_offset=m.sequence_offset, scale=None)
     Fn.rope_apply(dq, dq, m.cos, m.sin, pos_offset=m.sequence_offset, positions=m.positions, inverse=True)
     Fn.rope_apply(dk, dk, m.cos, m.sin, pos_offset=m.sequence_offset, positions=m.positions, inverse=True)
-    dn1 = torch.mm(dqkv, joined((wq, wk, wv)))
-    dwqkv = torch.mm(dqkv.t(), n1)
+    dn1 = Fn.mm(dqkv, joined((wq, wk, wv)))
+    dwqkv = Fn.mm(dqkv.t(), n1)
     dx, dw_in = Fn.rmsnorm_bwd(x2, w_in, dn1, m.eps, residual_grad=dh)
 
     qd = m.heads * m.head_dim

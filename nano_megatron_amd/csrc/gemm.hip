@@ -7,86 +7,199 @@
 // with A stored K-contiguous ([M, K]) or M-contiguous ([K, M]) and B stored
 // K-contiguous ([N, K], a weight used as W^T) or N-contiguous ([K, N]).
 //
-// Workgroup tile BM x BN x 64 with 4 wavefronts in a 2 x 2 arrangement; each
-// wavefront owns a (BM/2) x (BN/2) block of 16 x 16 MFMA tiles whose fp32
-// accumulators live in AGPRs.  Both operands are staged in LDS K-contiguous
-// ([row][k], 8 elements of padding) so every MFMA fragment is one 16-byte LDS
-// read; an M/N-contiguous operand is transposed on the way in (pairs of k rows
-// written as 32-bit words).  LDS is double-buffered and the next K tile's
-// global reads are issued before the current tile's MFMAs, one barrier per K
-// tile.  Each MFMA computes a D^T tile (B fragment as the A operand), so a
-// lane ends up with four consecutive columns of one output row and stores
-// them as one 8-byte write.  Blocks are mapped so that consecutive tiles along
-// N -- which share the A row block -- run on the same XCD.
+// Workgroup tile 256 x 128, 128 x 256 or 128 x 128, K tile 32, 4 wavefronts in
+// a 2 x 2 arrangement, two workgroups per CU: a single wavefront per SIMD
+// issues MFMAs at about 60% of the peak rate, and two workgroups (unlike one of
+// 8 wavefronts) do not meet at the same barriers, so one's MFMAs fill the
+// other's barrier and LDS-latency stalls.
+//
+// Operands go from HBM straight into LDS (buffer_load ... lds, 16 bytes per
+// lane, no VGPR round trip), each in the layout it has in memory:
+//  * K-contiguous tile [rows][32 k]: 64-byte rows, the 16-byte k chunk c of
+//    row r stored in slot c ^ kc_swizzle(r).  An MFMA fragment (16 rows x 8 k
+//    per lane group) is one ds_read_b128 per lane.
+//  * M/N-contiguous tile [32 k][R]: 2R-byte k rows, the 32-byte chunk pair p
+//    of k row k stored at pair slot p ^ rc_swizzle(k).  A fragment is two
+//    ds_read_b64_tr_b16 per lane: in each group of 16 lanes, lane i receives
+//    element i & 3 of the 8 bytes addressed by lane 4j + i/4 (j = 0..3), so
+//    lanes pointing at [k + i/4][n0 + 4 (i & 3)] deliver column n0 + i,
+//    k .. k + 3 -- the K-contiguous fragment without a transposing store.
+// Row, column and k tails: the loads of invalid chunks get an offset past the
+// buffer's num_records, which the hardware returns as zeros.
+//
+// LDS holds two K tiles; the next tile's loads are issued right after the
+// barrier that publishes the current one (one barrier per K tile).  Each MFMA
+// computes a D^T tile (B fragment as the A operand), so a lane ends up with
+// four consecutive columns of one output row.  Blocks are mapped so that tiles
+// sharing an operand row block run on the same XCD (its own L2).
+//
+// Split K (small M x N, long K -- the weight gradients): split s of a tile
+// covers K range [s * kps, (s + 1) * kps) and writes fp32 partials to the
+// caller's workspace; a second kernel sums the splits in a fixed order
+// (deterministic) and applies alpha, beta and the bf16 rounding.
+#include <algorithm>
+
 #include "common.h"
 
 namespace nmb {
 namespace {
 
-constexpr int BK = 64;
-constexpr int LDS_K = BK + 8;  // row stride (elements) of both LDS tiles
+constexpr uint32_t kOOB = 0x80000000u;  // offset past every num_records: the load returns zeros
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+using lds_void = __attribute__((address_space(3))) void;
+using lds_v4s = __attribute__((address_space(3))) v4s;
 
 __device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ bf16x8 zero8() {
-  bf16x8 z;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) z[i] = static_cast<bf16>(0.f);
-  return z;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer descriptor of a raw (untyped) byte range: base, stride 0, num_records
+// = bytes, dword 3 = 0x00020000 (32-bit data format on gfx9-class hardware).
+__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return i32x4{__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(a))),
+               __builtin_amdgcn_readfirstlane(static_cast<int>((a >> 32) & 0xffff)),
+               __builtin_amdgcn_readfirstlane(static_cast<int>(bytes)), 0x00020000};
 }
+
+// 16 bytes per lane from buffer offset voff into LDS at byte address
+// lds + 16 * lane (lds is wave-uniform; it goes to M0).  Written as inline asm
+// so that the compiler does not treat the LDS written in flight as a pending
+// store to every later LDS read (it would wait for all loads before each read);
+// the kernel waits for these loads itself with s_waitcnt vmcnt.
+__device__ __forceinline__ void load_lds16(const i32x4& r, const bf16* lds, uint32_t voff) {
+  // the address is uniform across the wave; readfirstlane makes it scalar
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)(const_cast<bf16*>(lds)))));
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(m0), "v"(voff), "s"(r)
+               : "memory");
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt bits [3:0] and [15:14]; expcnt and
+// lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier that orders memory accesses for the compiler but adds no
+// wait for outstanding loads (each wave waits for its own with wait_vmcnt).
+__device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 __device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 
-// A thread's share of one R-row x 64-k operand tile (R = BM or BN) in flight
-// between global memory and LDS.
-//  KC (k contiguous): item = (row, 16-byte k chunk), 8 consecutive k of a row.
-//  RC (row contiguous): item = (k pair, 16-byte row chunk): rows 8c..8c+7 at
-//     k and k+1, written to LDS as 32-bit (k, k+1) words.
-template <int R, bool KC>
-struct OperandTile {
-  static constexpr int kItems = KC ? R * (BK / 8) : (BK / 2) * (R / 8);
-  static constexpr int kPer = kItems / 256;
-  static_assert(kItems % 256 == 0, "tile must split evenly over 256 threads");
-  bf16x8 a[kPer], b[kPer];
+__device__ __forceinline__ bf16x8 ld_tr(const bf16* p0, const bf16* p1) {
+  const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(const_cast<bf16*>(p0)));
+  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(const_cast<bf16*>(p1)));
+  bf16x8 r;
+  __builtin_memcpy(&r, &lo, 8);
+  __builtin_memcpy(reinterpret_cast<char*>(&r) + 8, &hi, 8);
+  return r;
+}
 
-  // src points at element (row 0, k 0) of this tile; ld is the row stride of
-  // the stored matrix (elements); rows/ks give the valid extent.
-  __device__ __forceinline__ void load(const bf16* __restrict__ src, int64_t ld, int rows, int ks) {
+// 16-byte chunk slots of the K-contiguous tile.  64-deep K tiles (128-byte
+// rows, 8 chunks): row r keeps chunk c in slot c ^ (r & 7).  32-deep K tiles
+// (64-byte rows, 4 chunks): slot c ^ (((r >> 1) & 3) ^ ((r >> 3) & 1)), so that
+// the 16 rows of a fragment read spread over all banks whether the hardware
+// serves 8 or 16 lanes per pass.
+template <int BKT>
+__device__ __forceinline__ int kc_swizzle(int r) {
+  return BKT == 64 ? (r & 7) : (((r >> 1) & 3) ^ ((r >> 3) & 1));
+}
+// 32-byte pair slots of the M/N-contiguous tile: k row k keeps pair p in slot
+// p ^ rc_swizzle(k), so that the 8 k rows of a half-wave transposed read
+// (k .. k + 3 and k + 8 .. k + 11) land on distinct banks.
+__device__ __forceinline__ int rc_swizzle(int k) { return (k & 3) | ((k >> 1) & 4); }
+
+// One wave's share of the loads of an R-row operand tile per BKT-deep K tile:
+// R * BKT / 512 load instructions of 1 KB (64 lanes x 16 B), spread over NW
+// waves.
+template <int R, bool KC, int BKT, int NW>
+struct Loader {
+  static constexpr int kPer = R * BKT / (512 * NW);
+  static constexpr int kCpr = BKT / 8;   // K-contiguous: 16-byte chunks per row
+  static constexpr int kRpi = 64 / kCpr; // K-contiguous: rows per instruction
+  static constexpr int kChunks = R / 8;  // M/N-contiguous: 16-byte chunks per k row
+  static_assert(kPer >= 1 && R * BKT % (512 * NW) == 0, "tile must split evenly over the waves");
+  static_assert(KC || R == 128 || R == 256, "M/N-contiguous tiles have 128 or 256 columns");
+  i32x4 rsrc;
+  uint32_t off[kPer];  // byte offset at k0 = 0, kOOB for an invalid row / column
+  int kin[kPer];       // k index (within the K tile) where this lane's chunk starts
+  uint32_t kstride;    // bytes per unit of k
+
+  // base: element (row0, k 0) of the tile (K-contiguous) or (k 0, col0)
+  // (M/N-contiguous); valid: rows (K-contiguous) or columns of the tile inside
+  // the matrix; bytes: extent of the matrix from base.
+  __device__ void init(const bf16* base, int64_t ld, int valid, uint32_t bytes, int wave, int lane) {
+    rsrc = make_rsrc(base, bytes);
+    kstride = KC ? 2u : static_cast<uint32_t>(2 * ld);
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int c = threadIdx.x + 256 * i;
+    for (int j = 0; j < kPer; ++j) {
+      const int i = wave * kPer + j;
       if (KC) {
-        const int r = c / (BK / 8), kc = (c % (BK / 8)) * 8;
-        a[i] = (r < rows && kc < ks) ? ld8(src + static_cast<int64_t>(r) * ld + kc) : zero8();
+        // instruction i fills rows kRpi i ..; lane p: row kRpi i + p / kCpr, slot p % kCpr
+        const int r = kRpi * i + lane / kCpr;
+        const int c = (lane % kCpr) ^ kc_swizzle<BKT>(r);
+        kin[j] = 8 * c;
+        off[j] = r < valid ? static_cast<uint32_t>((r * ld + 8 * c) * 2) : kOOB;
       } else {
-        const int rc = (c % (R / 8)) * 8, kp = (c / (R / 8)) * 2;
-        // stored [k][row]: row chunk rc..rc+7 of k rows kp and kp+1
-        a[i] = (kp < ks && rc < rows) ? ld8(src + static_cast<int64_t>(kp) * ld + rc) : zero8();
-        b[i] = (kp + 1 < ks && rc < rows) ? ld8(src + static_cast<int64_t>(kp + 1) * ld + rc) : zero8();
+        const int q = 64 * i + lane;
+        const int kr = q / kChunks, s = q % kChunks;
+        const int c = s ^ (2 * rc_swizzle(kr));  // pair swizzle keeps the chunk's low bit
+        kin[j] = kr;
+        off[j] = 8 * c < valid ? static_cast<uint32_t>((kr * ld + 8 * c) * 2) : kOOB;
       }
     }
   }
 
-  __device__ __forceinline__ void store(bf16* __restrict__ dst) const {
+  // loads K tile [k0, k0 + BKT) (zeros at and past k_end) into the LDS tile
+  __device__ __forceinline__ void issue(const bf16* tile, int k0, int k_end, int wave) const {
+    const uint32_t koff = static_cast<uint32_t>(k0) * kstride;
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int c = threadIdx.x + 256 * i;
-      if (KC) {
-        const int r = c / (BK / 8), kc = (c % (BK / 8)) * 8;
-        *reinterpret_cast<bf16x8*>(dst + r * LDS_K + kc) = a[i];
-      } else {
-        const int rc = (c % (R / 8)) * 8, kp = (c / (R / 8)) * 2;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          bf16 pr[2] = {a[i][e], b[i][e]};
-          uint32_t w;
-          __builtin_memcpy(&w, pr, 4);
-          *reinterpret_cast<uint32_t*>(dst + (rc + e) * LDS_K + kp) = w;
-        }
-      }
+    for (int j = 0; j < kPer; ++j) {
+      const bool ok = off[j] != kOOB && k0 + kin[j] < k_end;
+      load_lds16(rsrc, tile + 512 * (wave * kPer + j), ok ? off[j] + koff : kOOB);
     }
+  }
+};
+
+// Per-lane LDS offsets (elements) of the MFMA fragments of T 16-row groups of
+// an R-row operand tile, starting at tile row row0: fragment t of k32 step kk
+// gives lane l op[row0 + 16 t + l % 16][kk + 8 (l / 16) .. + 7].
+template <int R, bool KC, int T, int BKT>
+struct Frags {
+  // K-contiguous: one offset (the swizzle depends on l % 16 only; the group
+  // offset 16 t BKT is an immediate, and for kk = 32 the chunk (4 + g) ^ x is
+  // (g ^ x) ^ 4).  M/N-contiguous: the two transposed reads of each fragment
+  // (the swizzle does not depend on k bit 5).
+  int off[KC ? 1 : 2 * T];
+
+  __device__ void init(int row0, int lane) {
+    const int l16 = lane & 15, g = lane >> 4;
+    if (KC) {
+      off[0] = (row0 + l16) * BKT + 8 * (g ^ kc_swizzle<BKT>(l16));
+    } else {
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          // lane p of group g: k row 8 g + 4 h + p / 4, columns 16 pair + 4 (p & 3) .. + 3
+          const int k = 8 * g + 4 * h + (l16 >> 2);
+          const int pair = (row0 >> 4) + t;
+          off[2 * t + h] = k * R + 16 * (pair ^ rc_swizzle(k)) + 4 * (l16 & 3);
+        }
+    }
+  }
+
+  __device__ __forceinline__ bf16x8 get(const bf16* tile, int t, int kk) const {
+    if (KC) return ld8(tile + t * 16 * BKT + (kk ? (off[0] ^ 32) : off[0]));
+    return ld_tr(tile + off[2 * t] + kk * R, tile + off[2 * t + 1] + kk * R);
   }
 };
 
@@ -95,40 +208,56 @@ struct GemmArgs {
   const bf16* b;
   const bf16* c;
   bf16* d;
+  float* partial;  // split K: [splits][M][N] fp32
   int64_t lda, ldb, ldc, ldd;
   int M, N, K;
   float alpha, beta;
-  int tiles_n, items, per_xcd;
+  int tiles_n, tiles, splits, kps, items, per_xcd;
 };
 
-template <int BM, int BN, bool A_KC, bool B_KC>
-__global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs g) {
-  constexpr int WM = BM / 2, WN = BN / 2;      // wave tile
-  constexpr int TM = WM / 16, TN = WN / 16;    // 16x16 MFMA tiles per wave
-  extern __shared__ __attribute__((aligned(16))) bf16 smem[];
-  // LDS: [A buffer 0][A buffer 1][B buffer 0][B buffer 1]
-  auto sA = [&](int buf) { return smem + buf * (BM * LDS_K); };
-  auto sB = [&](int buf) { return smem + 2 * BM * LDS_K + buf * (BN * LDS_K); };
+// TBM x TBN output tile, NW wavefronts (4: 2 x 2, two workgroups per CU;
+// 8: 2 x 4 or 4 x 2, one workgroup per CU), BKT-deep K tiles.
+template <int TBM, int TBN, int NW, int BKT, bool A_KC, bool B_KC>
+__global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void gemm_kernel(GemmArgs g) {
+  constexpr int WAVES_N = NW == 4 ? 2 : (TBN == 256 ? 4 : 2);
+  constexpr int WAVES_M = NW / WAVES_N;
+  constexpr int WM = TBM / WAVES_M, WN = TBN / WAVES_N;  // wave tile
+  constexpr int TM = WM / 16, TN = WN / 16;              // 16 x 16 MFMA tiles per wave
+  constexpr int KSTEPS = BKT / 32;
+  // LDS stages (K tiles in flight + 1) within the workgroup's share of 160 KB
+  constexpr int kStageBytes = (TBM + TBN) * BKT * 2;
+  constexpr int kBudget = NW == 4 ? 80 * 1024 : 160 * 1024;
+  constexpr int S = kBudget / kStageBytes >= 4 ? 4 : kBudget / kStageBytes;
+  static_assert(S >= 2, "two LDS stages at least");
+  __shared__ __attribute__((aligned(1024))) bf16 sA[S][TBM * BKT];
+  __shared__ __attribute__((aligned(1024))) bf16 sB[S][TBN * BKT];
 
   const int L = static_cast<int>(blockIdx.x);
   const int w = (L % 8) * g.per_xcd + L / 8;
   if (w >= g.items) return;
-  const int m0 = (w / g.tiles_n) * BM;
-  const int n0 = (w % g.tiles_n) * BN;
+  const int split = w / g.tiles;
+  const int t = w % g.tiles;
+  const int m0 = (t / g.tiles_n) * TBM;
+  const int n0 = (t % g.tiles_n) * TBN;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int l16 = lane & 15, q4 = lane >> 4;
-  const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
+  const int wm = (wave / WAVES_N) * WM, wn = (wave % WAVES_N) * WN;
+  const int k_begin = split * g.kps;
+  const int k_end = min(g.K, k_begin + g.kps);
 
-  // operand tile origins: A row block m0, B row (= output column) block n0
-  const bf16* a_base = A_KC ? g.a + static_cast<int64_t>(m0) * g.lda : g.a + m0;
-  const bf16* b_base = B_KC ? g.b + static_cast<int64_t>(n0) * g.ldb : g.b + n0;
-  const int rows_a = min(BM, g.M - m0), rows_b = min(BN, g.N - n0);
-  auto a_tile = [&](int k0) {
-    return A_KC ? a_base + k0 : a_base + static_cast<int64_t>(k0) * g.lda;
-  };
-  auto b_tile = [&](int k0) {
-    return B_KC ? b_base + k0 : b_base + static_cast<int64_t>(k0) * g.ldb;
-  };
+  Loader<TBM, A_KC, BKT, NW> la;
+  Loader<TBN, B_KC, BKT, NW> lb;
+  {
+    // tile origins and the extents (bytes) of the matrices from there
+    const bf16* a0 = A_KC ? g.a + static_cast<int64_t>(m0) * g.lda : g.a + m0;
+    const bf16* b0 = B_KC ? g.b + static_cast<int64_t>(n0) * g.ldb : g.b + n0;
+    const int va = min(TBM, g.M - m0), vb = min(TBN, g.N - n0);
+    const int64_t ea = A_KC ? (static_cast<int64_t>(va - 1) * g.lda + g.K) * 2
+                            : (static_cast<int64_t>(g.K - 1) * g.lda + (g.M - m0)) * 2;
+    const int64_t eb = B_KC ? (static_cast<int64_t>(vb - 1) * g.ldb + g.K) * 2
+                            : (static_cast<int64_t>(g.K - 1) * g.ldb + (g.N - n0)) * 2;
+    la.init(a0, g.lda, va, static_cast<uint32_t>(ea), wave, lane);
+    lb.init(b0, g.ldb, vb, static_cast<uint32_t>(eb), wave, lane);
+  }
 
   f32x4 acc[TM][TN];
 #pragma unroll
@@ -136,43 +265,67 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  OperandTile<BM, A_KC> ta;
-  OperandTile<BN, B_KC> tb;
-  const int nk = (g.K + BK - 1) / BK;
-  ta.load(a_tile(0), g.lda, rows_a, min(BK, g.K));
-  tb.load(b_tile(0), g.ldb, rows_b, min(BK, g.K));
-  ta.store(sA(0));
-  tb.store(sB(0));
-  __syncthreads();
+  Frags<TBM, A_KC, TM, BKT> fra;
+  Frags<TBN, B_KC, TN, BKT> frb;
+  fra.init(wm, lane);
+  frb.init(wn, lane);
+
+  // S - 1 K tiles in flight.  Each K tile kt: wait until this wave's loads of
+  // tile kt have landed (those of later tiles may stay in flight), barrier
+  // (everyone's have; everyone is done with the stage read last iteration),
+  // all fragment reads, the loads of tile kt + S - 1 into that freed stage,
+  // then the MFMAs.
+  constexpr int kLoads = Loader<TBM, A_KC, BKT, NW>::kPer + Loader<TBN, B_KC, BKT, NW>::kPer;
+  const int nk = (k_end - k_begin + BKT - 1) / BKT;
+  auto issue = [&](int kt) {
+    const int st = kt % S;
+    la.issue(&sA[st][0], k_begin + kt * BKT, k_end, wave);
+    lb.issue(&sB[st][0], k_begin + kt * BKT, k_end, wave);
+  };
+#pragma unroll
+  for (int p = 0; p < S - 1; ++p)
+    if (p < nk) issue(p);
   for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) {
-      const int k1 = (kt + 1) * BK;
-      ta.load(a_tile(k1), g.lda, rows_a, min(BK, g.K - k1));
-      tb.load(b_tile(k1), g.ldb, rows_b, min(BK, g.K - k1));
+    // tiles issued after tile kt: min(nk - 1, kt + S - 2) - kt
+    const int after = min(nk - 1, kt + S - 2) - kt;
+    if (after >= 2) wait_vmcnt<2 * kLoads>();
+    else if (after == 1) wait_vmcnt<kLoads>();
+    else wait_vmcnt<0>();
+    barrier();
+    const int st = kt % S;
+    bf16x8 fa[KSTEPS][TM], fb[KSTEPS][TN];
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb[ks][j] = frb.get(&sB[st][0], j, 32 * ks);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[ks][i] = fra.get(&sA[st][0], i, 32 * ks);
     }
-    const bf16* pa = sA(cur) + (wm + l16) * LDS_K + q4 * 8;
-    const bf16* pb = sB(cur) + (wn + l16) * LDS_K + q4 * 8;
+    if (kt + S - 1 < nk) issue(kt + S - 1);
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 32) {
-      bf16x8 fa[TM], fb[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) fa[i] = ld8(pa + i * 16 * LDS_K + kk);
-#pragma unroll
-      for (int j = 0; j < TN; ++j) fb[j] = ld8(pb + j * 16 * LDS_K + kk);
+    for (int ks = 0; ks < KSTEPS; ++ks)
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma16(fb[j], fa[i], acc[i][j]);
-    }
-    if (kt + 1 < nk) {
-      ta.store(sA(cur ^ 1));
-      tb.store(sB(cur ^ 1));
-    }
-    __syncthreads();
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma16(fb[ks][j], fa[ks][i], acc[i][j]);
   }
 
   // acc[i][j][e] = D[m0 + wm + 16 i + l16][n0 + wn + 16 j + 4 q4 + e]
+  const int l16 = lane & 15, q4 = lane >> 4;
+  if (g.splits > 1) {
+    float* part = g.partial + static_cast<int64_t>(split) * g.M * g.N;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + wm + 16 * i + l16;
+      if (m >= g.M) continue;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = n0 + wn + 16 * j + 4 * q4;
+        if (n < g.N) *reinterpret_cast<f32x4*>(part + static_cast<int64_t>(m) * g.N + n) = acc[i][j];
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int m = m0 + wm + 16 * i + l16;
@@ -185,73 +338,161 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = g.alpha * acc[i][j][e];
       if (g.beta != 0.f) {
-        const bf16* cp = g.c + static_cast<int64_t>(m) * g.ldc + n;
-        if (n + 4 <= g.N) {
-          const bf16x4 cv = *reinterpret_cast<const bf16x4*>(cp);
+        const bf16x4 cv = *reinterpret_cast<const bf16x4*>(g.c + static_cast<int64_t>(m) * g.ldc + n);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] += g.beta * static_cast<float>(cv[e]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (n + e < g.N) v[e] += g.beta * static_cast<float>(cp[e]);
-        }
+        for (int e = 0; e < 4; ++e) v[e] += g.beta * static_cast<float>(cv[e]);
       }
-      bf16* dp = g.d + static_cast<int64_t>(m) * g.ldd + n;
-      if (n + 4 <= g.N) {
-        bf16x4 ov;
+      bf16x4 ov;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) ov[e] = static_cast<bf16>(v[e]);
-        *reinterpret_cast<bf16x4*>(dp) = ov;
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (n + e < g.N) dp[e] = static_cast<bf16>(v[e]);
-      }
+      for (int e = 0; e < 4; ++e) ov[e] = static_cast<bf16>(v[e]);
+      *reinterpret_cast<bf16x4*>(g.d + static_cast<int64_t>(m) * g.ldd + n) = ov;
     }
   }
 }
 
-template <int BM, int BN, bool A_KC, bool B_KC>
+// D = alpha * sum_s partial[s] + beta * C, splits summed in order; 8 columns
+// per thread (N % 8 == 0).
+__global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
+  const int64_t groups = static_cast<int64_t>(g.M) * (g.N / 8);
+  const int64_t mn = static_cast<int64_t>(g.M) * g.N;
+  for (int64_t x = blockIdx.x * 256ll + threadIdx.x; x < groups; x += gridDim.x * 256ll) {
+    const int m = static_cast<int>(x / (g.N / 8));
+    const int n = static_cast<int>(x % (g.N / 8)) * 8;
+    const float* p = g.partial + static_cast<int64_t>(m) * g.N + n;
+    f32x4 s0 = *reinterpret_cast<const f32x4*>(p);
+    f32x4 s1 = *reinterpret_cast<const f32x4*>(p + 4);
+    for (int s = 1; s < g.splits; ++s) {
+      const f32x4 a0 = *reinterpret_cast<const f32x4*>(p + s * mn);
+      const f32x4 a1 = *reinterpret_cast<const f32x4*>(p + s * mn + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s0[e] += a0[e];
+        s1[e] += a1[e];
+      }
+    }
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = g.alpha * s0[e];
+      v[4 + e] = g.alpha * s1[e];
+    }
+    if (g.beta != 0.f) {
+      const bf16x8 cv = ld8(g.c + static_cast<int64_t>(m) * g.ldc + n);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] += g.beta * static_cast<float>(cv[e]);
+    }
+    bf16x8 ov;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ov[e] = static_cast<bf16>(v[e]);
+    *reinterpret_cast<bf16x8*>(g.d + static_cast<int64_t>(m) * g.ldd + n) = ov;
+  }
+}
+
+// Kernel configurations: tile, wavefronts per workgroup, K-tile depth, and the
+// measured throughput of one workgroup on these shapes (FLOP/s), used to rank
+// the configurations of a product.
+struct Config {
+  int tbm, tbn, nw, bkt;
+  double rate;
+};
+constexpr Config kConfigs[] = {
+    {256, 256, 8, 64, 3.9e12},  // one workgroup per CU
+    {256, 128, 8, 64, 3.0e12},
+    {128, 128, 4, 32, 1.6e12},  // two workgroups per CU
+    {128, 256, 4, 32, 1.7e12},
+};
+
+struct Plan {
+  int config;  // index into kConfigs
+  int splits;  // 1: no split K
+  int kps;     // K per split (multiple of the config's K tile)
+};
+
+// Configuration and K split for an M x N x K product on 256 CUs.  Products
+// with both operands M/N-contiguous (the weight gradients) or too few output
+// tiles for the CUs use the two-workgroups-per-CU configurations with a K
+// split; the others the one-workgroup configurations.  Among those, the
+// least estimated time = rounds of workgroups over the CUs x tile time + the
+// fp32 partials written and read back (~5 TB/s).
+Plan plan_for(int64_t m, int64_t n, int64_t k, bool a_kc, bool b_kc) {
+  constexpr int64_t kCUs = 256;
+  constexpr double kBytesPerS = 5e12;
+  const int64_t big_tiles = ((m + 255) / 256) * ((n + 127) / 128);
+  const bool small = (!a_kc && !b_kc) || big_tiles < kCUs;
+  Plan best{small ? 2 : 1, 1, 0};
+  double best_t = -1.0;
+  for (int c = 0; c < static_cast<int>(sizeof(kConfigs) / sizeof(kConfigs[0])); ++c) {
+    const Config& cf = kConfigs[c];
+    if ((cf.nw == 4) != small) continue;
+    const int64_t slots = cf.nw == 4 ? 2 * kCUs : kCUs;
+    const int64_t tiles = ((m + cf.tbm - 1) / cf.tbm) * ((n + cf.tbn - 1) / cf.tbn);
+    const int64_t kt = std::max<int64_t>((k + cf.bkt - 1) / cf.bkt, 1);  // K tiles
+    for (int64_t s = 1; s <= (small ? 16 : 1); ++s) {
+      const int64_t tps = (kt + s - 1) / s;  // K tiles per split
+      const int64_t splits = (kt + tps - 1) / tps;
+      if (splits != s || (s > 1 && tps * cf.bkt < 512)) continue;
+      const int64_t rounds = (tiles * splits + slots - 1) / slots;
+      double t = static_cast<double>(rounds) * 2.0 * cf.tbm * cf.tbn * (tps * cf.bkt) / cf.rate;
+      if (splits > 1) t += static_cast<double>(splits) * m * n * 8 / kBytesPerS;
+      if (best_t < 0 || t < best_t * 0.999) {
+        best_t = t;
+        best = Plan{c, static_cast<int>(splits), static_cast<int>(tps * cf.bkt)};
+      }
+    }
+  }
+  return best;
+}
+
+template <int TBM, int TBN, int NW, int BKT, bool A_KC, bool B_KC>
 int launch(GemmArgs g, hipStream_t stream) {
-  const int tiles_m = (g.M + BM - 1) / BM;
-  g.tiles_n = (g.N + BN - 1) / BN;
-  const int64_t items = static_cast<int64_t>(tiles_m) * g.tiles_n;
+  const int tiles_m = (g.M + TBM - 1) / TBM;
+  g.tiles_n = (g.N + TBN - 1) / TBN;
+  const int64_t tiles = static_cast<int64_t>(tiles_m) * g.tiles_n;
+  const int64_t items = tiles * g.splits;
   NMB_REQUIRE(items < (int64_t{1} << 30), "gemm: too many tiles");
+  g.tiles = static_cast<int>(tiles);
   g.items = static_cast<int>(items);
   g.per_xcd = static_cast<int>((items + 7) / 8);
-  const size_t lds = static_cast<size_t>(2 * (BM + BN) * LDS_K) * sizeof(bf16);
-  static bool configured = false;  // raise the dynamic-LDS limit once per instantiation
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<BM, BN, A_KC, B_KC>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       static_cast<int>(lds));
-    if (e != hipSuccess) {
-      set_error("gemm: cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(e));
-      return NMB_EHIP;
-    }
-    configured = true;
-  }
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, A_KC, B_KC>), dim3(static_cast<unsigned>(g.per_xcd * 8)),
-                     dim3(256), lds, stream, g);
+  hipLaunchKernelGGL((gemm_kernel<TBM, TBN, NW, BKT, A_KC, B_KC>),
+                     dim3(static_cast<unsigned>(g.per_xcd * 8)), dim3(NW * 64), 0, stream, g);
   NMB_CHECK_LAUNCH("gemm");
+  if (g.splits > 1) {
+    const int64_t groups = static_cast<int64_t>(g.M) * (g.N / 8);
+    const int64_t blocks = std::min<int64_t>((groups + 255) / 256, 4096);
+    hipLaunchKernelGGL(split_reduce_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, g);
+    NMB_CHECK_LAUNCH("gemm split reduce");
+  }
   return NMB_OK;
 }
 
-template <int BM, int BN>
+template <int TBM, int TBN, int NW, int BKT>
 int dispatch_layout(bool a_kc, bool b_kc, const GemmArgs& g, hipStream_t s) {
-  if (a_kc && b_kc) return launch<BM, BN, true, true>(g, s);
-  if (a_kc && !b_kc) return launch<BM, BN, true, false>(g, s);
-  if (!a_kc && b_kc) return launch<BM, BN, false, true>(g, s);
-  return launch<BM, BN, false, false>(g, s);
+  if (a_kc && b_kc) return launch<TBM, TBN, NW, BKT, true, true>(g, s);
+  if (a_kc && !b_kc) return launch<TBM, TBN, NW, BKT, true, false>(g, s);
+  if (!a_kc && b_kc) return launch<TBM, TBN, NW, BKT, false, true>(g, s);
+  return launch<TBM, TBN, NW, BKT, false, false>(g, s);
+}
+
+int64_t workspace_for(const Plan& p, int64_t m, int64_t n) {
+  return p.splits > 1 ? static_cast<int64_t>(p.splits) * m * n * 4 : 0;
 }
 
 }  // namespace
 }  // namespace nmb
 
+extern "C" int nmb_gemm_bf16_workspace_bytes(int a_layout, int b_layout, int64_t m, int64_t n, int64_t k,
+                                             int64_t* bytes) {
+  NMB_REQUIRE(bytes != nullptr, "gemm: null bytes");
+  NMB_REQUIRE(m >= 0 && n >= 0 && k >= 0 && m < (1 << 30) && n < (1 << 30) && k < (1 << 30),
+              "gemm: invalid shape");
+  *bytes = nmb::workspace_for(nmb::plan_for(m, n, k, a_layout == 0, b_layout == 0), m, n);
+  return NMB_OK;
+}
+
 extern "C" int nmb_gemm_bf16(int a_layout, int b_layout, int64_t m, int64_t n, int64_t k,
                              float alpha, const void* a, int64_t lda, const void* b, int64_t ldb,
                              float beta, const void* c, int64_t ldc, void* d, int64_t ldd,
-                             hipStream_t stream) {
+                             void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   NMB_REQUIRE(a != nullptr && b != nullptr && d != nullptr, "gemm: null operand");
   NMB_REQUIRE(a_layout == 0 || a_layout == 1, "gemm: a_layout must be 0 ([M,K]) or 1 ([K,M])");
   NMB_REQUIRE(b_layout == 0 || b_layout == 1, "gemm: b_layout must be 0 ([N,K]) or 1 ([K,N])");
@@ -259,24 +500,35 @@ extern "C" int nmb_gemm_bf16(int a_layout, int b_layout, int64_t m, int64_t n, i
               "gemm: invalid shape %lld x %lld x %lld", (long long)m, (long long)n, (long long)k);
   NMB_REQUIRE(beta == 0.f || c != nullptr, "gemm: beta != 0 needs C");
   const bool a_kc = a_layout == 0, b_kc = b_layout == 0;
-  // 16-byte operand reads: the contiguous dimension and the leading dimensions
-  // must be multiples of 8 elements, pointers 16-byte aligned
-  NMB_REQUIRE_SUPPORTED((a_kc ? k : m) % 8 == 0 && (b_kc ? k : n) % 8 == 0 && lda % 8 == 0 &&
-                            ldb % 8 == 0,
-                        "gemm: contiguous extents and leading dimensions must be multiples of 8");
-  NMB_REQUIRE(nmb::aligned16(a) && nmb::aligned16(b), "gemm: A and B must be 16-byte aligned");
+  // 16-byte operand chunks: the contiguous dimensions and the leading
+  // dimensions are multiples of 8 elements and the pointers 16-byte aligned
+  NMB_REQUIRE_SUPPORTED((a_kc ? k : m) % 8 == 0 && (b_kc ? k : n) % 8 == 0 && n % 8 == 0 &&
+                            lda % 8 == 0 && ldb % 8 == 0 && ldd % 8 == 0 &&
+                            (beta == 0.f || ldc % 8 == 0),
+                        "gemm: N, the contiguous extents and leading dimensions must be multiples of 8");
+  NMB_REQUIRE(nmb::aligned16(a) && nmb::aligned16(b) && nmb::aligned16(d) &&
+                  (beta == 0.f || nmb::aligned16(c)),
+              "gemm: operands must be 16-byte aligned");
   NMB_REQUIRE(lda >= (a_kc ? k : m) && ldb >= (b_kc ? k : n) && ldd >= n && (beta == 0.f || ldc >= n),
               "gemm: leading dimension too small");
-  NMB_REQUIRE(ldd % 4 == 0 && (beta == 0.f || ldc % 4 == 0) &&
-                  (reinterpret_cast<uintptr_t>(d) & 7) == 0 &&
-                  (beta == 0.f || (reinterpret_cast<uintptr_t>(c) & 7) == 0),
-              "gemm: C/D rows must be 8-byte aligned");
+  // the loads address a tile's operand with 32-bit byte offsets
+  const int64_t span_a = a_kc ? int64_t{256} * lda : k * lda;
+  const int64_t span_b = b_kc ? int64_t{256} * ldb : k * ldb;
+  NMB_REQUIRE_SUPPORTED(2 * span_a < (int64_t{1} << 31) && 2 * span_b < (int64_t{1} << 31),
+                        "gemm: an operand tile spans more than 2 GiB");
   if (m == 0 || n == 0) return NMB_OK;
+  const nmb::Plan p = nmb::plan_for(m, n, k, a_kc, b_kc);
+  const int64_t need = nmb::workspace_for(p, m, n);
+  NMB_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+              "gemm: workspace of %lld bytes needed, %lld given", (long long)need,
+              (long long)workspace_bytes);
+  NMB_REQUIRE(need == 0 || nmb::aligned16(workspace), "gemm: workspace must be 16-byte aligned");
   nmb::GemmArgs g{};
   g.a = static_cast<const nmb::bf16*>(a);
   g.b = static_cast<const nmb::bf16*>(b);
   g.c = static_cast<const nmb::bf16*>(c);
   g.d = static_cast<nmb::bf16*>(d);
+  g.partial = static_cast<float*>(workspace);
   g.lda = lda;
   g.ldb = ldb;
   g.ldc = ldc;
@@ -286,5 +538,12 @@ extern "C" int nmb_gemm_bf16(int a_layout, int b_layout, int64_t m, int64_t n, i
   g.K = static_cast<int>(k);
   g.alpha = alpha;
   g.beta = beta;
-  return nmb::dispatch_layout<256, 256>(a_kc, b_kc, g, stream);
+  g.splits = p.splits;
+  g.kps = p.kps;
+  switch (p.config) {
+    case 0: return nmb::dispatch_layout<256, 256, 8, 64>(a_kc, b_kc, g, stream);
+    case 1: return nmb::dispatch_layout<256, 128, 8, 64>(a_kc, b_kc, g, stream);
+    case 2: return nmb::dispatch_layout<128, 128, 4, 32>(a_kc, b_kc, g, stream);
+    default: return nmb::dispatch_layout<128, 256, 4, 32>(a_kc, b_kc, g, stream);
+  }
 }

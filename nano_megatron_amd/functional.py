@@ -1,9 +1,9 @@
 """Device ops of the GPT block: thin wrappers over libnmb.so plus autograd Functions.
 
 Every op runs on the GPU through the C ABI; a CPU tensor is an error, never a
-fallback.  Dense projections are plain library GEMMs (``torch.mm`` /
-``torch.addmm`` -> hipBLASLt); everything else is a hand-written gfx950
-kernel.
+fallback.  Every bf16 op, the dense projections included, is a hand-written
+gfx950 kernel; fp32 (the parity configuration) projections use the library
+GEMM.
 
 Attention tensors use one memory layout throughout: ``[batch, seq, heads,
 head_dim]`` (the layout of the Q/K/V projection outputs), seen through a
@@ -40,6 +40,9 @@ def _workspace(nbytes: int, device: torch.device) -> Tensor:
 
 
 # ---------------------------------------------------------------- GEMM
+_GEMM_WS: dict = {}  # (layouts, m, n, k) -> split-K workspace bytes (a pure function of the shape)
+
+
 def _operand_layout(t: Tensor, rows_dim: int) -> tuple[int, int]:
     """(layout, ld) of a 2-D operand: 0 if dim 1 is contiguous (ld = stride(0)),
     1 if dim 0 is contiguous (ld = stride(1))."""
@@ -64,7 +67,9 @@ def mm(a: Tensor, b: Tensor, *, out: Tensor | None = None, c: Tensor | None = No
     if out is None:
         out = torch.empty(m, n, dtype=a.dtype, device=a.device)
     if a.dtype != torch.bfloat16:
-        if beta != 0.0:
+        if beta != 0.0 and c is out:
+            out.addmm_(a, b, beta=beta, alpha=alpha)
+        elif beta != 0.0:
             torch.addmm(c, a, b, beta=beta, alpha=alpha, out=out)
         else:
             torch.mm(a, b, out=out) if alpha == 1.0 else torch.mm(a, b, out=out).mul_(alpha)
@@ -78,10 +83,17 @@ def mm(a: Tensor, b: Tensor, *, out: Tensor | None = None, c: Tensor | None = No
         raise ValueError("gemm: the output must be row-major")
     if beta != 0.0 and (c is None or c.stride(1) != 1):
         raise ValueError("gemm: beta != 0 needs a row-major C")
+    key = (la, lb, m, n, k)
+    nbytes = _GEMM_WS.get(key)
+    if nbytes is None:
+        q = _lib.ctypes.c_int64()
+        _lib.call("nmb_gemm_bf16_workspace_bytes", la, lb, m, n, k, _lib.ctypes.byref(q))
+        nbytes = _GEMM_WS[key] = q.value
+    ws = _workspace(nbytes, a.device) if nbytes else None
     _lib.call(
         "nmb_gemm_bf16", la, lb, m, n, k, float(alpha), a.data_ptr(), lda, b.data_ptr(), ldb,
         float(beta), _lib.ptr(c), c.stride(0) if c is not None else n, out.data_ptr(),
-        out.stride(0), _lib.stream_of(a),
+        out.stride(0), _lib.ptr(ws), ws.numel() if ws is not None else 0, _lib.stream_of(a),
     )
     return out
 
@@ -570,7 +582,7 @@ class LMHeadCrossEntropyFunction(torch.autograd.Function):
         buf = torch.empty(min(chunk, max(rows, 1)), weight.shape[0], dtype=x2.dtype, device=x2.device)
         for s, e in _chunks(rows, chunk):
             logits = buf[: e - s]
-            torch.mm(x2[s:e], weight.t(), out=logits)
+            mm(x2[s:e], weight.t(), out=logits)
             ce_fwd(logits, targets[s:e], ignore_index, loss[s:e], lse[s:e])
         ctx.save_for_backward(x2, weight, targets, lse)
         ctx.ignore_index = ignore_index
@@ -588,10 +600,10 @@ class LMHeadCrossEntropyFunction(torch.autograd.Function):
                           device=x2.device)
         for s, e in _chunks(rows, ctx.chunk):
             g = buf[: e - s]
-            torch.mm(x2[s:e], weight.t(), out=g)
+            mm(x2[s:e], weight.t(), out=g)
             ce_bwd_(g, targets[s:e], ctx.ignore_index, lse[s:e], grad_loss[s:e])
-            torch.mm(g, weight, out=dx[s:e])
-            dw.addmm_(g.t(), x2[s:e])
+            mm(g, weight, out=dx[s:e])
+            mm(g.t(), x2[s:e], out=dw, c=dw, beta=1.0)
         return dx, dw, None, None, None
 
 
