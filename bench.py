@@ -47,6 +47,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-kernels", action="store_true", help="skip the per-kernel roofline timing")
     p.add_argument("--no-eager", action="store_true", help="skip the no-checkpoint comparison run")
     p.add_argument("--only-kernels", action="store_true", help="time the kernels only (for profiling)")
+    p.add_argument("--kernel", default=None, help="with --only-kernels: time just this kernel")
     return p.parse_args()
 
 
@@ -112,9 +113,10 @@ def run_steps(mode: str, steps: int, warmup: int, device) -> dict:
     return result
 
 
-def kernel_rooflines(device) -> list[dict]:
+def kernel_rooflines(device, only: str | None = None) -> list[dict]:
     """Average launch time (HIP events on the launch stream) of each hand-written
-    kernel at the config-3 shapes, with algorithmic bytes / FLOPs per launch."""
+    kernel at the config-3 shapes, with algorithmic bytes / FLOPs per launch
+    (``only``: just the named one)."""
     import torch
 
     import nano_megatron_amd as nm
@@ -148,7 +150,7 @@ def kernel_rooflines(device) -> list[dict]:
     dq = dqkv[:, :H].view(BATCH, SEQ, nh, d)
     dk = dqkv[:, H:2 * H].view(BATCH, SEQ, nh, d)
     dv = dqkv[:, 2 * H:].view(BATCH, SEQ, nh, d)
-    chunk = 2048
+    chunk = chunk_rows = 2048
     logits = randn(chunk, V)
     targets = torch.randint(0, V, (chunk,), device=device, generator=g)
     loss = torch.empty(chunk, dtype=torch.float32, device=device)
@@ -159,6 +161,34 @@ def kernel_rooflines(device) -> list[dict]:
 
     causal_flops = 2 * 2 * BATCH * nh * SEQ * SEQ * d / 2
     E = 2  # bytes per bf16 element
+
+    # the step's GEMM shapes (fwd, recompute, backward, LM head chunks)
+    def gemm_case(name, m, n, k, a_t, b_t, per_step, residual=False):
+        a = randn(k, m).t() if a_t else randn(m, k)
+        b = randn(k, n) if b_t else randn(n, k).t()
+        c = randn(m, n) if residual else None
+        out = torch.empty(m, n, dtype=bf, device=device)
+        fn = (lambda: Fn.mm(a, b, out=out, c=c, beta=1.0)) if residual else (lambda: Fn.mm(a, b, out=out))
+        nbytes = (m * k + k * n + m * n * (2 if residual else 1)) * E
+        return (name, fn, nbytes, 2.0 * m * n * k, "mfma", per_step)
+
+    gemms = [
+        gemm_case("gemm_qkv", T, 3 * H, H, False, False, 2 * L),
+        gemm_case("gemm_o_residual", T, H, H, False, False, 2 * L, residual=True),
+        gemm_case("gemm_gate_up", T, 2 * F, H, False, False, 2 * L),
+        gemm_case("gemm_down_residual", T, H, F, False, False, L, residual=True),
+        gemm_case("gemm_d_swiglu", T, F, H, False, True, L),
+        gemm_case("gemm_dw_down", H, F, T, True, True, L),
+        gemm_case("gemm_d_norm2", T, H, 2 * F, False, True, L),
+        gemm_case("gemm_dw_gate_up", 2 * F, H, T, True, True, L),
+        gemm_case("gemm_d_attn_out", T, H, H, False, True, L),
+        gemm_case("gemm_dw_o", H, H, T, True, True, L),
+        gemm_case("gemm_d_norm1", T, H, 3 * H, False, True, L),
+        gemm_case("gemm_dw_qkv", 3 * H, H, T, True, True, L),
+        gemm_case("gemm_lm_logits", chunk_rows, V, H, False, False, 2 * T // chunk_rows),
+        gemm_case("gemm_lm_dx", chunk_rows, H, V, False, True, T // chunk_rows),
+        gemm_case("gemm_lm_dE", V, H, chunk_rows, True, True, T // chunk_rows, residual=True),
+    ]
     cases = [
         # name, fn, algorithmic bytes, flops, bound, launches per training step (full recompute)
         ("rmsnorm_fwd", lambda: Fn.rmsnorm_fwd(x, w, 1e-5), 2 * T * H * E + H * E, 0, "hbm", 4 * L + 1),
@@ -172,7 +202,11 @@ def kernel_rooflines(device) -> list[dict]:
          8 * T * H * E + BATCH * nh * SEQ * 4, 2.5 * causal_flops, "hbm", L),
         ("ce_fwd", lambda: Fn.ce_fwd(logits, targets, -100, loss, lse_c), chunk * V * E + chunk * 16, 0, "hbm", T // chunk),
         ("ce_bwd", lambda: Fn.ce_bwd_(logits, targets, -100, lse_c, grad_c), 2 * chunk * V * E + chunk * 16, 0, "hbm", T // chunk),
-    ]
+    ] + gemms
+    if only is not None:
+        cases = [c_ for c_ in cases if c_[0] == only]
+        if not cases:
+            raise SystemExit(f"bench.py: no kernel named {only!r}")
     out = []
     side = torch.cuda.Stream(device)
     for name, fn, nbytes, flops, bound, per_step in cases:
@@ -203,12 +237,38 @@ def kernel_rooflines(device) -> list[dict]:
         gbs = nbytes / us / 1e3
         entry = dict(kernel=name, us=round(us, 2), bytes=int(nbytes), gbs=round(gbs, 1),
                      hbm_frac=round(gbs / HBM_PEAK_GBS, 3), bound=bound,
-                     us_per_step=round(us * per_step, 1))
+                     us_per_step=round(us * per_step, 1), launches_per_step=per_step)
         if flops:
             tf = flops / us / 1e6
             entry.update(flops=int(flops), tflops=round(tf, 1), mfma_frac=round(tf / BF16_PEAK_TFLOPS, 4))
         out.append(entry)
     return out
+
+
+def measured_traffic(kernel: str) -> int | None:
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 counter
+    summary ``profiles/<kernel>_c3_traffic.md`` (FETCH_SIZE + WRITE_SIZE, each
+    scaled by the same counter's reading for a copy of known size), if any."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_c3_traffic.md")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    return None
+
+
+def copy_calibration(device) -> None:
+    """A plain device copy of 256 MiB (read 256 MiB, write 256 MiB), run once so
+    that a counter pass sees the HBM bytes one such copy reports."""
+    import torch
+
+    src = torch.empty(128 << 20, dtype=torch.bfloat16, device=device).fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
 
 
 def cpu_baseline() -> dict:
@@ -282,9 +342,11 @@ def main() -> None:
 
     kernels = None
     if not args.no_kernels:
-        kernels = kernel_rooflines(device)
+        kernels = kernel_rooflines(device, args.kernel if args.only_kernels else None)
         print("kernels: " + json.dumps(kernels), file=sys.stderr, flush=True)
     if args.only_kernels:
+        if args.kernel:
+            copy_calibration(device)
         return
     full = run_steps("full", args.steps, args.warmup, device)
     print("full: " + json.dumps(full), file=sys.stderr, flush=True)
@@ -295,9 +357,16 @@ def main() -> None:
 
     roofline = None
     if kernels:
+        # the kernel with the most time per training step
         dom = max(kernels, key=lambda k: k["us_per_step"])
-        roofline = dict(bound="hbm", achieved=dom["gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
-                        frac=dom["hbm_frac"], traffic=None, kernel=dom["kernel"])
+        if dom["bound"] == "mfma":
+            roofline = dict(bound="mfma", achieved=dom["tflops"], peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
+                            frac=dom["mfma_frac"])
+        else:
+            roofline = dict(bound="hbm", achieved=dom["gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
+                            frac=dom["hbm_frac"])
+        roofline.update(traffic=measured_traffic(dom["kernel"]), kernel=dom["kernel"],
+                        us_per_launch=dom["us"], algorithmic_bytes=dom["bytes"])
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline()

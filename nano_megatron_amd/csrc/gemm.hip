@@ -30,8 +30,8 @@
 // LDS holds two K tiles; the next tile's loads are issued right after the
 // barrier that publishes the current one (one barrier per K tile).  Each MFMA
 // computes a D^T tile (B fragment as the A operand), so a lane ends up with
-// four consecutive columns of one output row.  Blocks are mapped so that tiles
-// sharing an operand row block run on the same XCD (its own L2).
+// four consecutive columns of one output row.  Blocks are mapped so that the
+// tiles an XCD (with its own L2) runs together form a 4 x 8 block of tiles.
 //
 // Split K (small M x N, long K -- the weight gradients): split s of a tile
 // covers K range [s * kps, (s + 1) * kps) and writes fp32 partials to the
@@ -237,8 +237,16 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void gemm_kernel(GemmArgs
   if (w >= g.items) return;
   const int split = w / g.tiles;
   const int t = w % g.tiles;
-  const int m0 = (t / g.tiles_n) * TBM;
-  const int n0 = (t % g.tiles_n) * TBN;
+  // grouped order: 4 tile rows at a time, walking the rows fastest, so the
+  // 32 workgroups an XCD runs together cover 4 rows x 8 columns of tiles and
+  // share their operand blocks in its L2
+  constexpr int GM = 4;
+  const int tiles_m = g.tiles / g.tiles_n;
+  const int grp = t / (GM * g.tiles_n);
+  const int gsize = min(tiles_m - grp * GM, GM);
+  const int r = t - grp * GM * g.tiles_n;
+  const int m0 = (grp * GM + r % gsize) * TBM;
+  const int n0 = (r / gsize) * TBN;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = (wave / WAVES_N) * WM, wn = (wave % WAVES_N) * WN;
   const int k_begin = split * g.kps;
