@@ -193,7 +193,7 @@ def kernel_rooflines(device, only: str | None = None) -> list[dict]:
         # name, fn, algorithmic bytes, flops, bound, launches per training step (full recompute)
         ("rmsnorm_fwd", lambda: Fn.rmsnorm_fwd(x, w, 1e-5), 2 * T * H * E + H * E, 0, "hbm", 4 * L + 1),
         ("rmsnorm_bwd", lambda: Fn.rmsnorm_bwd(x, w, dy, 1e-5), 3 * T * H * E + 2 * H * E, 0, "hbm", 2 * L + 1),
-        ("rope_apply", lambda: Fn.rope_apply(q, rope_out, tab.cos, tab.sin), 2 * T * H * E, 0, "hbm", 6 * L),
+        ("rope_apply", lambda: Fn.rope_apply(q, rope_out, tab.cos, tab.sin), 2 * T * H * E, 0, "hbm", 2 * L),
         ("swiglu_fwd", lambda: Fn.swiglu_fwd(gate, up, act), 3 * T * F * E, 0, "hbm", L),
         ("swiglu_bwd", lambda: Fn.swiglu_bwd(gate, up, dh, dgu[:, :F], dgu[:, F:], act), 6 * T * F * E, 0, "hbm", L),
         ("attn_fwd", lambda: Fn.attn_fwd_bshd(q, [k], [v], (0,), causal=True, q_offset=0, scale=None, out=o, lse=lse),

@@ -169,6 +169,23 @@ int nmb_gemm_bf16(int a_layout, int b_layout, int64_t m, int64_t n, int64_t k, f
                   const void* c, int64_t ldc, void* d, int64_t ldd, void* workspace,
                   int64_t workspace_bytes, hipStream_t stream);
 
+/* GEMM with the rotary embedding as its epilogue: the Q/K/V projection and
+ * RoPE of q and k in one pass (reference models/gpt/attention.py:172-181 with
+ * nn/rotary.py:27-38, 55-70; replaces nmb_gemm_bf16 + two nmb_rope_apply).
+ *   D = A B (A row-major [M, K]; b_layout as in nmb_gemm_bf16), then each of
+ *   the first rope_cols columns of D, read as heads of head_dim (64 or 128),
+ *   is rotated with the reference's roundings: q = bf16(D), cos/sin = bf16 of
+ *   the fp32 tables [n_pos, head_dim/2], bf16 after each product and the sum.
+ * Row m is token (m / seq, m % seq); its position is positions[(m / seq) *
+ * pos_batch_stride + m % seq] (int32, nullable) or pos_offset + m % seq.
+ * The result equals nmb_gemm_bf16 followed by nmb_rope_apply on the q and k
+ * columns bit for bit.  No workspace (never split along K). */
+int nmb_gemm_bf16_rope(int b_layout, int64_t m, int64_t n, int64_t k, const void* a, int64_t lda,
+                       const void* b, int64_t ldb, void* d, int64_t ldd, const float* cos_table,
+                       const float* sin_table, int64_t n_pos, const int32_t* positions,
+                       int64_t pos_batch_stride, int64_t pos_offset, int64_t seq, int64_t head_dim,
+                       int64_t rope_cols, hipStream_t stream);
+
 /* ------------------------------------------------------------ optimizer
  * replaces FlatShardZeROStrategy.clip_grad_norm + optimizer_step at DP=1
  * (data_parallel/_zero.py:130-199; defaults config/schema.py:439-445):

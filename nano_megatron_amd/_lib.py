@@ -63,6 +63,10 @@ SIGNATURES: dict[str, list] = {
         _i32, _i32, _i64, _i64, _i64, _f32, _p, _i64, _p, _i64, _f32, _p, _i64, _p, _i64, _p,
         _i64, _p,
     ],
+    "nmb_gemm_bf16_rope": [
+        _i32, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i64,
+        _i64, _i64, _p,
+    ],
     "nmb_adamw_workspace_bytes": [_i64, _psz],
     "nmb_adamw_step": [
         _p, _p, _p, _i32, _i64, _p, _p, _p, _i32, _i32, _f32, _f32, _f32, _f32, _f32, _i64, _f32,

@@ -102,10 +102,11 @@ def block_forward(x: Tensor, w: tuple[Tensor, ...], m: BlockMeta, *, recompute: 
     b, s, hdim = x.shape
     x2 = x.reshape(b * s, hdim)
     n1 = Fn.rmsnorm_fwd(x2, w_in, m.eps)
-    qkv = Fn.mm(n1, joined((wq, wk, wv)).t())
+    # Q/K/V projection with RoPE of q and k as the GEMM epilogue
+    qkv = Fn.mm_rope(n1, joined((wq, wk, wv)).t(), seq=s, head_dim=m.head_dim,
+                     rope_cols=(m.heads + m.kv_heads) * m.head_dim, cos=m.cos, sin=m.sin,
+                     pos_offset=m.sequence_offset, positions=m.positions)
     q, k, v = _qkv_views(qkv, b, s, m)
-    Fn.rope_apply(q, q, m.cos, m.sin, pos_offset=m.sequence_offset, positions=m.positions)
-    Fn.rope_apply(k, k, m.cos, m.sin, pos_offset=m.sequence_offset, positions=m.positions)
     o, lse = Fn.attn_fwd_bshd(q, [k], [v], (0,), causal=True, q_offset=m.sequence_offset, scale=None)
     o2 = o.view(b * s, m.heads * m.head_dim)
     h = Fn.mm(o2, wo.t(), c=x2, beta=1.0)

@@ -213,11 +213,18 @@ struct GemmArgs {
   int M, N, K;
   float alpha, beta;
   int tiles_n, tiles, splits, kps, items, per_xcd;
+  // RoPE epilogue (head dim RD > 0): the first rope_cols output columns are
+  // heads of RD rotated by the position of their row
+  const float* rope_cos;  // fp32 [n_pos, RD/2]
+  const float* rope_sin;
+  const int32_t* rope_pos;  // [batch, pos_bstride] or null: rope_offset + row % rope_seq
+  int64_t rope_pos_bstride;
+  int rope_offset, rope_seq, rope_n_pos, rope_cols;
 };
 
 // TBM x TBN output tile, NW wavefronts (4: 2 x 2, two workgroups per CU;
 // 8: 2 x 4 or 4 x 2, one workgroup per CU), BKT-deep K tiles.
-template <int TBM, int TBN, int NW, int BKT, bool A_KC, bool B_KC>
+template <int TBM, int TBN, int NW, int BKT, bool A_KC, bool B_KC, int RD>
 __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void gemm_kernel(GemmArgs g) {
   constexpr int WAVES_N = NW == 4 ? 2 : (TBN == 256 ? 4 : 2);
   constexpr int WAVES_M = NW / WAVES_N;
@@ -334,6 +341,61 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void gemm_kernel(GemmArgs
     }
     return;
   }
+  if constexpr (RD > 0) {
+    static_assert(WN % RD == 0, "a wave's columns cover whole heads");
+    // RoPE as the rotary kernel does it (reference nn/rotary.py:36-38, 65-70):
+    // q rounded to bf16, cos/sin rounded to bf16, a rounding after each
+    // product and after the sum.  Column pairs (d, d + RD/2) of a head are
+    // tiles j and j + RD/32 of the same lane.
+    constexpr int HALF = RD / 2;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + wm + 16 * i + l16;
+      if (m >= g.M) continue;
+      const int sq = m % g.rope_seq;
+      int pos = g.rope_pos != nullptr
+                    ? g.rope_pos[static_cast<int64_t>(m / g.rope_seq) * g.rope_pos_bstride + sq]
+                    : g.rope_offset + sq;
+      // an out-of-table position is a caller error: read a valid row and poison the result
+      const bool bad = pos < 0 || pos >= g.rope_n_pos;
+      if (bad) pos = 0;
+      const float* crow = g.rope_cos + static_cast<int64_t>(pos) * HALF;
+      const float* srow = g.rope_sin + static_cast<int64_t>(pos) * HALF;
+      bf16* drow = g.d + static_cast<int64_t>(m) * g.ldd;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = n0 + wn + 16 * j + 4 * q4;
+        if (n >= g.N) continue;
+        if ((16 * j) % RD >= HALF) {
+          if (n0 + wn + 16 * j < g.rope_cols) continue;  // written with its first-half partner
+        } else if (n0 + wn + 16 * j < g.rope_cols) {
+          constexpr int JP = HALF / 16;
+          const int d = (16 * j) % RD + 4 * q4;
+          bf16x4 o1, o2;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float x1 = round_as<bf16>(acc[i][j][e]);
+            const float x2 = round_as<bf16>(acc[i][(j + JP) % TN][e]);
+            const float c = round_as<bf16>(crow[d + e]);
+            const float sn = round_as<bf16>(srow[d + e]);
+            float r1 = round_as<bf16>(add_rn(round_as<bf16>(mul_rn(x1, c)), round_as<bf16>(mul_rn(-x2, sn))));
+            float r2 = round_as<bf16>(add_rn(round_as<bf16>(mul_rn(x2, c)), round_as<bf16>(mul_rn(x1, sn))));
+            if (bad) r1 = r2 = __builtin_nanf("");
+            o1[e] = static_cast<bf16>(r1);
+            o2[e] = static_cast<bf16>(r2);
+          }
+          *reinterpret_cast<bf16x4*>(drow + n) = o1;
+          *reinterpret_cast<bf16x4*>(drow + n + HALF) = o2;
+          continue;
+        }
+        bf16x4 ov;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ov[e] = static_cast<bf16>(acc[i][j][e]);
+        *reinterpret_cast<bf16x4*>(drow + n) = ov;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int m = m0 + wm + 16 * i + l16;
@@ -422,7 +484,10 @@ struct Plan {
 // split; the others the one-workgroup configurations.  Among those, the
 // least estimated time = rounds of workgroups over the CUs x tile time + the
 // fp32 partials written and read back (~5 TB/s).
-Plan plan_for(int64_t m, int64_t n, int64_t k, bool a_kc, bool b_kc) {
+// Columns of one wavefront's share of a configuration's tile.
+constexpr int wave_cols(const Config& c) { return c.nw == 4 ? c.tbn / 2 : (c.tbn == 256 ? c.tbn / 4 : c.tbn / 2); }
+
+Plan plan_for(int64_t m, int64_t n, int64_t k, bool a_kc, bool b_kc, int rope_head_dim = 0) {
   constexpr int64_t kCUs = 256;
   constexpr double kBytesPerS = 5e12;
   const int64_t big_tiles = ((m + 255) / 256) * ((n + 127) / 128);
@@ -431,11 +496,12 @@ Plan plan_for(int64_t m, int64_t n, int64_t k, bool a_kc, bool b_kc) {
   double best_t = -1.0;
   for (int c = 0; c < static_cast<int>(sizeof(kConfigs) / sizeof(kConfigs[0])); ++c) {
     const Config& cf = kConfigs[c];
-    if ((cf.nw == 4) != small) continue;
+    // the RoPE epilogue needs whole heads per wavefront and no K split
+    if (rope_head_dim > 0 ? wave_cols(cf) % rope_head_dim != 0 : (cf.nw == 4) != small) continue;
     const int64_t slots = cf.nw == 4 ? 2 * kCUs : kCUs;
     const int64_t tiles = ((m + cf.tbm - 1) / cf.tbm) * ((n + cf.tbn - 1) / cf.tbn);
     const int64_t kt = std::max<int64_t>((k + cf.bkt - 1) / cf.bkt, 1);  // K tiles
-    for (int64_t s = 1; s <= (small ? 16 : 1); ++s) {
+    for (int64_t s = 1; s <= (small && rope_head_dim == 0 ? 16 : 1); ++s) {
       const int64_t tps = (kt + s - 1) / s;  // K tiles per split
       const int64_t splits = (kt + tps - 1) / tps;
       if (splits != s || (s > 1 && tps * cf.bkt < 512)) continue;
@@ -451,7 +517,7 @@ Plan plan_for(int64_t m, int64_t n, int64_t k, bool a_kc, bool b_kc) {
   return best;
 }
 
-template <int TBM, int TBN, int NW, int BKT, bool A_KC, bool B_KC>
+template <int TBM, int TBN, int NW, int BKT, bool A_KC, bool B_KC, int RD = 0>
 int launch(GemmArgs g, hipStream_t stream) {
   const int tiles_m = (g.M + TBM - 1) / TBM;
   g.tiles_n = (g.N + TBN - 1) / TBN;
@@ -461,7 +527,7 @@ int launch(GemmArgs g, hipStream_t stream) {
   g.tiles = static_cast<int>(tiles);
   g.items = static_cast<int>(items);
   g.per_xcd = static_cast<int>((items + 7) / 8);
-  hipLaunchKernelGGL((gemm_kernel<TBM, TBN, NW, BKT, A_KC, B_KC>),
+  hipLaunchKernelGGL((gemm_kernel<TBM, TBN, NW, BKT, A_KC, B_KC, RD>),
                      dim3(static_cast<unsigned>(g.per_xcd * 8)), dim3(NW * 64), 0, stream, g);
   NMB_CHECK_LAUNCH("gemm");
   if (g.splits > 1) {
@@ -481,6 +547,19 @@ int dispatch_layout(bool a_kc, bool b_kc, const GemmArgs& g, hipStream_t s) {
   return launch<TBM, TBN, NW, BKT, false, false>(g, s);
 }
 
+template <int RD>
+int dispatch_rope(int config, bool b_kc, const GemmArgs& g, hipStream_t s) {
+  if constexpr (RD == 64) {
+    switch (config) {
+      case 0: return b_kc ? launch<256, 256, 8, 64, true, true, RD>(g, s) : launch<256, 256, 8, 64, true, false, RD>(g, s);
+      case 1: return b_kc ? launch<256, 128, 8, 64, true, true, RD>(g, s) : launch<256, 128, 8, 64, true, false, RD>(g, s);
+      case 2: return b_kc ? launch<128, 128, 4, 32, true, true, RD>(g, s) : launch<128, 128, 4, 32, true, false, RD>(g, s);
+      default: break;
+    }
+  }
+  return b_kc ? launch<128, 256, 4, 32, true, true, RD>(g, s) : launch<128, 256, 4, 32, true, false, RD>(g, s);
+}
+
 int64_t workspace_for(const Plan& p, int64_t m, int64_t n) {
   return p.splits > 1 ? static_cast<int64_t>(p.splits) * m * n * 4 : 0;
 }
@@ -497,45 +576,45 @@ extern "C" int nmb_gemm_bf16_workspace_bytes(int a_layout, int b_layout, int64_t
   return NMB_OK;
 }
 
-extern "C" int nmb_gemm_bf16(int a_layout, int b_layout, int64_t m, int64_t n, int64_t k,
-                             float alpha, const void* a, int64_t lda, const void* b, int64_t ldb,
-                             float beta, const void* c, int64_t ldc, void* d, int64_t ldd,
-                             void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+namespace nmb {
+namespace {
+
+// Argument checks shared by the GEMM entry points.
+int check_gemm(int a_layout, int b_layout, int64_t m, int64_t n, int64_t k, const void* a, int64_t lda,
+               const void* b, int64_t ldb, bool use_c, const void* c, int64_t ldc, const void* d,
+               int64_t ldd) {
   NMB_REQUIRE(a != nullptr && b != nullptr && d != nullptr, "gemm: null operand");
   NMB_REQUIRE(a_layout == 0 || a_layout == 1, "gemm: a_layout must be 0 ([M,K]) or 1 ([K,M])");
   NMB_REQUIRE(b_layout == 0 || b_layout == 1, "gemm: b_layout must be 0 ([N,K]) or 1 ([K,N])");
   NMB_REQUIRE(m >= 0 && n >= 0 && k >= 0 && m < (1 << 30) && n < (1 << 30) && k < (1 << 30),
               "gemm: invalid shape %lld x %lld x %lld", (long long)m, (long long)n, (long long)k);
-  NMB_REQUIRE(beta == 0.f || c != nullptr, "gemm: beta != 0 needs C");
+  NMB_REQUIRE(!use_c || c != nullptr, "gemm: beta != 0 needs C");
   const bool a_kc = a_layout == 0, b_kc = b_layout == 0;
   // 16-byte operand chunks: the contiguous dimensions and the leading
   // dimensions are multiples of 8 elements and the pointers 16-byte aligned
   NMB_REQUIRE_SUPPORTED((a_kc ? k : m) % 8 == 0 && (b_kc ? k : n) % 8 == 0 && n % 8 == 0 &&
-                            lda % 8 == 0 && ldb % 8 == 0 && ldd % 8 == 0 &&
-                            (beta == 0.f || ldc % 8 == 0),
+                            lda % 8 == 0 && ldb % 8 == 0 && ldd % 8 == 0 && (!use_c || ldc % 8 == 0),
                         "gemm: N, the contiguous extents and leading dimensions must be multiples of 8");
-  NMB_REQUIRE(nmb::aligned16(a) && nmb::aligned16(b) && nmb::aligned16(d) &&
-                  (beta == 0.f || nmb::aligned16(c)),
+  NMB_REQUIRE(aligned16(a) && aligned16(b) && aligned16(d) && (!use_c || aligned16(c)),
               "gemm: operands must be 16-byte aligned");
-  NMB_REQUIRE(lda >= (a_kc ? k : m) && ldb >= (b_kc ? k : n) && ldd >= n && (beta == 0.f || ldc >= n),
+  NMB_REQUIRE(lda >= (a_kc ? k : m) && ldb >= (b_kc ? k : n) && ldd >= n && (!use_c || ldc >= n),
               "gemm: leading dimension too small");
   // the loads address a tile's operand with 32-bit byte offsets
   const int64_t span_a = a_kc ? int64_t{256} * lda : k * lda;
   const int64_t span_b = b_kc ? int64_t{256} * ldb : k * ldb;
   NMB_REQUIRE_SUPPORTED(2 * span_a < (int64_t{1} << 31) && 2 * span_b < (int64_t{1} << 31),
                         "gemm: an operand tile spans more than 2 GiB");
-  if (m == 0 || n == 0) return NMB_OK;
-  const nmb::Plan p = nmb::plan_for(m, n, k, a_kc, b_kc);
-  const int64_t need = nmb::workspace_for(p, m, n);
-  NMB_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr),
-              "gemm: workspace of %lld bytes needed, %lld given", (long long)need,
-              (long long)workspace_bytes);
-  NMB_REQUIRE(need == 0 || nmb::aligned16(workspace), "gemm: workspace must be 16-byte aligned");
-  nmb::GemmArgs g{};
-  g.a = static_cast<const nmb::bf16*>(a);
-  g.b = static_cast<const nmb::bf16*>(b);
-  g.c = static_cast<const nmb::bf16*>(c);
-  g.d = static_cast<nmb::bf16*>(d);
+  return NMB_OK;
+}
+
+GemmArgs make_args(int64_t m, int64_t n, int64_t k, float alpha, const void* a, int64_t lda,
+                   const void* b, int64_t ldb, float beta, const void* c, int64_t ldc, void* d,
+                   int64_t ldd, void* workspace, const Plan& p) {
+  GemmArgs g{};
+  g.a = static_cast<const bf16*>(a);
+  g.b = static_cast<const bf16*>(b);
+  g.c = static_cast<const bf16*>(c);
+  g.d = static_cast<bf16*>(d);
   g.partial = static_cast<float*>(workspace);
   g.lda = lda;
   g.ldb = ldb;
@@ -548,10 +627,69 @@ extern "C" int nmb_gemm_bf16(int a_layout, int b_layout, int64_t m, int64_t n, i
   g.beta = beta;
   g.splits = p.splits;
   g.kps = p.kps;
+  return g;
+}
+
+}  // namespace
+}  // namespace nmb
+
+extern "C" int nmb_gemm_bf16(int a_layout, int b_layout, int64_t m, int64_t n, int64_t k,
+                             float alpha, const void* a, int64_t lda, const void* b, int64_t ldb,
+                             float beta, const void* c, int64_t ldc, void* d, int64_t ldd,
+                             void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  const int st = nmb::check_gemm(a_layout, b_layout, m, n, k, a, lda, b, ldb, beta != 0.f, c, ldc, d, ldd);
+  if (st != NMB_OK) return st;
+  if (m == 0 || n == 0) return NMB_OK;
+  const bool a_kc = a_layout == 0, b_kc = b_layout == 0;
+  const nmb::Plan p = nmb::plan_for(m, n, k, a_kc, b_kc);
+  const int64_t need = nmb::workspace_for(p, m, n);
+  NMB_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+              "gemm: workspace of %lld bytes needed, %lld given", (long long)need,
+              (long long)workspace_bytes);
+  NMB_REQUIRE(need == 0 || nmb::aligned16(workspace), "gemm: workspace must be 16-byte aligned");
+  const nmb::GemmArgs g = nmb::make_args(m, n, k, alpha, a, lda, b, ldb, beta, c, ldc, d, ldd, workspace, p);
   switch (p.config) {
     case 0: return nmb::dispatch_layout<256, 256, 8, 64>(a_kc, b_kc, g, stream);
     case 1: return nmb::dispatch_layout<256, 128, 8, 64>(a_kc, b_kc, g, stream);
     case 2: return nmb::dispatch_layout<128, 128, 4, 32>(a_kc, b_kc, g, stream);
     default: return nmb::dispatch_layout<128, 256, 4, 32>(a_kc, b_kc, g, stream);
   }
+}
+
+extern "C" int nmb_gemm_bf16_rope(int b_layout, int64_t m, int64_t n, int64_t k, const void* a,
+                                  int64_t lda, const void* b, int64_t ldb, void* d, int64_t ldd,
+                                  const float* cos_table, const float* sin_table, int64_t n_pos,
+                                  const int32_t* positions, int64_t pos_batch_stride,
+                                  int64_t pos_offset, int64_t seq, int64_t head_dim,
+                                  int64_t rope_cols, hipStream_t stream) {
+  const int st = nmb::check_gemm(0, b_layout, m, n, k, a, lda, b, ldb, false, nullptr, 0, d, ldd);
+  if (st != NMB_OK) return st;
+  NMB_REQUIRE(cos_table != nullptr && sin_table != nullptr && n_pos > 0 && n_pos < (1 << 30),
+              "gemm_rope: cos/sin tables of n_pos rows needed");
+  NMB_REQUIRE_SUPPORTED(head_dim == 64 || head_dim == 128, "gemm_rope: head_dim %lld (64 or 128 supported)",
+                        (long long)head_dim);
+  NMB_REQUIRE(rope_cols >= 0 && rope_cols <= n && rope_cols % head_dim == 0,
+              "gemm_rope: rope_cols %lld must be a multiple of head_dim within N", (long long)rope_cols);
+  NMB_REQUIRE(seq > 0 && seq < (1 << 30) && m % seq == 0, "gemm_rope: M (%lld) must be batch x seq (%lld)",
+              (long long)m, (long long)seq);
+  if (positions == nullptr) {
+    NMB_REQUIRE(pos_offset >= 0 && pos_offset + seq <= n_pos,
+                "gemm_rope: positions [%lld, %lld) exceed the cos/sin table of %lld rows",
+                (long long)pos_offset, (long long)(pos_offset + seq), (long long)n_pos);
+  } else {
+    NMB_REQUIRE(pos_batch_stride >= 0, "gemm_rope: negative position batch stride");
+  }
+  if (m == 0 || n == 0) return NMB_OK;
+  const nmb::Plan p = nmb::plan_for(m, n, k, true, b_layout == 0, static_cast<int>(head_dim));
+  nmb::GemmArgs g = nmb::make_args(m, n, k, 1.f, a, lda, b, ldb, 0.f, nullptr, 0, d, ldd, nullptr, p);
+  g.rope_cos = cos_table;
+  g.rope_sin = sin_table;
+  g.rope_pos = positions;
+  g.rope_pos_bstride = pos_batch_stride;
+  g.rope_offset = static_cast<int>(positions == nullptr ? pos_offset : 0);
+  g.rope_seq = static_cast<int>(seq);
+  g.rope_n_pos = static_cast<int>(n_pos);
+  g.rope_cols = static_cast<int>(rope_cols);
+  return head_dim == 64 ? nmb::dispatch_rope<64>(p.config, b_layout == 0, g, stream)
+                        : nmb::dispatch_rope<128>(p.config, b_layout == 0, g, stream);
 }

@@ -98,6 +98,44 @@ def mm(a: Tensor, b: Tensor, *, out: Tensor | None = None, c: Tensor | None = No
     return out
 
 
+def mm_rope(a: Tensor, b: Tensor, *, seq: int, head_dim: int, rope_cols: int, cos: Tensor,
+            sin: Tensor, pos_offset: int = 0, positions: Tensor | None = None) -> Tensor:
+    """``a @ b`` with RoPE applied to the first ``rope_cols`` output columns
+    (heads of ``head_dim``; row r is token (r // seq, r % seq)), as the Q/K/V
+    projection followed by the rotary embedding of q and k
+    (models/gpt/attention.py:172-181).  bf16 runs the fused GEMM epilogue
+    ``nmb_gemm_bf16_rope`` (heads of 64 or 128); otherwise the GEMM and then the
+    rotary kernel."""
+    m, k = a.shape
+    n = b.shape[1]
+    if rope_cols % head_dim or rope_cols > n or m % seq:
+        raise ValueError("mm_rope: rope_cols must be whole heads within N and M = batch x seq")
+    if a.dtype != torch.bfloat16 or head_dim not in (64, 128):
+        # the fused epilogue covers bf16 heads of 64 and 128; otherwise GEMM, then rotary kernel
+        out = mm(a, b)
+        x = out.view(m // seq, seq, n)[:, :, :rope_cols].unflatten(2, (rope_cols // head_dim, head_dim))
+        rope_apply(x, x, cos, sin, pos_offset=pos_offset, positions=positions)
+        return out
+    _require_gpu(a, b, cos, sin)
+    out = torch.empty(m, n, dtype=a.dtype, device=a.device)
+    la, lda = _operand_layout(a, 0)
+    if la != 0:
+        raise ValueError("mm_rope: a must be row-major")
+    lb_rowmajor, ldb = _operand_layout(b, 0)
+    pos_ptr, pos_bstride = None, 0
+    if positions is not None:
+        if positions.dtype != torch.int32:
+            raise ValueError("mm_rope: positions must be int32")
+        pos_ptr = positions.data_ptr()
+        pos_bstride = positions.stride(0) if positions.ndim == 2 else 0
+    _lib.call(
+        "nmb_gemm_bf16_rope", 1 - lb_rowmajor, m, n, k, a.data_ptr(), lda, b.data_ptr(), ldb,
+        out.data_ptr(), out.stride(0), cos.data_ptr(), sin.data_ptr(), cos.shape[0], pos_ptr,
+        pos_bstride, int(pos_offset), seq, head_dim, rope_cols, _lib.stream_of(a),
+    )
+    return out
+
+
 # ---------------------------------------------------------------- RMSNorm
 def rmsnorm_fwd(x2: Tensor, weight: Tensor, eps: float) -> Tensor:
     """y = RMSNorm(x2) for a contiguous [rows, hidden] tensor (nn/norms.py:38-41)."""

@@ -270,3 +270,44 @@ def test_gemm_bf16_matches_fp32_product(device, m, n, k, layout) -> None:
     out2 = Fn.mm(a, b)
     torch.testing.assert_close(out2.float(), a.float() @ b.float(), rtol=2e-2,
                                atol=2e-2 * float((a.float() @ b.float()).abs().max()))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("batch,seq,hq,hkv,d,offset,explicit", [
+    (4, 128, 4, 2, 64, 0, False),
+    (2, 256, 2, 1, 128, 0, True),
+    (3, 64, 4, 4, 64, 37, False),
+])
+def test_gemm_rope_equals_gemm_then_rope(device, batch, seq, hq, hkv, d, offset, explicit) -> None:
+    """nmb_gemm_bf16_rope == nmb_gemm_bf16 followed by the rotary kernel on q and k, bit for bit."""
+    import nano_megatron_amd as nm
+
+    g = torch.Generator(device=device).manual_seed(seq + d + offset)
+    bf = torch.bfloat16
+    hidden = 256
+    n = (hq + 2 * hkv) * d
+    x = torch.randn(batch * seq, hidden, device=device, generator=g).to(bf)
+    w = (0.05 * torch.randn(n, hidden, device=device, generator=g)).to(bf)
+    tab = nm.RotaryEmbedding(d).tables(device, 1024)
+    positions = None
+    if explicit:
+        positions = torch.stack([torch.randperm(1024, device=device, generator=g)[:seq] for _ in range(batch)])
+        positions = positions.to(torch.int32)
+    rope_cols = (hq + hkv) * d
+    fused = Fn.mm_rope(x, w.t(), seq=seq, head_dim=d, rope_cols=rope_cols, cos=tab.cos, sin=tab.sin,
+                       pos_offset=offset, positions=positions)
+    ref = Fn.mm(x, w.t())
+    qk = ref.view(batch, seq, n)[:, :, :rope_cols].unflatten(2, (hq + hkv, d))
+    Fn.rope_apply(qk, qk, tab.cos, tab.sin, pos_offset=offset, positions=positions)
+    assert torch.equal(fused, ref)
+    # and against the fp32 product, rotated in fp32 (tolerance of the bf16 roundings)
+    ref32 = (x.float() @ w.float().t()).view(batch, seq, n)
+    pos = positions.long() if positions is not None else (offset + torch.arange(seq, device=device)).expand(batch, seq)
+    inv = 1.0 / (1e4 ** (torch.arange(0, d, 2, device=device).float() / d))
+    f = pos[..., None].float() * inv
+    cos, sin = torch.cat([f, f], -1).cos()[:, :, None], torch.cat([f, f], -1).sin()[:, :, None]
+    q = ref32[:, :, :rope_cols].unflatten(2, (hq + hkv, d))
+    rot = torch.cat([-q[..., d // 2:], q[..., : d // 2]], -1)
+    exp = ref32.clone()
+    exp[:, :, :rope_cols] = (q * cos + rot * sin).flatten(2)
+    torch.testing.assert_close(fused.view(batch, seq, n).float(), exp, rtol=2e-2, atol=2e-2)
