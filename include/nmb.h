@@ -133,6 +133,22 @@ int nmb_attn_bwd(const void* q, const void* const* k_blocks, const void* const* 
                  const int64_t* q_strides, const int64_t* kv_strides, const int64_t* o_strides,
                  int causal, int64_t q_offset, float scale, int dtype, hipStream_t stream);
 
+/* nmb_attn_bwd for one K/V block that holds the queries' own tokens (the
+ * block's self-attention; reference models/gpt/attention.py:180-206) with the
+ * RoPE backward of q and k fused into the dQ / dK stores (replaces
+ * nmb_attn_bwd + two nmb_rope_apply(inverse = 1); nn/rotary.py:27-38): dq and
+ * dk come out rotated by -theta with the rotary kernel's roundings, bit for
+ * bit.  Token i's position is positions[b * pos_batch_stride + i] (int32,
+ * nullable) or pos_offset + i.  bf16 only; head_dim 64 or 128. */
+int nmb_attn_bwd_rope(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                      const float* lse, void* dq, void* dk, void* dv, void* workspace,
+                      size_t workspace_bytes, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                      int64_t seq, int64_t head_dim, const int64_t* q_strides,
+                      const int64_t* kv_strides, const int64_t* o_strides, int causal,
+                      int64_t q_offset, float scale, const float* cos_table, const float* sin_table,
+                      int64_t n_pos, const int32_t* positions, int64_t pos_batch_stride,
+                      int64_t pos_offset, hipStream_t stream);
+
 /* ------------------------------------------------------------ cross entropy
  * replaces _VocabParallelCrossEntropy.forward/backward at TP=1
  * (tensor_parallel/cross_entropy.py:30-86) applied to one chunk of tied

@@ -150,10 +150,10 @@ def block_backward(acts: dict, dy: Tensor, w: tuple[Tensor, ...], m: BlockMeta, 
     dq, dk, dv = _qkv_views(dqkv, b, s, m)
     o4 = o2.view(b, s, m.heads, m.head_dim)
     do4 = do2.view(b, s, m.heads, m.head_dim)
-    Fn.attn_bwd_bshd(q, [k], [v], (0,), o4, do4, lse, dq, [dk], [dv],
-                     causal=True, q_offset=m.sequence_offset, scale=None)
-    Fn.rope_apply(dq, dq, m.cos, m.sin, pos_offset=m.sequence_offset, positions=m.positions, inverse=True)
-    Fn.rope_apply(dk, dk, m.cos, m.sin, pos_offset=m.sequence_offset, positions=m.positions, inverse=True)
+    # attention backward with the RoPE backward of q and k fused into the dq/dk stores
+    Fn.attn_bwd_rope_bshd(q, k, v, o4, do4, lse, dq, dk, dv, causal=True, q_offset=m.sequence_offset,
+                          scale=None, cos=m.cos, sin=m.sin, pos_offset=m.sequence_offset,
+                          positions=m.positions)
     dn1 = Fn.mm(dqkv, joined((wq, wk, wv)))
     dwqkv = Fn.mm(dqkv.t(), n1)
     dx, dw_in = Fn.rmsnorm_bwd(x2, w_in, dn1, m.eps, residual_grad=dh)

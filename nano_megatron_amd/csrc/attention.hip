@@ -51,6 +51,37 @@ struct AttnShape {
   float scale_log2;  // scale * log2(e)
 };
 
+// The RoPE backward fused into the dQ / dK stores: the gradient of the
+// rotated q (k) is rotated by -theta (reference nn/rotary.py:27-38; the
+// transpose of rotate_half is -rotate_half), with the rotary kernel's
+// roundings, the position of local token index i being pos[b * pos_bstride + i]
+// or pos_offset + i.
+struct RopeGrad {
+  const float* cos;  // fp32 [n_pos, D/2]
+  const float* sin;
+  const int32_t* pos;
+  int64_t pos_bstride, pos_offset;
+  int n_pos;
+};
+
+// Rotation by -theta of the pair (x1, x2) = (g[d], g[d + D/2]) at table entry
+// (crow, srow)[d]; bad poisons (out-of-table position).
+__device__ __forceinline__ void rope_back(float x1, float x2, float cf, float sf, bool bad, bf16& o1, bf16& o2) {
+  const float c = round_as<bf16>(cf);
+  const float sn = -round_as<bf16>(sf);
+  float r1 = round_as<bf16>(add_rn(round_as<bf16>(mul_rn(x1, c)), round_as<bf16>(mul_rn(-x2, sn))));
+  float r2 = round_as<bf16>(add_rn(round_as<bf16>(mul_rn(x2, c)), round_as<bf16>(mul_rn(x1, sn))));
+  if (bad) r1 = r2 = __builtin_nanf("");
+  o1 = static_cast<bf16>(r1);
+  o2 = static_cast<bf16>(r2);
+}
+
+__device__ __forceinline__ int64_t rope_pos(const RopeGrad& rg, int b, int i, bool* bad) {
+  int64_t pos = rg.pos != nullptr ? static_cast<int64_t>(rg.pos[b * rg.pos_bstride + i]) : rg.pos_offset + i;
+  *bad = pos < 0 || pos >= rg.n_pos;
+  return *bad ? 0 : pos;
+}
+
 __device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
@@ -412,11 +443,11 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(const T* __restrict__ o
 // Same tiling as the forward (S^T = K Q^T per wave).  The prologue computes
 // delta = rowsum(dO * O) for the workgroup's queries from the registers that
 // hold dO and writes it for the dK/dV kernel, which runs next on the stream.
-template <int D>
+template <int D, bool ROPE>
 __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
     const bf16* __restrict__ q, KVBlocks kv, const bf16* __restrict__ o,
     const bf16* __restrict__ dout, const float* __restrict__ lse, float* __restrict__ delta,
-    bf16* __restrict__ dq, AttnShape p, int n_qt, int items, int per_xcd) {
+    bf16* __restrict__ dq, AttnShape p, int n_qt, int items, int per_xcd, RopeGrad rg) {
   constexpr int BQ = 128, BK = 64, KS = D / 32, DT = D / 16;
   constexpr int LDK = D + 8, LDT = BK + 4;
   __shared__ __attribute__((aligned(16))) bf16 sK[BK * LDK];
@@ -546,17 +577,38 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
       }
     }
   }
+  // lane holds dQ[q0 + 16 t + l16][d = 16 dt + 4 g + e]; d and d + D/2 are dt and dt + DT/2
   bf16* dqb = dq + b * p.q_sb + h * p.q_sh;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int qi = q0 + 16 * t + l16;
     if (qi >= p.Sq) continue;
+    if constexpr (ROPE) {
+      bool bad;
+      const int64_t pos = rope_pos(rg, b, qi, &bad);
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      bf16x4 wv;
+      for (int dt = 0; dt < DT / 2; ++dt) {
+        bf16x4 w1, w2;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) wv[e] = static_cast<bf16>(acc[t][dt][e] * p.scale);
-      *reinterpret_cast<bf16x4*>(dqb + static_cast<int64_t>(qi) * p.q_ss + dt * 16 + g * 4) = wv;
+        for (int e = 0; e < 4; ++e) {
+          const int d = dt * 16 + g * 4 + e;
+          bf16 r1, r2;
+          rope_back(round_as<bf16>(acc[t][dt][e] * p.scale), round_as<bf16>(acc[t][dt + DT / 2][e] * p.scale),
+                    rg.cos[pos * (D / 2) + d], rg.sin[pos * (D / 2) + d], bad, r1, r2);
+          w1[e] = r1;
+          w2[e] = r2;
+        }
+        *reinterpret_cast<bf16x4*>(dqb + static_cast<int64_t>(qi) * p.q_ss + dt * 16 + g * 4) = w1;
+        *reinterpret_cast<bf16x4*>(dqb + static_cast<int64_t>(qi) * p.q_ss + D / 2 + dt * 16 + g * 4) = w2;
+      }
+    } else {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        bf16x4 wv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) wv[e] = static_cast<bf16>(acc[t][dt][e] * p.scale);
+        *reinterpret_cast<bf16x4*>(dqb + static_cast<int64_t>(qi) * p.q_ss + dt * 16 + g * 4) = wv;
+      }
     }
   }
 }
@@ -568,11 +620,11 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
 // LDS feeds two MFMA tiles.  Loops over the query heads of the GQA group and
 // over the 64-query tiles that can see these keys, with the next Q/dO tile's
 // global reads in flight during the current tile's MFMA work.
-template <int D>
+template <int D, bool ROPE>
 __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
     const bf16* __restrict__ q, KVBlocks kv, const bf16* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, AttnShape p, int n_kt,
-    int items, int per_xcd) {
+    int items, int per_xcd, RopeGrad rg) {
   constexpr int BQ = 64, KT = 2, BKW = 64 * KT, KS = D / 32, DT = D / 16;
   constexpr int LDQ = D + 8, LDT = BQ + 4;
   __shared__ __attribute__((aligned(16))) bf16 sQ[BQ * LDQ];
@@ -749,11 +801,24 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
     for (int e = 0; e < 4; ++e) {
       const int key = kbase + 64 * j + g * 4 + e;
       if (key >= p.Sk) continue;
+      bf16* dkr = dkb + static_cast<int64_t>(key) * p.kv_ss;
+      if constexpr (ROPE) {
+        // d = 16 dt + l16 and d + D/2 are dt and dt + DT/2 (one K/V block: key = token index)
+        bool bad;
+        const int64_t pos = rope_pos(rg, b, key, &bad);
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        dkb[static_cast<int64_t>(key) * p.kv_ss + dt * 16 + l16] = static_cast<bf16>(dka[j][dt][e] * p.scale);
-        dvb[static_cast<int64_t>(key) * p.kv_ss + dt * 16 + l16] = static_cast<bf16>(dva[j][dt][e]);
+        for (int dt = 0; dt < DT / 2; ++dt) {
+          const int d = dt * 16 + l16;
+          rope_back(round_as<bf16>(dka[j][dt][e] * p.scale), round_as<bf16>(dka[j][dt + DT / 2][e] * p.scale),
+                    rg.cos[pos * (D / 2) + d], rg.sin[pos * (D / 2) + d], bad, dkr[d], dkr[d + D / 2]);
+        }
+      } else {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) dkr[dt * 16 + l16] = static_cast<bf16>(dka[j][dt][e] * p.scale);
       }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        dvb[static_cast<int64_t>(key) * p.kv_ss + dt * 16 + l16] = static_cast<bf16>(dva[j][dt][e]);
     }
 }
 
@@ -1027,7 +1092,10 @@ extern "C" int nmb_attn_bwd_workspace_bytes(int64_t batch, int64_t q_heads, int6
   return NMB_OK;
 }
 
-extern "C" int nmb_attn_bwd(const void* q, const void* const* k_blocks,
+namespace nmb {
+namespace {
+
+int attn_bwd_impl(const void* q, const void* const* k_blocks,
                             const void* const* v_blocks, const int64_t* k_offsets, int n_blocks,
                             const void* o, const void* dout, const float* lse, void* dq,
                             void* const* dk_blocks, void* const* dv_blocks, void* workspace,
@@ -1035,7 +1103,7 @@ extern "C" int nmb_attn_bwd(const void* q, const void* const* k_blocks,
                             int64_t kv_heads, int64_t seq_q, int64_t seq_k, int64_t head_dim,
                             const int64_t* q_strides, const int64_t* kv_strides,
                             const int64_t* o_strides, int causal, int64_t q_offset, float scale,
-                            int dtype, hipStream_t stream) {
+                            int dtype, hipStream_t stream, const RopeGrad* rope) {
   AttnShape p;
   KVBlocks kv;
   int st = nmb::fill_shape(&p, &kv, q, k_blocks, v_blocks, k_offsets, n_blocks, batch, q_heads,
@@ -1072,12 +1140,16 @@ extern "C" int nmb_attn_bwd(const void* q, const void* const* k_blocks,
       int per_xcd;
       unsigned blocks;
       xcd_grid(items, &per_xcd, &blocks);
-      if (D == 64)
-        hipLaunchKernelGGL(nmb::attn_bwd_dq_kernel<64>, dim3(blocks), dim3(256), 0, stream, qp, kv,
-                           opp, dp, lse, delta, dqp, p, n_qt, static_cast<int>(items), per_xcd);
-      else
-        hipLaunchKernelGGL(nmb::attn_bwd_dq_kernel<128>, dim3(blocks), dim3(256), 0, stream, qp,
-                           kv, opp, dp, lse, delta, dqp, p, n_qt, static_cast<int>(items), per_xcd);
+      const RopeGrad rg = rope != nullptr ? *rope : RopeGrad{};
+#define NMB_DQ(DD, RR)                                                                          \
+  hipLaunchKernelGGL((nmb::attn_bwd_dq_kernel<DD, RR>), dim3(blocks), dim3(256), 0, stream, qp, kv, \
+                     opp, dp, lse, delta, dqp, p, n_qt, static_cast<int>(items), per_xcd, rg)
+      if (D == 64) {
+        if (rope) NMB_DQ(64, true); else NMB_DQ(64, false);
+      } else {
+        if (rope) NMB_DQ(128, true); else NMB_DQ(128, false);
+      }
+#undef NMB_DQ
       NMB_CHECK_LAUNCH("attn_bwd(dq)");
     }
     if (seq_k > 0) {
@@ -1087,12 +1159,16 @@ extern "C" int nmb_attn_bwd(const void* q, const void* const* k_blocks,
       int per_xcd;
       unsigned blocks;
       xcd_grid(items, &per_xcd, &blocks);
-      if (D == 64)
-        hipLaunchKernelGGL(nmb::attn_bwd_dkdv_kernel<64>, dim3(blocks), dim3(256), 0, stream, qp,
-                           kv, dp, lse, delta, p, n_kt, static_cast<int>(items), per_xcd);
-      else
-        hipLaunchKernelGGL(nmb::attn_bwd_dkdv_kernel<128>, dim3(blocks), dim3(256), 0, stream, qp,
-                           kv, dp, lse, delta, p, n_kt, static_cast<int>(items), per_xcd);
+      const RopeGrad rg = rope != nullptr ? *rope : RopeGrad{};
+#define NMB_DKDV(DD, RR)                                                                          \
+  hipLaunchKernelGGL((nmb::attn_bwd_dkdv_kernel<DD, RR>), dim3(blocks), dim3(256), 0, stream, qp, kv, \
+                     dp, lse, delta, p, n_kt, static_cast<int>(items), per_xcd, rg)
+      if (D == 64) {
+        if (rope) NMB_DKDV(64, true); else NMB_DKDV(64, false);
+      } else {
+        if (rope) NMB_DKDV(128, true); else NMB_DKDV(128, false);
+      }
+#undef NMB_DKDV
       NMB_CHECK_LAUNCH("attn_bwd(dkdv)");
     }
   } else {
@@ -1123,4 +1199,56 @@ extern "C" int nmb_attn_bwd(const void* q, const void* const* k_blocks,
     }
   }
   return NMB_OK;
+}
+
+}  // namespace
+}  // namespace nmb
+
+extern "C" int nmb_attn_bwd(const void* q, const void* const* k_blocks,
+                            const void* const* v_blocks, const int64_t* k_offsets, int n_blocks,
+                            const void* o, const void* dout, const float* lse, void* dq,
+                            void* const* dk_blocks, void* const* dv_blocks, void* workspace,
+                            size_t workspace_bytes, int64_t batch, int64_t q_heads,
+                            int64_t kv_heads, int64_t seq_q, int64_t seq_k, int64_t head_dim,
+                            const int64_t* q_strides, const int64_t* kv_strides,
+                            const int64_t* o_strides, int causal, int64_t q_offset, float scale,
+                            int dtype, hipStream_t stream) {
+  return nmb::attn_bwd_impl(q, k_blocks, v_blocks, k_offsets, n_blocks, o, dout, lse, dq, dk_blocks,
+                            dv_blocks, workspace, workspace_bytes, batch, q_heads, kv_heads, seq_q,
+                            seq_k, head_dim, q_strides, kv_strides, o_strides, causal, q_offset,
+                            scale, dtype, stream, nullptr);
+}
+
+extern "C" int nmb_attn_bwd_rope(const void* q, const void* k, const void* v, const void* o,
+                                 const void* dout, const float* lse, void* dq, void* dk, void* dv,
+                                 void* workspace, size_t workspace_bytes, int64_t batch,
+                                 int64_t q_heads, int64_t kv_heads, int64_t seq, int64_t head_dim,
+                                 const int64_t* q_strides, const int64_t* kv_strides,
+                                 const int64_t* o_strides, int causal, int64_t q_offset,
+                                 float scale, const float* cos_table, const float* sin_table,
+                                 int64_t n_pos,
+                                 const int32_t* positions, int64_t pos_batch_stride,
+                                 int64_t pos_offset, hipStream_t stream) {
+  NMB_REQUIRE(cos_table != nullptr && sin_table != nullptr && n_pos > 0 && n_pos < (1 << 30),
+              "attn_bwd_rope: cos/sin tables of n_pos rows needed");
+  NMB_REQUIRE_SUPPORTED(head_dim == 64 || head_dim == 128, "attn_bwd_rope: head_dim %lld (64 or 128 supported)",
+                        (long long)head_dim);
+  if (positions == nullptr) {
+    NMB_REQUIRE(pos_offset >= 0 && pos_offset + seq <= n_pos,
+                "attn_bwd_rope: positions [%lld, %lld) exceed the cos/sin table of %lld rows",
+                (long long)pos_offset, (long long)(pos_offset + seq), (long long)n_pos);
+  } else {
+    NMB_REQUIRE(pos_batch_stride >= 0, "attn_bwd_rope: negative position batch stride");
+  }
+  const nmb::RopeGrad rg{cos_table, sin_table, positions, pos_batch_stride,
+                         positions == nullptr ? pos_offset : 0, static_cast<int>(n_pos)};
+  const void* kb[1] = {k};
+  const void* vb[1] = {v};
+  void* dkb[1] = {dk};
+  void* dvb[1] = {dv};
+  const int64_t koff[1] = {0};
+  // one K/V block whose keys are the queries' tokens (self-attention of the local sequence)
+  return nmb::attn_bwd_impl(q, kb, vb, koff, 1, o, dout, lse, dq, dkb, dvb, workspace,
+                            workspace_bytes, batch, q_heads, kv_heads, seq, seq, head_dim, q_strides,
+                            kv_strides, o_strides, causal, q_offset, scale, NMB_BF16, stream, &rg);
 }

@@ -495,6 +495,47 @@ def attn_bwd_bshd(
     )
 
 
+def attn_bwd_rope_bshd(q: Tensor, k: Tensor, v: Tensor, o: Tensor, do: Tensor, lse: Tensor,
+                       dq: Tensor, dk: Tensor, dv: Tensor, *, causal: bool, q_offset: int,
+                       scale: float | None, cos: Tensor, sin: Tensor, pos_offset: int = 0,
+                       positions: Tensor | None = None) -> None:
+    """attn_bwd_bshd of one K/V block (self-attention of the local sequence) with the
+    RoPE backward of q and k fused into the dq / dk stores: dq and dk come out
+    rotated by -theta, as attn_bwd_bshd followed by rope_apply(inverse=True)."""
+    if q.dtype != torch.bfloat16 or q.shape[3] not in (64, 128):
+        attn_bwd_bshd(q, [k], [v], (0,), o, do, lse, dq, [dk], [dv], causal=causal,
+                      q_offset=q_offset, scale=scale)
+        rope_apply(dq, dq, cos, sin, pos_offset=pos_offset, positions=positions, inverse=True)
+        rope_apply(dk, dk, cos, sin, pos_offset=pos_offset, positions=positions, inverse=True)
+        return
+    _require_gpu(q, o, do, lse, dq, cos, sin)
+    b, s, hq, d = q.shape
+    hkv = k.shape[2]
+    kv_strides = _eff_strides(k)
+    for t in (v, dk, dv):
+        if _eff_strides(t) != kv_strides or t.stride(3) != 1:
+            raise ValueError("attention backward: K, V, dK, dV must share one stride layout")
+    if _eff_strides(dq) != _eff_strides(q) or _eff_strides(do) != _eff_strides(o):
+        raise ValueError("attention backward: dq must match q's strides and dO must match O's")
+    pos_ptr, pos_bstride = None, 0
+    if positions is not None:
+        if positions.dtype != torch.int32:
+            raise ValueError("attention backward: positions must be int32")
+        pos_ptr = positions.data_ptr()
+        pos_bstride = positions.stride(0) if positions.ndim == 2 else 0
+    nbytes = _lib.ctypes.c_size_t(0)
+    _lib.call("nmb_attn_bwd_workspace_bytes", b, hq, s, _lib.ctypes.byref(nbytes))
+    ws = _workspace(nbytes.value, q.device)
+    _lib.call(
+        "nmb_attn_bwd_rope", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
+        lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws.numel(),
+        b, hq, hkv, s, d, _lib.i64x3(_eff_strides(q)), _lib.i64x3(kv_strides),
+        _lib.i64x3(_eff_strides(o)), 1 if causal else 0, int(q_offset),
+        float(scale) if scale else 0.0, cos.data_ptr(), sin.data_ptr(), cos.shape[0], pos_ptr,
+        pos_bstride, int(pos_offset), _lib.stream_of(q),
+    )
+
+
 class AttentionFunction(torch.autograd.Function):
     """Attention over K/V blocks for [B,H,S,D] tensors (views of [B,S,H,D] memory).
 

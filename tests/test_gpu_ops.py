@@ -311,3 +311,44 @@ def test_gemm_rope_equals_gemm_then_rope(device, batch, seq, hq, hkv, d, offset,
     exp = ref32.clone()
     exp[:, :, :rope_cols] = (q * cos + rot * sin).flatten(2)
     torch.testing.assert_close(fused.view(batch, seq, n).float(), exp, rtol=2e-2, atol=2e-2)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("batch,seq,hq,hkv,d,offset,explicit", [
+    (2, 256, 4, 4, 64, 0, False),
+    (2, 192, 4, 2, 64, 5, False),
+    (1, 128, 2, 1, 128, 0, True),
+])
+def test_attn_bwd_rope_equals_bwd_then_rope(device, batch, seq, hq, hkv, d, offset, explicit) -> None:
+    """nmb_attn_bwd_rope == nmb_attn_bwd followed by the inverse rotary kernel on dq and dk, bit for bit."""
+    import nano_megatron_amd as nm
+
+    g = torch.Generator(device=device).manual_seed(seq * d + offset)
+    bf = torch.bfloat16
+    qkv = torch.randn(batch, seq, (hq + 2 * hkv) * d, device=device, generator=g).to(bf)
+    q = qkv[:, :, : hq * d].unflatten(2, (hq, d))
+    k = qkv[:, :, hq * d : (hq + hkv) * d].unflatten(2, (hkv, d))
+    v = qkv[:, :, (hq + hkv) * d :].unflatten(2, (hkv, d))
+    o, lse = Fn.attn_fwd_bshd(q, [k], [v], (0,), causal=True, q_offset=offset, scale=None)
+    do = torch.randn(batch, seq, hq, d, device=device, generator=g).to(bf)
+    tab = nm.RotaryEmbedding(d).tables(device, 1024)
+    positions = None
+    if explicit:
+        positions = torch.stack([torch.randperm(1024, device=device, generator=g)[:seq] for _ in range(batch)])
+        positions = positions.to(torch.int32)
+    grads = []
+    for fused in (True, False):
+        dqkv = torch.empty_like(qkv)
+        dq = dqkv[:, :, : hq * d].unflatten(2, (hq, d))
+        dk = dqkv[:, :, hq * d : (hq + hkv) * d].unflatten(2, (hkv, d))
+        dv = dqkv[:, :, (hq + hkv) * d :].unflatten(2, (hkv, d))
+        if fused:
+            Fn.attn_bwd_rope_bshd(q, k, v, o, do, lse, dq, dk, dv, causal=True, q_offset=offset, scale=None,
+                                  cos=tab.cos, sin=tab.sin, pos_offset=offset, positions=positions)
+        else:
+            Fn.attn_bwd_bshd(q, [k], [v], (0,), o, do, lse, dq, [dk], [dv], causal=True, q_offset=offset,
+                             scale=None)
+            Fn.rope_apply(dq, dq, tab.cos, tab.sin, pos_offset=offset, positions=positions, inverse=True)
+            Fn.rope_apply(dk, dk, tab.cos, tab.sin, pos_offset=offset, positions=positions, inverse=True)
+        grads.append(dqkv)
+    assert torch.equal(grads[0], grads[1])
