@@ -32,6 +32,44 @@ __device__ __forceinline__ int find_tensor(const int64_t* __restrict__ offsets, 
   return lo;
 }
 
+// 8 consecutive elements as fp32 (16- or 32-byte aligned loads and stores).
+__device__ __forceinline__ void load8(const bf16* p, float* o) {
+  const bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = static_cast<float>(v[e]);
+}
+__device__ __forceinline__ void load8(const float* p, float* o) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+  const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    o[e] = a[e];
+    o[4 + e] = b[e];
+  }
+}
+__device__ __forceinline__ void store8(bf16* p, const float* v) {
+  bf16x8 w;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) w[e] = static_cast<bf16>(v[e]);
+  *reinterpret_cast<bf16x8*>(p) = w;
+}
+__device__ __forceinline__ void store8(float* p, const float* v) {
+  *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
+  *reinterpret_cast<f32x4*>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
+}
+
+// The part [a, b) of segment [lo, hi) that runs 8 elements at a time: a and b
+// multiples of 8 (the flat fp32 arrays are then 32-byte aligned) and the
+// tensor's own pointers 16-byte aligned at a; the rest runs element by element.
+template <typename T>
+__device__ __forceinline__ void vector_span(const T* base, int64_t lo, int64_t hi, int64_t* a, int64_t* b) {
+  int64_t va = (lo + 7) & ~int64_t{7};
+  int64_t vb = hi & ~int64_t{7};
+  if (vb < va || (reinterpret_cast<uintptr_t>(base + va) & 15) != 0) va = vb = hi;
+  *a = va;
+  *b = vb;
+}
+
 template <typename G>
 __global__ __launch_bounds__(256) void sumsq_kernel(const uint64_t* __restrict__ grads,
                                                     const int64_t* __restrict__ offsets, int n,
@@ -43,7 +81,19 @@ __global__ __launch_bounds__(256) void sumsq_kernel(const uint64_t* __restrict__
   for (int t = find_tensor(offsets, n, c0); t < n && offsets[t] < c1; ++t) {
     const int64_t lo = max(c0, offsets[t]), hi = min(c1, offsets[t + 1]);
     const G* g = reinterpret_cast<const G*>(grads[t]) - offsets[t];
-    for (int64_t i = lo + threadIdx.x; i < hi; i += 256) {
+    int64_t a, b;
+    vector_span(g, lo, hi, &a, &b);
+    for (int64_t i = a + 8 * threadIdx.x; i < b; i += 8 * 256) {
+      float v[8];
+      load8(g + i, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc += v[e] * v[e];
+    }
+    for (int64_t i = lo + threadIdx.x; i < a; i += 256) {
+      const float v = to_f32(g[i]);
+      acc += v * v;
+    }
+    for (int64_t i = b + threadIdx.x; i < hi; i += 256) {
       const float v = to_f32(g[i]);
       acc += v * v;
     }
@@ -77,6 +127,14 @@ struct AdamArgs {
   float lr, beta1, beta2, eps, weight_decay, step_size, inv_sqrt_bc2;
 };
 
+// One element of the update (the reference's formula and rounding order).
+__device__ __forceinline__ void adam_elem(float gv, float& m, float& v, float& w, float decay, const AdamArgs& a) {
+  m = a.beta1 * m + (1.f - a.beta1) * gv;
+  v = a.beta2 * v + (1.f - a.beta2) * gv * gv;
+  if (a.weight_decay != 0.f) w *= decay;
+  w -= a.step_size * m / (sqrtf(v) * a.inv_sqrt_bc2 + a.eps);
+}
+
 template <typename P, typename G>
 __global__ __launch_bounds__(256) void adamw_kernel(const uint64_t* __restrict__ params,
                                                     const uint64_t* __restrict__ grads,
@@ -94,13 +152,26 @@ __global__ __launch_bounds__(256) void adamw_kernel(const uint64_t* __restrict__
     const int64_t lo = max(c0, offsets[t]), hi = min(c1, offsets[t + 1]);
     const G* g = reinterpret_cast<const G*>(grads[t]) - offsets[t];
     P* p = reinterpret_cast<P*>(params[t]) - offsets[t];
+    int64_t va, vb;
+    vector_span(g, lo, hi, &va, &vb);
+    if ((reinterpret_cast<uintptr_t>(p + va) & 15) != 0) va = vb = hi;  // both tensors vector-aligned
+    for (int64_t i = va + 8 * threadIdx.x; i < vb; i += 8 * 256) {
+      float gv[8], m[8], v[8], w[8];
+      load8(g + i, gv);
+      load8(exp_avg + i, m);
+      load8(exp_avg_sq + i, v);
+      load8(master + i, w);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) adam_elem(gv[e] * coef, m[e], v[e], w[e], decay, a);
+      store8(exp_avg + i, m);
+      store8(exp_avg_sq + i, v);
+      store8(master + i, w);
+      store8(p + i, w);
+    }
     for (int64_t i = lo + threadIdx.x; i < hi; i += 256) {
-      const float gv = to_f32(g[i]) * coef;
-      const float m = a.beta1 * exp_avg[i] + (1.f - a.beta1) * gv;
-      const float v = a.beta2 * exp_avg_sq[i] + (1.f - a.beta2) * gv * gv;
-      float w = master[i];
-      if (a.weight_decay != 0.f) w *= decay;
-      w -= a.step_size * m / (sqrtf(v) * a.inv_sqrt_bc2 + a.eps);
+      if (i >= va && i < vb) continue;  // done above
+      float m = exp_avg[i], v = exp_avg_sq[i], w = master[i];
+      adam_elem(to_f32(g[i]) * coef, m, v, w, decay, a);
       exp_avg[i] = m;
       exp_avg_sq[i] = v;
       master[i] = w;
