@@ -316,13 +316,34 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void gemm_kernel(GemmArgs
 #pragma unroll
       for (int i = 0; i < TM; ++i) fa[ks][i] = fra.get(&sA[st][0], i, 32 * ks);
     }
-    if (kt + S - 1 < nk) issue(kt + S - 1);
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks)
+    if constexpr (KSTEPS == 2) {
+      // The wave issues in order and a full LDS queue stalls it, MFMAs
+      // included: let the step-0 MFMAs start after the step-0 reads and put one
+      // step-1 read between every two of them (scheduling hints only).
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma16(fb[ks][j], fa[ks][i], acc[i][j]);
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma16(fb[0][j], fa[0][i], acc[i][j]);
+      constexpr int R = TM + TN;
+      __builtin_amdgcn_sched_group_barrier(0x100, R, 0);  // step-0 LDS reads
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // two MFMAs
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one step-1 LDS read
+      }
+      if constexpr (TM * TN > 2 * R) __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - 2 * R, 0);
+      if (kt + S - 1 < nk) issue(kt + S - 1);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma16(fb[1][j], fa[1][i], acc[i][j]);
+    } else {
+      if (kt + S - 1 < nk) issue(kt + S - 1);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma16(fb[0][j], fa[0][i], acc[i][j]);
+    }
   }
 
   // acc[i][j][e] = D[m0 + wm + 16 i + l16][n0 + wn + 16 j + 4 q4 + e]
