@@ -48,10 +48,12 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-eager", action="store_true", help="skip the no-checkpoint comparison run")
     p.add_argument("--only-kernels", action="store_true", help="time the kernels only (for profiling)")
     p.add_argument("--kernel", default=None, help="with --only-kernels: time just this kernel")
+    p.add_argument("--metrics-jsonl", default=None,
+                   help="append the timed interval as one train record of the reference's metric history")
     return p.parse_args()
 
 
-def run_steps(mode: str, steps: int, warmup: int, device) -> dict:
+def run_steps(mode: str, steps: int, warmup: int, device, metrics_jsonl: str | None = None) -> dict:
     import torch
 
     import nano_megatron_amd as nm
@@ -101,6 +103,16 @@ def run_steps(mode: str, steps: int, warmup: int, device) -> dict:
         loss = step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    if metrics_jsonl:
+        from nano_megatron_amd import metrics as M
+
+        m = M.train_metrics(loss=float(loss.item()), learning_rate=3e-4, samples=BATCH * steps,
+                            tokens=BATCH * SEQ * steps, seconds=elapsed,
+                            grad_norm=float(opt.last_grad_norm), device=device)
+        with open(metrics_jsonl, "a") as f:
+            f.write(M.history_line(sequence=0, step=warmup + 1 + steps, prefix="train", metrics=m,
+                                   consumed_samples=BATCH * (warmup + 1 + steps),
+                                   consumed_tokens=BATCH * SEQ * (warmup + 1 + steps)) + "\n")
     result = dict(
         ms_per_step=1e3 * elapsed / steps,
         tokens_per_s=BATCH * SEQ * steps / elapsed,
@@ -348,7 +360,7 @@ def main() -> None:
         if args.kernel:
             copy_calibration(device)
         return
-    full = run_steps("full", args.steps, args.warmup, device)
+    full = run_steps("full", args.steps, args.warmup, device, args.metrics_jsonl)
     print("full: " + json.dumps(full), file=sys.stderr, flush=True)
     eager = None
     if not args.no_eager:
