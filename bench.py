@@ -210,6 +210,8 @@ def kernel_rooflines(device, only: str | None = None) -> list[dict]:
         ("swiglu_bwd", lambda: Fn.swiglu_bwd(gate, up, dh, dgu[:, :F], dgu[:, F:], act), 6 * T * F * E, 0, "hbm", L),
         ("attn_fwd", lambda: Fn.attn_fwd_bshd(q, [k], [v], (0,), causal=True, q_offset=0, scale=None, out=o, lse=lse),
          4 * T * H * E + BATCH * nh * SEQ * 4, causal_flops, "hbm", 2 * L),
+        ("attn_fwd_from_lse", lambda: Fn.attn_fwd_from_lse_bshd(q, [k], [v], (0,), lse, causal=True, q_offset=0, scale=None, out=o),
+         4 * T * H * E + BATCH * nh * SEQ * 4, causal_flops, "hbm", 0),
         ("attn_bwd", lambda: Fn.attn_bwd_bshd(q, [k], [v], (0,), o, do, lse, dq, [dk], [dv], causal=True, q_offset=0, scale=None),
          8 * T * H * E + BATCH * nh * SEQ * 4, 2.5 * causal_flops, "hbm", L),
         ("ce_fwd", lambda: Fn.ce_fwd(logits, targets, -100, loss, lse_c), chunk * V * E + chunk * 16, 0, "hbm", T // chunk),

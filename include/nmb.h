@@ -120,6 +120,20 @@ int nmb_attn_fwd(const void* q, const void* const* k_blocks, const void* const* 
                  const int64_t* o_strides, int causal, int64_t q_offset, float scale, int dtype,
                  hipStream_t stream);
 
+/* The forward's output recomputed from its saved LSE (the reference
+ * recomputes attention in the checkpointed backward, nn/activation_checkpoint.py:
+ * 73-100 / context_parallel/ring.py:169-250 recompute P from the LSE): with the
+ * softmax statistics known, P = exp(S - lse) directly, no running maximum or
+ * rescale; o = P V.  Same arguments as nmb_attn_fwd, lse read.  Equal to the
+ * forward's o within bf16 rounding (not bit for bit: the forward normalises
+ * at the end).  bf16 only. */
+int nmb_attn_fwd_from_lse(const void* q, const void* const* k_blocks, const void* const* v_blocks,
+                          const int64_t* k_offsets, int n_blocks, const float* lse, void* o,
+                          int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                          int64_t seq_k, int64_t head_dim, const int64_t* q_strides,
+                          const int64_t* kv_strides, const int64_t* o_strides, int causal,
+                          int64_t q_offset, float scale, int dtype, hipStream_t stream);
+
 /* Bytes of workspace nmb_attn_bwd needs (the fp32 delta = rowsum(dO * O)). */
 int nmb_attn_bwd_workspace_bytes(int64_t batch, int64_t q_heads, int64_t seq_q, size_t* bytes);
 

@@ -51,6 +51,10 @@ SIGNATURES: dict[str, list] = {
         _p, _p, _p, _pi64, _i32, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
         _pi64, _pi64, _pi64, _i32, _i64, _f32, _i32, _p,
     ],
+    "nmb_attn_fwd_from_lse": [
+        _p, _p, _p, _pi64, _i32, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
+        _pi64, _pi64, _pi64, _i32, _i64, _f32, _i32, _p,
+    ],
     "nmb_attn_bwd_workspace_bytes": [_i64, _i64, _i64, _psz],
     "nmb_attn_bwd": [
         _p, _p, _p, _pi64, _i32, _p, _p, _p, _p, _p, _p, _p, _sz, _i64, _i64, _i64, _i64, _i64,

@@ -245,7 +245,16 @@ __device__ __forceinline__ int mask_limit(const AttnShape& p, int64_t koff, int 
 // through LDS in 64-key tiles; the next tile's global reads are issued before
 // the current tile's MFMA work.  Scores stay raw; exp2(s * c - m * c) folds
 // the softmax scale into one FMA per score.
-template <int D, int TQ>
+// log2-domain lse for P = exp2(S * scale_log2 - lse2); a query with no visible
+// key (lse = -inf) maps to +inf so that every P of its row is 0.
+__device__ __forceinline__ float lse_to_log2(float v) {
+  return v == -__builtin_inff() ? __builtin_inff() : v * kLog2e;
+}
+
+// FL (from LSE): the softmax statistics are given (lse read, not written), so
+// P = exp2(S * scale_log2 - lse2) directly: no running maximum, rescale or
+// row sum, and O = P V needs no final division.
+template <int D, int TQ, bool FL>
 __global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_kernel(
     const bf16* __restrict__ q, KVBlocks kv, bf16* __restrict__ o, float* __restrict__ lse,
     AttnShape p, int n_qt, int items, int per_xcd) {
@@ -280,6 +289,12 @@ __global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_ke
   for (int t = 0; t < TQ; ++t) {
     m[t] = -__builtin_inff();
     l[t] = 0.f;
+    if constexpr (FL) {
+      // m holds lse2 of this lane's query (+inf for a query past the end)
+      const int qi = qbase + 64 * t + l16;
+      m[t] = qi < p.Sq ? lse_to_log2(lse[(static_cast<int64_t>(b) * p.Hq + h) * p.Sq + qi])
+                       : __builtin_inff();
+    }
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
@@ -353,32 +368,39 @@ __global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_ke
             s[mk][e] = (mk * 16 + g * 4 + e > lim) ? -__builtin_inff() : sv;
           }
       }
+      if constexpr (FL) {
 #pragma unroll
-      for (int mk = 0; mk < 4; ++mk)
+        for (int mk = 0; mk < 4; ++mk)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) tmax = fmaxf(tmax, s[mk][e]);
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const float mnew = fmaxf(m[t], tmax);
-      const bool dead = mnew == -__builtin_inff();
-      const float alpha = dead ? 1.f : fast_exp2((m[t] - mnew) * c);
-      const float mc = dead ? 0.f : mnew * c;
-      float rs = 0.f;
+          for (int e = 0; e < 4; ++e) s[mk][e] = fast_exp2(fmaf(s[mk][e], c, -m[t]));
+      } else {
 #pragma unroll
-      for (int mk = 0; mk < 4; ++mk)
+        for (int mk = 0; mk < 4; ++mk)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float pv = fast_exp2(fmaf(s[mk][e], c, -mc));
-          s[mk][e] = pv;
-          rs += pv;
+          for (int e = 0; e < 4; ++e) tmax = fmaxf(tmax, s[mk][e]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float mnew = fmaxf(m[t], tmax);
+        const bool dead = mnew == -__builtin_inff();
+        const float alpha = dead ? 1.f : fast_exp2((m[t] - mnew) * c);
+        const float mc = dead ? 0.f : mnew * c;
+        float rs = 0.f;
+#pragma unroll
+        for (int mk = 0; mk < 4; ++mk)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float pv = fast_exp2(fmaf(s[mk][e], c, -mc));
+            s[mk][e] = pv;
+            rs += pv;
+          }
+        rs += __shfl_xor(rs, 16, 64);
+        rs += __shfl_xor(rs, 32, 64);
+        l[t] = l[t] * alpha + rs;
+        m[t] = mnew;
+        if (__any(alpha != 1.f)) {  // wave-uniform: skip the rescale when no max moved
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) acc[t][dt] *= alpha;
         }
-      rs += __shfl_xor(rs, 16, 64);
-      rs += __shfl_xor(rs, 32, 64);
-      l[t] = l[t] * alpha + rs;
-      m[t] = mnew;
-      if (__any(alpha != 1.f)) {  // wave-uniform: skip the rescale when no max moved
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[t][dt] *= alpha;
       }
       bf16x8 pf[2];
 #pragma unroll
@@ -400,7 +422,7 @@ __global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_ke
   for (int t = 0; t < TQ; ++t) {
     const int qi = qbase + 64 * t + l16;
     if (qi >= p.Sq) continue;
-    const float inv = l[t] > 0.f ? 1.f / l[t] : 0.f;
+    const float inv = FL ? 1.f : (l[t] > 0.f ? 1.f / l[t] : 0.f);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       bf16x4 wv;
@@ -408,14 +430,8 @@ __global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_ke
       for (int e = 0; e < 4; ++e) wv[e] = static_cast<bf16>(acc[t][dt][e] * inv);
       *reinterpret_cast<bf16x4*>(ob + static_cast<int64_t>(qi) * p.o_ss + dt * 16 + g * 4) = wv;
     }
-    if (g == 0) lb[qi] = l[t] > 0.f ? (m[t] * c + log2f(l[t])) * kLn2 : -__builtin_inff();
+    if (!FL && g == 0) lb[qi] = l[t] > 0.f ? (m[t] * c + log2f(l[t])) * kLn2 : -__builtin_inff();
   }
-}
-
-// log2-domain lse for P = exp2(S * scale_log2 - lse2); a query with no visible
-// key (lse = -inf) maps to +inf so that every P of its row is 0.
-__device__ __forceinline__ float lse_to_log2(float v) {
-  return v == -__builtin_inff() ? __builtin_inff() : v * kLog2e;
 }
 
 // ---------------------------------------------------------------- delta (fp32 path)
@@ -1040,7 +1056,10 @@ void xcd_grid(int64_t items, int* per_xcd, unsigned* blocks) {
 }
 }  // namespace
 
-extern "C" int nmb_attn_fwd(const void* q, const void* const* k_blocks,
+namespace nmb {
+namespace {
+
+int attn_fwd_impl(bool from_lse, const void* q, const void* const* k_blocks,
                             const void* const* v_blocks, const int64_t* k_offsets, int n_blocks,
                             void* o, float* lse, int64_t batch, int64_t q_heads, int64_t kv_heads,
                             int64_t seq_q, int64_t seq_k, int64_t head_dim,
@@ -1067,13 +1086,17 @@ extern "C" int nmb_attn_fwd(const void* q, const void* const* k_blocks,
     xcd_grid(items, &per_xcd, &blocks);
     const nmb::bf16* qp = static_cast<const nmb::bf16*>(q);
     nmb::bf16* op = static_cast<nmb::bf16*>(o);
-    if (head_dim == 64)
-      hipLaunchKernelGGL((nmb::attn_fwd_kernel<64, 4>), dim3(blocks), dim3(256), 0, stream, qp, kv,
-                         op, lse, p, n_qt, static_cast<int>(items), per_xcd);
-    else
-      hipLaunchKernelGGL((nmb::attn_fwd_kernel<128, 2>), dim3(blocks), dim3(256), 0, stream, qp, kv,
-                         op, lse, p, n_qt, static_cast<int>(items), per_xcd);
+#define NMB_FWD(DD, TT, FF)                                                                        \
+  hipLaunchKernelGGL((nmb::attn_fwd_kernel<DD, TT, FF>), dim3(blocks), dim3(256), 0, stream, qp, kv, \
+                     op, lse, p, n_qt, static_cast<int>(items), per_xcd)
+    if (head_dim == 64) {
+      if (from_lse) NMB_FWD(64, 4, true); else NMB_FWD(64, 4, false);
+    } else {
+      if (from_lse) NMB_FWD(128, 2, true); else NMB_FWD(128, 2, false);
+    }
+#undef NMB_FWD
   } else {
+    NMB_REQUIRE_SUPPORTED(!from_lse, "attn_fwd_from_lse: bf16 only");
     const dim3 grid(static_cast<unsigned>(seq_q), static_cast<unsigned>(q_heads),
                     static_cast<unsigned>(batch));
     hipLaunchKernelGGL(nmb::attn_fwd_f32_kernel, grid, dim3(64), 0, stream,
@@ -1082,6 +1105,36 @@ extern "C" int nmb_attn_fwd(const void* q, const void* const* k_blocks,
   }
   NMB_CHECK_LAUNCH("attn_fwd");
   return NMB_OK;
+}
+
+}  // namespace
+}  // namespace nmb
+
+extern "C" int nmb_attn_fwd(const void* q, const void* const* k_blocks,
+                            const void* const* v_blocks, const int64_t* k_offsets, int n_blocks,
+                            void* o, float* lse, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                            int64_t seq_q, int64_t seq_k, int64_t head_dim,
+                            const int64_t* q_strides, const int64_t* kv_strides,
+                            const int64_t* o_strides, int causal, int64_t q_offset, float scale,
+                            int dtype, hipStream_t stream) {
+  return nmb::attn_fwd_impl(false, q, k_blocks, v_blocks, k_offsets, n_blocks, o, lse, batch, q_heads,
+                            kv_heads, seq_q, seq_k, head_dim, q_strides, kv_strides, o_strides, causal,
+                            q_offset, scale, dtype, stream);
+}
+
+extern "C" int nmb_attn_fwd_from_lse(const void* q, const void* const* k_blocks,
+                                     const void* const* v_blocks, const int64_t* k_offsets,
+                                     int n_blocks, const float* lse, void* o, int64_t batch,
+                                     int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                                     int64_t seq_k, int64_t head_dim, const int64_t* q_strides,
+                                     const int64_t* kv_strides, const int64_t* o_strides,
+                                     int causal, int64_t q_offset, float scale, int dtype,
+                                     hipStream_t stream) {
+  // the kernel only reads lse in this mode
+  return nmb::attn_fwd_impl(true, q, k_blocks, v_blocks, k_offsets, n_blocks, o,
+                            const_cast<float*>(lse), batch, q_heads, kv_heads, seq_q, seq_k,
+                            head_dim, q_strides, kv_strides, o_strides, causal, q_offset, scale,
+                            dtype, stream);
 }
 
 extern "C" int nmb_attn_bwd_workspace_bytes(int64_t batch, int64_t q_heads, int64_t seq_q,

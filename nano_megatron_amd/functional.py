@@ -454,6 +454,36 @@ def attn_fwd_bshd(
     return out, lse
 
 
+def attn_fwd_from_lse_bshd(q: Tensor, ks: Sequence[Tensor], vs: Sequence[Tensor],
+                           k_offsets: Sequence[int], lse: Tensor, *, causal: bool, q_offset: int,
+                           scale: float | None, out: Tensor | None = None) -> Tensor:
+    """The attention output recomputed from a saved lse [B,Hq,S] (bf16):
+    P = exp(S - lse) without the online max/rescale; equal to attn_fwd_bshd's
+    output within bf16 rounding."""
+    _require_gpu(q, *ks, *vs, lse)
+    b, sq, hq, d = q.shape
+    _, sk, hkv, _ = ks[0].shape
+    if out is None:
+        out = torch.empty(b, sq, hq, d, dtype=q.dtype, device=q.device)
+    if lse.shape != (b, hq, sq) or lse.dtype != torch.float32 or not lse.is_contiguous():
+        raise ValueError("attention: lse must be a contiguous fp32 [B, Hq, S] tensor")
+    kv_strides = _eff_strides(ks[0])
+    for t in (*ks, *vs):
+        if _eff_strides(t) != kv_strides or t.stride(3) != 1:
+            raise ValueError("attention: all K/V blocks must share one [B,S,H,D] stride layout")
+    if q.stride(3) != 1 or out.stride(3) != 1:
+        raise ValueError("attention: head_dim must be the contiguous dimension")
+    _lib.call(
+        "nmb_attn_fwd_from_lse", q.data_ptr(), _lib.ptr_array(k.data_ptr() for k in ks),
+        _lib.ptr_array(v.data_ptr() for v in vs), _lib.i64_array(k_offsets), len(ks),
+        lse.data_ptr(), out.data_ptr(), b, hq, hkv, sq, sk, d,
+        _lib.i64x3(_eff_strides(q)), _lib.i64x3(kv_strides), _lib.i64x3(_eff_strides(out)),
+        1 if causal else 0, int(q_offset), float(scale) if scale else 0.0,
+        _lib.dtype_code(q.dtype), _lib.stream_of(q),
+    )
+    return out
+
+
 def attn_bwd_bshd(
     q: Tensor,
     ks: Sequence[Tensor],

@@ -352,3 +352,25 @@ def test_attn_bwd_rope_equals_bwd_then_rope(device, batch, seq, hq, hkv, d, offs
             Fn.rope_apply(dk, dk, tab.cos, tab.sin, pos_offset=offset, positions=positions, inverse=True)
         grads.append(dqkv)
     assert torch.equal(grads[0], grads[1])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b,s,hq,hkv,d,causal,blocks", [
+    (2, 512, 4, 4, 64, True, 1),
+    (1, 300, 8, 2, 64, True, 1),
+    (2, 256, 4, 4, 64, False, 1),
+    (1, 256, 2, 2, 128, True, 1),
+    (1, 128, 2, 1, 128, True, 3),
+])
+def test_attn_fwd_from_lse_matches_forward(device, b, s, hq, hkv, d, causal, blocks) -> None:
+    """O recomputed from the saved LSE equals the forward's O (bf16 tolerance)."""
+    g = torch.Generator(device=device).manual_seed(s + d + blocks)
+    bf = torch.bfloat16
+    q = torch.randn(b, s, hq, d, device=device, generator=g).to(bf)
+    ks = [torch.randn(b, s, hkv, d, device=device, generator=g).to(bf) for _ in range(blocks)]
+    vs = [torch.randn(b, s, hkv, d, device=device, generator=g).to(bf) for _ in range(blocks)]
+    offs = tuple(i * s for i in range(blocks))
+    q_offset = (blocks - 1) * s
+    o, lse = Fn.attn_fwd_bshd(q, ks, vs, offs, causal=causal, q_offset=q_offset, scale=None)
+    o2 = Fn.attn_fwd_from_lse_bshd(q, ks, vs, offs, lse, causal=causal, q_offset=q_offset, scale=None)
+    torch.testing.assert_close(o2.float(), o.float(), rtol=2e-2, atol=1e-2)
