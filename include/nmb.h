@@ -163,6 +163,21 @@ int nmb_attn_bwd_rope(const void* q, const void* k, const void* v, const void* o
                       int64_t n_pos, const int32_t* positions, int64_t pos_batch_stride,
                       int64_t pos_offset, hipStream_t stream);
 
+/* ------------------------------------------------------------ embedding
+ * replaces VocabParallelEmbedding.forward at TP=1 (tensor_parallel/
+ * embedding.py:60-74, F.embedding) and its backward.
+ * table / out / dout / grads: row-major [vocab, hidden] and [n_tokens, hidden]
+ * of dtype; ids: int64 [n_tokens].  An id outside [0, vocab) gives a NaN row.
+ * Backward: grad_out = grad_in + sum over tokens of dout rows (fp32 sums in
+ * token order, rounded to dtype, then added to grad_in, as autograd adds the
+ * tied LM head's gradient: models/gpt/model.py:125-142); grad_in may be null
+ * (then 0) and may alias grad_out.  Deterministic (no atomics). */
+int nmb_embedding_fwd(const void* table, const int64_t* ids, void* out, int64_t n_tokens,
+                      int64_t vocab, int64_t hidden, int dtype, hipStream_t stream);
+int nmb_embedding_bwd(const void* dout, const int64_t* ids, const void* grad_in, void* grad_out,
+                      int64_t n_tokens, int64_t vocab, int64_t hidden, int dtype,
+                      hipStream_t stream);
+
 /* ------------------------------------------------------------ cross entropy
  * replaces _VocabParallelCrossEntropy.forward/backward at TP=1
  * (tensor_parallel/cross_entropy.py:30-86) applied to one chunk of tied

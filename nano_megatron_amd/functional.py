@@ -669,6 +669,59 @@ def _chunks(rows: int, chunk: int):
         yield start, min(rows, start + chunk)
 
 
+# ---------------------------------------------------------------- embedding
+class TiedGrad:
+    """Hands the tied LM head's table gradient to the embedding's backward,
+    which adds it to its own in the same pass (models/gpt/model.py:125-142:
+    one weight shared by VocabParallelEmbedding and VocabParallelLinear).  The
+    LM head's backward always runs first: the embedding output feeds every
+    layer before the head."""
+
+    __slots__ = ("grad",)
+
+    def __init__(self) -> None:
+        self.grad: Tensor | None = None
+
+
+class EmbeddingFunction(torch.autograd.Function):
+    """Row gather of the [V, H] table (tensor_parallel/embedding.py:60-74 at TP=1)
+    and its deterministic scatter-add backward, merged with the tied LM-head
+    gradient when a ``TiedGrad`` carries it."""
+
+    @staticmethod
+    def forward(ctx: Any, weight: Tensor, ids: Tensor, tie: TiedGrad | None) -> Tensor:
+        _require_gpu(weight, ids)
+        vocab, hidden = weight.shape
+        out = torch.empty(*ids.shape, hidden, dtype=weight.dtype, device=weight.device)
+        _lib.call("nmb_embedding_fwd", weight.data_ptr(), ids.data_ptr(), out.data_ptr(), ids.numel(),
+                  vocab, hidden, _lib.dtype_code(weight.dtype), _lib.stream_of(weight))
+        ctx.save_for_backward(ids)
+        ctx.shape = (vocab, hidden, weight.dtype)
+        ctx.tie = tie
+        return out
+
+    @staticmethod
+    def backward(ctx: Any, dout: Tensor):
+        (ids,) = ctx.saved_tensors
+        vocab, hidden, dtype = ctx.shape
+        dout = dout.to(dtype).contiguous()
+        grad_in = None
+        if ctx.tie is not None:
+            grad_in, ctx.tie.grad = ctx.tie.grad, None
+        grad = torch.empty(vocab, hidden, dtype=dtype, device=dout.device)
+        _lib.call("nmb_embedding_bwd", dout.data_ptr(), ids.data_ptr(), _lib.ptr(grad_in), grad.data_ptr(),
+                  ids.numel(), vocab, hidden, _lib.dtype_code(dtype), _lib.stream_of(dout))
+        return grad, None, None
+
+
+def embedding(weight: Tensor, ids: Tensor, tie: TiedGrad | None = None) -> Tensor:
+    """``F.embedding(ids, weight)`` on the GPU kernels (an id outside the table
+    yields a NaN row)."""
+    if ids.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"input_ids must be an integer tensor, got {ids.dtype}")
+    return EmbeddingFunction.apply(weight, ids.to(torch.int64).contiguous(), tie)
+
+
 class LMHeadCrossEntropyFunction(torch.autograd.Function):
     """Tied LM head + token cross entropy without full logits.
 
@@ -683,7 +736,7 @@ class LMHeadCrossEntropyFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx: Any, x2: Tensor, weight: Tensor, targets: Tensor, ignore_index: int,
-                chunk: int) -> Tensor:
+                chunk: int, tie: TiedGrad | None = None) -> Tensor:
         _require_gpu(x2, weight, targets)
         rows = x2.shape[0]
         loss = torch.empty(rows, dtype=torch.float32, device=x2.device)
@@ -696,6 +749,7 @@ class LMHeadCrossEntropyFunction(torch.autograd.Function):
         ctx.save_for_backward(x2, weight, targets, lse)
         ctx.ignore_index = ignore_index
         ctx.chunk = chunk
+        ctx.tie = tie
         return loss
 
     @staticmethod
@@ -713,7 +767,10 @@ class LMHeadCrossEntropyFunction(torch.autograd.Function):
             ce_bwd_(g, targets[s:e], ctx.ignore_index, lse[s:e], grad_loss[s:e])
             mm(g, weight, out=dx[s:e])
             mm(g.t(), x2[s:e], out=dw, c=dw, beta=1.0)
-        return dx, dw, None, None, None
+        if ctx.tie is not None:  # the embedding's backward adds it to its own gradient
+            ctx.tie.grad = dw
+            return dx, None, None, None, None, None
+        return dx, dw, None, None, None, None
 
 
 def lm_head_cross_entropy(
@@ -725,6 +782,7 @@ def lm_head_cross_entropy(
     reduction: str = "mean",
     chunk: int = 2048,
     validate: bool = True,
+    tie: TiedGrad | None = None,
 ) -> Tensor:
     """Loss of ``F.linear(hidden, weight)`` under VocabParallelCrossEntropy
     (tensor_parallel/cross_entropy.py:89-123) without materialising logits."""
@@ -742,7 +800,7 @@ def lm_head_cross_entropy(
             raise ValueError("targets contain ids outside the original (unpadded) vocabulary")
     x2 = hidden.reshape(-1, hidden.shape[-1]).contiguous()
     t1 = targets.reshape(-1).to(torch.int64).contiguous()
-    loss = LMHeadCrossEntropyFunction.apply(x2, weight, t1, int(ignore_index), int(chunk))
+    loss = LMHeadCrossEntropyFunction.apply(x2, weight, t1, int(ignore_index), int(chunk), tie)
     if reduction == "none":
         return loss.view(targets.shape)
     if reduction == "sum":

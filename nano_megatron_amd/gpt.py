@@ -145,10 +145,8 @@ class VocabParallelEmbedding(nn.Module):
         self.weight = nn.Parameter(torch.empty(vocab_size, hidden_size, device=device, dtype=dtype))
         nn.init.normal_(self.weight, mean=0.0, std=init_std)
 
-    def forward(self, input_ids: Tensor) -> Tensor:
-        if input_ids.dtype not in (torch.int32, torch.int64):
-            raise TypeError(f"input_ids must be an integer tensor, got {input_ids.dtype}")
-        return F.embedding(input_ids, self.weight)
+    def forward(self, input_ids: Tensor, *, tie: "Fn.TiedGrad | None" = None) -> Tensor:
+        return Fn.embedding(self.weight, input_ids, tie)
 
 
 class VocabParallelLinear(nn.Module):
@@ -534,10 +532,15 @@ class GPTModel(nn.Module):
     def forward(self, input_ids: Tensor | None = None, *, labels: Tensor | None = None,
                 position_ids: Tensor | None = None, hidden_states: Tensor | None = None,
                 microbatch_index: int = 0) -> GPTOutput:
+        # the tied LM head passes its table gradient to the embedding's backward
+        tie = None
+        if (labels is not None and self.embedding is not None and self.lm_head is not None
+                and self.lm_head.weight is self.embedding.weight and torch.is_grad_enabled()):
+            tie = Fn.TiedGrad()
         if self.embedding is not None:
             if input_ids is None:
                 raise ValueError("the first pipeline stage requires input_ids")
-            hidden_states = self.embedding(input_ids)
+            hidden_states = self.embedding(input_ids, tie=tie)
         elif hidden_states is None:
             raise ValueError("a non-first pipeline stage requires hidden_states")
         Fn._require_gpu(hidden_states)
@@ -581,7 +584,7 @@ class GPTModel(nn.Module):
             if self.lm_head is None:
                 raise ValueError("labels may only be supplied to a stage that owns the LM head")
             loss = Fn.lm_head_cross_entropy(hidden_states, self.lm_head.weight, labels,
-                                            reduction="mean", chunk=self.ce_chunk)
+                                            reduction="mean", chunk=self.ce_chunk, tie=tie)
         elif self.lm_head is not None:
             logits = self.lm_head(hidden_states)
         return GPTOutput(logits=logits, loss=loss, hidden_states=hidden_states)

@@ -374,3 +374,53 @@ def test_attn_fwd_from_lse_matches_forward(device, b, s, hq, hkv, d, causal, blo
     o, lse = Fn.attn_fwd_bshd(q, ks, vs, offs, causal=causal, q_offset=q_offset, scale=None)
     o2 = Fn.attn_fwd_from_lse_bshd(q, ks, vs, offs, lse, causal=causal, q_offset=q_offset, scale=None)
     torch.testing.assert_close(o2.float(), o.float(), rtol=2e-2, atol=1e-2)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("vocab,hidden,tokens", [(1000, 256, 4096), (8192, 1024, 8192), (37, 1088, 300)])
+def test_embedding_matches_torch(device, dtype, vocab, hidden, tokens) -> None:
+    """Gather == F.embedding; backward == fp64 scatter-add rounded to dtype, then + the tied grad."""
+    g = torch.Generator(device=device).manual_seed(vocab + tokens)
+    table = torch.randn(vocab, hidden, device=device, generator=g).to(dtype)
+    ids = torch.randint(0, vocab, (tokens,), device=device, generator=g)
+    ids[:7] = ids[0]  # repeated ids
+    ids[7] = vocab - 1
+    out = Fn.embedding(table, ids)
+    assert torch.equal(out, torch.nn.functional.embedding(ids, table))
+    dout = torch.randn(tokens, hidden, device=device, generator=g).to(dtype)
+    lm = torch.randn(vocab, hidden, device=device, generator=g).to(dtype)
+    sums = torch.zeros(vocab, hidden, dtype=torch.float64, device=device).index_add_(0, ids, dout.double())
+    for grad_in in (None, lm):
+        grad = torch.empty_like(table)
+        Fn._lib.call("nmb_embedding_bwd", dout.data_ptr(), ids.data_ptr(), Fn._lib.ptr(grad_in), grad.data_ptr(),
+                     tokens, vocab, hidden, Fn._lib.dtype_code(dtype), Fn._lib.stream_of(dout))
+        exp = sums.to(dtype).float() + (grad_in.float() if grad_in is not None else 0.0)
+        tol = dict(rtol=1e-2, atol=2e-2) if dtype == torch.bfloat16 else dict(rtol=1e-5, atol=1e-5)
+        torch.testing.assert_close(grad.float(), exp.to(dtype).float(), **tol)
+        again = torch.empty_like(table)
+        Fn._lib.call("nmb_embedding_bwd", dout.data_ptr(), ids.data_ptr(), Fn._lib.ptr(grad_in), again.data_ptr(),
+                     tokens, vocab, hidden, Fn._lib.dtype_code(dtype), Fn._lib.stream_of(dout))
+        assert torch.equal(grad, again)  # deterministic
+
+
+@pytest.mark.gpu
+def test_tied_embedding_gradient_merge(device) -> None:
+    """Embedding + tied LM head in one graph: the merged table gradient equals
+    the sum of the two separate gradients."""
+    g = torch.Generator(device=device).manual_seed(5)
+    bf = torch.bfloat16
+    vocab, hidden, b, s = 512, 256, 2, 64
+    w = (0.05 * torch.randn(vocab, hidden, device=device, generator=g)).to(bf).requires_grad_()
+    ids = torch.randint(0, vocab, (b, s), device=device, generator=g)
+    tgt = torch.randint(0, vocab, (b, s), device=device, generator=g)
+    tie = Fn.TiedGrad()
+    h = Fn.embedding(w, ids, tie)
+    loss = Fn.lm_head_cross_entropy(h * 1.5, w, tgt, tie=tie)
+    loss.backward()
+    merged = w.grad.clone()
+    w.grad = None
+    h = Fn.embedding(w, ids)
+    loss = Fn.lm_head_cross_entropy(h * 1.5, w, tgt)
+    loss.backward()  # autograd adds the two gradients
+    assert torch.equal(merged, w.grad)
