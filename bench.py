@@ -36,6 +36,10 @@ METRIC = "train tokens/s + peak act GB/layer, 311M seq512 recompute, 1 MI355X; H
 C3 = dict(layers=24, hidden_size=1024, ffn_hidden_size=2736, heads=16, seq_length=512,
           vocab_size=8192, norm_epsilon=1e-5, rope_theta=1e4)
 BATCH, SEQ = 16, 512
+# GQA variant and one ring rank's attention share
+C4 = dict(layers=16, hidden_size=2048, ffn_hidden_size=5632, heads=32, kv_heads=8, seq_length=2048,
+          vocab_size=8192, norm_epsilon=1e-5, rope_theta=1e4)
+C4_BATCH, C4_SEQ = 4, 2048
 
 
 def parse() -> argparse.Namespace:
@@ -48,18 +52,21 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-eager", action="store_true", help="skip the no-checkpoint comparison run")
     p.add_argument("--only-kernels", action="store_true", help="time the kernels only (for profiling)")
     p.add_argument("--kernel", default=None, help="with --only-kernels: time just this kernel")
+    p.add_argument("--config", default="c3", choices=("c3", "c4", "c5"),
+                   help="c3: the metric's 311M step (default); c4: the GQA step; c5: one ring rank's attention")
     p.add_argument("--metrics-jsonl", default=None,
                    help="append the timed interval as one train record of the reference's metric history")
     return p.parse_args()
 
 
-def run_steps(mode: str, steps: int, warmup: int, device, metrics_jsonl: str | None = None) -> dict:
+def run_steps(mode: str, steps: int, warmup: int, device, metrics_jsonl: str | None = None,
+              model_cfg: dict = C3, batch: int = BATCH, seq: int = SEQ) -> dict:
     import torch
 
     import nano_megatron_amd as nm
 
     torch.manual_seed(1234)
-    cfg = nm.GPTConfig(**C3)
+    cfg = nm.GPTConfig(**model_cfg)
     model = nm.GPTModel(cfg, activation_checkpoint_config=nm.ActivationCheckpointConfig(mode=mode))
     model = model.to(device=device, dtype=torch.bfloat16).train()
     from nano_megatron_amd.optim import MasterAdamW
@@ -67,8 +74,8 @@ def run_steps(mode: str, steps: int, warmup: int, device, metrics_jsonl: str | N
     opt = MasterAdamW(model.parameters(), lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1,
                       clip_grad_norm=1.0)
     g = torch.Generator(device=device).manual_seed(1234)
-    ids = torch.randint(0, cfg.vocab_size, (BATCH, SEQ + 1), device=device, generator=g)
-    x, y = ids[:, :SEQ].contiguous(), ids[:, 1:].contiguous()
+    ids = torch.randint(0, cfg.vocab_size, (batch, seq + 1), device=device, generator=g)
+    x, y = ids[:, :seq].contiguous(), ids[:, 1:].contiguous()
 
     def step():
         opt.zero_grad()
@@ -106,16 +113,16 @@ def run_steps(mode: str, steps: int, warmup: int, device, metrics_jsonl: str | N
     if metrics_jsonl:
         from nano_megatron_amd import metrics as M
 
-        m = M.train_metrics(loss=float(loss.item()), learning_rate=3e-4, samples=BATCH * steps,
-                            tokens=BATCH * SEQ * steps, seconds=elapsed,
+        m = M.train_metrics(loss=float(loss.item()), learning_rate=3e-4, samples=batch * steps,
+                            tokens=batch * seq * steps, seconds=elapsed,
                             grad_norm=float(opt.last_grad_norm), device=device)
         with open(metrics_jsonl, "a") as f:
             f.write(M.history_line(sequence=0, step=warmup + 1 + steps, prefix="train", metrics=m,
-                                   consumed_samples=BATCH * (warmup + 1 + steps),
-                                   consumed_tokens=BATCH * SEQ * (warmup + 1 + steps)) + "\n")
+                                   consumed_samples=batch * (warmup + 1 + steps),
+                                   consumed_tokens=batch * seq * (warmup + 1 + steps)) + "\n")
     result = dict(
         ms_per_step=1e3 * elapsed / steps,
-        tokens_per_s=BATCH * SEQ * steps / elapsed,
+        tokens_per_s=batch * seq * steps / elapsed,
         loss=float(loss.item()),
         peak_act_gib_per_layer=peak / cfg.layers / 2**30,
         saved_act_mib_per_layer=saved_after_fwd / cfg.layers / 2**20,
@@ -337,6 +344,112 @@ def cpu_baseline() -> dict:
     )
 
 
+def model_step_flops(cfg: dict, batch: int, seq: int, recompute: bool) -> float:
+    """FLOPs of one training step (GEMMs, causal attention, LM head), the
+    arithmetic of the block's survey: per layer 3x the forward GEMMs and 3.5x the
+    causal attention forward, plus 3x the LM head; recompute adds one forward
+    without the down projection."""
+    t, h, f, v = batch * seq, cfg["hidden_size"], cfg["ffn_hidden_size"], cfg["vocab_size"]
+    hq = cfg["heads"]
+    hkv = cfg.get("kv_heads") or hq
+    d = h // hq
+    gemm = 2 * t * (h * hq * d + 2 * h * hkv * d + hq * d * h + 3 * h * f)
+    attn = 2 * batch * hq * seq * seq * d  # causal forward (half of the 4 b h s^2 d)
+    total = cfg["layers"] * (3 * gemm + 3.5 * attn) + 3 * 2 * t * h * v
+    if recompute:
+        total += cfg["layers"] * (gemm - 2 * t * h * f + attn)
+    return total
+
+
+def run_c4(args, device) -> None:
+    full = run_steps("full", args.steps, args.warmup, device, None, C4, C4_BATCH, C4_SEQ)
+    print("full: " + json.dumps(full), file=sys.stderr, flush=True)
+    eager = run_steps("none", args.steps, args.warmup, device, None, C4, C4_BATCH, C4_SEQ) if not args.no_eager else None
+    fl = model_step_flops(C4, C4_BATCH, C4_SEQ, recompute=True)
+    tf = fl / (full["ms_per_step"] * 1e-3) / 1e12
+    line = dict(
+        metric="train tokens/s, GQA 32q/8kv seq2048 full recompute, 1 MI355X",
+        value=round(full["tokens_per_s"], 1), unit="tokens/s", n_gpus=1, steps=args.steps,
+        warmup=args.warmup, ms_per_step=round(full["ms_per_step"], 3), higher_is_better=True,
+        scaling="weak", vs_baseline=None, dtype="bf16", data="synthetic",
+        config=dict(workload="C4: GQA GPT (16L, H2048, 32 query / 8 KV heads D64, ffn 5632, vocab 8192 "
+                             "tied) training step, full per-layer recompute, bf16 + fp32-master AdamW",
+                    global_batch=C4_BATCH, seq_len=C4_SEQ, parallelism="single GPU"),
+        model_tflops=round(tf, 1), mfma_frac=round(tf / BF16_PEAK_TFLOPS, 4),
+        peak_act_gib_per_layer=round(full["peak_act_gib_per_layer"], 4),
+        saved_act_mib_per_layer=round(full["saved_act_mib_per_layer"], 2), act_floor_mib_per_layer=33.0,
+    )
+    if eager:
+        line["no_checkpoint_tokens_per_s"] = round(eager["tokens_per_s"], 1)
+        line["recompute_overhead"] = round(full["ms_per_step"] / eager["ms_per_step"] - 1.0, 4)
+    print(json.dumps(line), flush=True)
+
+
+def run_c5(args, device) -> None:
+    """One ring rank's attention share: rank 3 of 4 (queries 24576..32767) over the
+    four K/V blocks in ring order 3, 2, 1, 0 (context_parallel/ring.py:104-250),
+    causal by absolute position, forward then backward (P recomputed from the
+    LSE); FLOPs as the survey counts them: visible scores only, backward 2.5x."""
+    import torch
+
+    from nano_megatron_amd import functional as Fn
+
+    s, h, d, nb = 8192, 16, 128, 4
+    g = torch.Generator(device=device).manual_seed(5)
+    bf = torch.bfloat16
+    q = torch.randn(1, s, h, d, device=device, generator=g).to(bf)
+    ks = [torch.randn(1, s, h, d, device=device, generator=g).to(bf) for _ in range(nb)]
+    vs = [torch.randn(1, s, h, d, device=device, generator=g).to(bf) for _ in range(nb)]
+    order = [3, 2, 1, 0]
+    kb, vb = [ks[i] for i in order], [vs[i] for i in order]
+    offs = tuple(i * s for i in order)
+    q_off = 3 * s
+    do = torch.randn(1, s, h, d, device=device, generator=g).to(bf)
+    dq = torch.empty_like(q)
+    dks = [torch.empty_like(k) for k in kb]
+    dvs = [torch.empty_like(v) for v in vb]
+    o, lse = Fn.attn_fwd_bshd(q, kb, vb, offs, causal=True, q_offset=q_off, scale=None)
+
+    def fwd():
+        Fn.attn_fwd_bshd(q, kb, vb, offs, causal=True, q_offset=q_off, scale=None, out=o, lse=lse)
+
+    def bwd():
+        Fn.attn_bwd_bshd(q, kb, vb, offs, o, do, lse, dq, dks, dvs, causal=True, q_offset=q_off, scale=None)
+
+    def timed(fn, n):
+        for _ in range(max(args.warmup, 1)):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) / n  # ms
+
+    full_blocks = 3 * 4 * h * s * s * d          # blocks 2, 1, 0: every score visible
+    fwd_flops = full_blocks + 4 * h * s * s * d / 2  # + the diagonal block's causal half
+    bwd_flops = 2.5 * fwd_flops
+    t_f, t_b = timed(fwd, args.steps), timed(bwd, args.steps)
+    tf_f, tf_b = fwd_flops / t_f / 1e9, bwd_flops / t_b / 1e9
+    total = (fwd_flops + bwd_flops) / (t_f + t_b) / 1e9
+    line = dict(
+        metric="ring-share attention fwd+bwd TFLOP/s, 8192 queries x 4 K/V blocks, D128, 1 MI355X",
+        value=round(total, 1), unit="TFLOP/s", n_gpus=1, steps=args.steps, warmup=args.warmup,
+        ms_per_step=round(t_f + t_b, 3), higher_is_better=True, scaling="weak", vs_baseline=None,
+        dtype="bf16", data="synthetic",
+        config=dict(workload="C5: rank 3 of a 4-way ring, local Q [1, 8192, 16, 128], K/V blocks "
+                             "visited 3, 2, 1, 0, causal by absolute position", global_batch=1,
+                    seq_len=s, parallelism="single GPU (one ring rank's share)"),
+        fwd_ms=round(t_f, 3), bwd_ms=round(t_b, 3), fwd_tflops=round(tf_f, 1), bwd_tflops=round(tf_b, 1),
+        fwd_gflop=round(fwd_flops / 1e9, 1), bwd_gflop=round(bwd_flops / 1e9, 1),
+        roofline=dict(bound="mfma", achieved=round(total, 1), peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
+                      frac=round(total / BF16_PEAK_TFLOPS, 4), traffic=None, kernel="attn_fwd + attn_bwd"),
+    )
+    print(json.dumps(line), flush=True)
+
+
 def main() -> None:
     args = parse()
     if args.gpus != 1:
@@ -353,6 +466,12 @@ def main() -> None:
     from nano_megatron_amd import _lib
 
     _lib.load()
+    if args.config == "c4":
+        run_c4(args, device)
+        return
+    if args.config == "c5":
+        run_c5(args, device)
+        return
 
     kernels = None
     if not args.no_kernels:
@@ -405,6 +524,7 @@ def main() -> None:
         peak_act_gib_per_layer=round(full["peak_act_gib_per_layer"], 4),
         saved_act_mib_per_layer=round(full["saved_act_mib_per_layer"], 2),
         act_floor_mib_per_layer=16.5,
+        model_tflops=round(model_step_flops(C3, BATCH, SEQ, recompute=True) / (full["ms_per_step"] * 1e-3) / 1e12, 1),
         loss=round(full["loss"], 4),
         roofline=roofline,
         cpu_baseline=cpu,
