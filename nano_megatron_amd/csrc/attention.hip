@@ -25,6 +25,7 @@
 #include <math.h>
 
 #include "common.h"
+#include "lds_dma.h"
 
 namespace nmb {
 namespace {
@@ -251,6 +252,60 @@ __device__ __forceinline__ float lse_to_log2(float v) {
   return v == -__builtin_inff() ? __builtin_inff() : v * kLog2e;
 }
 
+// K/V tiles of 64 keys x D stream from HBM straight into LDS (buffer_load
+// ... lds: no register round trip), kStages deep, so kStages - 1 tiles are in
+// flight while one is computed.  Both keep the row-major [key][d] layout with
+// 16-byte chunk swizzles:
+//  * K: chunk c of key row r in slot c ^ kswz(r).  A K fragment (16 keys x 8 d
+//    per lane group) is one ds_read_b128 per lane; the 16 rows of a lane group
+//    cover all 64 banks.
+//  * V: 32-byte chunk pair q of key row r in pair slot q ^ vswz(r).  The V^T
+//    fragment of the P V MFMA (16 d x keys 4g..4g+3 and 16+4g..16+4g+3 of a
+//    32-key chunk) is two ds_read_b64_tr_b16 per lane; the 8 rows a half-wave
+//    reads cover all 64 banks.
+template <int D>
+struct KVTile {
+  static constexpr int kElems = 64 * D;
+  static constexpr int kPer = kElems * 2 / 1024 / 4;  // 1 KB loads per wave per tile (4 waves)
+  __device__ static int kswz(int r) { return D == 64 ? (r >> 1) & 7 : r & 15; }
+  __device__ static int vswz(int r) { return D == 64 ? (r >> 1) & 3 : r & 7; }
+};
+
+// One wave's share of the direct loads of a K and a V tile: load j fills LDS
+// bytes [1024 (wave kPer + j), + 1024) of each tile; lane l's 16 bytes are
+// chunk slot s of key row r there, read from the swizzled global chunk.
+template <int D>
+struct KVStream {
+  using Tile = KVTile<D>;
+  static constexpr int P = Tile::kPer;
+  uint32_t koff[P], voff[P];  // byte offsets from key row 0 of the tile
+  int row[P];
+
+  __device__ void init(int64_t row_stride, int wave, int lane) {
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+      const int e = (1024 * (wave * P + j) + 16 * lane) / 2;  // element offset within the tile
+      const int r = e / D, sl = (e % D) / 8;
+      row[j] = r;
+      const uint32_t rb = static_cast<uint32_t>(r * row_stride * 2);
+      koff[j] = rb + 16u * static_cast<uint32_t>(sl ^ Tile::kswz(r));
+      voff[j] = rb + 16u * static_cast<uint32_t>(sl ^ (2 * Tile::vswz(r)));
+    }
+  }
+
+  // tile of keys k0 .. k0 + 63 (k0 * row bytes = k0_bytes) of a block with
+  // nkeys keys; keys at and past nkeys read as zeros
+  __device__ __forceinline__ void issue(const i32x4& rk, const i32x4& rv, bf16* sk, bf16* sv, int k0,
+                                        int nkeys, uint32_t k0_bytes, int wave) const {
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+      const bool ok = k0 + row[j] < nkeys;
+      load_lds16(rk, sk + 512 * (wave * P + j), ok ? k0_bytes + koff[j] : kOOB);
+      load_lds16(rv, sv + 512 * (wave * P + j), ok ? k0_bytes + voff[j] : kOOB);
+    }
+  }
+};
+
 // FL (from LSE): the softmax statistics are given (lse read, not written), so
 // P = exp2(S * scale_log2 - lse2) directly: no running maximum, rescale or
 // row sum, and O = P V needs no final division.
@@ -259,16 +314,19 @@ __global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_ke
     const bf16* __restrict__ q, KVBlocks kv, bf16* __restrict__ o, float* __restrict__ lse,
     AttnShape p, int n_qt, int items, int per_xcd) {
   constexpr int BQ = 64 * TQ, BK = 64, KS = D / 32, DT = D / 16;
-  constexpr int LDK = D + 8, LDV = BK + 4;
-  __shared__ __attribute__((aligned(16))) bf16 sK[BK * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sVt[D * LDV];
+  constexpr int kStages = 4;
+  using Tile = KVTile<D>;
+  constexpr int kLoads = 2 * Tile::kPer;  // this wave's loads per K/V tile pair
+  __shared__ __attribute__((aligned(1024))) bf16 sK[kStages][Tile::kElems];
+  __shared__ __attribute__((aligned(1024))) bf16 sV[kStages][Tile::kElems];
 
   const int w = xcd_item(items, per_xcd);
   if (w < 0) return;
   const int bh = w / n_qt;
   const int qt = n_qt - 1 - (w % n_qt);  // heavy causal tiles first within a head
   const int b = bh / p.Hq, h = bh % p.Hq;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int l16 = lane & 15, g = lane >> 4;
   const int hk = h / (p.Hq / p.Hkv);
   const int qbase = qt * BQ + 16 * wave;  // column tile t: qbase + 64 t + l16
@@ -300,29 +358,44 @@ __global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_ke
   }
   const int64_t qa_wg_last = p.q_offset + min(qt * BQ + BQ - 1, p.Sq - 1);
   const int64_t kv_off = b * p.kv_sb + hk * p.kv_sh;
+  // bytes from (b, key 0, hk) to the end of the last key row of a block (< 2^31, checked by the host)
+  const uint32_t kv_bytes = static_cast<uint32_t>(((p.Sk - 1) * p.kv_ss + D) * 2);
+  const uint32_t row_bytes = static_cast<uint32_t>(p.kv_ss * 2);
+  KVStream<D> ld;
+  ld.init(p.kv_ss, wave, lane);
 
-  PairTile<BK, D> kr, vr;
+  // compute cursor (blk, kt) and load cursor (pblk, pkt) over the visible tiles
   int nt = 0;
   int blk = first_block(p, kv, qa_wg_last, nt), kt = 0;
-  if (blk < p.nblk) {
-    kr.load(static_cast<const bf16*>(kv.k[blk]) + kv_off, p.kv_ss, 0, p.Sk);
-    vr.load(static_cast<const bf16*>(kv.v[blk]) + kv_off, p.kv_ss, 0, p.Sk);
-  }
-  while (blk < p.nblk) {
-    __syncthreads();
-    kr.template store_rows<LDK>(sK);
-    vr.template store_cols<LDV>(sVt);
-    __syncthreads();
+  int pnt = nt, pblk = blk, pkt = 0;
+  // loads of the load cursor's tile into a stage; past the last tile, loads of
+  // zeros (every iteration issues and waits for the same number of loads)
+  auto issue = [&](int stage) {
+    if (pblk < p.nblk) {
+      const i32x4 rk = make_rsrc(static_cast<const bf16*>(kv.k[pblk]) + kv_off, kv_bytes);
+      const i32x4 rv = make_rsrc(static_cast<const bf16*>(kv.v[pblk]) + kv_off, kv_bytes);
+      ld.issue(rk, rv, sK[stage], sV[stage], pkt * BK, p.Sk, static_cast<uint32_t>(pkt * BK) * row_bytes, wave);
+      next_tile(p, kv, qa_wg_last, pblk, pkt, pnt);
+    } else {
+      const i32x4 rz = make_rsrc(kv.k[0], 0);
+      ld.issue(rz, rz, sK[stage], sV[stage], 0, 0, 0u, wave);
+    }
+  };
+#pragma unroll
+  for (int st = 0; st < kStages - 1; ++st) issue(st);
+
+  for (int it = 0; blk < p.nblk; ++it) {
+    // this wave's loads of tile it have landed (those of the next kStages - 2
+    // may still fly); after the barrier, everyone's have, and nobody reads the
+    // stage of tile it - 1 any more: refill it with tile it + kStages - 1
+    wait_vmcnt<(kStages - 2) * kLoads>();
+    lds_barrier();
+    issue((it + kStages - 1) % kStages);
+    const bf16* tk = sK[it % kStages];
+    const bf16* tv = sV[it % kStages];
     const int64_t koff = kv.koff[blk];
     const int k0 = kt * BK;
-    int nb = blk, nk = kt;
-    next_tile(p, kv, qa_wg_last, nb, nk, nt);
-    if (nb < p.nblk) {
-      kr.load(static_cast<const bf16*>(kv.k[nb]) + kv_off, p.kv_ss, nk * BK, p.Sk);
-      vr.load(static_cast<const bf16*>(kv.v[nb]) + kv_off, p.kv_ss, nk * BK, p.Sk);
-    }
-    blk = nb;
-    kt = nk;
+    next_tile(p, kv, qa_wg_last, blk, kt, nt);
     // per column tile: is any key of this tile visible, is masking needed?
     bool live[TQ], need_mask[TQ];
 #pragma unroll
@@ -339,11 +412,18 @@ __global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_ke
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-      for (int mk = 0; mk < 4; ++mk) kfr[ks][mk] = ld8(sK + (mk * 16 + l16) * LDK + ks * 32 + g * 8);
+      for (int mk = 0; mk < 4; ++mk) {
+        const int r = mk * 16 + l16;
+        kfr[ks][mk] = ld8(tk + r * D + 8 * ((ks * 4 + g) ^ Tile::kswz(r)));
+      }
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) vfr[dt][s2] = ld4x2(sVt + (dt * 16 + l16) * LDV + 32 * s2 + g * 4);
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const int r0 = 32 * s2 + 4 * g + (l16 >> 2), c4 = 4 * (l16 & 3);
+        vfr[dt][s2] = ld_tr(tv + r0 * D + 16 * (dt ^ Tile::vswz(r0)) + c4,
+                            tv + (r0 + 16) * D + 16 * (dt ^ Tile::vswz(r0 + 16)) + c4);
+      }
 #pragma unroll
     for (int t = 0; t < TQ; ++t) {
       if (!live[t]) continue;
@@ -416,6 +496,8 @@ __global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_ke
         for (int s2 = 0; s2 < 2; ++s2) acc[t][dt] = mfma16(vfr[dt][s2], pf[s2], acc[t][dt]);
     }
   }
+  // no load may still write this workgroup's LDS when it ends
+  wait_vmcnt<0>();
   bf16* ob = o + b * p.o_sb + h * p.o_sh;
   float* lb = lse + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
 #pragma unroll
@@ -1076,6 +1158,9 @@ int attn_fwd_impl(bool from_lse, const void* q, const void* const* k_blocks,
   if (batch == 0 || seq_q == 0) return NMB_OK;
   if (dtype == NMB_BF16) {
     NMB_REQUIRE(nmb::aligned16(o), "attn_fwd: o must be 16-byte aligned");
+    // the forward addresses a K/V block through a 32-bit buffer offset
+    NMB_REQUIRE_SUPPORTED(seq_k == 0 || ((seq_k - 1) * kv_strides[1] + head_dim) * 2 < (int64_t{1} << 31),
+                          "attn_fwd: a K/V block spans more than 2 GiB");
     // queries per workgroup: 4 waves x TQ column tiles of 16 (TQ = 4 at D 64, 2 at D 128)
     const int bq = head_dim == 64 ? 256 : 128;
     const int n_qt = static_cast<int>((seq_q + bq - 1) / bq);
