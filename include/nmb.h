@@ -134,7 +134,8 @@ int nmb_attn_fwd_from_lse(const void* q, const void* const* k_blocks, const void
                           const int64_t* kv_strides, const int64_t* o_strides, int causal,
                           int64_t q_offset, float scale, int dtype, hipStream_t stream);
 
-/* Bytes of workspace nmb_attn_bwd needs (the fp32 delta = rowsum(dO * O)). */
+/* Bytes of workspace nmb_attn_bwd needs: the fp32 delta = rowsum(dO * O) and,
+ * for bf16, the softmax LSE in base 2 (both [batch, q_heads, seq_q]). */
 int nmb_attn_bwd_workspace_bytes(int64_t batch, int64_t q_heads, int64_t seq_q, size_t* bytes);
 
 /* Backward from the saved lse: dq (overwritten), and per block dk, dv

@@ -252,33 +252,43 @@ __device__ __forceinline__ float lse_to_log2(float v) {
   return v == -__builtin_inff() ? __builtin_inff() : v * kLog2e;
 }
 
-// K/V tiles of 64 keys x D stream from HBM straight into LDS (buffer_load
-// ... lds: no register round trip), kStages deep, so kStages - 1 tiles are in
-// flight while one is computed.  Both keep the row-major [key][d] layout with
-// 16-byte chunk swizzles:
-//  * K: chunk c of key row r in slot c ^ kswz(r).  A K fragment (16 keys x 8 d
-//    per lane group) is one ds_read_b128 per lane; the 16 rows of a lane group
-//    cover all 64 banks.
-//  * V: 32-byte chunk pair q of key row r in pair slot q ^ vswz(r).  The V^T
-//    fragment of the P V MFMA (16 d x keys 4g..4g+3 and 16+4g..16+4g+3 of a
-//    32-key chunk) is two ds_read_b64_tr_b16 per lane; the 8 rows a half-wave
-//    reads cover all 64 banks.
+// 64-row x D bf16 tiles (K, V, Q, dO) stream from HBM straight into LDS
+// (buffer_load ... lds: no register round trip), kStages deep, so kStages - 1
+// tiles are in flight while one is computed.  A tile keeps the row-major
+// layout with its 16-byte chunks swizzled: chunk c of row r in slot
+// c ^ swz(r).  The swizzle serves both fragment kinds without bank conflicts:
+//  * row fragments (an MFMA operand holding 8 consecutive columns of a row per
+//    lane; 16 rows per lane group): one ds_read_b128;
+//  * column fragments (8 rows of one column per lane: rows r0 + 4g .. +3 and
+//    r0 + 16 + 4g .. +3 of a 32-row chunk, the key/query order in which the
+//    score accumulators hold P and dS): two ds_read_b64_tr_b16.
 template <int D>
-struct KVTile {
+struct Tile64 {
   static constexpr int kElems = 64 * D;
   static constexpr int kPer = kElems * 2 / 1024 / 4;  // 1 KB loads per wave per tile (4 waves)
-  __device__ static int kswz(int r) { return D == 64 ? (r >> 1) & 7 : r & 15; }
-  __device__ static int vswz(int r) { return D == 64 ? (r >> 1) & 3 : r & 7; }
+  // rows of a 16-lane group take 16 distinct (row parity, slot) pairs; the 8
+  // rows of a half-wave column read take 8 distinct (row parity, slot pair)s
+  __device__ static int swz(int r) {
+    return D == 64 ? 2 * ((r >> 1) & 3) + ((r >> 3) & 1) : 2 * (r & 7) + ((r >> 3) & 1);
+  }
+  __device__ static int at(int r, int col) { return r * D + 8 * ((col >> 3) ^ swz(r)) + (col & 7); }
+  // row r, columns col .. col + 7 (col a multiple of 8)
+  __device__ static bf16x8 row8(const bf16* t, int r, int col) { return ld8(t + at(r, col)); }
+  // lane (l16, g): column c0 + l16, rows r0 + 4g .. +3 then r0 + 16 + 4g .. +3
+  __device__ static bf16x8 col8(const bf16* t, int r0, int c0, int l16, int g) {
+    const int r = r0 + 4 * g + (l16 >> 2), cc = c0 + 4 * (l16 & 3);
+    return ld_tr(t + at(r, cc), t + at(r + 16, cc));
+  }
 };
 
-// One wave's share of the direct loads of a K and a V tile: load j fills LDS
-// bytes [1024 (wave kPer + j), + 1024) of each tile; lane l's 16 bytes are
-// chunk slot s of key row r there, read from the swizzled global chunk.
+// One wave's share of the direct loads of a 64-row tile: load j fills LDS
+// bytes [1024 (wave kPer + j), + 1024) of the tile; lane l's 16 bytes are
+// chunk slot s of row r there, read from global chunk s ^ swz(r).
 template <int D>
-struct KVStream {
-  using Tile = KVTile<D>;
+struct TileStream {
+  using Tile = Tile64<D>;
   static constexpr int P = Tile::kPer;
-  uint32_t koff[P], voff[P];  // byte offsets from key row 0 of the tile
+  uint32_t off[P];  // byte offset from row 0 of the tile
   int row[P];
 
   __device__ void init(int64_t row_stride, int wave, int lane) {
@@ -287,22 +297,17 @@ struct KVStream {
       const int e = (1024 * (wave * P + j) + 16 * lane) / 2;  // element offset within the tile
       const int r = e / D, sl = (e % D) / 8;
       row[j] = r;
-      const uint32_t rb = static_cast<uint32_t>(r * row_stride * 2);
-      koff[j] = rb + 16u * static_cast<uint32_t>(sl ^ Tile::kswz(r));
-      voff[j] = rb + 16u * static_cast<uint32_t>(sl ^ (2 * Tile::vswz(r)));
+      off[j] = static_cast<uint32_t>(r * row_stride * 2) + 16u * static_cast<uint32_t>(sl ^ Tile::swz(r));
     }
   }
 
-  // tile of keys k0 .. k0 + 63 (k0 * row bytes = k0_bytes) of a block with
-  // nkeys keys; keys at and past nkeys read as zeros
-  __device__ __forceinline__ void issue(const i32x4& rk, const i32x4& rv, bf16* sk, bf16* sv, int k0,
-                                        int nkeys, uint32_t k0_bytes, int wave) const {
+  // rows r0 .. r0 + 63 (r0 * row bytes = r0_bytes) of a matrix of nrows rows;
+  // rows at and past nrows read as zeros
+  __device__ __forceinline__ void issue(const i32x4& rs, bf16* dst, int r0, int nrows, uint32_t r0_bytes,
+                                        int wave) const {
 #pragma unroll
-    for (int j = 0; j < P; ++j) {
-      const bool ok = k0 + row[j] < nkeys;
-      load_lds16(rk, sk + 512 * (wave * P + j), ok ? k0_bytes + koff[j] : kOOB);
-      load_lds16(rv, sv + 512 * (wave * P + j), ok ? k0_bytes + voff[j] : kOOB);
-    }
+    for (int j = 0; j < P; ++j)
+      load_lds16(rs, dst + 512 * (wave * P + j), r0 + row[j] < nrows ? r0_bytes + off[j] : kOOB);
   }
 };
 
@@ -315,7 +320,7 @@ __global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_ke
     AttnShape p, int n_qt, int items, int per_xcd) {
   constexpr int BQ = 64 * TQ, BK = 64, KS = D / 32, DT = D / 16;
   constexpr int kStages = 4;
-  using Tile = KVTile<D>;
+  using Tile = Tile64<D>;
   constexpr int kLoads = 2 * Tile::kPer;  // this wave's loads per K/V tile pair
   __shared__ __attribute__((aligned(1024))) bf16 sK[kStages][Tile::kElems];
   __shared__ __attribute__((aligned(1024))) bf16 sV[kStages][Tile::kElems];
@@ -361,7 +366,7 @@ __global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_ke
   // bytes from (b, key 0, hk) to the end of the last key row of a block (< 2^31, checked by the host)
   const uint32_t kv_bytes = static_cast<uint32_t>(((p.Sk - 1) * p.kv_ss + D) * 2);
   const uint32_t row_bytes = static_cast<uint32_t>(p.kv_ss * 2);
-  KVStream<D> ld;
+  TileStream<D> ld;
   ld.init(p.kv_ss, wave, lane);
 
   // compute cursor (blk, kt) and load cursor (pblk, pkt) over the visible tiles
@@ -372,13 +377,14 @@ __global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_ke
   // zeros (every iteration issues and waits for the same number of loads)
   auto issue = [&](int stage) {
     if (pblk < p.nblk) {
-      const i32x4 rk = make_rsrc(static_cast<const bf16*>(kv.k[pblk]) + kv_off, kv_bytes);
-      const i32x4 rv = make_rsrc(static_cast<const bf16*>(kv.v[pblk]) + kv_off, kv_bytes);
-      ld.issue(rk, rv, sK[stage], sV[stage], pkt * BK, p.Sk, static_cast<uint32_t>(pkt * BK) * row_bytes, wave);
+      const uint32_t r0b = static_cast<uint32_t>(pkt * BK) * row_bytes;
+      ld.issue(make_rsrc(static_cast<const bf16*>(kv.k[pblk]) + kv_off, kv_bytes), sK[stage], pkt * BK, p.Sk, r0b, wave);
+      ld.issue(make_rsrc(static_cast<const bf16*>(kv.v[pblk]) + kv_off, kv_bytes), sV[stage], pkt * BK, p.Sk, r0b, wave);
       next_tile(p, kv, qa_wg_last, pblk, pkt, pnt);
     } else {
       const i32x4 rz = make_rsrc(kv.k[0], 0);
-      ld.issue(rz, rz, sK[stage], sV[stage], 0, 0, 0u, wave);
+      ld.issue(rz, sK[stage], 0, 0, 0u, wave);
+      ld.issue(rz, sV[stage], 0, 0, 0u, wave);
     }
   };
 #pragma unroll
@@ -412,18 +418,11 @@ __global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_ke
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-      for (int mk = 0; mk < 4; ++mk) {
-        const int r = mk * 16 + l16;
-        kfr[ks][mk] = ld8(tk + r * D + 8 * ((ks * 4 + g) ^ Tile::kswz(r)));
-      }
+      for (int mk = 0; mk < 4; ++mk) kfr[ks][mk] = Tile::row8(tk, mk * 16 + l16, ks * 32 + g * 8);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const int r0 = 32 * s2 + 4 * g + (l16 >> 2), c4 = 4 * (l16 & 3);
-        vfr[dt][s2] = ld_tr(tv + r0 * D + 16 * (dt ^ Tile::vswz(r0)) + c4,
-                            tv + (r0 + 16) * D + 16 * (dt ^ Tile::vswz(r0 + 16)) + c4);
-      }
+      for (int s2 = 0; s2 < 2; ++s2) vfr[dt][s2] = Tile::col8(tv, 32 * s2, dt * 16, l16, g);
 #pragma unroll
     for (int t = 0; t < TQ; ++t) {
       if (!live[t]) continue;
@@ -545,19 +544,22 @@ template <int D, bool ROPE>
 __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
     const bf16* __restrict__ q, KVBlocks kv, const bf16* __restrict__ o,
     const bf16* __restrict__ dout, const float* __restrict__ lse, float* __restrict__ delta,
-    bf16* __restrict__ dq, AttnShape p, int n_qt, int items, int per_xcd, RopeGrad rg) {
+    float* __restrict__ lse2_out, bf16* __restrict__ dq, AttnShape p, int n_qt, int items, int per_xcd,
+    RopeGrad rg) {
   constexpr int BQ = 128, BK = 64, KS = D / 32, DT = D / 16;
-  constexpr int LDK = D + 8, LDT = BK + 4;
-  __shared__ __attribute__((aligned(16))) bf16 sK[BK * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sKt[D * LDT];
-  __shared__ __attribute__((aligned(16))) bf16 sV[BK * LDK];
+  constexpr int kStages = 4;
+  using Tile = Tile64<D>;
+  constexpr int kLoads = 2 * Tile::kPer;  // this wave's loads per K/V tile pair
+  __shared__ __attribute__((aligned(1024))) bf16 sK[kStages][Tile::kElems];
+  __shared__ __attribute__((aligned(1024))) bf16 sV[kStages][Tile::kElems];
 
   const int w = xcd_item(items, per_xcd);
   if (w < 0) return;
   const int bh = w / n_qt;
   const int qt = n_qt - 1 - (w % n_qt);
   const int b = bh / p.Hq, h = bh % p.Hq;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int l16 = lane & 15, g = lane >> 4;
   const int hk = h / (p.Hq / p.Hkv);
   const int q0 = qt * BQ + wave * 32;
@@ -568,6 +570,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
   const bf16* db = dout + b * p.o_sb + h * p.o_sh;
   const float* lb = lse + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
   float* deb = delta + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
+  float* l2b = lse2_out + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
   bf16x8 qf[2][KS], df[2][KS];
   float lse2[2], dl[2];
 #pragma unroll
@@ -586,8 +589,12 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
     part += __shfl_xor(part, 16, 64);
     part += __shfl_xor(part, 32, 64);
     dl[t] = part;
-    if (ok && g == 0) deb[qi] = part;
     lse2[t] = ok ? lse_to_log2(lb[qi]) : __builtin_inff();
+    // delta and the log2-domain lse for the dK/dV kernel, which runs next
+    if (ok && g == 0) {
+      deb[qi] = part;
+      l2b[qi] = lse2[t];
+    }
   }
   f32x4 acc[2][DT];
 #pragma unroll
@@ -599,30 +606,39 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
   const int64_t qa_wave_last = p.q_offset + min(q0 + 31, p.Sq - 1);
   const int64_t qa_wg_last = p.q_offset + min(qt * BQ + BQ - 1, p.Sq - 1);
   const int64_t kv_off = b * p.kv_sb + hk * p.kv_sh;
+  const uint32_t kv_bytes = static_cast<uint32_t>(((p.Sk - 1) * p.kv_ss + D) * 2);
+  const uint32_t row_bytes = static_cast<uint32_t>(p.kv_ss * 2);
+  TileStream<D> ld;
+  ld.init(p.kv_ss, wave, lane);
 
-  PairTile<BK, D> kr, vr;
+  // K/V tiles stream through LDS as in the forward (same cursors and waits)
   int nt = 0;
   int blk = first_block(p, kv, qa_wg_last, nt), kt = 0;
-  if (blk < p.nblk) {
-    kr.load(static_cast<const bf16*>(kv.k[blk]) + kv_off, p.kv_ss, 0, p.Sk);
-    vr.load(static_cast<const bf16*>(kv.v[blk]) + kv_off, p.kv_ss, 0, p.Sk);
-  }
-  while (blk < p.nblk) {
-    __syncthreads();
-    kr.template store_rows<LDK>(sK);
-    kr.template store_cols<LDT>(sKt);
-    vr.template store_rows<LDK>(sV);
-    __syncthreads();
+  int pnt = nt, pblk = blk, pkt = 0;
+  auto issue = [&](int stage) {
+    if (pblk < p.nblk) {
+      const uint32_t r0b = static_cast<uint32_t>(pkt * BK) * row_bytes;
+      ld.issue(make_rsrc(static_cast<const bf16*>(kv.k[pblk]) + kv_off, kv_bytes), sK[stage], pkt * BK, p.Sk, r0b, wave);
+      ld.issue(make_rsrc(static_cast<const bf16*>(kv.v[pblk]) + kv_off, kv_bytes), sV[stage], pkt * BK, p.Sk, r0b, wave);
+      next_tile(p, kv, qa_wg_last, pblk, pkt, pnt);
+    } else {
+      const i32x4 rz = make_rsrc(kv.k[0], 0);
+      ld.issue(rz, sK[stage], 0, 0, 0u, wave);
+      ld.issue(rz, sV[stage], 0, 0, 0u, wave);
+    }
+  };
+#pragma unroll
+  for (int st = 0; st < kStages - 1; ++st) issue(st);
+
+  for (int it = 0; blk < p.nblk; ++it) {
+    wait_vmcnt<(kStages - 2) * kLoads>();
+    lds_barrier();
+    issue((it + kStages - 1) % kStages);
+    const bf16* tk = sK[it % kStages];
+    const bf16* tv = sV[it % kStages];
     const int64_t koff = kv.koff[blk];
     const int k0 = kt * BK;
-    int nb = blk, nk = kt;
-    next_tile(p, kv, qa_wg_last, nb, nk, nt);
-    if (nb < p.nblk) {
-      kr.load(static_cast<const bf16*>(kv.k[nb]) + kv_off, p.kv_ss, nk * BK, p.Sk);
-      vr.load(static_cast<const bf16*>(kv.v[nb]) + kv_off, p.kv_ss, nk * BK, p.Sk);
-    }
-    blk = nb;
-    kt = nk;
+    next_tile(p, kv, qa_wg_last, blk, kt, nt);
     if (p.causal && koff + k0 > qa_wave_last) continue;
     const bool need_mask = (k0 + BK > p.Sk) || (p.causal && koff + k0 + BK - 1 > qa_wave_first);
 
@@ -636,8 +652,8 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
       }
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 ak = ld8(sK + (mk * 16 + l16) * LDK + ks * 32 + g * 8);
-        const bf16x8 av = ld8(sV + (mk * 16 + l16) * LDK + ks * 32 + g * 8);
+        const bf16x8 ak = Tile::row8(tk, mk * 16 + l16, ks * 32 + g * 8);
+        const bf16x8 av = Tile::row8(tv, mk * 16 + l16, ks * 32 + g * 8);
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           s[mk][t] = mfma16(ak, qf[t][ks], s[mk][t]);
@@ -669,12 +685,14 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
     for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
-        const bf16x8 a = ld4x2(sKt + (dt * 16 + l16) * LDT + 32 * s2 + g * 4);
+        const bf16x8 a = Tile::col8(tk, 32 * s2, dt * 16, l16, g);
 #pragma unroll
         for (int t = 0; t < 2; ++t) acc[t][dt] = mfma16(a, dsf[s2][t], acc[t][dt]);
       }
     }
   }
+  // no load may still write this workgroup's LDS when it ends
+  wait_vmcnt<0>();
   // lane holds dQ[q0 + 16 t + l16][d = 16 dt + 4 g + e]; d and d + D/2 are dt and dt + DT/2
   bf16* dqb = dq + b * p.q_sb + h * p.q_sh;
 #pragma unroll
@@ -721,15 +739,17 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
 template <int D, bool ROPE>
 __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
     const bf16* __restrict__ q, KVBlocks kv, const bf16* __restrict__ dout,
-    const float* __restrict__ lse, const float* __restrict__ delta, AttnShape p, int n_kt,
+    const float* __restrict__ lse2, const float* __restrict__ delta, AttnShape p, int n_kt,
     int items, int per_xcd, RopeGrad rg) {
   constexpr int BQ = 64, KT = 2, BKW = 64 * KT, KS = D / 32, DT = D / 16;
-  constexpr int LDQ = D + 8, LDT = BQ + 4;
-  __shared__ __attribute__((aligned(16))) bf16 sQ[BQ * LDQ];
-  __shared__ __attribute__((aligned(16))) bf16 sQt[D * LDT];
-  __shared__ __attribute__((aligned(16))) bf16 sD[BQ * LDQ];
-  __shared__ __attribute__((aligned(16))) bf16 sDt[D * LDT];
-  __shared__ float sL[BQ], sDl[BQ];
+  constexpr int kStages = 4;
+  using Tile = Tile64<D>;
+  // this wave's loads per query tile: Q, dO, and one 256-byte row statistic
+  // (waves 0 and 2 fetch lse2, waves 1 and 3 delta)
+  constexpr int kLoads = 2 * Tile::kPer + 1;
+  __shared__ __attribute__((aligned(1024))) bf16 sQ[kStages][Tile::kElems];
+  __shared__ __attribute__((aligned(1024))) bf16 sD[kStages][Tile::kElems];
+  __shared__ __attribute__((aligned(256))) float sStat[kStages][4][BQ];
 
   const int w = xcd_item(items, per_xcd);
   if (w < 0) return;
@@ -740,7 +760,8 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
   const int bb = rest / p.Hkv;
   const int blk = bb % p.nblk;
   const int b = bb / p.nblk;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int l16 = lane & 15, g = lane >> 4;
   const int k0 = ktile * BKW;
   const int kbase = k0 + 16 * wave;  // key tile j: kbase + 64 j + l16
@@ -780,34 +801,43 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
   const int per_head = n_qt - qt_begin;
   const int n_iter = per_head > 0 ? group * per_head : 0;
 
-  PairTile<BQ, D> qr, dr;
-  float lv = 0.f, dv = 0.f;
-  auto load = [&](int it) {
-    const int h = hk * group + it / per_head;
-    const int q0 = (qt_begin + it % per_head) * BQ;
-    qr.load(q + b * p.q_sb + h * p.q_sh, p.q_ss, q0, p.Sq);
-    dr.load(dout + b * p.o_sb + h * p.o_sh, p.o_ss, q0, p.Sq);
-    if (threadIdx.x < BQ) {
-      const int qi = q0 + threadIdx.x;
-      const int64_t row = (static_cast<int64_t>(b) * p.Hq + h) * p.Sq + qi;
-      lv = qi < p.Sq ? lse_to_log2(lse[row]) : __builtin_inff();
-      dv = qi < p.Sq ? delta[row] : 0.f;
+  // Q / dO tiles and their row statistics stream through LDS (kStages deep);
+  // iteration it covers query head hk * group + it / per_head, query tile
+  // qt_begin + it % per_head.  Past the last iteration the loads read zeros.
+  TileStream<D> lq, ldo;
+  lq.init(p.q_ss, wave, lane);
+  ldo.init(p.o_ss, wave, lane);
+  const uint32_t q_bytes = static_cast<uint32_t>(((p.Sq - 1) * p.q_ss + D) * 2);
+  const uint32_t o_bytes = static_cast<uint32_t>(((p.Sq - 1) * p.o_ss + D) * 2);
+  auto issue = [&](int it, int stage) {
+    if (it < n_iter) {
+      const int h = hk * group + it / per_head;
+      const int q0 = (qt_begin + it % per_head) * BQ;
+      lq.issue(make_rsrc(q + b * p.q_sb + h * p.q_sh, q_bytes), sQ[stage], q0, p.Sq,
+               static_cast<uint32_t>(q0) * static_cast<uint32_t>(p.q_ss * 2), wave);
+      ldo.issue(make_rsrc(dout + b * p.o_sb + h * p.o_sh, o_bytes), sD[stage], q0, p.Sq,
+                static_cast<uint32_t>(q0) * static_cast<uint32_t>(p.o_ss * 2), wave);
+      const float* stat = ((wave & 1) ? delta : lse2) + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
+      load_lds4(make_rsrc(stat, static_cast<uint32_t>(p.Sq * 4)), &sStat[stage][wave][0],
+                q0 + lane < p.Sq ? static_cast<uint32_t>(4 * (q0 + lane)) : kOOB);
+    } else {
+      const i32x4 rz = make_rsrc(q, 0);
+      lq.issue(rz, sQ[stage], 0, 0, 0u, wave);
+      ldo.issue(rz, sD[stage], 0, 0, 0u, wave);
+      load_lds4(rz, &sStat[stage][wave][0], kOOB);
     }
   };
-  if (n_iter > 0) load(0);
+#pragma unroll
+  for (int st = 0; st < kStages - 1; ++st) issue(st, st);
   for (int it = 0; it < n_iter; ++it) {
-    __syncthreads();
-    qr.template store_rows<LDQ>(sQ);
-    qr.template store_cols<LDT>(sQt);
-    dr.template store_rows<LDQ>(sD);
-    dr.template store_cols<LDT>(sDt);
-    if (threadIdx.x < BQ) {
-      sL[threadIdx.x] = lv;
-      sDl[threadIdx.x] = dv;
-    }
-    __syncthreads();
+    wait_vmcnt<(kStages - 2) * kLoads>();
+    lds_barrier();
+    issue(it + kStages - 1, (it + kStages - 1) % kStages);
+    const bf16* tq = sQ[it % kStages];
+    const bf16* td = sD[it % kStages];
+    const float* sL = sStat[it % kStages][0];
+    const float* sDl = sStat[it % kStages][1];
     const int q0 = (qt_begin + it % per_head) * BQ;
-    if (it + 1 < n_iter) load(it + 1);
     const int64_t qa_last = p.q_offset + min(q0 + BQ - 1, p.Sq - 1);
     bool live[KT], need_mask[KT];
     bool any = false;
@@ -833,8 +863,8 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
     for (int mq = 0; mq < 4; ++mq) {
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 aq = ld8(sQ + (mq * 16 + l16) * LDQ + ks * 32 + g * 8);
-        const bf16x8 ad = ld8(sD + (mq * 16 + l16) * LDQ + ks * 32 + g * 8);
+        const bf16x8 aq = Tile::row8(tq, mq * 16 + l16, ks * 32 + g * 8);
+        const bf16x8 ad = Tile::row8(td, mq * 16 + l16, ks * 32 + g * 8);
 #pragma unroll
         for (int j = 0; j < KT; ++j)
           if (live[j]) {
@@ -847,8 +877,10 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
 #pragma unroll
     for (int j = 0; j < KT; ++j) {
       if (!live[j]) continue;
-      // smallest tile-relative query index that sees this lane's key (BQ: none)
+      // tile-relative queries [qmin, qend) see this lane's key (qend: the
+      // queries past Sq, whose zero-filled rows must not count)
       int qmin = 0;
+      const int qend = min(BQ, p.Sq - q0);
       if (need_mask[j]) {
         const int key = kbase + 64 * j + l16;
         int64_t f = p.causal ? koff + key - p.q_offset - q0 : 0;
@@ -861,7 +893,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
         for (int e = 0; e < 4; ++e) {
           const int ql = mq * 16 + g * 4 + e;
           float pv = fast_exp2(fmaf(s[mq][j][e], c, -sL[ql]));
-          pv = ql < qmin ? 0.f : pv;
+          pv = (ql < qmin || ql >= qend) ? 0.f : pv;
           s[mq][j][e] = pv;
           dp[mq][j][e] = pv * (dp[mq][j][e] - sDl[ql]);
         }
@@ -879,8 +911,8 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
     for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
-        const bf16x8 bd = ld4x2(sDt + (dt * 16 + l16) * LDT + 32 * s2 + g * 4);
-        const bf16x8 bq = ld4x2(sQt + (dt * 16 + l16) * LDT + 32 * s2 + g * 4);
+        const bf16x8 bd = Tile::col8(td, 32 * s2, dt * 16, l16, g);
+        const bf16x8 bq = Tile::col8(tq, 32 * s2, dt * 16, l16, g);
 #pragma unroll
         for (int j = 0; j < KT; ++j)
           if (live[j]) {
@@ -890,6 +922,8 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
       }
     }
   }
+  // no load may still write this workgroup's LDS when it ends
+  wait_vmcnt<0>();
   // lane holds dK[key = kbase + 64 j + 4 g + e][d = 16 dt + l16]
   bf16* dkb = static_cast<bf16*>(kv.dk[blk]) + kv_off;
   bf16* dvb = static_cast<bf16*>(kv.dv[blk]) + kv_off;
@@ -1226,7 +1260,7 @@ extern "C" int nmb_attn_bwd_workspace_bytes(int64_t batch, int64_t q_heads, int6
                                             size_t* bytes) {
   NMB_REQUIRE(bytes != nullptr && batch >= 0 && q_heads >= 0 && seq_q >= 0,
               "attn_bwd_workspace_bytes: bad args");
-  *bytes = static_cast<size_t>(batch * q_heads * seq_q) * sizeof(float);
+  *bytes = 2 * static_cast<size_t>(batch * q_heads * seq_q) * sizeof(float);
   return NMB_OK;
 }
 
@@ -1256,16 +1290,24 @@ int attn_bwd_impl(const void* q, const void* const* k_blocks,
     kv.dk[i] = dk_blocks[i];
     kv.dv[i] = dv_blocks[i];
   }
-  const size_t need = static_cast<size_t>(batch * q_heads * seq_q) * sizeof(float);
+  const size_t need = 2 * static_cast<size_t>(batch * q_heads * seq_q) * sizeof(float);
   NMB_REQUIRE(workspace != nullptr && workspace_bytes >= need,
               "attn_bwd: workspace of %zu bytes is smaller than the %zu required",
               workspace_bytes, need);
   if (batch == 0) return NMB_OK;
+  // workspace: delta [B, Hq, Sq], then the log2-domain lse [B, Hq, Sq]
   float* delta = static_cast<float*>(workspace);
+  float* lse2 = delta + batch * q_heads * seq_q;
   const int D = static_cast<int>(head_dim);
   if (dtype == NMB_BF16) {
     NMB_REQUIRE(nmb::aligned16(dq) && nmb::aligned16(dout) && nmb::aligned16(o),
                 "attn_bwd: dq/dout/o must be 16-byte aligned");
+    // the kernels address K/V, Q and dO through 32-bit buffer offsets
+    NMB_REQUIRE_SUPPORTED(
+        (seq_k == 0 || ((seq_k - 1) * kv_strides[1] + head_dim) * 2 < (int64_t{1} << 31)) &&
+            (seq_q == 0 || (((seq_q - 1) * q_strides[1] + head_dim) * 2 < (int64_t{1} << 31) &&
+                            ((seq_q - 1) * o_strides[1] + head_dim) * 2 < (int64_t{1} << 31))),
+        "attn_bwd: a Q, dO or K/V block spans more than 2 GiB");
     const nmb::bf16* qp = static_cast<const nmb::bf16*>(q);
     const nmb::bf16* opp = static_cast<const nmb::bf16*>(o);
     const nmb::bf16* dp = static_cast<const nmb::bf16*>(dout);
@@ -1281,7 +1323,7 @@ int attn_bwd_impl(const void* q, const void* const* k_blocks,
       const RopeGrad rg = rope != nullptr ? *rope : RopeGrad{};
 #define NMB_DQ(DD, RR)                                                                          \
   hipLaunchKernelGGL((nmb::attn_bwd_dq_kernel<DD, RR>), dim3(blocks), dim3(256), 0, stream, qp, kv, \
-                     opp, dp, lse, delta, dqp, p, n_qt, static_cast<int>(items), per_xcd, rg)
+                     opp, dp, lse, delta, lse2, dqp, p, n_qt, static_cast<int>(items), per_xcd, rg)
       if (D == 64) {
         if (rope) NMB_DQ(64, true); else NMB_DQ(64, false);
       } else {
@@ -1300,7 +1342,7 @@ int attn_bwd_impl(const void* q, const void* const* k_blocks,
       const RopeGrad rg = rope != nullptr ? *rope : RopeGrad{};
 #define NMB_DKDV(DD, RR)                                                                          \
   hipLaunchKernelGGL((nmb::attn_bwd_dkdv_kernel<DD, RR>), dim3(blocks), dim3(256), 0, stream, qp, kv, \
-                     dp, lse, delta, p, n_kt, static_cast<int>(items), per_xcd, rg)
+                     dp, lse2, delta, p, n_kt, static_cast<int>(items), per_xcd, rg)
       if (D == 64) {
         if (rope) NMB_DKDV(64, true); else NMB_DKDV(64, false);
       } else {

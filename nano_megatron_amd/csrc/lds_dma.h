@@ -42,6 +42,17 @@ __device__ __forceinline__ void load_lds16(const i32x4& r, const bf16* lds, uint
                : "memory");
 }
 
+// 4 bytes per lane from buffer offset voff into LDS at byte address
+// lds + 4 * lane (as load_lds16).
+__device__ __forceinline__ void load_lds4(const i32x4& r, const void* lds, uint32_t voff) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)(const_cast<void*>(lds)))));
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :
+               : "s"(m0), "v"(voff), "s"(r)
+               : "memory");
+}
+
 // s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt bits [3:0] and [15:14]; expcnt and
 // lgkmcnt left at their maxima).
 template <int N>
