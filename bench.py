@@ -153,6 +153,7 @@ def kernel_rooflines(device, only: str | None = None) -> list[dict]:
     x = randn(T, H)
     w = (1 + randn(H, scale=0.02).float()).to(bf)
     dy = randn(T, H)
+    dres = randn(T, H)
     qkv = randn(T, 3 * H)
     q = qkv[:, :H].view(BATCH, SEQ, nh, d)
     k = qkv[:, H:2 * H].view(BATCH, SEQ, nh, d)
@@ -191,8 +192,15 @@ def kernel_rooflines(device, only: str | None = None) -> list[dict]:
         nbytes = (m * k + k * n + m * n * (2 if residual else 1)) * E
         return (name, fn, nbytes, 2.0 * m * n * k, "mfma", per_step)
 
+    # the Q/K/V projection with RoPE of q and k in its epilogue, as the block runs it
+    w_qkv = randn(3 * H, H)
+    qkv_out = torch.empty(T, 3 * H, dtype=bf, device=device)
+    qkv_rope = ("gemm_qkv_rope",
+                lambda: Fn.mm_rope(x, w_qkv.t(), seq=SEQ, head_dim=d, rope_cols=2 * H, cos=tab.cos, sin=tab.sin,
+                                   out=qkv_out),
+                (T * H + 3 * H * H + 3 * T * H) * E, 2.0 * T * 3 * H * H, "mfma", 2 * L)
     gemms = [
-        gemm_case("gemm_qkv", T, 3 * H, H, False, False, 2 * L),
+        qkv_rope,
         gemm_case("gemm_o_residual", T, H, H, False, False, 2 * L, residual=True),
         gemm_case("gemm_gate_up", T, 2 * F, H, False, False, 2 * L),
         gemm_case("gemm_down_residual", T, H, F, False, False, L, residual=True),
@@ -211,16 +219,21 @@ def kernel_rooflines(device, only: str | None = None) -> list[dict]:
     cases = [
         # name, fn, algorithmic bytes, flops, bound, launches per training step (full recompute)
         ("rmsnorm_fwd", lambda: Fn.rmsnorm_fwd(x, w, 1e-5), 2 * T * H * E + H * E, 0, "hbm", 4 * L + 1),
-        ("rmsnorm_bwd", lambda: Fn.rmsnorm_bwd(x, w, dy, 1e-5), 3 * T * H * E + 2 * H * E, 0, "hbm", 2 * L + 1),
-        ("rope_apply", lambda: Fn.rope_apply(q, rope_out, tab.cos, tab.sin), 2 * T * H * E, 0, "hbm", 2 * L),
+        # in the block the norm backward also adds the residual branch's gradient
+        ("rmsnorm_bwd", lambda: Fn.rmsnorm_bwd(x, w, dy, 1e-5, residual_grad=dres), 4 * T * H * E + 2 * H * E, 0,
+         "hbm", 2 * L + 1),
+        # the standalone rotary kernel; the step fuses RoPE into the QKV GEMM and the attention backward
+        ("rope_apply", lambda: Fn.rope_apply(q, rope_out, tab.cos, tab.sin), 2 * T * H * E, 0, "hbm", 0),
         ("swiglu_fwd", lambda: Fn.swiglu_fwd(gate, up, act), 3 * T * F * E, 0, "hbm", L),
         ("swiglu_bwd", lambda: Fn.swiglu_bwd(gate, up, dh, dgu[:, :F], dgu[:, F:], act), 6 * T * F * E, 0, "hbm", L),
         ("attn_fwd", lambda: Fn.attn_fwd_bshd(q, [k], [v], (0,), causal=True, q_offset=0, scale=None, out=o, lse=lse),
-         4 * T * H * E + BATCH * nh * SEQ * 4, causal_flops, "hbm", 2 * L),
+         4 * T * H * E + BATCH * nh * SEQ * 4, causal_flops, "mfma", 2 * L),
         ("attn_fwd_from_lse", lambda: Fn.attn_fwd_from_lse_bshd(q, [k], [v], (0,), lse, causal=True, q_offset=0, scale=None, out=o),
-         4 * T * H * E + BATCH * nh * SEQ * 4, causal_flops, "hbm", 0),
-        ("attn_bwd", lambda: Fn.attn_bwd_bshd(q, [k], [v], (0,), o, do, lse, dq, [dk], [dv], causal=True, q_offset=0, scale=None),
-         8 * T * H * E + BATCH * nh * SEQ * 4, 2.5 * causal_flops, "hbm", L),
+         4 * T * H * E + BATCH * nh * SEQ * 4, causal_flops, "mfma", 0),
+        # the backward with the inverse RoPE of dq and dk in its stores, as the block runs it
+        ("attn_bwd_rope", lambda: Fn.attn_bwd_rope_bshd(q, k, v, o, do, lse, dq, dk, dv, causal=True, q_offset=0,
+                                                        scale=None, cos=tab.cos, sin=tab.sin),
+         8 * T * H * E + BATCH * nh * SEQ * 4, 2.5 * causal_flops, "mfma", L),
         ("ce_fwd", lambda: Fn.ce_fwd(logits, targets, -100, loss, lse_c), chunk * V * E + chunk * 16, 0, "hbm", T // chunk),
         ("ce_bwd", lambda: Fn.ce_bwd_(logits, targets, -100, lse_c, grad_c), 2 * chunk * V * E + chunk * 16, 0, "hbm", T // chunk),
     ] + gemms

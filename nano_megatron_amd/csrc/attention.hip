@@ -457,8 +457,7 @@ __global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_ke
         for (int mk = 0; mk < 4; ++mk)
 #pragma unroll
           for (int e = 0; e < 4; ++e) tmax = fmaxf(tmax, s[mk][e]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        tmax = xor32_max(xor16_max(tmax));
         const float mnew = fmaxf(m[t], tmax);
         const bool dead = mnew == -__builtin_inff();
         const float alpha = dead ? 1.f : fast_exp2((m[t] - mnew) * c);
@@ -472,8 +471,7 @@ __global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_ke
             s[mk][e] = pv;
             rs += pv;
           }
-        rs += __shfl_xor(rs, 16, 64);
-        rs += __shfl_xor(rs, 32, 64);
+        rs = xor32_sum(xor16_sum(rs));
         l[t] = l[t] * alpha + rs;
         m[t] = mnew;
         if (__any(alpha != 1.f)) {  // wave-uniform: skip the rescale when no max moved
@@ -586,8 +584,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
 #pragma unroll
       for (int e = 0; e < 8; ++e) part += static_cast<float>(df[t][ks][e]) * static_cast<float>(of[e]);
     }
-    part += __shfl_xor(part, 16, 64);
-    part += __shfl_xor(part, 32, 64);
+    part = xor32_sum(xor16_sum(part));
     dl[t] = part;
     lse2[t] = ok ? lse_to_log2(lb[qi]) : __builtin_inff();
     // delta and the log2-domain lse for the dK/dV kernel, which runs next

@@ -45,16 +45,50 @@ template <typename T> __device__ __forceinline__ float round_as(float x) {
 __device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
 __device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
 
+// Cross-lane exchanges without an LDS round trip (ds_bpermute costs a full LDS
+// latency per step).  v_permlane32_swap a, b swaps the upper 32 lanes of a
+// with the lower 32 lanes of b, so with a = b = v it leaves a = [v_lo, v_lo]
+// and b = [v_hi, v_hi]; v_permlane16_swap does the same for the odd 16-lane
+// rows of a and the even rows of b.  Written as inline asm: this compiler
+// folds the builtin's second result into the first when both operands are the
+// same value.  The s_nops give the VALU-to-permlane distances.
+__device__ __forceinline__ void permlane32_swap(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void permlane16_swap(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+// v + v of lane l ^ 16 (resp. l ^ 32), and the max of the two, in every lane
+__device__ __forceinline__ float xor16_sum(float v) { float a = v, b = v; permlane16_swap(a, b); return a + b; }
+__device__ __forceinline__ float xor32_sum(float v) { float a = v, b = v; permlane32_swap(a, b); return a + b; }
+__device__ __forceinline__ float xor16_max(float v) { float a = v, b = v; permlane16_swap(a, b); return fmaxf(a, b); }
+__device__ __forceinline__ float xor32_max(float v) { float a = v, b = v; permlane32_swap(a, b); return fmaxf(a, b); }
+
+// DPP source of lane l within its 16-lane row: quad_perm [1,0,3,2] (l ^ 1),
+// quad_perm [2,3,0,1] (l ^ 2), row_half_mirror (7 - l within 8), row_mirror
+// (15 - l within 16)
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 64 lanes, the same bits in every lane (each step adds two
+// values that every lane of a group sees in some order, and IEEE addition is
+// commutative): pairs, quads, half rows, rows by DPP; then rows by permlane.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  return v;
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  v += dpp<0x140>(v);
+  return xor32_sum(xor16_sum(v));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-  return v;
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  return xor32_max(xor16_max(v));
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

@@ -67,24 +67,42 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const T* __restrict__ 
   if (rstd != nullptr && lane == 0) rstd[row] = r;
 }
 
-// Backward: 8 wavefronts per workgroup, each owning rows r0 + wave, r0 + wave
-// + 8, ...; two rows are processed per iteration so their loads overlap.
+// Backward: 8 wavefronts per workgroup; the workgroup walks its rows in groups
+// of 8 x rows_per_wave, wave w taking rows w, w + 8, w + 16, ... of a group.
+// A wave issues the loads of all its rows of a group (x, dy and the residual
+// gradient, 8 rows' worth of 16-byte vectors per lane) before it computes any,
+// so one memory latency covers several rows and a CU keeps ~200 KB of reads in
+// flight.
 constexpr int kBwdWaves = 8;
+constexpr int rows_per_wave(int iters) { return iters <= 2 ? 4 : 1; }
 
+template <typename T>
+__device__ __forceinline__ void unpack(const uint4& raw, float (&out)[VecTraits<T>::N]) {
+  T e[VecTraits<T>::N];
+  __builtin_memcpy(e, &raw, 16);
+#pragma unroll
+  for (int i = 0; i < VecTraits<T>::N; ++i) out[i] = to_f32(e[i]);
+}
+
+// One row: dx = rstd * (g - n * mean(g * n)) (+ the residual gradient), with
+// g = round(dy * w) and n = x * rstd; acc += round(dy * round(n)) (the weight
+// gradient's per-row term, rounded as the reference's product tensor is).
 template <typename T, int ITERS>
-__device__ __forceinline__ void bwd_row(const T* __restrict__ xr, const T* __restrict__ dyr,
-                                        const T* __restrict__ dresr, T* __restrict__ dxr,
+__device__ __forceinline__ void bwd_row(const uint4 (&xr)[ITERS], const uint4 (&dr)[ITERS],
+                                        const uint4 (&rr)[ITERS], bool has_res,
                                         const float (&wv)[ITERS][VecTraits<T>::N],
-                                        float (&acc)[ITERS][VecTraits<T>::N],
-                                        float (&xv)[ITERS][VecTraits<T>::N],
-                                        float (&dv)[ITERS][VecTraits<T>::N], int lane, int cols,
-                                        float eps) {
+                                        float (&acc)[ITERS][VecTraits<T>::N], T* __restrict__ dxr,
+                                        int lane, int cols, float eps) {
   constexpr int V = VecTraits<T>::N;
+  float xv[ITERS][V], dv[ITERS][V];
   float ss = 0.f;
 #pragma unroll
-  for (int it = 0; it < ITERS; ++it)
+  for (int it = 0; it < ITERS; ++it) {
+    unpack<T>(xr[it], xv[it]);
+    unpack<T>(dr[it], dv[it]);
 #pragma unroll
     for (int i = 0; i < V; ++i) ss += xv[it][i] * xv[it][i];
+  }
   ss = wave_sum(ss);
   const float r = inv_rms<T>(ss, cols, eps);
   float dot = 0.f;
@@ -95,8 +113,6 @@ __device__ __forceinline__ void bwd_row(const T* __restrict__ xr, const T* __res
       const float n = mul_rn(xv[it][i], r);
       const float g = round_as<T>(mul_rn(dv[it][i], wv[it][i]));
       dot += g * n;
-      // weight gradient of y = cast(n) * w: dy * cast(n), rounded as the
-      // reference's per-element product tensor is.
       acc[it][i] += round_as<T>(mul_rn(dv[it][i], round_as<T>(n)));
       xv[it][i] = n;
       dv[it][i] = g;
@@ -111,9 +127,9 @@ __device__ __forceinline__ void bwd_row(const T* __restrict__ xr, const T* __res
       float o[V];
 #pragma unroll
       for (int i = 0; i < V; ++i) o[i] = r * (dv[it][i] - xv[it][i] * mean_dot);
-      if (dresr != nullptr) {
+      if (has_res) {
         float rv[V];
-        load_vec<T>(dresr + c, rv);
+        unpack<T>(rr[it], rv);
 #pragma unroll
         for (int i = 0; i < V; ++i) o[i] += rv[i];
       }
@@ -156,25 +172,29 @@ __global__ __launch_bounds__(512) void rmsnorm_bwd_kernel(
     for (int i = 0; i < V; ++i) acc[it][i] = 0.f;
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rows_per_block;
   const int64_t r1 = min(rows, r0 + rows_per_block);
-  int64_t row = r0 + wave;
-  for (; row + kBwdWaves < r1; row += 2 * kBwdWaves) {
-    const int64_t rb = row + kBwdWaves;
-    float xa[ITERS][V], da[ITERS][V], xb[ITERS][V], db[ITERS][V];
-    load_row<T, ITERS>(x + row * cols, xa, lane, cols);
-    load_row<T, ITERS>(dy + row * cols, da, lane, cols);
-    load_row<T, ITERS>(x + rb * cols, xb, lane, cols);
-    load_row<T, ITERS>(dy + rb * cols, db, lane, cols);
-    bwd_row<T, ITERS>(x + row * cols, dy + row * cols, dres ? dres + row * cols : nullptr,
-                      dx + row * cols, wv, acc, xa, da, lane, cols, eps);
-    bwd_row<T, ITERS>(x + rb * cols, dy + rb * cols, dres ? dres + rb * cols : nullptr,
-                      dx + rb * cols, wv, acc, xb, db, lane, cols, eps);
-  }
-  if (row < r1) {
-    float xa[ITERS][V], da[ITERS][V];
-    load_row<T, ITERS>(x + row * cols, xa, lane, cols);
-    load_row<T, ITERS>(dy + row * cols, da, lane, cols);
-    bwd_row<T, ITERS>(x + row * cols, dy + row * cols, dres ? dres + row * cols : nullptr,
-                      dx + row * cols, wv, acc, xa, da, lane, cols, eps);
+  const bool has_res = dres != nullptr;
+  constexpr int kRowsPerWave = rows_per_wave(ITERS);
+  for (int64_t base = r0; base < r1; base += kBwdWaves * kRowsPerWave) {
+    uint4 xr[kRowsPerWave][ITERS], dr[kRowsPerWave][ITERS], rr[kRowsPerWave][ITERS];
+#pragma unroll
+    for (int k = 0; k < kRowsPerWave; ++k) {
+      const int64_t row = base + wave + kBwdWaves * k;
+#pragma unroll
+      for (int it = 0; it < ITERS; ++it) {
+        const int c = (it * 64 + lane) * V;
+        const bool ok = row < r1 && c < cols;
+        const int64_t o = row * cols + c;
+        xr[k][it] = ok ? *reinterpret_cast<const uint4*>(x + o) : uint4{0, 0, 0, 0};
+        dr[k][it] = ok ? *reinterpret_cast<const uint4*>(dy + o) : uint4{0, 0, 0, 0};
+        rr[k][it] = ok && has_res ? *reinterpret_cast<const uint4*>(dres + o) : uint4{0, 0, 0, 0};
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kRowsPerWave; ++k) {
+      const int64_t row = base + wave + kBwdWaves * k;
+      if (row < r1)  // wave-uniform
+        bwd_row<T, ITERS>(xr[k], dr[k], rr[k], has_res, wv, acc, dx + row * cols, lane, cols, eps);
+    }
   }
   // fold the 8 wave partials in two rounds through 4 LDS rows (<= 64 KiB)
   const int slot = wave & 3;

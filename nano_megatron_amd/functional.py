@@ -99,7 +99,8 @@ def mm(a: Tensor, b: Tensor, *, out: Tensor | None = None, c: Tensor | None = No
 
 
 def mm_rope(a: Tensor, b: Tensor, *, seq: int, head_dim: int, rope_cols: int, cos: Tensor,
-            sin: Tensor, pos_offset: int = 0, positions: Tensor | None = None) -> Tensor:
+            sin: Tensor, pos_offset: int = 0, positions: Tensor | None = None,
+            out: Tensor | None = None) -> Tensor:
     """``a @ b`` with RoPE applied to the first ``rope_cols`` output columns
     (heads of ``head_dim``; row r is token (r // seq, r % seq)), as the Q/K/V
     projection followed by the rotary embedding of q and k
@@ -112,12 +113,15 @@ def mm_rope(a: Tensor, b: Tensor, *, seq: int, head_dim: int, rope_cols: int, co
         raise ValueError("mm_rope: rope_cols must be whole heads within N and M = batch x seq")
     if a.dtype != torch.bfloat16 or head_dim not in (64, 128):
         # the fused epilogue covers bf16 heads of 64 and 128; otherwise GEMM, then rotary kernel
-        out = mm(a, b)
+        out = mm(a, b, out=out)
         x = out.view(m // seq, seq, n)[:, :, :rope_cols].unflatten(2, (rope_cols // head_dim, head_dim))
         rope_apply(x, x, cos, sin, pos_offset=pos_offset, positions=positions)
         return out
     _require_gpu(a, b, cos, sin)
-    out = torch.empty(m, n, dtype=a.dtype, device=a.device)
+    if out is None:
+        out = torch.empty(m, n, dtype=a.dtype, device=a.device)
+    elif out.shape != (m, n) or out.dtype != a.dtype or out.stride(1) != 1:
+        raise ValueError("mm_rope: out must be a row-major [M, N] tensor of a's dtype")
     la, lda = _operand_layout(a, 0)
     if la != 0:
         raise ValueError("mm_rope: a must be row-major")
