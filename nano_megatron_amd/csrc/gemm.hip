@@ -463,23 +463,29 @@ Plan plan_for(int64_t m, int64_t n, int64_t k, bool a_kc, bool b_kc, int rope_he
   const bool small = (!a_kc && !b_kc) || big_tiles < kCUs;
   Plan best{small ? 2 : 1, 1, 0};
   double best_t = -1.0;
-  for (int c = 0; c < static_cast<int>(sizeof(kConfigs) / sizeof(kConfigs[0])); ++c) {
-    const Config& cf = kConfigs[c];
-    // the RoPE epilogue needs whole heads per wavefront and no K split
-    if (rope_head_dim > 0 ? wave_cols(cf) % rope_head_dim != 0 : (cf.nw == 4) != small) continue;
-    const int64_t slots = cf.nw == 4 ? 2 * kCUs : kCUs;
-    const int64_t tiles = ((m + cf.tbm - 1) / cf.tbm) * ((n + cf.tbn - 1) / cf.tbn);
-    const int64_t kt = std::max<int64_t>((k + cf.bkt - 1) / cf.bkt, 1);  // K tiles
-    for (int64_t s = 1; s <= (small && rope_head_dim == 0 ? 16 : 1); ++s) {
-      const int64_t tps = (kt + s - 1) / s;  // K tiles per split
-      const int64_t splits = (kt + tps - 1) / tps;
-      if (splits != s || (s > 1 && tps * cf.bkt < 512)) continue;
-      const int64_t rounds = (tiles * splits + slots - 1) / slots;
-      double t = static_cast<double>(rounds) * 2.0 * cf.tbm * cf.tbn * (tps * cf.bkt) / cf.rate;
-      if (splits > 1) t += static_cast<double>(splits) * m * n * 8 / kBytesPerS;
-      if (best_t < 0 || t < best_t * 0.999) {
-        best_t = t;
-        best = Plan{c, static_cast<int>(splits), static_cast<int>(tps * cf.bkt)};
+  // pass 0: the configurations of the problem's size class; pass 1 (RoPE only,
+  // when none of those fits the head): any configuration that fits
+  for (int pass = 0; pass < 2 && best_t < 0; ++pass) {
+    for (int c = 0; c < static_cast<int>(sizeof(kConfigs) / sizeof(kConfigs[0])); ++c) {
+      const Config& cf = kConfigs[c];
+      // the RoPE epilogue needs whole heads per wavefront and no K split
+      if (pass == 0 && (cf.nw == 4) != small) continue;
+      if (rope_head_dim > 0 && wave_cols(cf) % rope_head_dim != 0) continue;
+      if (pass == 1 && rope_head_dim == 0) continue;
+      const int64_t slots = cf.nw == 4 ? 2 * kCUs : kCUs;
+      const int64_t tiles = ((m + cf.tbm - 1) / cf.tbm) * ((n + cf.tbn - 1) / cf.tbn);
+      const int64_t kt = std::max<int64_t>((k + cf.bkt - 1) / cf.bkt, 1);  // K tiles
+      for (int64_t s = 1; s <= (small && rope_head_dim == 0 ? 16 : 1); ++s) {
+        const int64_t tps = (kt + s - 1) / s;  // K tiles per split
+        const int64_t splits = (kt + tps - 1) / tps;
+        if (splits != s || (s > 1 && tps * cf.bkt < 512)) continue;
+        const int64_t rounds = (tiles * splits + slots - 1) / slots;
+        double t = static_cast<double>(rounds) * 2.0 * cf.tbm * cf.tbn * (tps * cf.bkt) / cf.rate;
+        if (splits > 1) t += static_cast<double>(splits) * m * n * 8 / kBytesPerS;
+        if (best_t < 0 || t < best_t * 0.999) {
+          best_t = t;
+          best = Plan{c, static_cast<int>(splits), static_cast<int>(tps * cf.bkt)};
+        }
       }
     }
   }
