@@ -96,85 +96,10 @@ __device__ __forceinline__ bf16x8 zero8() {
 
 __device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 
-// Two 4-element halves at p and p + 16 (the key permutation of a 32-deep MFMA
-// K index: lane group g holds keys 4g..4g+3 and 16+4g..16+4g+3).
-__device__ __forceinline__ bf16x8 ld4x2(const bf16* p) {
-  const bf16x4 lo = *reinterpret_cast<const bf16x4*>(p);
-  const bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + 16);
-  bf16x8 r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    r[i] = lo[i];
-    r[4 + i] = hi[i];
-  }
-  return r;
-}
-
 // exp2 as the raw v_exp_f32: results below 2^-126 flush to 0, which is
 // immaterial for softmax weights (the library exp2 adds a 5-instruction
 // denormal range fix-up around every exponential).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// A thread's share of an R x D bf16 tile, read from global memory as pairs of
-// rows (16 bytes of each row per item, consecutive lanes on consecutive
-// 16-byte chunks of a row, so the reads are coalesced).  One read feeds both
-// the row-major LDS copy and the transposed copy (written as 32-bit words
-// holding the two rows' values).  Loading into registers ahead of use lets a
-// tile's global reads overlap the MFMA work on the previous tile.
-template <int R, int D>
-struct PairTile {
-  static constexpr int kChunks = D / 8;
-  static constexpr int kItems = (R / 2) * kChunks;
-  static constexpr int kPer = (kItems + 255) / 256;
-  bf16x8 a[kPer], b[kPer];
-
-  __device__ __forceinline__ void load(const bf16* __restrict__ src, int64_t row_stride, int r0,
-                                       int nrows) {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int c = threadIdx.x + 256 * i;
-      const int dc = c % kChunks, rp = c / kChunks;
-      const int ra = r0 + 2 * rp;
-      a[i] = zero8();
-      b[i] = zero8();
-      if (c < kItems) {
-        if (ra < nrows) a[i] = ld8(src + static_cast<int64_t>(ra) * row_stride + dc * 8);
-        if (ra + 1 < nrows) b[i] = ld8(src + static_cast<int64_t>(ra + 1) * row_stride + dc * 8);
-      }
-    }
-  }
-
-  template <int LD>
-  __device__ __forceinline__ void store_rows(bf16* __restrict__ dst) const {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int c = threadIdx.x + 256 * i;
-      const int dc = c % kChunks, rp = c / kChunks;
-      if (c < kItems) {
-        *reinterpret_cast<bf16x8*>(dst + (2 * rp) * LD + dc * 8) = a[i];
-        *reinterpret_cast<bf16x8*>(dst + (2 * rp + 1) * LD + dc * 8) = b[i];
-      }
-    }
-  }
-
-  template <int LD>
-  __device__ __forceinline__ void store_cols(bf16* __restrict__ dst) const {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int c = threadIdx.x + 256 * i;
-      const int dc = c % kChunks, rp = c / kChunks;
-      if (c < kItems) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          bf16 pr[2] = {a[i][e], b[i][e]};
-          uint32_t w;
-          __builtin_memcpy(&w, pr, 4);
-          *reinterpret_cast<uint32_t*>(dst + (dc * 8 + e) * LD + 2 * rp) = w;
-        }
-      }
-    }
-  }
-};
 
 // Number of 64-key tiles of a block that any query up to absolute position
 // q_last can see.
@@ -238,14 +163,13 @@ __device__ __forceinline__ int mask_limit(const AttnShape& p, int64_t koff, int 
 }
 
 // ---------------------------------------------------------------- forward
-// Workgroup = 4 wavefronts x TQ column tiles of 16 queries of one (batch,
-// head): column tile t of wave w holds queries 64 t + 16 w .. +15 of the
-// workgroup's 64 TQ queries, so under causal masking every wave sees about the
-// same keys (balanced), and a tile whose first key lies beyond all queries of
-// a column tile is skipped for that column tile (wave-uniform).  K/V stream
-// through LDS in 64-key tiles; the next tile's global reads are issued before
-// the current tile's MFMA work.  Scores stay raw; exp2(s * c - m * c) folds
-// the softmax scale into one FMA per score.
+// Workgroup = NWV wavefronts x TQ column tiles of 16 queries of one (batch,
+// head): column tile t of wave w holds queries 16 NWV t + 16 w .. +15 of the
+// workgroup's 16 NWV TQ queries, so under causal masking every wave sees about
+// the same keys (balanced), and a tile whose first key lies beyond all queries
+// of a column tile is skipped for that column tile (wave-uniform).  K/V stream
+// through LDS in 64-key tiles, three tiles ahead of the one computed.  Scores
+// stay raw; exp2(s * c - m * c) folds the softmax scale into one FMA per score.
 // log2-domain lse for P = exp2(S * scale_log2 - lse2); a query with no visible
 // key (lse = -inf) maps to +inf so that every P of its row is 0.
 __device__ __forceinline__ float lse_to_log2(float v) {
@@ -265,7 +189,6 @@ __device__ __forceinline__ float lse_to_log2(float v) {
 template <int D>
 struct Tile64 {
   static constexpr int kElems = 64 * D;
-  static constexpr int kPer = kElems * 2 / 1024 / 4;  // 1 KB loads per wave per tile (4 waves)
   // rows of a 16-lane group take 16 distinct (row parity, slot) pairs; the 8
   // rows of a half-wave column read take 8 distinct (row parity, slot pair)s
   __device__ static int swz(int r) {
@@ -281,13 +204,14 @@ struct Tile64 {
   }
 };
 
-// One wave's share of the direct loads of a 64-row tile: load j fills LDS
-// bytes [1024 (wave kPer + j), + 1024) of the tile; lane l's 16 bytes are
-// chunk slot s of row r there, read from global chunk s ^ swz(r).
-template <int D>
+// One wave's share (of NW waves) of the direct loads of a 64-row tile: load j
+// fills LDS bytes [1024 (wave P + j), + 1024) of the tile; lane l's 16 bytes
+// are chunk slot s of row r there, read from global chunk s ^ swz(r).
+template <int D, int NW = 4>
 struct TileStream {
   using Tile = Tile64<D>;
-  static constexpr int P = Tile::kPer;
+  static constexpr int P = Tile::kElems * 2 / 1024 / NW;  // 1 KB loads per wave per tile
+  static_assert(P >= 1 && Tile::kElems * 2 % (1024 * NW) == 0, "a tile splits evenly over the waves");
   uint32_t off[P];  // byte offset from row 0 of the tile
   int row[P];
 
@@ -314,14 +238,21 @@ struct TileStream {
 // FL (from LSE): the softmax statistics are given (lse read, not written), so
 // P = exp2(S * scale_log2 - lse2) directly: no running maximum, rescale or
 // row sum, and O = P V needs no final division.
-template <int D, int TQ, bool FL>
-__global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_kernel(
+//
+// NWV wavefronts per workgroup (4 or 8).  With 8 at head dim 64 a workgroup
+// holds 512 queries, all of one (batch, head) at sequence length 512, so a CU
+// runs one head's whole causal triangle with every wave busy to the end,
+// instead of a light and a heavy query tile whose light half leaves one wave
+// per SIMD for the second half.
+template <int D, int TQ, int NWV, bool FL>
+__global__ __launch_bounds__(64 * NWV, (D == 64 && TQ <= 4 && NWV == 4) ? 2 : 1) void attn_fwd_kernel(
     const bf16* __restrict__ q, KVBlocks kv, bf16* __restrict__ o, float* __restrict__ lse,
     AttnShape p, int n_qt, int items, int per_xcd) {
-  constexpr int BQ = 64 * TQ, BK = 64, KS = D / 32, DT = D / 16;
+  constexpr int CT = 16 * NWV;  // query stride between a wave's column tiles
+  constexpr int BQ = CT * TQ, BK = 64, KS = D / 32, DT = D / 16;
   constexpr int kStages = 4;
   using Tile = Tile64<D>;
-  constexpr int kLoads = 2 * Tile::kPer;  // this wave's loads per K/V tile pair
+  constexpr int kLoads = 2 * TileStream<D, NWV>::P;  // this wave's loads per K/V tile pair
   __shared__ __attribute__((aligned(1024))) bf16 sK[kStages][Tile::kElems];
   __shared__ __attribute__((aligned(1024))) bf16 sV[kStages][Tile::kElems];
 
@@ -334,14 +265,14 @@ __global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_ke
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int l16 = lane & 15, g = lane >> 4;
   const int hk = h / (p.Hq / p.Hkv);
-  const int qbase = qt * BQ + 16 * wave;  // column tile t: qbase + 64 t + l16
+  const int qbase = qt * BQ + 16 * wave;  // column tile t: qbase + CT t + l16
   const float c = p.scale_log2;
 
   const bf16* qb = q + b * p.q_sb + h * p.q_sh;
   bf16x8 qf[TQ][KS];
 #pragma unroll
   for (int t = 0; t < TQ; ++t) {
-    const int qi = qbase + 64 * t + l16;
+    const int qi = qbase + CT * t + l16;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
       qf[t][ks] = qi < p.Sq ? ld8(qb + static_cast<int64_t>(qi) * p.q_ss + ks * 32 + g * 8) : zero8();
@@ -354,7 +285,7 @@ __global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_ke
     l[t] = 0.f;
     if constexpr (FL) {
       // m holds lse2 of this lane's query (+inf for a query past the end)
-      const int qi = qbase + 64 * t + l16;
+      const int qi = qbase + CT * t + l16;
       m[t] = qi < p.Sq ? lse_to_log2(lse[(static_cast<int64_t>(b) * p.Hq + h) * p.Sq + qi])
                        : __builtin_inff();
     }
@@ -366,7 +297,7 @@ __global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_ke
   // bytes from (b, key 0, hk) to the end of the last key row of a block (< 2^31, checked by the host)
   const uint32_t kv_bytes = static_cast<uint32_t>(((p.Sk - 1) * p.kv_ss + D) * 2);
   const uint32_t row_bytes = static_cast<uint32_t>(p.kv_ss * 2);
-  TileStream<D> ld;
+  TileStream<D, NWV> ld;
   ld.init(p.kv_ss, wave, lane);
 
   // compute cursor (blk, kt) and load cursor (pblk, pkt) over the visible tiles
@@ -406,9 +337,9 @@ __global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_ke
     bool live[TQ], need_mask[TQ];
 #pragma unroll
     for (int t = 0; t < TQ; ++t) {
-      const int64_t qfirst = p.q_offset + qbase + 64 * t;
-      const int64_t qlast = p.q_offset + min(qbase + 64 * t + 15, p.Sq - 1);
-      live[t] = !(p.causal && koff + k0 > qlast) && (qbase + 64 * t < p.Sq);
+      const int64_t qfirst = p.q_offset + qbase + CT * t;
+      const int64_t qlast = p.q_offset + min(qbase + CT * t + 15, p.Sq - 1);
+      live[t] = !(p.causal && koff + k0 > qlast) && (qbase + CT * t < p.Sq);
       need_mask[t] = (k0 + BK > p.Sk) || (p.causal && koff + k0 + BK - 1 > qfirst);
     }
 
@@ -436,7 +367,7 @@ __global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_ke
       float tmax = -__builtin_inff();
       if (need_mask[t]) {
         // last visible tile-relative key index of this lane's query
-        const int lim = mask_limit(p, koff, k0, p.q_offset + qbase + 64 * t + l16);
+        const int lim = mask_limit(p, koff, k0, p.q_offset + qbase + CT * t + l16);
 #pragma unroll
         for (int mk = 0; mk < 4; ++mk)
 #pragma unroll
@@ -499,7 +430,7 @@ __global__ __launch_bounds__(256, (D == 64 && TQ <= 4) ? 2 : 1) void attn_fwd_ke
   float* lb = lse + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
 #pragma unroll
   for (int t = 0; t < TQ; ++t) {
-    const int qi = qbase + 64 * t + l16;
+    const int qi = qbase + CT * t + l16;
     if (qi >= p.Sq) continue;
     const float inv = FL ? 1.f : (l[t] > 0.f ? 1.f / l[t] : 0.f);
 #pragma unroll
@@ -547,7 +478,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
   constexpr int BQ = 128, BK = 64, KS = D / 32, DT = D / 16;
   constexpr int kStages = 4;
   using Tile = Tile64<D>;
-  constexpr int kLoads = 2 * Tile::kPer;  // this wave's loads per K/V tile pair
+  constexpr int kLoads = 2 * TileStream<D>::P;  // this wave's loads per K/V tile pair
   __shared__ __attribute__((aligned(1024))) bf16 sK[kStages][Tile::kElems];
   __shared__ __attribute__((aligned(1024))) bf16 sV[kStages][Tile::kElems];
 
@@ -743,7 +674,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
   using Tile = Tile64<D>;
   // this wave's loads per query tile: Q, dO, and one 256-byte row statistic
   // (waves 0 and 2 fetch lse2, waves 1 and 3 delta)
-  constexpr int kLoads = 2 * Tile::kPer + 1;
+  constexpr int kLoads = 2 * TileStream<D>::P + 1;
   __shared__ __attribute__((aligned(1024))) bf16 sQ[kStages][Tile::kElems];
   __shared__ __attribute__((aligned(1024))) bf16 sD[kStages][Tile::kElems];
   __shared__ __attribute__((aligned(256))) float sStat[kStages][4][BQ];
@@ -1192,8 +1123,10 @@ int attn_fwd_impl(bool from_lse, const void* q, const void* const* k_blocks,
     // the forward addresses a K/V block through a 32-bit buffer offset
     NMB_REQUIRE_SUPPORTED(seq_k == 0 || ((seq_k - 1) * kv_strides[1] + head_dim) * 2 < (int64_t{1} << 31),
                           "attn_fwd: a K/V block spans more than 2 GiB");
-    // queries per workgroup: 4 waves x TQ column tiles of 16 (TQ = 4 at D 64, 2 at D 128)
-    const int bq = head_dim == 64 ? 256 : 128;
+    // queries per workgroup: NWV waves x TQ column tiles of 16 (TQ = 4 at D 64, 2 at D 128);
+    // 8 waves at D 64 once a head has 512 queries
+    const int nwv = head_dim == 64 && seq_q >= 512 ? 8 : 4;
+    const int bq = 16 * nwv * (head_dim == 64 ? 4 : 2);
     const int n_qt = static_cast<int>((seq_q + bq - 1) / bq);
     const int64_t items = static_cast<int64_t>(n_qt) * q_heads * batch;
     NMB_REQUIRE(items < (int64_t{1} << 30), "attn_fwd: problem too large for one launch");
@@ -1202,13 +1135,15 @@ int attn_fwd_impl(bool from_lse, const void* q, const void* const* k_blocks,
     xcd_grid(items, &per_xcd, &blocks);
     const nmb::bf16* qp = static_cast<const nmb::bf16*>(q);
     nmb::bf16* op = static_cast<nmb::bf16*>(o);
-#define NMB_FWD(DD, TT, FF)                                                                        \
-  hipLaunchKernelGGL((nmb::attn_fwd_kernel<DD, TT, FF>), dim3(blocks), dim3(256), 0, stream, qp, kv, \
+#define NMB_FWD(DD, TT, NW, FF)                                                                        \
+  hipLaunchKernelGGL((nmb::attn_fwd_kernel<DD, TT, NW, FF>), dim3(blocks), dim3(64 * NW), 0, stream, qp, kv, \
                      op, lse, p, n_qt, static_cast<int>(items), per_xcd)
-    if (head_dim == 64) {
-      if (from_lse) NMB_FWD(64, 4, true); else NMB_FWD(64, 4, false);
+    if (head_dim == 64 && nwv == 8) {
+      if (from_lse) NMB_FWD(64, 4, 8, true); else NMB_FWD(64, 4, 8, false);
+    } else if (head_dim == 64) {
+      if (from_lse) NMB_FWD(64, 4, 4, true); else NMB_FWD(64, 4, 4, false);
     } else {
-      if (from_lse) NMB_FWD(128, 2, true); else NMB_FWD(128, 2, false);
+      if (from_lse) NMB_FWD(128, 2, 4, true); else NMB_FWD(128, 2, 4, false);
     }
 #undef NMB_FWD
   } else {
