@@ -273,6 +273,25 @@ def test_gemm_bf16_matches_fp32_product(device, m, n, k, layout) -> None:
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("m,n,k,layout", [
+    (4100, 2056, 512, "NT"), (8192, 1032, 1024, "NN"), (2056, 4104, 264, "NN"), (3000, 5472, 1024, "NT"),
+])
+def test_gemm_bf16_many_tiles_per_workgroup(device, m, n, k, layout) -> None:
+    """Products with more output tiles than resident workgroups (each workgroup
+    then computes several tiles back to back), ragged edges and a K tail."""
+    g = torch.Generator(device=device).manual_seed(m * 7 + n + k)
+    bf = torch.bfloat16
+    a = torch.randn(m, k, device=device, generator=g).to(bf)
+    b = (torch.randn(n, k, device=device, generator=g).to(bf).t() if layout == "NT"
+         else torch.randn(k, n, device=device, generator=g).to(bf))
+    ref = a.float() @ b.float()
+    out = Fn.mm(a, b)
+    torch.testing.assert_close(out.float(), ref, rtol=2e-2, atol=2e-2 * float(ref.abs().max()))
+    # the same product twice gives the same bits
+    assert torch.equal(Fn.mm(a, b), out)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("batch,seq,hq,hkv,d,offset,explicit", [
     (4, 128, 4, 2, 64, 0, False),
     (2, 256, 2, 1, 128, 0, True),
