@@ -13,10 +13,10 @@
 //   per-lane scalars, the O^T / dQ^T accumulators are rescaled per lane, and the
 //   probabilities feed the next MFMA as its B operand straight from registers
 //   (the 32-deep K index of that MFMA is a fixed permutation of keys that the
-//   A operand, read from a transposed LDS tile, follows as well).
+//   A operand, read from LDS with transposing reads, follows as well).
 //   The dK/dV kernel uses S = Q K^T the same way with the roles of queries and
-//   keys exchanged.  K/V (or Q/dO) tiles are staged through LDS, once per
-//   workgroup; transposed copies are written as packed 32-bit key pairs.
+//   keys exchanged.  K/V (or Q/dO) tiles stream from HBM into LDS by direct
+//   loads, once per workgroup, in their row-major layout.
 //   GQA reads KV head h / (Hq / Hkv) directly; the dK/dV workgroup of a KV
 //   head loops over its query heads, so no repeat is materialised and no
 //   atomics are used (deterministic).
