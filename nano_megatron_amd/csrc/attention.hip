@@ -277,12 +277,18 @@ __global__ __launch_bounds__(64 * NWV, (D == 64 && TQ <= 4 && NWV == 4) ? 2 : 1)
     for (int ks = 0; ks < KS; ++ks)
       qf[t][ks] = qi < p.Sq ? ld8(qb + static_cast<int64_t>(qi) * p.q_ss + ks * 32 + g * 8) : zero8();
   }
-  float m[TQ], l[TQ];
-  f32x4 acc[TQ][DT];
+  // acc[t][DT] (without FL) accumulates the row sum of P: its A operand is a
+  // ones row (lane group 0, l16 == 0), so the P V MFMAs sum P and the sum is
+  // rescaled together with O
+  constexpr int NA = FL ? DT : DT + 1;
+  float m[TQ];
+  f32x4 acc[TQ][NA];
+  bf16x8 ones;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones[e] = static_cast<bf16>(l16 == 0 ? 1.f : 0.f);
 #pragma unroll
   for (int t = 0; t < TQ; ++t) {
     m[t] = -__builtin_inff();
-    l[t] = 0.f;
     if constexpr (FL) {
       // m holds lse2 of this lane's query (+inf for a query past the end)
       const int qi = qbase + CT * t + l16;
@@ -290,7 +296,7 @@ __global__ __launch_bounds__(64 * NWV, (D == 64 && TQ <= 4 && NWV == 4) ? 2 : 1)
                        : __builtin_inff();
     }
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) acc[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int dt = 0; dt < NA; ++dt) acc[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   const int64_t qa_wg_last = p.q_offset + min(qt * BQ + BQ - 1, p.Sq - 1);
   const int64_t kv_off = b * p.kv_sb + hk * p.kv_sh;
@@ -389,26 +395,23 @@ __global__ __launch_bounds__(64 * NWV, (D == 64 && TQ <= 4 && NWV == 4) ? 2 : 1)
 #pragma unroll
           for (int e = 0; e < 4; ++e) tmax = fmaxf(tmax, s[mk][e]);
         tmax = xor32_max(xor16_max(tmax));
-        const float mnew = fmaxf(m[t], tmax);
-        const bool dead = mnew == -__builtin_inff();
-        const float alpha = dead ? 1.f : fast_exp2((m[t] - mnew) * c);
-        const float mc = dead ? 0.f : mnew * c;
-        float rs = 0.f;
+        // Lazy rescaling: the running maximum m moves only when the tile's
+        // maximum exceeds it by more than 8 in the exp2 domain; otherwise P
+        // stays below 2^8 and the fp32 accumulators absorb it.  O and the row
+        // sum are rescaled together, so O / sum and m + log(sum) are unchanged.
+        const bool grow = tmax > m[t] && (m[t] == -__builtin_inff() || (tmax - m[t]) * c > 8.f);
+        if (__any(grow)) {  // wave-uniform
+          const float alpha = grow ? fast_exp2((m[t] - tmax) * c) : 1.f;  // m = -inf: alpha = 0
+          m[t] = grow ? tmax : m[t];
+#pragma unroll
+          for (int dt = 0; dt < NA; ++dt) acc[t][dt] *= alpha;
+        }
+        // no visible key yet: m = -inf, every score -inf, P = 0
+        const float mc = m[t] == -__builtin_inff() ? 0.f : m[t] * c;
 #pragma unroll
         for (int mk = 0; mk < 4; ++mk)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float pv = fast_exp2(fmaf(s[mk][e], c, -mc));
-            s[mk][e] = pv;
-            rs += pv;
-          }
-        rs = xor32_sum(xor16_sum(rs));
-        l[t] = l[t] * alpha + rs;
-        m[t] = mnew;
-        if (__any(alpha != 1.f)) {  // wave-uniform: skip the rescale when no max moved
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) acc[t][dt] *= alpha;
-        }
+          for (int e = 0; e < 4; ++e) s[mk][e] = fast_exp2(fmaf(s[mk][e], c, -mc));
       }
       bf16x8 pf[2];
 #pragma unroll
@@ -422,6 +425,10 @@ __global__ __launch_bounds__(64 * NWV, (D == 64 && TQ <= 4 && NWV == 4) ? 2 : 1)
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) acc[t][dt] = mfma16(vfr[dt][s2], pf[s2], acc[t][dt]);
+      if constexpr (!FL) {
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) acc[t][NA - 1] = mfma16(ones, pf[s2], acc[t][NA - 1]);
+      }
     }
   }
   // no load may still write this workgroup's LDS when it ends
@@ -431,8 +438,12 @@ __global__ __launch_bounds__(64 * NWV, (D == 64 && TQ <= 4 && NWV == 4) ? 2 : 1)
 #pragma unroll
   for (int t = 0; t < TQ; ++t) {
     const int qi = qbase + CT * t + l16;
+    // the row sum sits in element 0 of the sum tile in lane group 0; every
+    // lane group of the query needs it
+    float l = 0.f;
+    if constexpr (!FL) l = xor32_sum(xor16_sum(g == 0 ? acc[t][NA - 1][0] : 0.f));
     if (qi >= p.Sq) continue;
-    const float inv = FL ? 1.f : (l[t] > 0.f ? 1.f / l[t] : 0.f);
+    const float inv = FL ? 1.f : (l > 0.f ? 1.f / l : 0.f);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       bf16x4 wv;
@@ -440,7 +451,7 @@ __global__ __launch_bounds__(64 * NWV, (D == 64 && TQ <= 4 && NWV == 4) ? 2 : 1)
       for (int e = 0; e < 4; ++e) wv[e] = static_cast<bf16>(acc[t][dt][e] * inv);
       *reinterpret_cast<bf16x4*>(ob + static_cast<int64_t>(qi) * p.o_ss + dt * 16 + g * 4) = wv;
     }
-    if (!FL && g == 0) lb[qi] = l[t] > 0.f ? (m[t] * c + log2f(l[t])) * kLn2 : -__builtin_inff();
+    if (!FL && g == 0) lb[qi] = l > 0.f ? (m[t] * c + log2f(l)) * kLn2 : -__builtin_inff();
   }
 }
 
