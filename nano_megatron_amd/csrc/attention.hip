@@ -243,14 +243,16 @@ struct TileStream {
 // holds 512 queries, all of one (batch, head) at sequence length 512, so a CU
 // runs one head's whole causal triangle with every wave busy to the end,
 // instead of a light and a heavy query tile whose light half leaves one wave
-// per SIMD for the second half.
+// per SIMD for the second half.  For longer sequences (many query tiles per
+// head) two column tiles per wave and three 4-wave workgroups per CU (three
+// waves per SIMD, three LDS stages) hide more latency.
 template <int D, int TQ, int NWV, bool FL>
-__global__ __launch_bounds__(64 * NWV, (D == 64 && TQ <= 4 && NWV == 4) ? 2 : 1) void attn_fwd_kernel(
+__global__ __launch_bounds__(64 * NWV, (D == 64 && NWV == 4) ? (TQ <= 2 ? 3 : 2) : 1) void attn_fwd_kernel(
     const bf16* __restrict__ q, KVBlocks kv, bf16* __restrict__ o, float* __restrict__ lse,
     AttnShape p, int n_qt, int items, int per_xcd) {
   constexpr int CT = 16 * NWV;  // query stride between a wave's column tiles
   constexpr int BQ = CT * TQ, BK = 64, KS = D / 32, DT = D / 16;
-  constexpr int kStages = 4;
+  constexpr int kStages = (D == 64 && NWV == 4 && TQ <= 2) ? 3 : 4;  // 48 or 64 KB of LDS at D 64
   using Tile = Tile64<D>;
   constexpr int kLoads = 2 * TileStream<D, NWV>::P;  // this wave's loads per K/V tile pair
   __shared__ __attribute__((aligned(1024))) bf16 sK[kStages][Tile::kElems];
@@ -1134,10 +1136,12 @@ int attn_fwd_impl(bool from_lse, const void* q, const void* const* k_blocks,
     // the forward addresses a K/V block through a 32-bit buffer offset
     NMB_REQUIRE_SUPPORTED(seq_k == 0 || ((seq_k - 1) * kv_strides[1] + head_dim) * 2 < (int64_t{1} << 31),
                           "attn_fwd: a K/V block spans more than 2 GiB");
-    // queries per workgroup: NWV waves x TQ column tiles of 16 (TQ = 4 at D 64, 2 at D 128);
-    // 8 waves at D 64 once a head has 512 queries
-    const int nwv = head_dim == 64 && seq_q >= 512 ? 8 : 4;
-    const int bq = 16 * nwv * (head_dim == 64 ? 4 : 2);
+    // queries per workgroup: NWV waves x TQ column tiles of 16.  D 64: 8 waves x 4
+    // for 512 .. 1023 queries, 4 x 2 (three workgroups per CU) from 1024, else
+    // 4 x 4; D 128: 4 x 2
+    const bool long_seq = head_dim == 64 && seq_q >= 1024;
+    const int nwv = head_dim == 64 && seq_q >= 512 && !long_seq ? 8 : 4;
+    const int bq = 16 * nwv * (head_dim == 64 && !long_seq ? 4 : 2);
     const int n_qt = static_cast<int>((seq_q + bq - 1) / bq);
     const int64_t items = static_cast<int64_t>(n_qt) * q_heads * batch;
     NMB_REQUIRE(items < (int64_t{1} << 30), "attn_fwd: problem too large for one launch");
@@ -1151,6 +1155,8 @@ int attn_fwd_impl(bool from_lse, const void* q, const void* const* k_blocks,
                      op, lse, p, n_qt, static_cast<int>(items), per_xcd)
     if (head_dim == 64 && nwv == 8) {
       if (from_lse) NMB_FWD(64, 4, 8, true); else NMB_FWD(64, 4, 8, false);
+    } else if (long_seq) {
+      if (from_lse) NMB_FWD(64, 2, 4, true); else NMB_FWD(64, 2, 4, false);
     } else if (head_dim == 64) {
       if (from_lse) NMB_FWD(64, 4, 4, true); else NMB_FWD(64, 4, 4, false);
     } else {
