@@ -694,66 +694,120 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
 
   const int w = xcd_item(items, per_xcd);
   if (w < 0) return;
-  // item = ((b * nblk + blk) * Hkv + hk) * n_kt + key tile
-  const int ktile = w % n_kt;
-  const int rest = w / n_kt;
+  // item = ((b * nblk + blk) * Hkv + hk) * n_pairs + pair.  At head dim 64
+  // pair j covers key tiles j and n_kt - 1 - j one after the other, so under
+  // causal masking every workgroup sees about the same number of query tiles
+  // (the middle tile of an odd n_kt is alone); at 128 the registers of a
+  // second tile's state do not fit, and a workgroup takes one key tile.
+  constexpr bool kPair = D == 64;
+  const int n_pairs = kPair ? (n_kt + 1) / 2 : n_kt;
+  const int pj = w % n_pairs;
+  const int rest = w / n_pairs;
   const int hk = rest % p.Hkv;
   const int bb = rest / p.Hkv;
   const int blk = bb % p.nblk;
   const int b = bb / p.nblk;
+  const int n_sub = kPair && n_kt - 1 - pj != pj ? 2 : 1;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int l16 = lane & 15, g = lane >> 4;
-  const int k0 = ktile * BKW;
-  const int kbase = k0 + 16 * wave;  // key tile j: kbase + 64 j + l16
   const int64_t koff = kv.koff[blk];
   const int group = p.Hq / p.Hkv;
   const float c = p.scale_log2;
+  const int n_qt = (p.Sq + BQ - 1) / BQ;
+
+  // per sub-item (key tile): first visible query tile and the iteration count
+  auto sub_tile = [&](int sub) { return sub == 0 ? pj : n_kt - 1 - pj; };
+  auto qt_begin_of = [&](int sub) {
+    int first_q = 0;
+    if (p.causal) {
+      const int64_t fq = koff + sub_tile(sub) * BKW - p.q_offset;
+      first_q = fq <= 0 ? 0 : (fq >= p.Sq ? p.Sq : static_cast<int>(fq));
+    }
+    return first_q / BQ;
+  };
+  const int qtb0 = qt_begin_of(0), qtb1 = n_sub == 2 ? qt_begin_of(1) : 0;
+  const int n_iter0 = group * (n_qt - qtb0);
+  const int n_iter1 = n_sub == 2 ? group * (n_qt - qtb1) : 0;
+  const int total = n_iter0 + n_iter1;
 
   const int64_t kv_off = b * p.kv_sb + hk * p.kv_sh;
   const bf16* kb = static_cast<const bf16*>(kv.k[blk]) + kv_off;
   const bf16* vb = static_cast<const bf16*>(kv.v[blk]) + kv_off;
+  bf16* dkb = static_cast<bf16*>(kv.dk[blk]) + kv_off;
+  bf16* dvb = static_cast<bf16*>(kv.dv[blk]) + kv_off;
   bf16x8 kf[KT][KS], vf[KT][KS];
-#pragma unroll
-  for (int j = 0; j < KT; ++j) {
-    const int key = kbase + 64 * j + l16;
-    const bool ok = key < p.Sk;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      kf[j][ks] = ok ? ld8(kb + static_cast<int64_t>(key) * p.kv_ss + ks * 32 + g * 8) : zero8();
-      vf[j][ks] = ok ? ld8(vb + static_cast<int64_t>(key) * p.kv_ss + ks * 32 + g * 8) : zero8();
-    }
-  }
   f32x4 dka[KT][DT], dva[KT][DT];
+  int kbase = 0;  // key tile j of this wave: kbase + 64 j + l16
+  // a sub-item's K/V fragments into registers and its accumulators to zero
+  auto start = [&](int sub) {
+    kbase = sub_tile(sub) * BKW + 16 * wave;
 #pragma unroll
-  for (int j = 0; j < KT; ++j)
+    for (int j = 0; j < KT; ++j) {
+      const int key = kbase + 64 * j + l16;
+      const bool ok = key < p.Sk;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      dka[j][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      dva[j][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int ks = 0; ks < KS; ++ks) {
+        kf[j][ks] = ok ? ld8(kb + static_cast<int64_t>(key) * p.kv_ss + ks * 32 + g * 8) : zero8();
+        vf[j][ks] = ok ? ld8(vb + static_cast<int64_t>(key) * p.kv_ss + ks * 32 + g * 8) : zero8();
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        dka[j][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        dva[j][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
     }
-  int first_q = 0;
-  if (p.causal) {
-    const int64_t fq = koff + k0 - p.q_offset;
-    first_q = fq <= 0 ? 0 : (fq >= p.Sq ? p.Sq : static_cast<int>(fq));
-  }
-  const int qt_begin = first_q / BQ;
-  const int n_qt = (p.Sq + BQ - 1) / BQ;
-  const int per_head = n_qt - qt_begin;
-  const int n_iter = per_head > 0 ? group * per_head : 0;
+  };
+  // lane holds dK[key = kbase + 64 j + 4 g + e][d = 16 dt + l16]
+  auto finish = [&]() {
+#pragma unroll
+    for (int j = 0; j < KT; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int key = kbase + 64 * j + g * 4 + e;
+        if (key >= p.Sk) continue;
+        bf16* dkr = dkb + static_cast<int64_t>(key) * p.kv_ss;
+        if constexpr (ROPE) {
+          // d = 16 dt + l16 and d + D/2 are dt and dt + DT/2 (one K/V block: key = token index)
+          bool bad;
+          const int64_t pos = rope_pos(rg, b, key, &bad);
+#pragma unroll
+          for (int dt = 0; dt < DT / 2; ++dt) {
+            const int d = dt * 16 + l16;
+            rope_back(round_as<bf16>(dka[j][dt][e] * p.scale), round_as<bf16>(dka[j][dt + DT / 2][e] * p.scale),
+                      rg.cos[pos * (D / 2) + d], rg.sin[pos * (D / 2) + d], bad, dkr[d], dkr[d + D / 2]);
+          }
+        } else {
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) dkr[dt * 16 + l16] = static_cast<bf16>(dka[j][dt][e] * p.scale);
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+          dvb[static_cast<int64_t>(key) * p.kv_ss + dt * 16 + l16] = static_cast<bf16>(dva[j][dt][e]);
+      }
+  };
+  // stream iteration it: query head hk * group + i / per_head, query tile
+  // qt_begin + i % per_head of its sub-item (i = it, or it - n_iter0)
+  auto locate = [&](int it, int& h, int& q0) {
+    const bool second = it >= n_iter0;
+    const int i = second ? it - n_iter0 : it;
+    const int qtb = second ? qtb1 : qtb0;
+    const int per_head = n_qt - qtb;
+    h = hk * group + i / per_head;
+    q0 = (qtb + i % per_head) * BQ;
+  };
 
-  // Q / dO tiles and their row statistics stream through LDS (kStages deep);
-  // iteration it covers query head hk * group + it / per_head, query tile
-  // qt_begin + it % per_head.  Past the last iteration the loads read zeros.
+  // Q / dO tiles and their row statistics stream through LDS (kStages deep),
+  // across the two sub-items.  Past the last iteration the loads read zeros.
   TileStream<D> lq, ldo;
   lq.init(p.q_ss, wave, lane);
   ldo.init(p.o_ss, wave, lane);
   const uint32_t q_bytes = static_cast<uint32_t>(((p.Sq - 1) * p.q_ss + D) * 2);
   const uint32_t o_bytes = static_cast<uint32_t>(((p.Sq - 1) * p.o_ss + D) * 2);
   auto issue = [&](int it, int stage) {
-    if (it < n_iter) {
-      const int h = hk * group + it / per_head;
-      const int q0 = (qt_begin + it % per_head) * BQ;
+    if (it < total) {
+      int h, q0;
+      locate(it, h, q0);
       lq.issue(make_rsrc(q + b * p.q_sb + h * p.q_sh, q_bytes), sQ[stage], q0, p.Sq,
                static_cast<uint32_t>(q0) * static_cast<uint32_t>(p.q_ss * 2), wave);
       ldo.issue(make_rsrc(dout + b * p.o_sb + h * p.o_sh, o_bytes), sD[stage], q0, p.Sq,
@@ -768,17 +822,30 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
       load_lds4(rz, &sStat[stage][wave][0], kOOB);
     }
   };
+  start(0);
 #pragma unroll
   for (int st = 0; st < kStages - 1; ++st) issue(st, st);
-  for (int it = 0; it < n_iter; ++it) {
-    wait_vmcnt<(kStages - 2) * kLoads>();
+  bool switched = false;
+  for (int it = 0; it < total; ++it) {
+    if (it == n_iter0 && n_sub == 2) {
+      // first iteration of the second key tile: store the first one's dK/dV
+      // and load the second's K/V; the stores share vmcnt with the tile
+      // loads and need not retire in order, so wait for everything
+      finish();
+      start(1);
+      switched = true;
+      wait_vmcnt<0>();
+    } else {
+      wait_vmcnt<(kStages - 2) * kLoads>();
+    }
     lds_barrier();
     issue(it + kStages - 1, (it + kStages - 1) % kStages);
     const bf16* tq = sQ[it % kStages];
     const bf16* td = sD[it % kStages];
     const float* sL = sStat[it % kStages][0];
     const float* sDl = sStat[it % kStages][1];
-    const int q0 = (qt_begin + it % per_head) * BQ;
+    int h_unused, q0;
+    locate(it, h_unused, q0);
     const int64_t qa_last = p.q_offset + min(q0 + BQ - 1, p.Sq - 1);
     bool live[KT], need_mask[KT];
     bool any = false;
@@ -865,34 +932,11 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
   }
   // no load may still write this workgroup's LDS when it ends
   wait_vmcnt<0>();
-  // lane holds dK[key = kbase + 64 j + 4 g + e][d = 16 dt + l16]
-  bf16* dkb = static_cast<bf16*>(kv.dk[blk]) + kv_off;
-  bf16* dvb = static_cast<bf16*>(kv.dv[blk]) + kv_off;
-#pragma unroll
-  for (int j = 0; j < KT; ++j)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int key = kbase + 64 * j + g * 4 + e;
-      if (key >= p.Sk) continue;
-      bf16* dkr = dkb + static_cast<int64_t>(key) * p.kv_ss;
-      if constexpr (ROPE) {
-        // d = 16 dt + l16 and d + D/2 are dt and dt + DT/2 (one K/V block: key = token index)
-        bool bad;
-        const int64_t pos = rope_pos(rg, b, key, &bad);
-#pragma unroll
-        for (int dt = 0; dt < DT / 2; ++dt) {
-          const int d = dt * 16 + l16;
-          rope_back(round_as<bf16>(dka[j][dt][e] * p.scale), round_as<bf16>(dka[j][dt + DT / 2][e] * p.scale),
-                    rg.cos[pos * (D / 2) + d], rg.sin[pos * (D / 2) + d], bad, dkr[d], dkr[d + D / 2]);
-        }
-      } else {
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) dkr[dt * 16 + l16] = static_cast<bf16>(dka[j][dt][e] * p.scale);
-      }
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-        dvb[static_cast<int64_t>(key) * p.kv_ss + dt * 16 + l16] = static_cast<bf16>(dva[j][dt][e]);
-    }
+  if (n_sub == 2 && !switched) {  // the second key tile saw no query tile
+    finish();
+    start(1);
+  }
+  finish();
 }
 
 // ---------------------------------------------------------------- fp32 path
@@ -1282,8 +1326,8 @@ int attn_bwd_impl(const void* q, const void* const* k_blocks,
       NMB_CHECK_LAUNCH("attn_bwd(dq)");
     }
     if (seq_k > 0) {
-      const int n_kt = static_cast<int>((seq_k + 127) / 128);  // 128 keys per workgroup
-      const int64_t items = static_cast<int64_t>(n_kt) * kv_heads * batch * n_blocks;
+      const int n_kt = static_cast<int>((seq_k + 127) / 128);  // 128-key tiles, two per workgroup at D 64
+      const int64_t items = static_cast<int64_t>(D == 64 ? (n_kt + 1) / 2 : n_kt) * kv_heads * batch * n_blocks;
       NMB_REQUIRE(items < (int64_t{1} << 30), "attn_bwd: problem too large for one launch");
       int per_xcd;
       unsigned blocks;
