@@ -497,14 +497,21 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
 
   const int w = xcd_item(items, per_xcd);
   if (w < 0) return;
-  const int bh = w / n_qt;
-  const int qt = n_qt - 1 - (w % n_qt);
+  // item = (b * Hq + h) * n_pairs + pair.  At head dim 64 pair j covers query
+  // tiles n_qt - 1 - j and j one after the other (equal causal work per
+  // workgroup; the middle tile of an odd n_qt is alone); at 128 a workgroup
+  // takes one query tile (heavy ones first).
+  constexpr bool kPair = D == 64;
+  const int n_pairs = kPair ? (n_qt + 1) / 2 : n_qt;
+  const int bh = w / n_pairs;
+  const int pj = w % n_pairs;
+  const int n_sub = kPair && n_qt - 1 - pj != pj ? 2 : 1;
+  auto qtile = [&](int sub) { return sub == 0 ? n_qt - 1 - pj : pj; };
   const int b = bh / p.Hq, h = bh % p.Hq;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int l16 = lane & 15, g = lane >> 4;
   const int hk = h / (p.Hq / p.Hkv);
-  const int q0 = qt * BQ + wave * 32;
   const float c = p.scale_log2;
 
   const bf16* qb = q + b * p.q_sb + h * p.q_sh;
@@ -513,73 +520,143 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
   const float* lb = lse + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
   float* deb = delta + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
   float* l2b = lse2_out + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
+  bf16* dqb = dq + b * p.q_sb + h * p.q_sh;
   bf16x8 qf[2][KS], df[2][KS];
   float lse2[2], dl[2];
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int qi = q0 + 16 * t + l16;
-    const bool ok = qi < p.Sq;
-    float part = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      qf[t][ks] = ok ? ld8(qb + static_cast<int64_t>(qi) * p.q_ss + ks * 32 + g * 8) : zero8();
-      df[t][ks] = ok ? ld8(db + static_cast<int64_t>(qi) * p.o_ss + ks * 32 + g * 8) : zero8();
-      const bf16x8 of = ok ? ld8(ob + static_cast<int64_t>(qi) * p.o_ss + ks * 32 + g * 8) : zero8();
-#pragma unroll
-      for (int e = 0; e < 8; ++e) part += static_cast<float>(df[t][ks][e]) * static_cast<float>(of[e]);
-    }
-    part = xor32_sum(xor16_sum(part));
-    dl[t] = part;
-    lse2[t] = ok ? lse_to_log2(lb[qi]) : __builtin_inff();
-    // delta and the log2-domain lse for the dK/dV kernel, which runs next
-    if (ok && g == 0) {
-      deb[qi] = part;
-      l2b[qi] = lse2[t];
-    }
-  }
   f32x4 acc[2][DT];
+  int q0 = 0;  // this wave's first query of the current sub-item
+  // a sub-item's Q and dO fragments, delta = rowsum(dO * O) and the base-2
+  // LSE (both also written for the dK/dV kernel, which runs next); dQ to zero
+  auto start = [&](int sub) {
+    q0 = qtile(sub) * BQ + wave * 32;
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < 2; ++t) {
+      const int qi = q0 + 16 * t + l16;
+      const bool ok = qi < p.Sq;
+      float part = 0.f;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) acc[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int ks = 0; ks < KS; ++ks) {
+        qf[t][ks] = ok ? ld8(qb + static_cast<int64_t>(qi) * p.q_ss + ks * 32 + g * 8) : zero8();
+        df[t][ks] = ok ? ld8(db + static_cast<int64_t>(qi) * p.o_ss + ks * 32 + g * 8) : zero8();
+        const bf16x8 of = ok ? ld8(ob + static_cast<int64_t>(qi) * p.o_ss + ks * 32 + g * 8) : zero8();
+#pragma unroll
+        for (int e = 0; e < 8; ++e) part += static_cast<float>(df[t][ks][e]) * static_cast<float>(of[e]);
+      }
+      part = xor32_sum(xor16_sum(part));
+      dl[t] = part;
+      lse2[t] = ok ? lse_to_log2(lb[qi]) : __builtin_inff();
+      if (ok && g == 0) {
+        deb[qi] = part;
+        l2b[qi] = lse2[t];
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) acc[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  // lane holds dQ[q0 + 16 t + l16][d = 16 dt + 4 g + e]; d and d + D/2 are dt and dt + DT/2
+  auto finish = [&]() {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int qi = q0 + 16 * t + l16;
+      if (qi >= p.Sq) continue;
+      if constexpr (ROPE) {
+        bool bad;
+        const int64_t pos = rope_pos(rg, b, qi, &bad);
+#pragma unroll
+        for (int dt = 0; dt < DT / 2; ++dt) {
+          bf16x4 w1, w2;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int d = dt * 16 + g * 4 + e;
+            bf16 r1, r2;
+            rope_back(round_as<bf16>(acc[t][dt][e] * p.scale), round_as<bf16>(acc[t][dt + DT / 2][e] * p.scale),
+                      rg.cos[pos * (D / 2) + d], rg.sin[pos * (D / 2) + d], bad, r1, r2);
+            w1[e] = r1;
+            w2[e] = r2;
+          }
+          *reinterpret_cast<bf16x4*>(dqb + static_cast<int64_t>(qi) * p.q_ss + dt * 16 + g * 4) = w1;
+          *reinterpret_cast<bf16x4*>(dqb + static_cast<int64_t>(qi) * p.q_ss + D / 2 + dt * 16 + g * 4) = w2;
+        }
+      } else {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          bf16x4 wv;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) wv[e] = static_cast<bf16>(acc[t][dt][e] * p.scale);
+          *reinterpret_cast<bf16x4*>(dqb + static_cast<int64_t>(qi) * p.q_ss + dt * 16 + g * 4) = wv;
+        }
+      }
+    }
+  };
+  // last absolute query position of a sub-item's workgroup tile
+  auto wg_last = [&](int sub) { return p.q_offset + min(qtile(sub) * BQ + BQ - 1, p.Sq - 1); };
 
-  const int64_t qa_wave_first = p.q_offset + q0;
-  const int64_t qa_wave_last = p.q_offset + min(q0 + 31, p.Sq - 1);
-  const int64_t qa_wg_last = p.q_offset + min(qt * BQ + BQ - 1, p.Sq - 1);
   const int64_t kv_off = b * p.kv_sb + hk * p.kv_sh;
   const uint32_t kv_bytes = static_cast<uint32_t>(((p.Sk - 1) * p.kv_ss + D) * 2);
   const uint32_t row_bytes = static_cast<uint32_t>(p.kv_ss * 2);
   TileStream<D> ld;
   ld.init(p.kv_ss, wave, lane);
 
-  // K/V tiles stream through LDS as in the forward (same cursors and waits)
-  int nt = 0;
-  int blk = first_block(p, kv, qa_wg_last, nt), kt = 0;
-  int pnt = nt, pblk = blk, pkt = 0;
+  // K/V tiles stream through LDS as in the forward: the visible tiles of the
+  // first sub-item, then those of the second (load cursor psub/pblk/pkt,
+  // compute cursor csub/blk/kt)
+  int pnt = 0, psub = 0;
+  int pblk = first_block(p, kv, wg_last(0), pnt), pkt = 0;
+  auto advance_load = [&]() {
+    next_tile(p, kv, wg_last(psub), pblk, pkt, pnt);
+    while (pblk >= p.nblk && psub + 1 < n_sub) {
+      ++psub;
+      pblk = first_block(p, kv, wg_last(psub), pnt);
+      pkt = 0;
+    }
+  };
+  if (pblk >= p.nblk && n_sub == 2) {  // the first sub-item sees no key
+    psub = 1;
+    pblk = first_block(p, kv, wg_last(1), pnt);
+  }
   auto issue = [&](int stage) {
     if (pblk < p.nblk) {
       const uint32_t r0b = static_cast<uint32_t>(pkt * BK) * row_bytes;
       ld.issue(make_rsrc(static_cast<const bf16*>(kv.k[pblk]) + kv_off, kv_bytes), sK[stage], pkt * BK, p.Sk, r0b, wave);
       ld.issue(make_rsrc(static_cast<const bf16*>(kv.v[pblk]) + kv_off, kv_bytes), sV[stage], pkt * BK, p.Sk, r0b, wave);
-      next_tile(p, kv, qa_wg_last, pblk, pkt, pnt);
+      advance_load();
     } else {
       const i32x4 rz = make_rsrc(kv.k[0], 0);
       ld.issue(rz, sK[stage], 0, 0, 0u, wave);
       ld.issue(rz, sV[stage], 0, 0, 0u, wave);
     }
   };
+  start(0);
 #pragma unroll
   for (int st = 0; st < kStages - 1; ++st) issue(st);
 
-  for (int it = 0; blk < p.nblk; ++it) {
-    wait_vmcnt<(kStages - 2) * kLoads>();
+  int nt = 0, csub = 0;
+  int blk = first_block(p, kv, wg_last(0), nt), kt = 0;
+  for (int it = 0;; ++it) {
+    bool switched = false;
+    while (blk >= p.nblk && csub + 1 < n_sub) {
+      // the next sub-item: store this one's dQ, load the next one's Q/dO; the
+      // stores share vmcnt with the tile loads and need not retire in order,
+      // so this iteration waits for everything
+      finish();
+      ++csub;
+      start(csub);
+      blk = first_block(p, kv, wg_last(csub), nt);
+      kt = 0;
+      switched = true;
+    }
+    if (blk >= p.nblk) break;
+    if (switched) wait_vmcnt<0>();
+    else wait_vmcnt<(kStages - 2) * kLoads>();
     lds_barrier();
     issue((it + kStages - 1) % kStages);
     const bf16* tk = sK[it % kStages];
     const bf16* tv = sV[it % kStages];
     const int64_t koff = kv.koff[blk];
     const int k0 = kt * BK;
-    next_tile(p, kv, qa_wg_last, blk, kt, nt);
+    next_tile(p, kv, wg_last(csub), blk, kt, nt);
+    const int64_t qa_wave_first = p.q_offset + q0;
+    const int64_t qa_wave_last = p.q_offset + min(q0 + 31, p.Sq - 1);
     if (p.causal && koff + k0 > qa_wave_last) continue;
     const bool need_mask = (k0 + BK > p.Sk) || (p.causal && koff + k0 + BK - 1 > qa_wave_first);
 
@@ -634,40 +711,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
   }
   // no load may still write this workgroup's LDS when it ends
   wait_vmcnt<0>();
-  // lane holds dQ[q0 + 16 t + l16][d = 16 dt + 4 g + e]; d and d + D/2 are dt and dt + DT/2
-  bf16* dqb = dq + b * p.q_sb + h * p.q_sh;
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int qi = q0 + 16 * t + l16;
-    if (qi >= p.Sq) continue;
-    if constexpr (ROPE) {
-      bool bad;
-      const int64_t pos = rope_pos(rg, b, qi, &bad);
-#pragma unroll
-      for (int dt = 0; dt < DT / 2; ++dt) {
-        bf16x4 w1, w2;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int d = dt * 16 + g * 4 + e;
-          bf16 r1, r2;
-          rope_back(round_as<bf16>(acc[t][dt][e] * p.scale), round_as<bf16>(acc[t][dt + DT / 2][e] * p.scale),
-                    rg.cos[pos * (D / 2) + d], rg.sin[pos * (D / 2) + d], bad, r1, r2);
-          w1[e] = r1;
-          w2[e] = r2;
-        }
-        *reinterpret_cast<bf16x4*>(dqb + static_cast<int64_t>(qi) * p.q_ss + dt * 16 + g * 4) = w1;
-        *reinterpret_cast<bf16x4*>(dqb + static_cast<int64_t>(qi) * p.q_ss + D / 2 + dt * 16 + g * 4) = w2;
-      }
-    } else {
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        bf16x4 wv;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) wv[e] = static_cast<bf16>(acc[t][dt][e] * p.scale);
-        *reinterpret_cast<bf16x4*>(dqb + static_cast<int64_t>(qi) * p.q_ss + dt * 16 + g * 4) = wv;
-      }
-    }
-  }
+  finish();
 }
 
 // ---------------------------------------------------------------- dK, dV
@@ -1307,8 +1351,8 @@ int attn_bwd_impl(const void* q, const void* const* k_blocks,
     nmb::bf16* dqp = static_cast<nmb::bf16*>(dq);
     // the dQ kernel also writes delta, which the dK/dV kernel reads: keep this order
     if (seq_q > 0) {
-      const int n_qt = static_cast<int>((seq_q + 127) / 128);
-      const int64_t items = static_cast<int64_t>(n_qt) * q_heads * batch;
+      const int n_qt = static_cast<int>((seq_q + 127) / 128);  // 128-query tiles, two per workgroup at D 64
+      const int64_t items = static_cast<int64_t>(D == 64 ? (n_qt + 1) / 2 : n_qt) * q_heads * batch;
       NMB_REQUIRE(items < (int64_t{1} << 30), "attn_bwd: problem too large for one launch");
       int per_xcd;
       unsigned blocks;
