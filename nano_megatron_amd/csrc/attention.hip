@@ -253,6 +253,9 @@ __global__ __launch_bounds__(64 * NWV, (D == 64 && NWV == 4) ? (TQ <= 2 ? 3 : 2)
   constexpr int CT = 16 * NWV;  // query stride between a wave's column tiles
   constexpr int BQ = CT * TQ, BK = 64, KS = D / 32, DT = D / 16;
   constexpr int kStages = (D == 64 && NWV == 4 && TQ <= 2) ? 3 : 4;  // 48 or 64 KB of LDS at D 64
+  // two column tiles: fragments read per MFMA step (fewer registers); four:
+  // fragments held across the column tiles (the scores of four would not fit)
+  constexpr bool kPhased = TQ <= 2;
   using Tile = Tile64<D>;
   constexpr int kLoads = 2 * TileStream<D, NWV>::P;  // this wave's loads per K/V tile pair
   __shared__ __attribute__((aligned(1024))) bf16 sK[kStages][Tile::kElems];
@@ -351,27 +354,9 @@ __global__ __launch_bounds__(64 * NWV, (D == 64 && NWV == 4) ? (TQ <= 2 ? 3 : 2)
       need_mask[t] = (k0 + BK > p.Sk) || (p.causal && koff + k0 + BK - 1 > qfirst);
     }
 
-    // K and V^T fragments of this tile, read from LDS once and reused by every
-    // column tile of the wave
-    bf16x8 kfr[KS][4], vfr[DT][2];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int mk = 0; mk < 4; ++mk) kfr[ks][mk] = Tile::row8(tk, mk * 16 + l16, ks * 32 + g * 8);
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) vfr[dt][s2] = Tile::col8(tv, 32 * s2, dt * 16, l16, g);
-#pragma unroll
-    for (int t = 0; t < TQ; ++t) {
-      if (!live[t]) continue;
-      f32x4 s[4];
-#pragma unroll
-      for (int mk = 0; mk < 4; ++mk) s[mk] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int mk = 0; mk < 4; ++mk) s[mk] = mfma16(kfr[ks][mk], qf[t][ks], s[mk]);
+    // softmax of one column tile's scores (in place, then packed into P, the
+    // B operand of the P V MFMAs); rescales that tile's O and row sum
+    auto softmax = [&](int t, f32x4 (&sc)[4], bf16x8 (&pt)[2]) {
       float tmax = -__builtin_inff();
       if (need_mask[t]) {
         // last visible tile-relative key index of this lane's query
@@ -382,20 +367,20 @@ __global__ __launch_bounds__(64 * NWV, (D == 64 && NWV == 4) ? (TQ <= 2 ? 3 : 2)
           for (int e = 0; e < 4; ++e) {
             // branch-free select: a conditional store into the vector element
             // under short-circuit control flow is not reliably kept
-            const float sv = s[mk][e];
-            s[mk][e] = (mk * 16 + g * 4 + e > lim) ? -__builtin_inff() : sv;
+            const float sv = sc[mk][e];
+            sc[mk][e] = (mk * 16 + g * 4 + e > lim) ? -__builtin_inff() : sv;
           }
       }
       if constexpr (FL) {
 #pragma unroll
         for (int mk = 0; mk < 4; ++mk)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) s[mk][e] = fast_exp2(fmaf(s[mk][e], c, -m[t]));
+          for (int e = 0; e < 4; ++e) sc[mk][e] = fast_exp2(fmaf(sc[mk][e], c, -m[t]));
       } else {
 #pragma unroll
         for (int mk = 0; mk < 4; ++mk)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) tmax = fmaxf(tmax, s[mk][e]);
+          for (int e = 0; e < 4; ++e) tmax = fmaxf(tmax, sc[mk][e]);
         tmax = xor32_max(xor16_max(tmax));
         // Lazy rescaling: the running maximum m moves only when the tile's
         // maximum exceeds it by more than 8 in the exp2 domain; otherwise P
@@ -413,23 +398,94 @@ __global__ __launch_bounds__(64 * NWV, (D == 64 && NWV == 4) ? (TQ <= 2 ? 3 : 2)
 #pragma unroll
         for (int mk = 0; mk < 4; ++mk)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) s[mk][e] = fast_exp2(fmaf(s[mk][e], c, -mc));
+          for (int e = 0; e < 4; ++e) sc[mk][e] = fast_exp2(fmaf(sc[mk][e], c, -mc));
       }
-      bf16x8 pf[2];
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          pf[s2][e] = static_cast<bf16>(s[2 * s2][e]);
-          pf[s2][4 + e] = static_cast<bf16>(s[2 * s2 + 1][e]);
+          pt[s2][e] = static_cast<bf16>(sc[2 * s2][e]);
+          pt[s2][4 + e] = static_cast<bf16>(sc[2 * s2 + 1][e]);
         }
+    };
+    if constexpr (kPhased) {
+      // Three phases over the wave's column tiles: scores of every live
+      // column tile (K fragments read per k step), softmax, then P V (V^T
+      // fragments read per d tile).  Each fragment is still read from LDS once
+      // per tile, but none is held across the phases.
+      f32x4 s[TQ][4];
+      bf16x8 pf[TQ][2];
+#pragma unroll
+      for (int t = 0; t < TQ; ++t)
+#pragma unroll
+        for (int mk = 0; mk < 4; ++mk) s[t][mk] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        bf16x8 kk[4];
+#pragma unroll
+        for (int mk = 0; mk < 4; ++mk) kk[mk] = Tile::row8(tk, mk * 16 + l16, ks * 32 + g * 8);
+#pragma unroll
+        for (int t = 0; t < TQ; ++t)
+          if (live[t]) {
+#pragma unroll
+            for (int mk = 0; mk < 4; ++mk) s[t][mk] = mfma16(kk[mk], qf[t][ks], s[t][mk]);
+          }
+      }
+#pragma unroll
+      for (int t = 0; t < TQ; ++t)
+        if (live[t]) softmax(t, s[t], pf[t]);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        bf16x8 vv[2];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) vv[s2] = Tile::col8(tv, 32 * s2, dt * 16, l16, g);
+#pragma unroll
+        for (int t = 0; t < TQ; ++t)
+          if (live[t]) {
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) acc[t][dt] = mfma16(vv[s2], pf[t][s2], acc[t][dt]);
+          }
+      }
+      if constexpr (!FL) {
+#pragma unroll
+        for (int t = 0; t < TQ; ++t)
+          if (live[t]) {
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) acc[t][NA - 1] = mfma16(ones, pf[t][s2], acc[t][NA - 1]);
+          }
+      }
+    } else {
+      // K and V^T fragments of this tile, read from LDS once and held while
+      // each column tile of the wave runs scores, softmax and P V in turn
+      bf16x8 kfr[KS][4], vfr[DT][2];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int mk = 0; mk < 4; ++mk) kfr[ks][mk] = Tile::row8(tk, mk * 16 + l16, ks * 32 + g * 8);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) acc[t][dt] = mfma16(vfr[dt][s2], pf[s2], acc[t][dt]);
-      if constexpr (!FL) {
+        for (int s2 = 0; s2 < 2; ++s2) vfr[dt][s2] = Tile::col8(tv, 32 * s2, dt * 16, l16, g);
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) acc[t][NA - 1] = mfma16(ones, pf[s2], acc[t][NA - 1]);
+      for (int t = 0; t < TQ; ++t) {
+        if (!live[t]) continue;
+        f32x4 s[4];
+#pragma unroll
+        for (int mk = 0; mk < 4; ++mk) s[mk] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+          for (int mk = 0; mk < 4; ++mk) s[mk] = mfma16(kfr[ks][mk], qf[t][ks], s[mk]);
+        bf16x8 pf[2];
+        softmax(t, s, pf);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) acc[t][dt] = mfma16(vfr[dt][s2], pf[s2], acc[t][dt]);
+        if constexpr (!FL) {
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) acc[t][NA - 1] = mfma16(ones, pf[s2], acc[t][NA - 1]);
+        }
       }
     }
   }
@@ -1226,9 +1282,9 @@ int attn_fwd_impl(bool from_lse, const void* q, const void* const* k_blocks,
                           "attn_fwd: a K/V block spans more than 2 GiB");
     // queries per workgroup: NWV waves x TQ column tiles of 16.  D 64: 8 waves x 4
     // for 512 .. 1023 queries, 4 x 2 (three workgroups per CU) from 1024, else
-    // 4 x 4; D 128: 4 x 2
+    // 4 x 4; D 128: 8 x 2 (two waves per SIMD)
     const bool long_seq = head_dim == 64 && seq_q >= 1024;
-    const int nwv = head_dim == 64 && seq_q >= 512 && !long_seq ? 8 : 4;
+    const int nwv = (head_dim == 64 && seq_q >= 512 && !long_seq) || head_dim == 128 ? 8 : 4;
     const int bq = 16 * nwv * (head_dim == 64 && !long_seq ? 4 : 2);
     const int n_qt = static_cast<int>((seq_q + bq - 1) / bq);
     const int64_t items = static_cast<int64_t>(n_qt) * q_heads * batch;
@@ -1248,7 +1304,7 @@ int attn_fwd_impl(bool from_lse, const void* q, const void* const* k_blocks,
     } else if (head_dim == 64) {
       if (from_lse) NMB_FWD(64, 4, 4, true); else NMB_FWD(64, 4, 4, false);
     } else {
-      if (from_lse) NMB_FWD(128, 2, 4, true); else NMB_FWD(128, 2, 4, false);
+      if (from_lse) NMB_FWD(128, 2, 8, true); else NMB_FWD(128, 2, 8, false);
     }
 #undef NMB_FWD
   } else {
