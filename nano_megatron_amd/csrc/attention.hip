@@ -535,19 +535,20 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(const T* __restrict__ o
 }
 
 // ---------------------------------------------------------------- dQ
-// Same tiling as the forward (S^T = K Q^T per wave).  The prologue computes
-// delta = rowsum(dO * O) for the workgroup's queries from the registers that
-// hold dO and writes it for the dK/dV kernel, which runs next on the stream.
-template <int D, bool ROPE>
-__global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
+// Same tiling as the forward (S^T = K Q^T per wave), NW waves of 32 queries.
+// The prologue computes delta = rowsum(dO * O) for the workgroup's queries
+// from the registers that hold dO and writes it for the dK/dV kernel, which
+// runs next on the stream.  At head dim 128, 8 waves (two per SIMD).
+template <int D, bool ROPE, int NW>
+__global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
     const bf16* __restrict__ q, KVBlocks kv, const bf16* __restrict__ o,
     const bf16* __restrict__ dout, const float* __restrict__ lse, float* __restrict__ delta,
     float* __restrict__ lse2_out, bf16* __restrict__ dq, AttnShape p, int n_qt, int items, int per_xcd,
     RopeGrad rg) {
-  constexpr int BQ = 128, BK = 64, KS = D / 32, DT = D / 16;
+  constexpr int BQ = 32 * NW, BK = 64, KS = D / 32, DT = D / 16;
   constexpr int kStages = 4;
   using Tile = Tile64<D>;
-  constexpr int kLoads = 2 * TileStream<D>::P;  // this wave's loads per K/V tile pair
+  constexpr int kLoads = 2 * TileStream<D, NW>::P;  // this wave's loads per K/V tile pair
   __shared__ __attribute__((aligned(1024))) bf16 sK[kStages][Tile::kElems];
   __shared__ __attribute__((aligned(1024))) bf16 sV[kStages][Tile::kElems];
 
@@ -650,7 +651,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
   const int64_t kv_off = b * p.kv_sb + hk * p.kv_sh;
   const uint32_t kv_bytes = static_cast<uint32_t>(((p.Sk - 1) * p.kv_ss + D) * 2);
   const uint32_t row_bytes = static_cast<uint32_t>(p.kv_ss * 2);
-  TileStream<D> ld;
+  TileStream<D, NW> ld;
   ld.init(p.kv_ss, wave, lane);
 
   // K/V tiles stream through LDS as in the forward: the visible tiles of the
@@ -716,13 +717,21 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
     if (p.causal && koff + k0 > qa_wave_last) continue;
     const bool need_mask = (k0 + BK > p.Sk) || (p.causal && koff + k0 + BK - 1 > qa_wave_first);
 
-    f32x4 s[4][2], dp[4][2];
+    bf16x8 dsf[2][2];
+    int lim[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      lim[t] = need_mask ? mask_limit(p, koff, k0, p.q_offset + q0 + 16 * t + l16) : BK;
+    // per 16-key slice mk: S^T and dP^T (K and V row fragments), then
+    // dS = P (dP - delta) packed into the B operand of the dQ MFMAs; only one
+    // slice's scores are live at a time
 #pragma unroll
     for (int mk = 0; mk < 4; ++mk) {
+      f32x4 s[2], dp[2];
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        s[mk][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-        dp[mk][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        s[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        dp[t] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
@@ -730,29 +739,17 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
         const bf16x8 av = Tile::row8(tv, mk * 16 + l16, ks * 32 + g * 8);
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          s[mk][t] = mfma16(ak, qf[t][ks], s[mk][t]);
-          dp[mk][t] = mfma16(av, df[t][ks], dp[mk][t]);
+          s[t] = mfma16(ak, qf[t][ks], s[t]);
+          dp[t] = mfma16(av, df[t][ks], dp[t]);
         }
       }
-    }
-    bf16x8 dsf[2][2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int lim = need_mask ? mask_limit(p, koff, k0, p.q_offset + q0 + 16 * t + l16) : BK;
-#pragma unroll
-      for (int mk = 0; mk < 4; ++mk)
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float pv = fast_exp2(fmaf(s[mk][t][e], c, -lse2[t]));
-          pv = (mk * 16 + g * 4 + e > lim) ? 0.f : pv;
-          s[mk][t][e] = pv * (dp[mk][t][e] - dl[t]);
-        }
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          dsf[s2][t][e] = static_cast<bf16>(s[2 * s2][t][e]);
-          dsf[s2][t][4 + e] = static_cast<bf16>(s[2 * s2 + 1][t][e]);
+          float pv = fast_exp2(fmaf(s[t][e], c, -lse2[t]));
+          pv = (mk * 16 + g * 4 + e > lim[t]) ? 0.f : pv;
+          dsf[mk >> 1][t][4 * (mk & 1) + e] = static_cast<bf16>(pv * (dp[t][e] - dl[t]));
         }
     }
 #pragma unroll
@@ -771,26 +768,33 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
 }
 
 // ---------------------------------------------------------------- dK, dV
-// Workgroup = 128 keys of one (batch, KV head, block): key tile j (16 keys) of
-// wave w holds keys 64 j + 16 w .. +15 of the workgroup's range (interleaved,
-// so causal work is balanced across waves), so each Q/dO fragment read from
-// LDS feeds two MFMA tiles.  Loops over the query heads of the GQA group and
+// Workgroup = 128 keys of one (batch, KV head, block).  Head dim 64: 4 waves,
+// key tile j (16 keys) of wave w holds keys 64 j + 16 w .. +15 of the
+// workgroup's range (interleaved, so causal work is balanced across waves),
+// so each Q/dO fragment read from LDS feeds two MFMA tiles.  Head dim 128:
+// 8 waves of one 16-key tile each (two waves per SIMD; the dK/dV accumulators
+// of a second tile would not fit beside them).  Loops over the query heads of the GQA group and
 // over the 64-query tiles that can see these keys, with the next Q/dO tile's
 // global reads in flight during the current tile's MFMA work.
-template <int D, bool ROPE>
-__global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
+template <int D, bool ROPE, int NW>
+__global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
     const bf16* __restrict__ q, KVBlocks kv, const bf16* __restrict__ dout,
     const float* __restrict__ lse2, const float* __restrict__ delta, AttnShape p, int n_kt,
     int items, int per_xcd, RopeGrad rg) {
-  constexpr int BQ = 64, KT = 2, BKW = 64 * KT, KS = D / 32, DT = D / 16;
+  // KT key tiles of 16 per wave, KSTR keys apart
+  constexpr int BQ = 64, KT = 128 / (16 * NW), KSTR = 16 * NW, BKW = KSTR * KT, KS = D / 32, DT = D / 16;
+  static_assert(BKW == 128, "128 keys per workgroup");
   constexpr int kStages = 4;
+  // P and dS per 32-query half (fewer registers: two waves per SIMD at D 128)
+  // or for all 64 queries at once (more independent MFMAs: faster at D 64)
+  constexpr bool kSliced = D == 128;
   using Tile = Tile64<D>;
   // this wave's loads per query tile: Q, dO, and one 256-byte row statistic
-  // (waves 0 and 2 fetch lse2, waves 1 and 3 delta)
-  constexpr int kLoads = 2 * TileStream<D>::P + 1;
+  // (even waves fetch lse2, odd waves delta)
+  constexpr int kLoads = 2 * TileStream<D, NW>::P + 1;
   __shared__ __attribute__((aligned(1024))) bf16 sQ[kStages][Tile::kElems];
   __shared__ __attribute__((aligned(1024))) bf16 sD[kStages][Tile::kElems];
-  __shared__ __attribute__((aligned(256))) float sStat[kStages][4][BQ];
+  __shared__ __attribute__((aligned(256))) float sStat[kStages][NW][BQ];
 
   const int w = xcd_item(items, per_xcd);
   if (w < 0) return;
@@ -838,13 +842,13 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
   bf16* dvb = static_cast<bf16*>(kv.dv[blk]) + kv_off;
   bf16x8 kf[KT][KS], vf[KT][KS];
   f32x4 dka[KT][DT], dva[KT][DT];
-  int kbase = 0;  // key tile j of this wave: kbase + 64 j + l16
+  int kbase = 0;  // key tile j of this wave: kbase + KSTR j + l16
   // a sub-item's K/V fragments into registers and its accumulators to zero
   auto start = [&](int sub) {
     kbase = sub_tile(sub) * BKW + 16 * wave;
 #pragma unroll
     for (int j = 0; j < KT; ++j) {
-      const int key = kbase + 64 * j + l16;
+      const int key = kbase + KSTR * j + l16;
       const bool ok = key < p.Sk;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
@@ -858,13 +862,13 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
       }
     }
   };
-  // lane holds dK[key = kbase + 64 j + 4 g + e][d = 16 dt + l16]
+  // lane holds dK[key = kbase + KSTR j + 4 g + e][d = 16 dt + l16]
   auto finish = [&]() {
 #pragma unroll
     for (int j = 0; j < KT; ++j)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int key = kbase + 64 * j + g * 4 + e;
+        const int key = kbase + KSTR * j + g * 4 + e;
         if (key >= p.Sk) continue;
         bf16* dkr = dkb + static_cast<int64_t>(key) * p.kv_ss;
         if constexpr (ROPE) {
@@ -899,7 +903,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
 
   // Q / dO tiles and their row statistics stream through LDS (kStages deep),
   // across the two sub-items.  Past the last iteration the loads read zeros.
-  TileStream<D> lq, ldo;
+  TileStream<D, NW> lq, ldo;
   lq.init(p.q_ss, wave, lane);
   ldo.init(p.o_ss, wave, lane);
   const uint32_t q_bytes = static_cast<uint32_t>(((p.Sq - 1) * p.q_ss + D) * 2);
@@ -951,82 +955,155 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(
     bool any = false;
 #pragma unroll
     for (int j = 0; j < KT; ++j) {
-      const int kt0 = kbase + 64 * j;
+      const int kt0 = kbase + KSTR * j;
       live[j] = kt0 < p.Sk && !(p.causal && koff + kt0 > qa_last);
       need_mask[j] = (kt0 + 16 > p.Sk) || (p.causal && koff + kt0 + 15 > p.q_offset + q0);
       any = any || live[j];
     }
     if (!any) continue;
 
-    // S = Q K^T and dP = dO V^T: lane holds S[q = 16 mq + 4 g + e][key = kbase + 64 j + l16]
-    f32x4 s[4][KT], dp[4][KT];
-#pragma unroll
-    for (int mq = 0; mq < 4; ++mq)
+    if constexpr (kSliced) {
+      // tile-relative queries [qmin, qend) see key tile j's key of this lane
+      // (qend: the queries past Sq, whose zero-filled rows must not count)
+      int qmin[KT];
+      const int qend = min(BQ, p.Sq - q0);
 #pragma unroll
       for (int j = 0; j < KT; ++j) {
-        s[mq][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-        dp[mq][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        qmin[j] = 0;
+        if (need_mask[j]) {
+          const int key = kbase + KSTR * j + l16;
+          int64_t f = p.causal ? koff + key - p.q_offset - q0 : 0;
+          if (key >= p.Sk) f = BQ;
+          qmin[j] = f < 0 ? 0 : (f > BQ ? BQ : static_cast<int>(f));
+        }
       }
+      // per 32-query half s2: S = Q K^T and dP = dO V^T for its two 16-query
+      // slices (lane holds S[q = 16 mq + 4 g + e][key = kbase + KSTR j + l16]),
+      // P and dS = P (dP - delta) packed into the A operands, then the dV += P^T dO
+      // and dK += dS^T Q MFMAs over the half's dO^T / Q^T column fragments
 #pragma unroll
-    for (int mq = 0; mq < 4; ++mq) {
+      for (int s2 = 0; s2 < 2; ++s2) {
+        f32x4 s[2][KT], dp[2][KT];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 aq = Tile::row8(tq, mq * 16 + l16, ks * 32 + g * 8);
-        const bf16x8 ad = Tile::row8(td, mq * 16 + l16, ks * 32 + g * 8);
+        for (int m2 = 0; m2 < 2; ++m2)
 #pragma unroll
-        for (int j = 0; j < KT; ++j)
-          if (live[j]) {
-            s[mq][j] = mfma16(aq, kf[j][ks], s[mq][j]);
-            dp[mq][j] = mfma16(ad, vf[j][ks], dp[mq][j]);
+          for (int j = 0; j < KT; ++j) {
+            s[m2][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+            dp[m2][j] = f32x4{0.f, 0.f, 0.f, 0.f};
           }
-      }
-    }
-    bf16x8 pa[2][KT], da[2][KT];
 #pragma unroll
-    for (int j = 0; j < KT; ++j) {
-      if (!live[j]) continue;
-      // tile-relative queries [qmin, qend) see this lane's key (qend: the
-      // queries past Sq, whose zero-filled rows must not count)
-      int qmin = 0;
-      const int qend = min(BQ, p.Sq - q0);
-      if (need_mask[j]) {
-        const int key = kbase + 64 * j + l16;
-        int64_t f = p.causal ? koff + key - p.q_offset - q0 : 0;
-        if (key >= p.Sk) f = BQ;
-        qmin = f < 0 ? 0 : (f > BQ ? BQ : static_cast<int>(f));
+        for (int m2 = 0; m2 < 2; ++m2) {
+          const int mq = 2 * s2 + m2;
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) {
+            const bf16x8 aq = Tile::row8(tq, mq * 16 + l16, ks * 32 + g * 8);
+            const bf16x8 ad = Tile::row8(td, mq * 16 + l16, ks * 32 + g * 8);
+#pragma unroll
+            for (int j = 0; j < KT; ++j)
+              if (live[j]) {
+                s[m2][j] = mfma16(aq, kf[j][ks], s[m2][j]);
+                dp[m2][j] = mfma16(ad, vf[j][ks], dp[m2][j]);
+              }
+          }
+        }
+        bf16x8 pa[KT], da[KT];
+#pragma unroll
+        for (int j = 0; j < KT; ++j) {
+          if (!live[j]) continue;
+#pragma unroll
+          for (int m2 = 0; m2 < 2; ++m2)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int ql = (2 * s2 + m2) * 16 + g * 4 + e;
+              float pv = fast_exp2(fmaf(s[m2][j][e], c, -sL[ql]));
+              pv = (ql < qmin[j] || ql >= qend) ? 0.f : pv;
+              pa[j][4 * m2 + e] = static_cast<bf16>(pv);
+              da[j][4 * m2 + e] = static_cast<bf16>(pv * (dp[m2][j][e] - sDl[ql]));
+            }
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const bf16x8 bd = Tile::col8(td, 32 * s2, dt * 16, l16, g);
+          const bf16x8 bq = Tile::col8(tq, 32 * s2, dt * 16, l16, g);
+#pragma unroll
+          for (int j = 0; j < KT; ++j)
+            if (live[j]) {
+              dva[j][dt] = mfma16(pa[j], bd, dva[j][dt]);
+              dka[j][dt] = mfma16(da[j], bq, dka[j][dt]);
+            }
+        }
       }
+    } else {
+      // S = Q K^T and dP = dO V^T: lane holds S[q = 16 mq + 4 g + e][key = kbase + KSTR j + l16]
+      f32x4 s[4][KT], dp[4][KT];
 #pragma unroll
       for (int mq = 0; mq < 4; ++mq)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int ql = mq * 16 + g * 4 + e;
-          float pv = fast_exp2(fmaf(s[mq][j][e], c, -sL[ql]));
-          pv = (ql < qmin || ql >= qend) ? 0.f : pv;
-          s[mq][j][e] = pv;
-          dp[mq][j][e] = pv * (dp[mq][j][e] - sDl[ql]);
+        for (int j = 0; j < KT; ++j) {
+          s[mq][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+          dp[mq][j] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
+      for (int mq = 0; mq < 4; ++mq) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          pa[s2][j][e] = static_cast<bf16>(s[2 * s2][j][e]);
-          pa[s2][j][4 + e] = static_cast<bf16>(s[2 * s2 + 1][j][e]);
-          da[s2][j][e] = static_cast<bf16>(dp[2 * s2][j][e]);
-          da[s2][j][4 + e] = static_cast<bf16>(dp[2 * s2 + 1][j][e]);
+        for (int ks = 0; ks < KS; ++ks) {
+          const bf16x8 aq = Tile::row8(tq, mq * 16 + l16, ks * 32 + g * 8);
+          const bf16x8 ad = Tile::row8(td, mq * 16 + l16, ks * 32 + g * 8);
+#pragma unroll
+          for (int j = 0; j < KT; ++j)
+            if (live[j]) {
+              s[mq][j] = mfma16(aq, kf[j][ks], s[mq][j]);
+              dp[mq][j] = mfma16(ad, vf[j][ks], dp[mq][j]);
+            }
         }
-    }
+      }
+      bf16x8 pa[2][KT], da[2][KT];
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
+      for (int j = 0; j < KT; ++j) {
+        if (!live[j]) continue;
+        // tile-relative queries [qmin, qend) see this lane's key (qend: the
+        // queries past Sq, whose zero-filled rows must not count)
+        int qmin = 0;
+        const int qend = min(BQ, p.Sq - q0);
+        if (need_mask[j]) {
+          const int key = kbase + KSTR * j + l16;
+          int64_t f = p.causal ? koff + key - p.q_offset - q0 : 0;
+          if (key >= p.Sk) f = BQ;
+          qmin = f < 0 ? 0 : (f > BQ ? BQ : static_cast<int>(f));
+        }
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const bf16x8 bd = Tile::col8(td, 32 * s2, dt * 16, l16, g);
-        const bf16x8 bq = Tile::col8(tq, 32 * s2, dt * 16, l16, g);
+        for (int mq = 0; mq < 4; ++mq)
 #pragma unroll
-        for (int j = 0; j < KT; ++j)
-          if (live[j]) {
-            dva[j][dt] = mfma16(pa[s2][j], bd, dva[j][dt]);
-            dka[j][dt] = mfma16(da[s2][j], bq, dka[j][dt]);
+          for (int e = 0; e < 4; ++e) {
+            const int ql = mq * 16 + g * 4 + e;
+            float pv = fast_exp2(fmaf(s[mq][j][e], c, -sL[ql]));
+            pv = (ql < qmin || ql >= qend) ? 0.f : pv;
+            s[mq][j][e] = pv;
+            dp[mq][j][e] = pv * (dp[mq][j][e] - sDl[ql]);
           }
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            pa[s2][j][e] = static_cast<bf16>(s[2 * s2][j][e]);
+            pa[s2][j][4 + e] = static_cast<bf16>(s[2 * s2 + 1][j][e]);
+            da[s2][j][e] = static_cast<bf16>(dp[2 * s2][j][e]);
+            da[s2][j][4 + e] = static_cast<bf16>(dp[2 * s2 + 1][j][e]);
+          }
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const bf16x8 bd = Tile::col8(td, 32 * s2, dt * 16, l16, g);
+          const bf16x8 bq = Tile::col8(tq, 32 * s2, dt * 16, l16, g);
+#pragma unroll
+          for (int j = 0; j < KT; ++j)
+            if (live[j]) {
+              dva[j][dt] = mfma16(pa[s2][j], bd, dva[j][dt]);
+              dka[j][dt] = mfma16(da[s2][j], bq, dka[j][dt]);
+            }
+        }
       }
     }
   }
@@ -1407,20 +1484,22 @@ int attn_bwd_impl(const void* q, const void* const* k_blocks,
     nmb::bf16* dqp = static_cast<nmb::bf16*>(dq);
     // the dQ kernel also writes delta, which the dK/dV kernel reads: keep this order
     if (seq_q > 0) {
-      const int n_qt = static_cast<int>((seq_q + 127) / 128);  // 128-query tiles, two per workgroup at D 64
+      // query tiles of 128 (D 64, two per workgroup) or 256 (D 128, 8 waves)
+      const int bq = D == 64 ? 128 : 256;
+      const int n_qt = static_cast<int>((seq_q + bq - 1) / bq);
       const int64_t items = static_cast<int64_t>(D == 64 ? (n_qt + 1) / 2 : n_qt) * q_heads * batch;
       NMB_REQUIRE(items < (int64_t{1} << 30), "attn_bwd: problem too large for one launch");
       int per_xcd;
       unsigned blocks;
       xcd_grid(items, &per_xcd, &blocks);
       const RopeGrad rg = rope != nullptr ? *rope : RopeGrad{};
-#define NMB_DQ(DD, RR)                                                                          \
-  hipLaunchKernelGGL((nmb::attn_bwd_dq_kernel<DD, RR>), dim3(blocks), dim3(256), 0, stream, qp, kv, \
-                     opp, dp, lse, delta, lse2, dqp, p, n_qt, static_cast<int>(items), per_xcd, rg)
+#define NMB_DQ(DD, RR, NW)                                                                            \
+  hipLaunchKernelGGL((nmb::attn_bwd_dq_kernel<DD, RR, NW>), dim3(blocks), dim3(64 * NW), 0, stream, qp, \
+                     kv, opp, dp, lse, delta, lse2, dqp, p, n_qt, static_cast<int>(items), per_xcd, rg)
       if (D == 64) {
-        if (rope) NMB_DQ(64, true); else NMB_DQ(64, false);
+        if (rope) NMB_DQ(64, true, 4); else NMB_DQ(64, false, 4);
       } else {
-        if (rope) NMB_DQ(128, true); else NMB_DQ(128, false);
+        if (rope) NMB_DQ(128, true, 8); else NMB_DQ(128, false, 8);
       }
 #undef NMB_DQ
       NMB_CHECK_LAUNCH("attn_bwd(dq)");
@@ -1433,13 +1512,13 @@ int attn_bwd_impl(const void* q, const void* const* k_blocks,
       unsigned blocks;
       xcd_grid(items, &per_xcd, &blocks);
       const RopeGrad rg = rope != nullptr ? *rope : RopeGrad{};
-#define NMB_DKDV(DD, RR)                                                                          \
-  hipLaunchKernelGGL((nmb::attn_bwd_dkdv_kernel<DD, RR>), dim3(blocks), dim3(256), 0, stream, qp, kv, \
-                     dp, lse2, delta, p, n_kt, static_cast<int>(items), per_xcd, rg)
+#define NMB_DKDV(DD, RR, NW)                                                                            \
+  hipLaunchKernelGGL((nmb::attn_bwd_dkdv_kernel<DD, RR, NW>), dim3(blocks), dim3(64 * NW), 0, stream, qp, \
+                     kv, dp, lse2, delta, p, n_kt, static_cast<int>(items), per_xcd, rg)
       if (D == 64) {
-        if (rope) NMB_DKDV(64, true); else NMB_DKDV(64, false);
+        if (rope) NMB_DKDV(64, true, 4); else NMB_DKDV(64, false, 4);
       } else {
-        if (rope) NMB_DKDV(128, true); else NMB_DKDV(128, false);
+        if (rope) NMB_DKDV(128, true, 8); else NMB_DKDV(128, false, 8);
       }
 #undef NMB_DKDV
       NMB_CHECK_LAUNCH("attn_bwd(dkdv)");
