@@ -41,9 +41,22 @@ template <typename T> __device__ __forceinline__ float round_as(float x) {
 }
 
 // Products and sums without FMA contraction, so fp32 results reproduce the
-// separately rounded tensor ops of the reference.
-__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
-__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
+// separately rounded tensor ops of the reference.  __fmul_rn / __fadd_rn are
+// plain operators in this HIP header, which HIP's default -ffp-contract fuses
+// (add_rn(c, mul_rn(a, b)) became one v_fmac); the pragma keeps each
+// operation rounded on its own.
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+__device__ __forceinline__ float sub_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a - b;
+}
 
 // Cross-lane exchanges without an LDS round trip (ds_bpermute costs a full LDS
 // latency per step).  v_permlane32_swap a, b swaps the upper 32 lanes of a

@@ -19,6 +19,25 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kBwdBlocks = 256;
 
+// Loads are issued unconditionally: a lane whose 16-byte vector lies past the
+// row's end reads column 0 instead and drops the value at unpack time.  (A
+// load under a lane condition is followed by a wait for its data where the
+// branches join, which serialises a wave's loads.)
+__device__ __forceinline__ int clamp_col(int it, int lane, int vec, int cols) {
+  const int c = (it * 64 + lane) * vec;
+  return c < cols ? c : 0;
+}
+
+__device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+
+template <typename T>
+__device__ __forceinline__ void unpack_masked(const uint4& raw, bool keep, float (&out)[VecTraits<T>::N]) {
+  T e[VecTraits<T>::N];
+  __builtin_memcpy(e, &raw, 16);
+#pragma unroll
+  for (int i = 0; i < VecTraits<T>::N; ++i) out[i] = keep ? to_f32(e[i]) : 0.f;
+}
+
 template <typename T>
 __device__ __forceinline__ float inv_rms(float sum_sq, int cols, float eps) {
   const float var = __fdiv_rn(sum_sq, static_cast<float>(cols));
@@ -36,33 +55,39 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const T* __restrict__ 
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
   if (row >= rows) return;  // wave-uniform
   const T* xr = x + row * cols;
+  // every load (x and w) is issued before any value is used
+  uint4 xraw[ITERS], wraw[ITERS];
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const int c = clamp_col(it, lane, V, cols);
+    xraw[it] = ld16(xr + c);
+    wraw[it] = ld16(w + c);
+  }
   float v[ITERS][V];
   float ss = 0.f;
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
-    const int c = (it * 64 + lane) * V;
-    if (c < cols) {
-      load_vec<T>(xr + c, v[it]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < V; ++i) v[it][i] = 0.f;
-    }
+    unpack_masked<T>(xraw[it], (it * 64 + lane) * V < cols, v[it]);
 #pragma unroll
     for (int i = 0; i < V; ++i) ss += v[it][i] * v[it][i];
   }
   ss = wave_sum(ss);
   const float r = inv_rms<T>(ss, cols, eps);
+  // the weights are needed here (an empty asm use), so their loads stay with
+  // those of x instead of being sunk into the conditional stores below
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) asm volatile("" ::"v"(wraw[it].x), "v"(wraw[it].y), "v"(wraw[it].z), "v"(wraw[it].w));
   T* yr = y + row * cols;
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
+    // computed by every lane (only the store is conditional), so no load is
+    // moved into the conditional block
     const int c = (it * 64 + lane) * V;
-    if (c < cols) {
-      float wv[V], o[V];
-      load_vec<T>(w + c, wv);
+    float wv[V], o[V];
+    unpack_masked<T>(wraw[it], true, wv);
 #pragma unroll
-      for (int i = 0; i < V; ++i) o[i] = mul_rn(round_as<T>(mul_rn(v[it][i], r)), wv[i]);
-      store_vec<T>(yr + c, o);
-    }
+    for (int i = 0; i < V; ++i) o[i] = mul_rn(round_as<T>(mul_rn(v[it][i], r)), wv[i]);
+    if (c < cols) store_vec<T>(yr + c, o);
   }
   if (rstd != nullptr && lane == 0) rstd[row] = r;
 }
@@ -76,20 +101,12 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const T* __restrict__ 
 constexpr int kBwdWaves = 8;
 constexpr int rows_per_wave(int iters) { return iters <= 2 ? 4 : 1; }
 
-template <typename T>
-__device__ __forceinline__ void unpack(const uint4& raw, float (&out)[VecTraits<T>::N]) {
-  T e[VecTraits<T>::N];
-  __builtin_memcpy(e, &raw, 16);
-#pragma unroll
-  for (int i = 0; i < VecTraits<T>::N; ++i) out[i] = to_f32(e[i]);
-}
-
 // One row: dx = rstd * (g - n * mean(g * n)) (+ the residual gradient), with
 // g = round(dy * w) and n = x * rstd; acc += round(dy * round(n)) (the weight
 // gradient's per-row term, rounded as the reference's product tensor is).
-template <typename T, int ITERS>
+template <typename T, int ITERS, bool RES>
 __device__ __forceinline__ void bwd_row(const uint4 (&xr)[ITERS], const uint4 (&dr)[ITERS],
-                                        const uint4 (&rr)[ITERS], bool has_res,
+                                        const uint4 (&rr)[ITERS],
                                         const float (&wv)[ITERS][VecTraits<T>::N],
                                         float (&acc)[ITERS][VecTraits<T>::N], T* __restrict__ dxr,
                                         int lane, int cols, float eps) {
@@ -98,8 +115,9 @@ __device__ __forceinline__ void bwd_row(const uint4 (&xr)[ITERS], const uint4 (&
   float ss = 0.f;
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
-    unpack<T>(xr[it], xv[it]);
-    unpack<T>(dr[it], dv[it]);
+    const bool in_row = (it * 64 + lane) * V < cols;
+    unpack_masked<T>(xr[it], in_row, xv[it]);
+    unpack_masked<T>(dr[it], in_row, dv[it]);
 #pragma unroll
     for (int i = 0; i < V; ++i) ss += xv[it][i] * xv[it][i];
   }
@@ -112,7 +130,7 @@ __device__ __forceinline__ void bwd_row(const uint4 (&xr)[ITERS], const uint4 (&
     for (int i = 0; i < V; ++i) {
       const float n = mul_rn(xv[it][i], r);
       const float g = round_as<T>(mul_rn(dv[it][i], wv[it][i]));
-      dot += g * n;
+      dot = add_rn(dot, mul_rn(g, n));
       acc[it][i] += round_as<T>(mul_rn(dv[it][i], round_as<T>(n)));
       xv[it][i] = n;
       dv[it][i] = g;
@@ -126,10 +144,12 @@ __device__ __forceinline__ void bwd_row(const uint4 (&xr)[ITERS], const uint4 (&
     if (c < cols) {
       float o[V];
 #pragma unroll
-      for (int i = 0; i < V; ++i) o[i] = r * (dv[it][i] - xv[it][i] * mean_dot);
-      if (has_res) {
+      // each product and difference rounded on its own (no contraction), as
+      // the reference's separate tensor operations round them
+      for (int i = 0; i < V; ++i) o[i] = mul_rn(r, sub_rn(dv[it][i], mul_rn(xv[it][i], mean_dot)));
+      if constexpr (RES) {
         float rv[V];
-        unpack<T>(rr[it], rv);
+        unpack_masked<T>(rr[it], true, rv);
 #pragma unroll
         for (int i = 0; i < V; ++i) o[i] += rv[i];
       }
@@ -142,19 +162,14 @@ template <typename T, int ITERS>
 __device__ __forceinline__ void load_row(const T* __restrict__ p, float (&v)[ITERS][VecTraits<T>::N],
                                          int lane, int cols) {
   constexpr int V = VecTraits<T>::N;
+  uint4 raw[ITERS];
 #pragma unroll
-  for (int it = 0; it < ITERS; ++it) {
-    const int c = (it * 64 + lane) * V;
-    if (c < cols) {
-      load_vec<T>(p + c, v[it]);
-    } else {
+  for (int it = 0; it < ITERS; ++it) raw[it] = ld16(p + clamp_col(it, lane, V, cols));
 #pragma unroll
-      for (int i = 0; i < V; ++i) v[it][i] = 0.f;
-    }
-  }
+  for (int it = 0; it < ITERS; ++it) unpack_masked<T>(raw[it], (it * 64 + lane) * V < cols, v[it]);
 }
 
-template <typename T, int ITERS>
+template <typename T, int ITERS, bool RES>
 __global__ __launch_bounds__(512) void rmsnorm_bwd_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ dy,
     const T* __restrict__ dres, T* __restrict__ dx, float* __restrict__ partial, int64_t rows,
@@ -172,7 +187,6 @@ __global__ __launch_bounds__(512) void rmsnorm_bwd_kernel(
     for (int i = 0; i < V; ++i) acc[it][i] = 0.f;
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rows_per_block;
   const int64_t r1 = min(rows, r0 + rows_per_block);
-  const bool has_res = dres != nullptr;
   constexpr int kRowsPerWave = rows_per_wave(ITERS);
   for (int64_t base = r0; base < r1; base += kBwdWaves * kRowsPerWave) {
     uint4 xr[kRowsPerWave][ITERS], dr[kRowsPerWave][ITERS], rr[kRowsPerWave][ITERS];
@@ -181,19 +195,18 @@ __global__ __launch_bounds__(512) void rmsnorm_bwd_kernel(
       const int64_t row = base + wave + kBwdWaves * k;
 #pragma unroll
       for (int it = 0; it < ITERS; ++it) {
-        const int c = (it * 64 + lane) * V;
-        const bool ok = row < r1 && c < cols;
-        const int64_t o = row * cols + c;
-        xr[k][it] = ok ? *reinterpret_cast<const uint4*>(x + o) : uint4{0, 0, 0, 0};
-        dr[k][it] = ok ? *reinterpret_cast<const uint4*>(dy + o) : uint4{0, 0, 0, 0};
-        rr[k][it] = ok && has_res ? *reinterpret_cast<const uint4*>(dres + o) : uint4{0, 0, 0, 0};
+        // rows past the block's end read row r0 (never used)
+        const int64_t o = (row < r1 ? row : r0) * cols + clamp_col(it, lane, V, cols);
+        xr[k][it] = ld16(x + o);
+        dr[k][it] = ld16(dy + o);
+        rr[k][it] = RES ? ld16(dres + o) : uint4{0, 0, 0, 0};
       }
     }
 #pragma unroll
     for (int k = 0; k < kRowsPerWave; ++k) {
       const int64_t row = base + wave + kBwdWaves * k;
       if (row < r1)  // wave-uniform
-        bwd_row<T, ITERS>(xr[k], dr[k], rr[k], has_res, wv, acc, dx + row * cols, lane, cols, eps);
+        bwd_row<T, ITERS, RES>(xr[k], dr[k], rr[k], wv, acc, dx + row * cols, lane, cols, eps);
     }
   }
   // fold the 8 wave partials in two rounds through 4 LDS rows (<= 64 KiB)
@@ -341,10 +354,14 @@ int bwd_impl(const void* x, const void* w, const void* dy, const void* dres, voi
   float* part = static_cast<float*>(ws);
   const size_t lds = static_cast<size_t>(4) * cols * sizeof(float);
   switch (iters_for(c, VecTraits<T>::N)) {
-#define NMB_CASE(I)                                                                       \
-  case I:                                                                                 \
-    hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, I>), dim3(nblocks), dim3(512), lds, stream, \
-                       xp, wp, dyp, drp, dxp, part, rows, c, eps, rpb);                   \
+#define NMB_CASE(I)                                                                              \
+  case I:                                                                                        \
+    if (drp != nullptr)                                                                          \
+      hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, I, true>), dim3(nblocks), dim3(512), lds, stream, \
+                         xp, wp, dyp, drp, dxp, part, rows, c, eps, rpb);                        \
+    else                                                                                         \
+      hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, I, false>), dim3(nblocks), dim3(512), lds,        \
+                         stream, xp, wp, dyp, drp, dxp, part, rows, c, eps, rpb);                \
     break;
     NMB_CASE(1) NMB_CASE(2) NMB_CASE(3) NMB_CASE(4) NMB_CASE(5) NMB_CASE(6) NMB_CASE(7)
     NMB_CASE(8)

@@ -88,6 +88,23 @@ def test_rope_matches_oracle(device, shape, dtype) -> None:
     close(kd.grad, kr.grad, dtype)
 
 
+@pytest.mark.parametrize("d", [64, 128])
+def test_rope_bf16_forward_is_bit_exact(device, d) -> None:
+    """Given the same bf16 cos/sin tables, the kernel rounds where the reference's
+    three bf16 tensor ops round (q*cos, rotate_half(q)*sin, their sum), so the
+    rotated q and k are bit-equal to the oracle's (nn/rotary.py:27-38)."""
+    g = gen(5)
+    b, h, s = 2, 4, 96
+    q = torch.randn(b, s, h, d, generator=g).to(torch.bfloat16).transpose(1, 2)
+    k = torch.randn(b, s, h // 2, d, generator=g).to(torch.bfloat16).transpose(1, 2)
+    # positions far from 0, so cos/sin take many distinct values
+    cos, sin = R.rope_cos_sin(torch.arange(s) + 3000, d, 1e4, torch.bfloat16)
+    oq, ok = R.apply_rotary_pos_emb(q, k, cos, sin)
+    pq, pk = nm.apply_rotary_pos_emb(q.to(device), k.to(device), cos.to(device), sin.to(device))
+    assert torch.equal(pq.cpu(), oq)
+    assert torch.equal(pk.cpu(), ok)
+
+
 def test_rope_offset_positions_and_inverse(device) -> None:
     """Offset form (positions offset + s) equals explicit ids; inverse undoes forward."""
     g = gen(2)
