@@ -38,13 +38,35 @@ __device__ __forceinline__ void unpack_masked(const uint4& raw, bool keep, float
   for (int i = 0; i < VecTraits<T>::N; ++i) out[i] = keep ? to_f32(e[i]) : 0.f;
 }
 
+// 16 bytes of T from V floats (bf16: pairs through one two-wide conversion,
+// v_cvt_pk_bf16_f32, straight into the register that is stored)
+template <typename T>
+__device__ __forceinline__ uint4 pack16(const float (&v)[VecTraits<T>::N]) {
+  uint4 r;
+  if constexpr (sizeof(T) == 2) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const b2 p = __builtin_convertvector(f2{v[2 * j], v[2 * j + 1]}, b2);
+      __builtin_memcpy(&w[j], &p, 4);
+    }
+    r = uint4{w[0], w[1], w[2], w[3]};
+  } else {
+    __builtin_memcpy(&r, v, 16);
+  }
+  return r;
+}
+
 template <typename T>
 __device__ __forceinline__ float inv_rms(float sum_sq, int cols, float eps) {
   const float var = __fdiv_rn(sum_sq, static_cast<float>(cols));
   return __fdiv_rn(1.0f, __fsqrt_rn(add_rn(var, eps)));
 }
 
-template <typename T, int ITERS>
+// FULL: the row is exactly ITERS vectors per lane (no column masks)
+template <typename T, int ITERS, bool FULL>
 __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const T* __restrict__ x,
                                                           const T* __restrict__ w,
                                                           T* __restrict__ y,
@@ -59,7 +81,7 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const T* __restrict__ 
   uint4 xraw[ITERS], wraw[ITERS];
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
-    const int c = clamp_col(it, lane, V, cols);
+    const int c = FULL ? (it * 64 + lane) * V : clamp_col(it, lane, V, cols);
     xraw[it] = ld16(xr + c);
     wraw[it] = ld16(w + c);
   }
@@ -67,7 +89,7 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const T* __restrict__ 
   float ss = 0.f;
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
-    unpack_masked<T>(xraw[it], (it * 64 + lane) * V < cols, v[it]);
+    unpack_masked<T>(xraw[it], FULL || (it * 64 + lane) * V < cols, v[it]);
 #pragma unroll
     for (int i = 0; i < V; ++i) ss += v[it][i] * v[it][i];
   }
@@ -87,7 +109,7 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const T* __restrict__ 
     unpack_masked<T>(wraw[it], true, wv);
 #pragma unroll
     for (int i = 0; i < V; ++i) o[i] = mul_rn(round_as<T>(mul_rn(v[it][i], r)), wv[i]);
-    if (c < cols) store_vec<T>(yr + c, o);
+    if (FULL || c < cols) store_vec<T>(yr + c, o);
   }
   if (rstd != nullptr && lane == 0) rstd[row] = r;
 }
@@ -104,18 +126,22 @@ constexpr int rows_per_wave(int iters) { return iters <= 2 ? 4 : 1; }
 // One row: dx = rstd * (g - n * mean(g * n)) (+ the residual gradient), with
 // g = round(dy * w) and n = x * rstd; acc += round(dy * round(n)) (the weight
 // gradient's per-row term, rounded as the reference's product tensor is).
-template <typename T, int ITERS, bool RES>
+// dx of the row goes to out (packed), not to memory: the caller stores a
+// wave's rows after computing all of them.  FULL: whole tiles (the row is
+// exactly ITERS vectors per lane and every block row exists), so nothing is
+// masked and no branch splits the stores.
+template <typename T, int ITERS, bool RES, bool FULL>
 __device__ __forceinline__ void bwd_row(const uint4 (&xr)[ITERS], const uint4 (&dr)[ITERS],
                                         const uint4 (&rr)[ITERS],
                                         const float (&wv)[ITERS][VecTraits<T>::N],
-                                        float (&acc)[ITERS][VecTraits<T>::N], T* __restrict__ dxr,
+                                        float (&acc)[ITERS][VecTraits<T>::N], uint4 (&out)[ITERS],
                                         int lane, int cols, float eps) {
   constexpr int V = VecTraits<T>::N;
   float xv[ITERS][V], dv[ITERS][V];
   float ss = 0.f;
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
-    const bool in_row = (it * 64 + lane) * V < cols;
+    const bool in_row = FULL || (it * 64 + lane) * V < cols;
     unpack_masked<T>(xr[it], in_row, xv[it]);
     unpack_masked<T>(dr[it], in_row, dv[it]);
 #pragma unroll
@@ -140,21 +166,18 @@ __device__ __forceinline__ void bwd_row(const uint4 (&xr)[ITERS], const uint4 (&
   const float mean_dot = __fdiv_rn(dot, static_cast<float>(cols));
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
-    const int c = (it * 64 + lane) * V;
-    if (c < cols) {
-      float o[V];
+    float o[V];
+    // each product and difference rounded on its own (no contraction), as
+    // the reference's separate tensor operations round them
 #pragma unroll
-      // each product and difference rounded on its own (no contraction), as
-      // the reference's separate tensor operations round them
-      for (int i = 0; i < V; ++i) o[i] = mul_rn(r, sub_rn(dv[it][i], mul_rn(xv[it][i], mean_dot)));
-      if constexpr (RES) {
-        float rv[V];
-        unpack_masked<T>(rr[it], true, rv);
+    for (int i = 0; i < V; ++i) o[i] = mul_rn(r, sub_rn(dv[it][i], mul_rn(xv[it][i], mean_dot)));
+    if constexpr (RES) {
+      float rv[V];
+      unpack_masked<T>(rr[it], true, rv);
 #pragma unroll
-        for (int i = 0; i < V; ++i) o[i] += rv[i];
-      }
-      store_vec<T>(dxr + c, o);
+      for (int i = 0; i < V; ++i) o[i] += rv[i];
     }
+    out[it] = pack16<T>(o);
   }
 }
 
@@ -169,7 +192,7 @@ __device__ __forceinline__ void load_row(const T* __restrict__ p, float (&v)[ITE
   for (int it = 0; it < ITERS; ++it) unpack_masked<T>(raw[it], (it * 64 + lane) * V < cols, v[it]);
 }
 
-template <typename T, int ITERS, bool RES>
+template <typename T, int ITERS, bool RES, bool FULL>
 __global__ __launch_bounds__(512) void rmsnorm_bwd_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ dy,
     const T* __restrict__ dres, T* __restrict__ dx, float* __restrict__ partial, int64_t rows,
@@ -196,17 +219,33 @@ __global__ __launch_bounds__(512) void rmsnorm_bwd_kernel(
 #pragma unroll
       for (int it = 0; it < ITERS; ++it) {
         // rows past the block's end read row r0 (never used)
-        const int64_t o = (row < r1 ? row : r0) * cols + clamp_col(it, lane, V, cols);
+        const int64_t o = (FULL || row < r1 ? row : r0) * cols + (FULL ? (it * 64 + lane) * V : clamp_col(it, lane, V, cols));
         xr[k][it] = ld16(x + o);
         dr[k][it] = ld16(dy + o);
         rr[k][it] = RES ? ld16(dres + o) : uint4{0, 0, 0, 0};
       }
     }
+    // rows are computed as their loads land (loads complete in order); the
+    // stores wait until every row of the group is done, because a wait after
+    // a store covers every outstanding load (loads and stores share one
+    // counter and complete out of order)
+    uint4 dxo[kRowsPerWave][ITERS];
 #pragma unroll
     for (int k = 0; k < kRowsPerWave; ++k) {
       const int64_t row = base + wave + kBwdWaves * k;
-      if (row < r1)  // wave-uniform
-        bwd_row<T, ITERS, RES>(xr[k], dr[k], rr[k], wv, acc, dx + row * cols, lane, cols, eps);
+      if (FULL || row < r1)  // wave-uniform
+        bwd_row<T, ITERS, RES, FULL>(xr[k], dr[k], rr[k], wv, acc, dxo[k], lane, cols, eps);
+    }
+#pragma unroll
+    for (int k = 0; k < kRowsPerWave; ++k) {
+      const int64_t row = base + wave + kBwdWaves * k;
+      if (FULL || row < r1) {  // wave-uniform
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+          const int c = (it * 64 + lane) * V;
+          if (FULL || c < cols) *reinterpret_cast<uint4*>(dx + row * cols + c) = dxo[k][it];
+        }
+      }
     }
   }
   // fold the 8 wave partials in two rounds through 4 LDS rows (<= 64 KiB)
@@ -314,10 +353,14 @@ int fwd_impl(const void* x, const void* w, void* y, float* rstd, int64_t rows, i
   const T* wp = static_cast<const T*>(w);
   T* yp = static_cast<T*>(y);
   switch (iters_for(c, VecTraits<T>::N)) {
-#define NMB_CASE(I)                                                                        \
-  case I:                                                                                  \
-    hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, I>), grid, dim3(256), 0, stream, xp, wp, yp, \
-                       rstd, rows, c, eps);                                                \
+#define NMB_CASE(I)                                                                               \
+  case I:                                                                                         \
+    if (c == I * 64 * VecTraits<T>::N)                                                            \
+      hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, I, true>), grid, dim3(256), 0, stream, xp, wp, yp, \
+                         rstd, rows, c, eps);                                                     \
+    else                                                                                          \
+      hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, I, false>), grid, dim3(256), 0, stream, xp, wp,    \
+                         yp, rstd, rows, c, eps);                                                 \
     break;
     NMB_CASE(1) NMB_CASE(2) NMB_CASE(3) NMB_CASE(4) NMB_CASE(5) NMB_CASE(6) NMB_CASE(7)
     NMB_CASE(8)
@@ -354,18 +397,22 @@ int bwd_impl(const void* x, const void* w, const void* dy, const void* dres, voi
   float* part = static_cast<float*>(ws);
   const size_t lds = static_cast<size_t>(4) * cols * sizeof(float);
   switch (iters_for(c, VecTraits<T>::N)) {
+#define NMB_LAUNCH(I, RES, FULL)                                                                     \
+  hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, I, RES, FULL>), dim3(nblocks), dim3(512), lds, stream, xp, \
+                     wp, dyp, drp, dxp, part, rows, c, eps, rpb)
 #define NMB_CASE(I)                                                                              \
   case I:                                                                                        \
-    if (drp != nullptr)                                                                          \
-      hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, I, true>), dim3(nblocks), dim3(512), lds, stream, \
-                         xp, wp, dyp, drp, dxp, part, rows, c, eps, rpb);                        \
-    else                                                                                         \
-      hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, I, false>), dim3(nblocks), dim3(512), lds,        \
-                         stream, xp, wp, dyp, drp, dxp, part, rows, c, eps, rpb);                \
+    if (c == I * 64 * VecTraits<T>::N && rows == nblocks * rpb &&                              \
+        rpb % (kBwdWaves * rows_per_wave(I)) == 0) {                                             \
+      if (drp != nullptr) NMB_LAUNCH(I, true, true); else NMB_LAUNCH(I, false, true);            \
+    } else {                                                                                     \
+      if (drp != nullptr) NMB_LAUNCH(I, true, false); else NMB_LAUNCH(I, false, false);          \
+    }                                                                                            \
     break;
     NMB_CASE(1) NMB_CASE(2) NMB_CASE(3) NMB_CASE(4) NMB_CASE(5) NMB_CASE(6) NMB_CASE(7)
     NMB_CASE(8)
 #undef NMB_CASE
+#undef NMB_LAUNCH
   }
   NMB_CHECK_LAUNCH("rmsnorm_bwd");
   hipLaunchKernelGGL((column_sum_kernel<T>), dim3((c + 15) / 16), dim3(256), 0, stream, part,
