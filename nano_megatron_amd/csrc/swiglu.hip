@@ -7,38 +7,126 @@
 //   d_gate = cast(ds * sigmoid(g) * (1 + g * (1 - sigmoid(g))))
 // and it re-emits `out` for the down-projection weight gradient, so the
 // forward never has to keep it.  Pure HBM streaming with 16-byte accesses.
+// d_gate uses the fast sigmoid below (a few fp32 ulps before its bf16
+// rounding); the activation itself rounds exactly as the exact formula does.
 #include "common.h"
 #include "vec.h"
 
 namespace nmb {
 namespace {
 
-__device__ __forceinline__ float sigmoid_f(float g) { return __fdiv_rn(1.0f, 1.0f + expf(-g)); }
+// sigmoid(g) = 1 / (1 + 2^(-g log2 e)) from the hardware exp2 and reciprocal
+// (v_exp_f32, v_rcp_f32), against ~25 VALU instructions for expf plus an IEEE
+// division, which made these kernels VALU-bound.  Relative error: the rounded
+// argument t = -g log2 e contributes |t| ln2 / 2 fp32 ulps (<= 45 for |t| <=
+// 128, beyond which 2^t saturates to inf or 0), exp2, rcp and the final
+// product ~3 more.  Limits: g -> -inf: 2^+inf = inf, 1/inf = 0; g -> +inf:
+// sigmoid 1; NaN propagates.
+__device__ __forceinline__ float sigmoid_f(float g) {
+  constexpr float kLog2e = 1.4426950408889634f;
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * kLog2e));
+}
+
+// silu(g) = g sigmoid(g), rounded to T where the reference's F.silu output is
+// rounded.  For bf16 the result equals that of the exact formula the reference
+// evaluates in fp32 (g / (1 + exp(-g)), IEEE division): the fast product is
+// used unless it lies within 64 fp32 ulps of a bf16 rounding tie (low 16 bits
+// near 0x8000; the fast error bound above plus expf's own error is below 64),
+// or g < -87 (2^t near the fp32 range end, where the reciprocal's result is
+// subnormal); there the exact formula is evaluated (~0.2% of elements).
+template <typename T>
+__device__ __forceinline__ float silu_t(float g, float sig) {
+  float s = mul_rn(g, sig);
+  if constexpr (sizeof(T) == 2) {
+    const uint32_t b = __float_as_uint(s);
+    if (((b - 0x8000u + 64u) & 0xFFFFu) <= 128u || g < -87.0f) s = __fdiv_rn(g, 1.0f + expf(-g));
+  }
+  return round_as<T>(s);
+}
 
 struct SwigluArgs {
   int64_t g_ld, u_ld, d_ld, dg_ld, du_ld, o_ld;
   int64_t rows, cols, vec_cols, total;
 };
 
+// Launch shape (both kernels): wavefront w takes kVec x 64 consecutive 16-byte
+// vectors of the flattened [rows, cols / V] index space (one coalesced
+// 1 KB access per k, split only where a row ends), every load issued before
+// any is used; the row of a vector index comes from a multiply-high division.
+// Indices past the end re-read the last vector and are not stored.
+constexpr int kVec = 2;
+
+// n / d for n < 2^31 by a precomputed multiplier (round-up method of
+// Granlund and Montgomery): s = ceil(log2 d), m = floor(2^32 (2^s - d) / d) + 1,
+// n / d = (mulhi(n, m) + n) >> s.
+struct FastDiv {
+  uint32_t d, m, s;
+};
+
+FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f{d, 0, 0};
+  while ((uint64_t{1} << f.s) < d) ++f.s;
+  f.m = static_cast<uint32_t>(((uint64_t{1} << 32) * ((uint64_t{1} << f.s) - d)) / d + 1);
+  return f;
+}
+
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv& f) {
+  return (__umulhi(n, f.m) + n) >> f.s;
+}
+
+__device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+
+template <typename T>
+__device__ __forceinline__ void unpack(const uint4& raw, float (&out)[VecTraits<T>::N]) {
+  T e[VecTraits<T>::N];
+  __builtin_memcpy(e, &raw, 16);
+#pragma unroll
+  for (int i = 0; i < VecTraits<T>::N; ++i) out[i] = to_f32(e[i]);
+}
+
+// row and vector column of vector slot k of this lane (clamped to the last
+// vector); fd divides by the vectors per row
+__device__ __forceinline__ void locate(const SwigluArgs& a, const FastDiv& fd, int k, bool& ok,
+                                       int64_t& row, int64_t& vcol) {
+  const uint32_t w = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const uint32_t i = (w * kVec + k) * 64 + (threadIdx.x & 63);
+  ok = i < static_cast<uint32_t>(a.total);
+  const uint32_t ic = ok ? i : static_cast<uint32_t>(a.total) - 1;
+  const uint32_t r = fast_div(ic, fd);
+  row = r;
+  vcol = ic - r * fd.d;
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void swiglu_fwd_kernel(const T* __restrict__ g,
                                                          const T* __restrict__ u,
-                                                         T* __restrict__ o, SwigluArgs a) {
+                                                         T* __restrict__ o, SwigluArgs a,
+                                                         FastDiv fd) {
   constexpr int V = VecTraits<T>::N;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < a.total;
-       i += static_cast<int64_t>(gridDim.x) * 256) {
-    const int64_t r = i / a.vec_cols;
-    const int64_t c = (i - r * a.vec_cols) * V;
-    float gv[V], uv[V], ov[V];
-    load_vec<T>(g + r * a.g_ld + c, gv);
-    load_vec<T>(u + r * a.u_ld + c, uv);
+  bool ok[kVec];
+  int64_t row[kVec], c[kVec];
+  uint4 graw[kVec], uraw[kVec];
 #pragma unroll
-    for (int k = 0; k < V; ++k) {
-      const float s = round_as<T>(__fdiv_rn(gv[k], 1.0f + expf(-gv[k])));
-      ov[k] = mul_rn(s, uv[k]);
-    }
-    store_vec<T>(o + r * a.o_ld + c, ov);
+  for (int k = 0; k < kVec; ++k) {
+    locate(a, fd, k, ok[k], row[k], c[k]);
+    c[k] *= V;
+    graw[k] = ld16(g + row[k] * a.g_ld + c[k]);
+    uraw[k] = ld16(u + row[k] * a.u_ld + c[k]);
   }
+  // every vector computed before any store: a wait after a store would cover
+  // every outstanding load (loads and stores share one counter)
+  float ov[kVec][V];
+#pragma unroll
+  for (int k = 0; k < kVec; ++k) {
+    float gv[V], uv[V];
+    unpack<T>(graw[k], gv);
+    unpack<T>(uraw[k], uv);
+#pragma unroll
+    for (int e = 0; e < V; ++e) ov[k][e] = mul_rn(silu_t<T>(gv[e], sigmoid_f(gv[e])), uv[e]);
+  }
+#pragma unroll
+  for (int k = 0; k < kVec; ++k)
+    if (ok[k]) store_vec<T>(o + row[k] * a.o_ld + c[k], ov[k]);
 }
 
 template <typename T>
@@ -46,29 +134,50 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const T* __restrict__ g
                                                          const T* __restrict__ u,
                                                          const T* __restrict__ dout,
                                                          T* __restrict__ dg, T* __restrict__ du,
-                                                         T* __restrict__ o, SwigluArgs a) {
+                                                         T* __restrict__ o, SwigluArgs a,
+                                                         FastDiv fd) {
   constexpr int V = VecTraits<T>::N;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < a.total;
-       i += static_cast<int64_t>(gridDim.x) * 256) {
-    const int64_t r = i / a.vec_cols;
-    const int64_t c = (i - r * a.vec_cols) * V;
-    float gv[V], uv[V], dv[V], dgv[V], duv[V], ov[V];
-    load_vec<T>(g + r * a.g_ld + c, gv);
-    load_vec<T>(u + r * a.u_ld + c, uv);
-    load_vec<T>(dout + r * a.d_ld + c, dv);
+  bool ok[kVec];
+  int64_t row[kVec], c[kVec];
+  uint4 graw[kVec], uraw[kVec], draw[kVec];
 #pragma unroll
-    for (int k = 0; k < V; ++k) {
-      const float sig = sigmoid_f(gv[k]);
-      const float s = round_as<T>(__fdiv_rn(gv[k], 1.0f + expf(-gv[k])));
-      ov[k] = mul_rn(s, uv[k]);
-      duv[k] = mul_rn(dv[k], s);
-      const float ds = round_as<T>(mul_rn(dv[k], uv[k]));
-      dgv[k] = ds * sig * (1.0f + gv[k] * (1.0f - sig));
-    }
-    store_vec<T>(dg + r * a.dg_ld + c, dgv);
-    store_vec<T>(du + r * a.du_ld + c, duv);
-    if (o != nullptr) store_vec<T>(o + r * a.o_ld + c, ov);
+  for (int k = 0; k < kVec; ++k) {
+    locate(a, fd, k, ok[k], row[k], c[k]);
+    c[k] *= V;
+    graw[k] = ld16(g + row[k] * a.g_ld + c[k]);
+    uraw[k] = ld16(u + row[k] * a.u_ld + c[k]);
+    draw[k] = ld16(dout + row[k] * a.d_ld + c[k]);
   }
+  // every vector computed before any store (see the forward)
+  float dgv[kVec][V], duv[kVec][V], ov[kVec][V];
+#pragma unroll
+  for (int k = 0; k < kVec; ++k) {
+    float gv[V], uv[V], dv[V];
+    unpack<T>(graw[k], gv);
+    unpack<T>(uraw[k], uv);
+    unpack<T>(draw[k], dv);
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const float sig = sigmoid_f(gv[e]);
+      const float s = silu_t<T>(gv[e], sig);
+      ov[k][e] = mul_rn(s, uv[e]);
+      duv[k][e] = mul_rn(dv[e], s);
+      const float ds = round_as<T>(mul_rn(dv[e], uv[e]));
+      dgv[k][e] = ds * sig * (1.0f + gv[e] * (1.0f - sig));
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kVec; ++k) {
+    if (!ok[k]) continue;
+    store_vec<T>(dg + row[k] * a.dg_ld + c[k], dgv[k]);
+    store_vec<T>(du + row[k] * a.du_ld + c[k], duv[k]);
+    if (o != nullptr) store_vec<T>(o + row[k] * a.o_ld + c[k], ov[k]);
+  }
+}
+
+// one wavefront per kVec x 64 vectors, four per workgroup
+unsigned swiglu_blocks(const SwigluArgs& a) {
+  return static_cast<unsigned>((a.total + 256 * kVec - 1) / (256 * kVec));
 }
 
 template <typename T>
@@ -91,11 +200,11 @@ int launch_fwd(const void* g, int64_t g_ld, const void* u, int64_t u_ld, void* o
   a.vec_cols = cols / V;
   a.total = rows * a.vec_cols;
   if (a.total == 0) return NMB_OK;
-  int64_t blocks = (a.total + 255) / 256;
-  if (blocks > 16384) blocks = 16384;
-  hipLaunchKernelGGL((swiglu_fwd_kernel<T>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+  NMB_REQUIRE_SUPPORTED(a.total < (int64_t{1} << 31) - 256 * kVec,
+                        "swiglu_fwd: more than 2^31 vectors of %d elements", V);
+  hipLaunchKernelGGL((swiglu_fwd_kernel<T>), dim3(swiglu_blocks(a)), dim3(256), 0,
                      stream, static_cast<const T*>(g), static_cast<const T*>(u),
-                     static_cast<T*>(o), a);
+                     static_cast<T*>(o), a, make_fastdiv(static_cast<uint32_t>(a.vec_cols)));
   NMB_CHECK_LAUNCH("swiglu_fwd");
   return NMB_OK;
 }
@@ -127,12 +236,12 @@ int launch_bwd(const void* g, int64_t g_ld, const void* u, int64_t u_ld, const v
   a.vec_cols = cols / V;
   a.total = rows * a.vec_cols;
   if (a.total == 0) return NMB_OK;
-  int64_t blocks = (a.total + 255) / 256;
-  if (blocks > 16384) blocks = 16384;
-  hipLaunchKernelGGL((swiglu_bwd_kernel<T>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+  NMB_REQUIRE_SUPPORTED(a.total < (int64_t{1} << 31) - 256 * kVec,
+                        "swiglu_bwd: more than 2^31 vectors of %d elements", V);
+  hipLaunchKernelGGL((swiglu_bwd_kernel<T>), dim3(swiglu_blocks(a)), dim3(256), 0,
                      stream, static_cast<const T*>(g), static_cast<const T*>(u),
                      static_cast<const T*>(d), static_cast<T*>(dg), static_cast<T*>(du),
-                     static_cast<T*>(o), a);
+                     static_cast<T*>(o), a, make_fastdiv(static_cast<uint32_t>(a.vec_cols)));
   NMB_CHECK_LAUNCH("swiglu_bwd");
   return NMB_OK;
 }
