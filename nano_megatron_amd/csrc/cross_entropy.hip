@@ -9,8 +9,8 @@
 // full [tokens, vocab] logits never exist: the forward keeps only the fp32 lse
 // per token, and the backward recomputes a chunk's logits and overwrites them
 // in place with the gradient.  One 256-thread workgroup owns one row; the row
-// (16 KiB at vocab 8192 in bf16) is read with 16-byte accesses, the second
-// pass hits the cache.
+// (16 KiB at vocab 8192 in bf16) is read with 16-byte accesses, once into
+// registers when its length is 256, 512, 1024 or 2048 vectors.
 #include "common.h"
 #include "vec.h"
 
@@ -37,7 +37,28 @@ __device__ __forceinline__ float block_sum(float v, float* sh) {
   return v;
 }
 
+// e^x as 2^(x log2 e) on the hardware exp2 (v_exp_f32): a few fp32 ulps, for
+// x <= 0 here (logits minus their maximum or the row's lse); the loss and the
+// gradients are fp32 sums and bf16 roundings of these terms, not bit-exact
+// reproductions of the reference's reduction order anyway.
+__device__ __forceinline__ float fexp(float x) {
+  constexpr float kLog2e = 1.4426950408889634f;
+  return __builtin_amdgcn_exp2f(x * kLog2e);
+}
+
+__device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+
 template <typename T>
+__device__ __forceinline__ void unpack(const uint4& raw, float (&out)[VecTraits<T>::N]) {
+  T e[VecTraits<T>::N];
+  __builtin_memcpy(e, &raw, 16);
+#pragma unroll
+  for (int i = 0; i < VecTraits<T>::N; ++i) out[i] = to_f32(e[i]);
+}
+
+// VPT > 0: the row is exactly 256 x VPT vectors, read once into registers
+// (all loads in flight together); VPT = 0: any row length, two passes.
+template <typename T, int VPT>
 __global__ __launch_bounds__(256) void ce_fwd_kernel(const T* __restrict__ logits, int64_t ld,
                                                      const int64_t* __restrict__ targets,
                                                      int64_t vocab, int64_t ignore_index,
@@ -48,19 +69,37 @@ __global__ __launch_bounds__(256) void ce_fwd_kernel(const T* __restrict__ logit
   const int64_t row = blockIdx.x;
   const T* z = logits + row * ld;
   float m = -__builtin_inff();
-  for (int64_t c = static_cast<int64_t>(threadIdx.x) * V; c < vocab; c += 256 * V) {
-    float v[V];
-    load_vec<T>(z + c, v);
-#pragma unroll
-    for (int k = 0; k < V; ++k) m = fmaxf(m, v[k]);
-  }
-  m = block_max(m, sh);
   float s = 0.f;
-  for (int64_t c = static_cast<int64_t>(threadIdx.x) * V; c < vocab; c += 256 * V) {
-    float v[V];
-    load_vec<T>(z + c, v);
+  if constexpr (VPT > 0) {
+    uint4 raw[VPT];
 #pragma unroll
-    for (int k = 0; k < V; ++k) s += expf(v[k] - m);
+    for (int j = 0; j < VPT; ++j) raw[j] = ld16(z + (j * 256 + threadIdx.x) * V);
+    float v[VPT][V];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      unpack<T>(raw[j], v[j]);
+#pragma unroll
+      for (int k = 0; k < V; ++k) m = fmaxf(m, v[j][k]);
+    }
+    m = block_max(m, sh);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j)
+#pragma unroll
+      for (int k = 0; k < V; ++k) s += fexp(v[j][k] - m);
+  } else {
+    for (int64_t c = static_cast<int64_t>(threadIdx.x) * V; c < vocab; c += 256 * V) {
+      float v[V];
+      load_vec<T>(z + c, v);
+#pragma unroll
+      for (int k = 0; k < V; ++k) m = fmaxf(m, v[k]);
+    }
+    m = block_max(m, sh);
+    for (int64_t c = static_cast<int64_t>(threadIdx.x) * V; c < vocab; c += 256 * V) {
+      float v[V];
+      load_vec<T>(z + c, v);
+#pragma unroll
+      for (int k = 0; k < V; ++k) s += fexp(v[k] - m);
+    }
   }
   s = block_sum(s, sh);
   if (threadIdx.x == 0) {
@@ -77,7 +116,8 @@ __global__ __launch_bounds__(256) void ce_fwd_kernel(const T* __restrict__ logit
   }
 }
 
-template <typename T>
+// in place: z <- (softmax(z) - onehot(t)) * grad, or 0 for an ignored row
+template <typename T, int VPT>
 __global__ __launch_bounds__(256) void ce_bwd_kernel(T* __restrict__ logits, int64_t ld,
                                                      const int64_t* __restrict__ targets,
                                                      int64_t vocab, int64_t ignore_index,
@@ -90,18 +130,59 @@ __global__ __launch_bounds__(256) void ce_bwd_kernel(T* __restrict__ logits, int
   const bool ignored = t == ignore_index;
   const float l = lse[row];
   const float gr = grad[row];
-  for (int64_t c = static_cast<int64_t>(threadIdx.x) * V; c < vocab; c += 256 * V) {
-    float v[V];
-    load_vec<T>(z + c, v);
+  auto grad_of = [&](float (&v)[V], int64_t c) {
 #pragma unroll
     for (int k = 0; k < V; ++k) {
-      float p = expf(v[k] - l);
+      float p = fexp(v[k] - l);
       if (c + k == t) p -= 1.0f;
       v[k] = ignored ? 0.f : p * gr;
     }
-    store_vec<T>(z + c, v);
+  };
+  if constexpr (VPT > 0) {
+    uint4 raw[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) raw[j] = ld16(z + (j * 256 + threadIdx.x) * V);
+    float v[VPT][V];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      unpack<T>(raw[j], v[j]);
+      grad_of(v[j], static_cast<int64_t>(j * 256 + threadIdx.x) * V);
+    }
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) store_vec<T>(z + (j * 256 + threadIdx.x) * V, v[j]);
+  } else {
+    for (int64_t c = static_cast<int64_t>(threadIdx.x) * V; c < vocab; c += 256 * V) {
+      float v[V];
+      load_vec<T>(z + c, v);
+      grad_of(v, c);
+      store_vec<T>(z + c, v);
+    }
   }
 }
+
+// launch with VPT = vocab / (256 V) when that is 1, 2, 4 or 8, else the loop form
+template <typename T, template <typename, int> class K, typename... Args>
+void launch_rows(int64_t rows, int64_t vocab, hipStream_t stream, Args... args) {
+  constexpr int V = VecTraits<T>::N;
+  const int64_t vpt = vocab % (256 * V) == 0 ? vocab / (256 * V) : 0;
+  const dim3 grid(static_cast<unsigned>(rows));
+  switch (vpt) {
+    case 1: hipLaunchKernelGGL((K<T, 1>::fn), grid, dim3(256), 0, stream, args...); break;
+    case 2: hipLaunchKernelGGL((K<T, 2>::fn), grid, dim3(256), 0, stream, args...); break;
+    case 4: hipLaunchKernelGGL((K<T, 4>::fn), grid, dim3(256), 0, stream, args...); break;
+    case 8: hipLaunchKernelGGL((K<T, 8>::fn), grid, dim3(256), 0, stream, args...); break;
+    default: hipLaunchKernelGGL((K<T, 0>::fn), grid, dim3(256), 0, stream, args...); break;
+  }
+}
+
+template <typename T, int VPT>
+struct FwdK {
+  static constexpr auto fn = ce_fwd_kernel<T, VPT>;
+};
+template <typename T, int VPT>
+struct BwdK {
+  static constexpr auto fn = ce_bwd_kernel<T, VPT>;
+};
 
 template <typename T>
 int check(const void* logits, int64_t ld, const int64_t* targets, int64_t rows, int64_t vocab) {
@@ -126,16 +207,14 @@ extern "C" int nmb_ce_fwd(const void* logits, int64_t ld, const int64_t* targets
     int st = nmb::check<nmb::bf16>(logits, ld, targets, rows, vocab);
     if (st) return st;
     if (rows == 0) return NMB_OK;
-    hipLaunchKernelGGL(nmb::ce_fwd_kernel<nmb::bf16>, dim3(static_cast<unsigned>(rows)),
-                       dim3(256), 0, stream, static_cast<const nmb::bf16*>(logits), ld, targets,
-                       vocab, ignore_index, loss, lse);
+    nmb::launch_rows<nmb::bf16, nmb::FwdK>(rows, vocab, stream, static_cast<const nmb::bf16*>(logits),
+                                           ld, targets, vocab, ignore_index, loss, lse);
   } else if (dtype == NMB_F32) {
     int st = nmb::check<float>(logits, ld, targets, rows, vocab);
     if (st) return st;
     if (rows == 0) return NMB_OK;
-    hipLaunchKernelGGL(nmb::ce_fwd_kernel<float>, dim3(static_cast<unsigned>(rows)), dim3(256), 0,
-                       stream, static_cast<const float*>(logits), ld, targets, vocab,
-                       ignore_index, loss, lse);
+    nmb::launch_rows<float, nmb::FwdK>(rows, vocab, stream, static_cast<const float*>(logits), ld,
+                                       targets, vocab, ignore_index, loss, lse);
   } else {
     NMB_REQUIRE_SUPPORTED(false, "ce_fwd: unsupported dtype code %d", dtype);
   }
@@ -151,16 +230,14 @@ extern "C" int nmb_ce_bwd(void* logits, int64_t ld, const int64_t* targets, int6
     int st = nmb::check<nmb::bf16>(logits, ld, targets, rows, vocab);
     if (st) return st;
     if (rows == 0) return NMB_OK;
-    hipLaunchKernelGGL(nmb::ce_bwd_kernel<nmb::bf16>, dim3(static_cast<unsigned>(rows)),
-                       dim3(256), 0, stream, static_cast<nmb::bf16*>(logits), ld, targets, vocab,
-                       ignore_index, lse, grad);
+    nmb::launch_rows<nmb::bf16, nmb::BwdK>(rows, vocab, stream, static_cast<nmb::bf16*>(logits), ld,
+                                           targets, vocab, ignore_index, lse, grad);
   } else if (dtype == NMB_F32) {
     int st = nmb::check<float>(logits, ld, targets, rows, vocab);
     if (st) return st;
     if (rows == 0) return NMB_OK;
-    hipLaunchKernelGGL(nmb::ce_bwd_kernel<float>, dim3(static_cast<unsigned>(rows)), dim3(256), 0,
-                       stream, static_cast<float*>(logits), ld, targets, vocab, ignore_index, lse,
-                       grad);
+    nmb::launch_rows<float, nmb::BwdK>(rows, vocab, stream, static_cast<float*>(logits), ld, targets,
+                                       vocab, ignore_index, lse, grad);
   } else {
     NMB_REQUIRE_SUPPORTED(false, "ce_bwd: unsupported dtype code %d", dtype);
   }
