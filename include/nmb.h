@@ -242,13 +242,18 @@ int nmb_gemm_bf16_rope(int b_layout, int64_t m, int64_t n, int64_t k, const void
  * array of n_tensors + 1 element prefix sums (offsets[n] = total_elements);
  * master / exp_avg / exp_avg_sq: flat fp32 [total_elements] in that order.
  * norm_out (nullable, device, 2 floats): receives the pre-clip norm and the
- * clip coefficient.  Deterministic (fixed-order reductions). */
+ * clip coefficient.  Deterministic (fixed-order reductions).  The
+ * hyper-parameters are doubles, as the reference's Python floats are: the
+ * derived scalars (1 - beta, 1 - lr wd, sqrt(bias correction 2), lr / bias
+ * correction 1) are formed in double and rounded to fp32 once, as torch rounds
+ * a Python scalar meeting an fp32 tensor; the update then runs the
+ * reference's tensor operations in their order, each rounded once. */
 int nmb_adamw_workspace_bytes(int64_t total_elements, size_t* bytes);
 
 int nmb_adamw_step(const uint64_t* params, const uint64_t* grads, const int64_t* offsets,
                    int n_tensors, int64_t total_elements, float* master, float* exp_avg,
-                   float* exp_avg_sq, int param_dtype, int grad_dtype, float lr, float beta1,
-                   float beta2, float eps, float weight_decay, int64_t step, float max_norm,
+                   float* exp_avg_sq, int param_dtype, int grad_dtype, double lr, double beta1,
+                   double beta2, double eps, double weight_decay, int64_t step, float max_norm,
                    float* norm_out, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus

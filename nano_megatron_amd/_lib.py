@@ -28,6 +28,7 @@ _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int
 _f32 = ctypes.c_float
+_f64 = ctypes.c_double
 _sz = ctypes.c_size_t
 _pi64 = ctypes.POINTER(ctypes.c_int64)
 _psz = ctypes.POINTER(ctypes.c_size_t)
@@ -79,7 +80,7 @@ SIGNATURES: dict[str, list] = {
     ],
     "nmb_adamw_workspace_bytes": [_i64, _psz],
     "nmb_adamw_step": [
-        _p, _p, _p, _i32, _i64, _p, _p, _p, _i32, _i32, _f32, _f32, _f32, _f32, _f32, _i64, _f32,
+        _p, _p, _p, _i32, _i64, _p, _p, _p, _i32, _i32, _f64, _f64, _f64, _f64, _f64, _i64, _f32,
         _p, _p, _sz, _p,
     ],
 }

@@ -123,16 +123,32 @@ __global__ __launch_bounds__(256) void clip_coef_kernel(const float* __restrict_
   }
 }
 
+// fp32 scalars of the update, each formed in double on the host and rounded
+// once (as torch rounds a Python float meeting an fp32 tensor)
 struct AdamArgs {
-  float lr, beta1, beta2, eps, weight_decay, step_size, inv_sqrt_bc2;
+  float b1, one_minus_b1, b2, one_minus_b2, decay, eps, sqrt_bc2, neg_step;
+  int has_decay;
 };
 
-// One element of the update (the reference's formula and rounding order).
-__device__ __forceinline__ void adam_elem(float gv, float& m, float& v, float& w, float decay, const AdamArgs& a) {
-  m = a.beta1 * m + (1.f - a.beta1) * gv;
-  v = a.beta2 * v + (1.f - a.beta2) * gv * gv;
-  if (a.weight_decay != 0.f) w *= decay;
-  w -= a.step_size * m / (sqrtf(v) * a.inv_sqrt_bc2 + a.eps);
+// One element of the update, the reference's tensor operations in their order
+// (data_parallel/_zero.py:184-189), rounded as torch's kernels round them:
+//   m.mul_(b1).add_(g, alpha=1-b1)       m = fma(1-b1, g, m*b1)  (add with alpha is a fused multiply-add)
+//   v.mul_(b2).addcmul_(g, g, value=1-b2) v = fma((1-b2)*g, g, v*b2)  (self + value*t1*t2, last step fused)
+//   w.mul_(1 - lr wd)
+//   den = v.sqrt().div_(sqrt(bc2)).add_(eps)  (correctly rounded sqrt and division)
+//   w.addcdiv_(m, den, value=-lr/bc1)     w = w + ((-lr/bc1)*m)/den  (self + value*t1/t2)
+// Every other step is rounded on its own (no contraction).  Checked against
+// the oracle, which runs these torch operations on the CPU: the moments match
+// bit for bit; the master can differ by an ulp where torch's CPU square root is
+// not correctly rounded.
+__device__ __forceinline__ void adam_elem(float gv, float& m, float& v, float& w, const AdamArgs& a) {
+  m = __builtin_fmaf(a.one_minus_b1, gv, mul_rn(m, a.b1));
+  v = __builtin_fmaf(mul_rn(a.one_minus_b2, gv), gv, mul_rn(v, a.b2));
+  if (a.has_decay) w = mul_rn(w, a.decay);
+  // sqrtf is the correctly rounded square root (this HIP header maps
+  // __fsqrt_rn to the approximate hardware one)
+  const float den = add_rn(__fdiv_rn(sqrtf(v), a.sqrt_bc2), a.eps);
+  w = add_rn(w, __fdiv_rn(mul_rn(a.neg_step, m), den));
 }
 
 template <typename P, typename G>
@@ -147,7 +163,6 @@ __global__ __launch_bounds__(256) void adamw_kernel(const uint64_t* __restrict__
   const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kChunk;
   const int64_t c1 = min(total, c0 + kChunk);
   const float coef = scalars[1];
-  const float decay = 1.f - a.lr * a.weight_decay;
   for (int t = find_tensor(offsets, n, c0); t < n && offsets[t] < c1; ++t) {
     const int64_t lo = max(c0, offsets[t]), hi = min(c1, offsets[t + 1]);
     const G* g = reinterpret_cast<const G*>(grads[t]) - offsets[t];
@@ -155,23 +170,44 @@ __global__ __launch_bounds__(256) void adamw_kernel(const uint64_t* __restrict__
     int64_t va, vb;
     vector_span(g, lo, hi, &va, &vb);
     if ((reinterpret_cast<uintptr_t>(p + va) & 15) != 0) va = vb = hi;  // both tensors vector-aligned
-    for (int64_t i = va + 8 * threadIdx.x; i < vb; i += 8 * 256) {
-      float gv[8], m[8], v[8], w[8];
-      load8(g + i, gv);
-      load8(exp_avg + i, m);
-      load8(exp_avg_sq + i, v);
-      load8(master + i, w);
+    // two groups of 8 per thread and iteration, all loads before any store: a
+    // wait after a store covers every outstanding load (loads and stores share
+    // one counter), so one group per iteration leaves the loads idle half the
+    // time.  A second group past vb re-reads the first and is not stored.
+    for (int64_t i = va + 8 * threadIdx.x; i < vb; i += 16 * 256) {
+      const bool two = i + 8 * 256 < vb;
+      const int64_t j = two ? i + 8 * 256 : i;
+      float gv[2][8], m[2][8], v[2][8], w[2][8];
+      load8(g + i, gv[0]);
+      load8(g + j, gv[1]);
+      load8(exp_avg + i, m[0]);
+      load8(exp_avg + j, m[1]);
+      load8(exp_avg_sq + i, v[0]);
+      load8(exp_avg_sq + j, v[1]);
+      load8(master + i, w[0]);
+      load8(master + j, w[1]);
+      // keeps the scheduler from moving loads below the stores (it does, to
+      // save registers, which brings back the shared-counter wait)
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) adam_elem(gv[e] * coef, m[e], v[e], w[e], decay, a);
-      store8(exp_avg + i, m);
-      store8(exp_avg_sq + i, v);
-      store8(master + i, w);
-      store8(p + i, w);
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) adam_elem(mul_rn(gv[h][e], coef), m[h][e], v[h][e], w[h][e], a);
+      store8(exp_avg + i, m[0]);
+      store8(exp_avg_sq + i, v[0]);
+      store8(master + i, w[0]);
+      store8(p + i, w[0]);
+      if (two) {
+        store8(exp_avg + j, m[1]);
+        store8(exp_avg_sq + j, v[1]);
+        store8(master + j, w[1]);
+        store8(p + j, w[1]);
+      }
     }
     for (int64_t i = lo + threadIdx.x; i < hi; i += 256) {
       if (i >= va && i < vb) continue;  // done above
       float m = exp_avg[i], v = exp_avg_sq[i], w = master[i];
-      adam_elem(to_f32(g[i]) * coef, m, v, w, decay, a);
+      adam_elem(mul_rn(to_f32(g[i]), coef), m, v, w, a);
       exp_avg[i] = m;
       exp_avg_sq[i] = v;
       master[i] = w;
@@ -193,14 +229,14 @@ extern "C" int nmb_adamw_workspace_bytes(int64_t total_elements, size_t* bytes) 
 extern "C" int nmb_adamw_step(const uint64_t* params, const uint64_t* grads,
                               const int64_t* offsets, int n_tensors, int64_t total_elements,
                               float* master, float* exp_avg, float* exp_avg_sq, int param_dtype,
-                              int grad_dtype, float lr, float beta1, float beta2, float eps,
-                              float weight_decay, int64_t step, float max_norm, float* norm_out,
+                              int grad_dtype, double lr, double beta1, double beta2, double eps,
+                              double weight_decay, int64_t step, float max_norm, float* norm_out,
                               void* workspace, size_t workspace_bytes, hipStream_t stream) {
   NMB_REQUIRE(params && grads && offsets && master && exp_avg && exp_avg_sq,
               "adamw_step: null argument");
   NMB_REQUIRE(n_tensors > 0 && total_elements > 0, "adamw_step: empty parameter set");
   NMB_REQUIRE(step >= 1, "adamw_step: step must be >= 1, got %lld", (long long)step);
-  NMB_REQUIRE(lr > 0.f && eps > 0.f && beta1 >= 0.f && beta1 < 1.f && beta2 >= 0.f && beta2 < 1.f,
+  NMB_REQUIRE(lr > 0.0 && eps > 0.0 && beta1 >= 0.0 && beta1 < 1.0 && beta2 >= 0.0 && beta2 < 1.0,
               "adamw_step: invalid hyper-parameters");
   const int64_t nblocks = (total_elements + nmb::kChunk - 1) / nmb::kChunk;
   NMB_REQUIRE(nblocks < (int64_t{1} << 30), "adamw_step: too many elements");
@@ -223,16 +259,19 @@ extern "C" int nmb_adamw_step(const uint64_t* params, const uint64_t* grads,
   hipLaunchKernelGGL(nmb::clip_coef_kernel, dim3(1), dim3(256), 0, stream, partial,
                      static_cast<int>(nblocks), max_norm, scalars);
   NMB_CHECK_LAUNCH("adamw_step(clip)");
+  // the reference's Python scalars (_zero.py:176-189), in double
+  const double bc1 = 1.0 - pow(beta1, static_cast<double>(step));
+  const double bc2 = 1.0 - pow(beta2, static_cast<double>(step));
   nmb::AdamArgs a;
-  a.lr = lr;
-  a.beta1 = beta1;
-  a.beta2 = beta2;
-  a.eps = eps;
-  a.weight_decay = weight_decay;
-  const double bc1 = 1.0 - pow(static_cast<double>(beta1), static_cast<double>(step));
-  const double bc2 = 1.0 - pow(static_cast<double>(beta2), static_cast<double>(step));
-  a.step_size = static_cast<float>(lr / bc1);
-  a.inv_sqrt_bc2 = static_cast<float>(1.0 / sqrt(bc2));
+  a.b1 = static_cast<float>(beta1);
+  a.one_minus_b1 = static_cast<float>(1.0 - beta1);
+  a.b2 = static_cast<float>(beta2);
+  a.one_minus_b2 = static_cast<float>(1.0 - beta2);
+  a.has_decay = weight_decay != 0.0;
+  a.decay = static_cast<float>(1.0 - lr * weight_decay);
+  a.eps = static_cast<float>(eps);
+  a.sqrt_bc2 = static_cast<float>(pow(bc2, 0.5));
+  a.neg_step = static_cast<float>(-(lr / bc1));
 #define NMB_ADAM(P, G)                                                                        \
   hipLaunchKernelGGL((nmb::adamw_kernel<P, G>), dim3(grid), dim3(256), 0, stream, params, grads, \
                      offsets, n_tensors, total_elements, master, exp_avg, exp_avg_sq, scalars, a)

@@ -62,7 +62,10 @@ __device__ __forceinline__ uint4 pack16(const float (&v)[VecTraits<T>::N]) {
 template <typename T>
 __device__ __forceinline__ float inv_rms(float sum_sq, int cols, float eps) {
   const float var = __fdiv_rn(sum_sq, static_cast<float>(cols));
-  return __fdiv_rn(1.0f, __fsqrt_rn(add_rn(var, eps)));
+  // rsqrt as torch evaluates it on the CPU: a correctly rounded square root,
+  // then a correctly rounded division (sqrtf is the correctly rounded one;
+  // this HIP header maps __fsqrt_rn to the approximate hardware square root)
+  return __fdiv_rn(1.0f, sqrtf(add_rn(var, eps)));
 }
 
 // FULL: the row is exactly ITERS vectors per lane (no column masks)
