@@ -489,6 +489,28 @@ Plan plan_for(int64_t m, int64_t n, int64_t k, bool a_kc, bool b_kc, int rope_he
       }
     }
   }
+  // Weight gradients (both operands M/N-contiguous, long K): also the 256 x 256
+  // configuration in a single round of workgroups, each split at least 1024
+  // deep; its per-workgroup rate on this layout was measured at ~5.8e12 FLOP/s
+  // (the 16-tile-row 32-deep tiles of the other family read twice the LDS
+  // bytes per MFMA through the transposing reads).
+  if (!a_kc && !b_kc && rope_head_dim == 0) {
+    constexpr double kRateMN = 5.8e12;
+    const Config& cf = kConfigs[0];
+    const int64_t tiles = ((m + cf.tbm - 1) / cf.tbm) * ((n + cf.tbn - 1) / cf.tbn);
+    const int64_t kt = std::max<int64_t>((k + cf.bkt - 1) / cf.bkt, 1);
+    for (int64_t s = 1; s <= 16; ++s) {
+      const int64_t tps = (kt + s - 1) / s;
+      const int64_t splits = (kt + tps - 1) / tps;
+      if (splits != s || tiles * splits > kCUs || (s > 1 && tps * cf.bkt < 1024)) continue;
+      double t = 2.0 * cf.tbm * cf.tbn * (tps * cf.bkt) / kRateMN;
+      if (splits > 1) t += static_cast<double>(splits) * m * n * 8 / kBytesPerS;
+      if (t < best_t * 0.999) {
+        best_t = t;
+        best = Plan{0, static_cast<int>(splits), static_cast<int>(tps * cf.bkt)};
+      }
+    }
+  }
   return best;
 }
 
