@@ -132,6 +132,34 @@ def run_steps(mode: str, steps: int, warmup: int, device, metrics_jsonl: str | N
     return result
 
 
+def block_saved_mib(mode: str, device, model_cfg: dict = C3, batch: int = BATCH, seq: int = SEQ) -> float:
+    """Activation memory one block leaves saved for the backward: what a forward
+    of a 2-layer model keeps allocated minus what a 1-layer model keeps, at the
+    configuration's width and batch (the embedding, final norm and LM head keep
+    the same in both, so the difference is one block's share)."""
+    import torch
+
+    import nano_megatron_amd as nm
+
+    saved = []
+    for layers in (1, 2):
+        torch.manual_seed(1234)
+        cfg = nm.GPTConfig(**{**model_cfg, "layers": layers})
+        model = nm.GPTModel(cfg, activation_checkpoint_config=nm.ActivationCheckpointConfig(mode=mode))
+        model = model.to(device=device, dtype=torch.bfloat16).train()
+        g = torch.Generator(device=device).manual_seed(1234)
+        ids = torch.randint(0, cfg.vocab_size, (batch, seq + 1), device=device, generator=g)
+        x, y = ids[:, :seq].contiguous(), ids[:, 1:].contiguous()
+        torch.cuda.synchronize()
+        start = torch.cuda.memory_allocated()
+        out = model(x, labels=y)
+        torch.cuda.synchronize()
+        saved.append(torch.cuda.memory_allocated() - start)
+        del out, model, x, y, ids
+        torch.cuda.empty_cache()
+    return (saved[1] - saved[0]) / 2**20
+
+
 def kernel_rooflines(device, only: str | None = None) -> list[dict]:
     """Average launch time (HIP events on the launch stream) of each hand-written
     kernel at the config-3 shapes, with algorithmic bytes / FLOPs per launch
@@ -394,7 +422,11 @@ def run_c4(args, device) -> None:
                     global_batch=C4_BATCH, seq_len=C4_SEQ, parallelism="single GPU"),
         model_tflops=round(tf, 1), mfma_frac=round(tf / BF16_PEAK_TFLOPS, 4),
         peak_act_gib_per_layer=round(full["peak_act_gib_per_layer"], 4),
-        saved_act_mib_per_layer=round(full["saved_act_mib_per_layer"], 2), act_floor_mib_per_layer=33.0,
+        # one block's saved activation (2-layer minus 1-layer model); the
+        # whole-model figure spreads the head's saved state over the layers
+        saved_act_mib_per_layer=round(block_saved_mib("full", device, C4, C4_BATCH, C4_SEQ), 2),
+        act_floor_mib_per_layer=33.0,
+        saved_act_mib_whole_model_per_layer=round(full["saved_act_mib_per_layer"], 2),
     )
     if eager:
         line["no_checkpoint_tokens_per_s"] = round(eager["tokens_per_s"], 1)
@@ -539,8 +571,11 @@ def main() -> None:
             global_batch=BATCH, seq_len=SEQ, parallelism="single GPU",
         ),
         peak_act_gib_per_layer=round(full["peak_act_gib_per_layer"], 4),
-        saved_act_mib_per_layer=round(full["saved_act_mib_per_layer"], 2),
+        # one block's saved activation (2-layer minus 1-layer model); the
+        # whole-model figure spreads the head's saved state over the layers
+        saved_act_mib_per_layer=round(block_saved_mib("full", device), 2),
         act_floor_mib_per_layer=16.5,
+        saved_act_mib_whole_model_per_layer=round(full["saved_act_mib_per_layer"], 2),
         model_tflops=round(model_step_flops(C3, BATCH, SEQ, recompute=True) / (full["ms_per_step"] * 1e-3) / 1e12, 1),
         loss=round(full["loss"], 4),
         roofline=roofline,
@@ -549,7 +584,7 @@ def main() -> None:
     )
     if eager:
         line["no_checkpoint_tokens_per_s"] = round(eager["tokens_per_s"], 1)
-        line["no_checkpoint_saved_act_mib_per_layer"] = round(eager["saved_act_mib_per_layer"], 2)
+        line["no_checkpoint_saved_act_mib_per_layer"] = round(block_saved_mib("none", device), 2)
         line["recompute_overhead"] = round(full["ms_per_step"] / eager["ms_per_step"] - 1.0, 4)
     print(json.dumps(line), flush=True)
 
