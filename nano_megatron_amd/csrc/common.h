@@ -40,6 +40,24 @@ template <typename T> __device__ __forceinline__ float round_as(float x) {
   return to_f32(from_f32<T>(x));
 }
 
+// n / d for n < 2^31 by a precomputed multiplier (round-up method of
+// Granlund and Montgomery): s = ceil(log2 d), m = floor(2^32 (2^s - d) / d) + 1,
+// n / d = (mulhi(n, m) + n) >> s.
+struct FastDiv {
+  uint32_t d, m, s;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f{d, 0, 0};
+  while ((uint64_t{1} << f.s) < d) ++f.s;
+  f.m = static_cast<uint32_t>(((uint64_t{1} << 32) * ((uint64_t{1} << f.s) - d)) / d + 1);
+  return f;
+}
+
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv& f) {
+  return (__umulhi(n, f.m) + n) >> f.s;
+}
+
 // Products and sums without FMA contraction, so fp32 results reproduce the
 // separately rounded tensor ops of the reference.  __fmul_rn / __fadd_rn are
 // plain operators in this HIP header, which HIP's default -ffp-contract fuses

@@ -10,8 +10,9 @@
 // -theta), since rotate_half^T = -rotate_half.
 //
 // One thread owns V consecutive pairs (i, i + D/2) of one (b, s, h) row, so
-// the operation can run in place.  The cos/sin table is fp32 [n_pos, D/2]
-// and stays in L2.
+// the operation can run in place; the row comes from the thread index by
+// multiply-high divisions, and both halves and both table rows are loaded
+// before any is used.  The cos/sin table is fp32 [n_pos, D/2] and stays in L2.
 #include "common.h"
 #include "vec.h"
 
@@ -37,9 +38,10 @@ struct RopeArgs {
   int64_t seq, heads, half, n_pos;
   int64_t xs_b, xs_s, xs_h, os_b, os_s, os_h;
   int64_t pos_bstride, pos_offset;
-  int64_t total;  // rows * vecs_per_row
+  int64_t total;  // rows * vecs_per_row (< 2^31)
   int vecs_per_row;
   float sin_sign;
+  FastDiv by_vecs, by_heads, by_seq;  // index divisions by vecs_per_row, heads, seq
 };
 
 template <typename T>
@@ -49,40 +51,53 @@ __global__ __launch_bounds__(256) void rope_kernel(const T* __restrict__ x, T* _
                                                    const int32_t* __restrict__ positions,
                                                    RopeArgs a) {
   constexpr int V = VecTraits<T>::N;
-  for (int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; gid < a.total;
-       gid += static_cast<int64_t>(gridDim.x) * 256) {
-    const int64_t row = gid / a.vecs_per_row;
-    const int i0 = static_cast<int>(gid - row * a.vecs_per_row) * V;
-    const int64_t h = row % a.heads;
-    const int64_t bs = row / a.heads;
-    const int64_t s = bs % a.seq;
-    const int64_t b = bs / a.seq;
-    int64_t pos = positions != nullptr ? static_cast<int64_t>(positions[b * a.pos_bstride + s])
-                                       : a.pos_offset + s;
-    // An out-of-table position is a caller error; read a valid row and poison
-    // the result rather than touch memory outside the table.
-    const bool bad = pos < 0 || pos >= a.n_pos;
-    if (bad) pos = 0;
-    const T* xr = x + b * a.xs_b + s * a.xs_s + h * a.xs_h;
-    T* orow = out + b * a.os_b + s * a.os_s + h * a.os_h;
-    float x1[V], x2[V];
-    load_vec<T>(xr + i0, x1);
-    load_vec<T>(xr + a.half + i0, x2);
-    const float* cr = cos_t + pos * a.half + i0;
-    const float* sr = sin_t + pos * a.half + i0;
-    float o1[V], o2[V];
+  const uint32_t gid = blockIdx.x * 256 + threadIdx.x;
+  if (gid >= static_cast<uint32_t>(a.total)) return;
+  // gid = ((b seq + s) heads + h) vecs_per_row + v, by multiply-high divisions
+  const uint32_t row = fast_div(gid, a.by_vecs);
+  const int i0 = static_cast<int>(gid - row * a.by_vecs.d) * V;
+  const uint32_t bs = fast_div(row, a.by_heads);
+  const int64_t h = row - bs * a.by_heads.d;
+  const uint32_t b32 = fast_div(bs, a.by_seq);
+  const int64_t s = bs - b32 * a.by_seq.d, b = b32;
+  const T* xr = x + b * a.xs_b + s * a.xs_s + h * a.xs_h;
+  // x first (independent of the position), then the table rows
+  const uint4 raw1 = *reinterpret_cast<const uint4*>(xr + i0);
+  const uint4 raw2 = *reinterpret_cast<const uint4*>(xr + a.half + i0);
+  int64_t pos = positions != nullptr ? static_cast<int64_t>(positions[b * a.pos_bstride + s])
+                                     : a.pos_offset + s;
+  // An out-of-table position is a caller error; read a valid row and poison
+  // the result rather than touch memory outside the table.
+  const bool bad = pos < 0 || pos >= a.n_pos;
+  if (bad) pos = 0;
+  float cv[V], sv[V];
 #pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const float c = round_as<T>(cr[i]);
-      const float sn = round_as<T>(sr[i]) * a.sin_sign;
-      // first half:  x1*c + (-x2)*s ; second half: x2*c + x1*s
-      o1[i] = round_as<T>(add_rn(round_as<T>(mul_rn(x1[i], c)), round_as<T>(mul_rn(-x2[i], sn))));
-      o2[i] = round_as<T>(add_rn(round_as<T>(mul_rn(x2[i], c)), round_as<T>(mul_rn(x1[i], sn))));
-      if (bad) o1[i] = o2[i] = __builtin_nanf("");
+  for (int k = 0; k < V; k += 4) {
+    const f32x4 c4 = *reinterpret_cast<const f32x4*>(cos_t + pos * a.half + i0 + k);
+    const f32x4 s4 = *reinterpret_cast<const f32x4*>(sin_t + pos * a.half + i0 + k);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      cv[k + e] = c4[e];
+      sv[k + e] = s4[e];
     }
-    store_vec<T>(orow + i0, o1);
-    store_vec<T>(orow + a.half + i0, o2);
   }
+  T e1[V], e2[V];
+  __builtin_memcpy(e1, &raw1, 16);
+  __builtin_memcpy(e2, &raw2, 16);
+  float o1[V], o2[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const float x1 = to_f32(e1[i]), x2 = to_f32(e2[i]);
+    const float c = round_as<T>(cv[i]);
+    const float sn = round_as<T>(sv[i]) * a.sin_sign;
+    // first half:  x1*c + (-x2)*s ; second half: x2*c + x1*s
+    o1[i] = round_as<T>(add_rn(round_as<T>(mul_rn(x1, c)), round_as<T>(mul_rn(-x2, sn))));
+    o2[i] = round_as<T>(add_rn(round_as<T>(mul_rn(x2, c)), round_as<T>(mul_rn(x1, sn))));
+    if (bad) o1[i] = o2[i] = __builtin_nanf("");
+  }
+  T* orow = out + b * a.os_b + s * a.os_s + h * a.os_h;
+  store_vec<T>(orow + i0, o1);
+  store_vec<T>(orow + a.half + i0, o2);
 }
 
 template <typename T>
@@ -128,8 +143,12 @@ int apply_impl(const void* x, void* out, const float* cos_t, const float* sin_t,
   a.total = batch * seq * heads * a.vecs_per_row;
   a.sin_sign = inverse ? -1.f : 1.f;
   if (a.total == 0) return NMB_OK;
-  int64_t blocks = (a.total + 255) / 256;
-  if (blocks > 65536) blocks = 65536;
+  NMB_REQUIRE_SUPPORTED(a.total < (int64_t{1} << 31) - 256,
+                        "rope_apply: more than 2^31 vectors of %d elements", V);
+  a.by_vecs = make_fastdiv(static_cast<uint32_t>(a.vecs_per_row));
+  a.by_heads = make_fastdiv(static_cast<uint32_t>(heads));
+  a.by_seq = make_fastdiv(static_cast<uint32_t>(seq));
+  const int64_t blocks = (a.total + 255) / 256;  // one vector per thread
   hipLaunchKernelGGL((rope_kernel<T>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
                      static_cast<const T*>(x), static_cast<T*>(out), cos_t, sin_t, positions, a);
   NMB_CHECK_LAUNCH("rope_apply");

@@ -56,24 +56,6 @@ struct SwigluArgs {
 // Indices past the end re-read the last vector and are not stored.
 constexpr int kVec = 2;
 
-// n / d for n < 2^31 by a precomputed multiplier (round-up method of
-// Granlund and Montgomery): s = ceil(log2 d), m = floor(2^32 (2^s - d) / d) + 1,
-// n / d = (mulhi(n, m) + n) >> s.
-struct FastDiv {
-  uint32_t d, m, s;
-};
-
-FastDiv make_fastdiv(uint32_t d) {
-  FastDiv f{d, 0, 0};
-  while ((uint64_t{1} << f.s) < d) ++f.s;
-  f.m = static_cast<uint32_t>(((uint64_t{1} << 32) * ((uint64_t{1} << f.s) - d)) / d + 1);
-  return f;
-}
-
-__device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv& f) {
-  return (__umulhi(n, f.m) + n) >> f.s;
-}
-
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
 template <typename T>
