@@ -156,6 +156,13 @@ ATTN_CASES = [
     (2, 4, 2, 100, 100, 64, torch.float32, 0, True),
     (1, 2, 2, 48, 112, 64, torch.float32, 64, True),
     (1, 8, 2, 256, 256, 128, torch.bfloat16, 0, True),
+    # head dim 128: two 256-query workgroups with a ragged tail, GQA; and an offset
+    # query block over a longer key range (ring share shape)
+    (1, 4, 2, 300, 300, 128, torch.bfloat16, 0, True),
+    (2, 2, 2, 130, 260, 128, torch.bfloat16, 130, True),
+    # head dim 64 from 1024 queries (two column tiles per wave, three workgroups per CU),
+    # ragged last tile
+    (1, 2, 2, 1100, 1100, 64, torch.bfloat16, 0, True),
 ]
 
 
