@@ -230,10 +230,19 @@ def kernel_rooflines(device, only: str | None = None) -> list[dict]:
                 lambda: Fn.mm_rope(x, w_qkv.t(), seq=SEQ, head_dim=d, rope_cols=2 * H, cos=tab.cos, sin=tab.sin,
                                    out=qkv_out),
                 (T * H + 3 * H * H + 3 * T * H) * E, 2.0 * T * 3 * H * H, "mfma", 2 * L)
+    # the gate/up projection: the forward's applies the SwiGLU activation in its
+    # epilogue; the recompute's writes the product [g|u] (same kernel and plan)
+    w_gu = randn(2 * F, H)
+    gu_buf = torch.empty(T, 2 * F, dtype=bf, device=device)
+    gu_swiglu = ("gemm_gate_up_swiglu", lambda: Fn.mm_gate_up(x, w_gu, act=True, act_out=act),
+                 (T * H + 2 * F * H + T * F) * E, 2.0 * T * 2 * F * H, "mfma", L)
+    gu_product = ("gemm_gate_up", lambda: Fn.mm_gate_up(x, w_gu, act=False, gu=True, gu_out=gu_buf),
+                  (T * H + 2 * F * H + 2 * T * F) * E, 2.0 * T * 2 * F * H, "mfma", L)
     gemms = [
         qkv_rope,
         gemm_case("gemm_o_residual", T, H, H, False, False, 2 * L, residual=True),
-        gemm_case("gemm_gate_up", T, 2 * F, H, False, False, 2 * L),
+        gu_product,
+        gu_swiglu,
         gemm_case("gemm_down_residual", T, H, F, False, False, L, residual=True),
         gemm_case("gemm_d_swiglu", T, F, H, False, True, L),
         gemm_case("gemm_dw_down", H, F, T, True, True, L),
@@ -255,7 +264,8 @@ def kernel_rooflines(device, only: str | None = None) -> list[dict]:
          "hbm", 2 * L + 1),
         # the standalone rotary kernel; the step fuses RoPE into the QKV GEMM and the attention backward
         ("rope_apply", lambda: Fn.rope_apply(q, rope_out, tab.cos, tab.sin), 2 * T * H * E, 0, "hbm", 0),
-        ("swiglu_fwd", lambda: Fn.swiglu_fwd(gate, up, act), 3 * T * F * E, 0, "hbm", L),
+        # the standalone activation; the checkpointed step fuses it into the gate/up GEMM
+        ("swiglu_fwd", lambda: Fn.swiglu_fwd(gate, up, act), 3 * T * F * E, 0, "hbm", 0),
         ("swiglu_bwd", lambda: Fn.swiglu_bwd(gate, up, dh, dgu[:, :F], dgu[:, F:], act), 6 * T * F * E, 0, "hbm", L),
         ("attn_fwd", lambda: Fn.attn_fwd_bshd(q, [k], [v], (0,), causal=True, q_offset=0, scale=None, out=o, lse=lse),
          4 * T * H * E + BATCH * nh * SEQ * 4, causal_flops, "mfma", 2 * L),

@@ -232,6 +232,21 @@ int nmb_gemm_bf16_rope(int b_layout, int64_t m, int64_t n, int64_t k, const void
                        int64_t pos_batch_stride, int64_t pos_offset, int64_t seq, int64_t head_dim,
                        int64_t rope_cols, hipStream_t stream);
 
+/* The gate/up projection GEMM with the SwiGLU activation as its epilogue
+ * (reference models/gpt/mlp.py:44-70, 77: gate_proj, up_proj, F.silu(gate) *
+ * up; replaces nmb_gemm_bf16 of [Wg; Wu] + nmb_swiglu_fwd).
+ *   P = A [Wg; Wu]^T, A row-major [M, K], b = [2F, K] K-contiguous (rows 0..F-1
+ *   the gate weight, F..2F-1 the up weight, row stride ldb);
+ *   gu (nullable) [M, 2F] receives bf16(P);
+ *   d (nullable) [M, F] receives bf16(silu(bf16(P_gate)) * bf16(P_up)) with
+ *   the roundings of nmb_swiglu_fwd.
+ * One plan per shape, never split along K: gu is the same bits whether or not
+ * d is written, and d equals nmb_swiglu_fwd of that gu bit for bit.  F, K,
+ * lda, ldb, ldd, ldgu multiples of 8; no workspace. */
+int nmb_gemm_bf16_swiglu(int64_t m, int64_t f, int64_t k, const void* a, int64_t lda, const void* b,
+                         int64_t ldb, void* d, int64_t ldd, void* gu, int64_t ldgu,
+                         hipStream_t stream);
+
 /* ------------------------------------------------------------ optimizer
  * replaces FlatShardZeROStrategy.clip_grad_norm + optimizer_step at DP=1
  * (data_parallel/_zero.py:130-199; defaults config/schema.py:439-445):

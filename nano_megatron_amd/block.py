@@ -4,22 +4,21 @@ Both run the same device sequence (reference GPTLayer.forward,
 models/gpt/layer.py:91-137):
 
     n1 = RMSNorm(x)                          nmb_rmsnorm_fwd
-    [q|k|v] = n1 [Wq;Wk;Wv]^T                one GEMM (hipBLASLt)
-    q, k = RoPE(q, k)                        nmb_rope_apply, in place
+    [q|k|v] = n1 [Wq;Wk;Wv]^T, RoPE(q, k)    nmb_gemm_bf16_rope (RoPE in the epilogue)
     o, lse = attention(q, k, v)              nmb_attn_fwd (MFMA, online softmax)
-    h = x + o Wo^T                           GEMM with the residual as C input
+    h = x + o Wo^T                           nmb_gemm_bf16 with the residual as C input
     n2 = RMSNorm(h)                          nmb_rmsnorm_fwd
-    [g|u] = n2 [Wg;Wu]^T                     one GEMM
-    s = silu(g) * u                          nmb_swiglu_fwd
-    y = h + s Wd^T                           GEMM with the residual as C input
+    s = silu(n2 Wg^T) * (n2 Wu^T)            nmb_gemm_bf16_swiglu (activation in the epilogue)
+    y = h + s Wd^T                           nmb_gemm_bf16 with the residual as C input
 
 ``CheckpointedBlockFunction`` is the full-recompute policy of
 ``activation_checkpoint`` (nn/activation_checkpoint.py:73-100, selected by
 models/gpt/model.py:162-170, 215-233): it saves only the block input x and
-the attention lse.  Its backward re-runs the sequence above up to [g|u] with
-the same kernels and shapes (so the recomputed tensors are bit-identical to
-the forward's) and never re-runs the down projection, whose output the
-backward does not need; ``nmb_swiglu_bwd`` re-emits s for the Wd gradient.
+the attention lse.  Its backward re-runs the sequence above with the same
+kernels and shapes (so the recomputed tensors are bit-identical to the
+forward's), except that the gate/up GEMM writes the product [g|u] instead of
+s (same plan, same bits), and never re-runs the down projection, whose output
+the backward does not need; ``nmb_swiglu_bwd`` re-emits s for the Wd gradient.
 ``EagerBlockFunction`` (activation_checkpoint.mode = "none") keeps the
 intermediates instead and shares the backward.
 """
@@ -96,8 +95,11 @@ def _qkv_views(qkv: Tensor, b: int, s: int, m: BlockMeta) -> tuple[Tensor, Tenso
     return q, k, v
 
 
-def block_forward(x: Tensor, w: tuple[Tensor, ...], m: BlockMeta, *, recompute: bool) -> dict:
-    """Run the block on x [B,S,H].  With recompute=True stop after [g|u] (no s, no y)."""
+def block_forward(x: Tensor, w: tuple[Tensor, ...], m: BlockMeta, *, recompute: bool,
+                  keep_gu: bool = True) -> dict:
+    """Run the block on x [B,S,H].  With recompute=True stop after [g|u] (no s, no y).
+    With keep_gu=False (a forward whose intermediates are dropped) the gate/up
+    GEMM applies the activation in its epilogue and [g|u] is never written."""
     w_in, wq, wk, wv, wo, w_post, wg, wu, wd = w
     b, s, hdim = x.shape
     x2 = x.reshape(b * s, hdim)
@@ -111,12 +113,14 @@ def block_forward(x: Tensor, w: tuple[Tensor, ...], m: BlockMeta, *, recompute: 
     o2 = o.view(b * s, m.heads * m.head_dim)
     h = Fn.mm(o2, wo.t(), c=x2, beta=1.0)
     n2 = Fn.rmsnorm_fwd(h, w_post, m.eps)
-    gu = Fn.mm(n2, joined((wg, wu)).t())
-    acts = dict(x2=x2, n1=n1, qkv=qkv, o2=o2, lse=lse, h=h, n2=n2, gu=gu)
+    # one gate/up GEMM plan for the forward and the recompute: the same [g|u]
+    # bits whether or not the activation is applied in the epilogue
+    act, gu = Fn.mm_gate_up(n2, joined((wg, wu)), act=not recompute, gu=recompute or keep_gu)
+    acts = dict(x2=x2, n1=n1, qkv=qkv, o2=o2, lse=lse, h=h, n2=n2)
+    if gu is not None:
+        acts["gu"] = gu
     if recompute:
         return acts
-    f = wg.shape[0]
-    act = Fn.swiglu_fwd(gu[:, :f], gu[:, f:])
     acts["s"] = act
     acts["y"] = Fn.mm(act, wd.t(), c=h, beta=1.0).view(b, s, hdim)
     return acts
@@ -173,7 +177,7 @@ class CheckpointedBlockFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx: Any, x: Tensor, meta: BlockMeta, *weights: Tensor) -> Tensor:
         with torch.no_grad():
-            acts = block_forward(x.contiguous(), weights, meta, recompute=False)
+            acts = block_forward(x.contiguous(), weights, meta, recompute=False, keep_gu=False)
         ctx.meta = meta
         ctx.shape = tuple(x.shape)
         ctx.save_for_backward(x, acts["lse"], *weights)

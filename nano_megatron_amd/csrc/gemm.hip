@@ -41,6 +41,7 @@
 
 #include "common.h"
 #include "lds_dma.h"
+#include "swiglu_math.h"
 
 namespace nmb {
 namespace {
@@ -106,6 +107,26 @@ struct Loader {
     }
   }
 
+  // SwiGLU tiles (K-contiguous [2F, K] weights, gate rows then up rows): tile
+  // row r reads gate (r & 32 clear) or up row j0 + 32 (r / 64) + r % 32, so a
+  // wave's 64 columns hold 32 gate columns and the matching 32 up columns.
+  __device__ void init_pairs(const bf16* base, int64_t ld, int f, int j0, uint32_t bytes, int wave,
+                             int lane) {
+    static_assert(KC, "paired rows need K-contiguous weights");
+    rsrc = make_rsrc(base, bytes);
+    kstride = 2u;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = wave * kPer + j;
+      const int r = kRpi * i + lane / kCpr;
+      const int c = (lane % kCpr) ^ kc_swizzle<BKT>(r);
+      const int col = j0 + 32 * (r >> 6) + (r & 31);
+      const int64_t row = col + ((r >> 5) & 1) * static_cast<int64_t>(f);
+      kin[j] = 8 * c;
+      off[j] = col < f ? static_cast<uint32_t>((row * ld + 8 * c) * 2) : kOOB;
+    }
+  }
+
   // loads K tile [k0, k0 + BKT) (zeros at and past k_end) into the LDS tile
   __device__ __forceinline__ void issue(const bf16* tile, int k0, int k_end, int wave) const {
     const uint32_t koff = static_cast<uint32_t>(k0) * kstride;
@@ -168,11 +189,21 @@ struct GemmArgs {
   const int32_t* rope_pos;  // [batch, pos_bstride] or null: rope_offset + row % rope_seq
   int64_t rope_pos_bstride;
   int rope_offset, rope_seq, rope_n_pos, rope_cols;
+  // SwiGLU epilogue: the [M, 2F] gate/up product (nullable; d nullable too)
+  bf16* gu;
+  int64_t ldgu;
 };
 
+// Columns of D covered by one TBN-wide tile: TBN, or TBN / 2 with the SwiGLU
+// epilogue (each output column takes a gate and an up column of the product).
+template <int TBN, bool SWI>
+constexpr int out_cols() { return SWI ? TBN / 2 : TBN; }
+
 // TBM x TBN output tile, NW wavefronts (4: 2 x 2, two workgroups per CU;
-// 8: 2 x 4 or 4 x 2, one workgroup per CU), BKT-deep K tiles.
-template <int TBM, int TBN, int NW, int BKT, bool A_KC, bool B_KC, int RD>
+// 8: 2 x 4 or 4 x 2, one workgroup per CU), BKT-deep K tiles.  RD > 0: RoPE
+// epilogue on heads of RD.  SWI: B is [2F, K] (gate rows, then up rows), N = F,
+// and D = swiglu(gate product, up product).
+template <int TBM, int TBN, int NW, int BKT, bool A_KC, bool B_KC, int RD, bool SWI = false>
 __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void gemm_kernel(GemmArgs g) {
   constexpr int WAVES_N = NW == 4 ? 2 : (TBN == 256 ? 4 : 2);
   constexpr int WAVES_M = NW / WAVES_N;
@@ -201,7 +232,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void gemm_kernel(GemmArgs
   const int gsize = min(tiles_m - grp * GM, GM);
   const int r = t - grp * GM * g.tiles_n;
   const int m0 = (grp * GM + r % gsize) * TBM;
-  const int n0 = (r / gsize) * TBN;
+  const int n0 = (r / gsize) * out_cols<TBN, SWI>();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = (wave / WAVES_N) * WM, wn = (wave % WAVES_N) * WN;
   const int k_begin = split * g.kps;
@@ -219,7 +250,12 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void gemm_kernel(GemmArgs
     const int64_t eb = B_KC ? (static_cast<int64_t>(vb - 1) * g.ldb + g.K) * 2
                             : (static_cast<int64_t>(g.K - 1) * g.ldb + (g.N - n0)) * 2;
     la.init(a0, g.lda, va, static_cast<uint32_t>(ea), wave, lane);
-    lb.init(b0, g.ldb, vb, static_cast<uint32_t>(eb), wave, lane);
+    if constexpr (SWI) {
+      const int64_t e2 = (static_cast<int64_t>(2 * g.N - 1) * g.ldb + g.K) * 2;
+      lb.init_pairs(g.b, g.ldb, g.N, n0, static_cast<uint32_t>(e2), wave, lane);
+    } else {
+      lb.init(b0, g.ldb, vb, static_cast<uint32_t>(eb), wave, lane);
+    }
   }
 
   f32x4 acc[TM][TN];
@@ -306,6 +342,46 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void gemm_kernel(GemmArgs
       for (int j = 0; j < TN; ++j) {
         const int n = n0 + wn + 16 * j + 4 * q4;
         if (n < g.N) *reinterpret_cast<f32x4*>(part + static_cast<int64_t>(m) * g.N + n) = acc[i][j];
+      }
+    }
+    return;
+  }
+  if constexpr (SWI) {
+    // acc[i][j] (j & 2 clear) holds gate columns, acc[i][j + 2] the matching up
+    // columns: output column n0 + 32 ((wn + 16 j) / 64) + 16 (j & 1) + 4 q4 + e.
+    // The swiglu kernel's roundings: gate and up to bf16, then the activation;
+    // the rounded gate and up go to gu when it is given.
+    static_assert(WN % 64 == 0 && RD == 0, "a wave's columns pair whole 32-column groups");
+    // the product only (the recompute): no activation math in this epilogue,
+    // whose time adds to the kernel's (every workgroup reaches it together)
+    const bool act = g.d != nullptr;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + wm + 16 * i + l16;
+      if (m >= g.M) continue;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        if (j & 2) continue;
+        const int n = n0 + 32 * ((wn + 16 * j) >> 6) + 16 * (j & 1) + 4 * q4;
+        if (n >= g.N) continue;
+        bf16x4 gv, uv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          gv[e] = static_cast<bf16>(acc[i][j][e]);
+          uv[e] = static_cast<bf16>(acc[i][j + 2][e]);
+        }
+        if (g.gu != nullptr) {
+          bf16* row = g.gu + static_cast<int64_t>(m) * g.ldgu;
+          *reinterpret_cast<bf16x4*>(row + n) = gv;
+          *reinterpret_cast<bf16x4*>(row + g.N + n) = uv;
+        }
+        if (act) {
+          bf16x4 ov;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            ov[e] = static_cast<bf16>(swiglu_t<bf16>(static_cast<float>(gv[e]), static_cast<float>(uv[e])));
+          *reinterpret_cast<bf16x4*>(g.d + static_cast<int64_t>(m) * g.ldd + n) = ov;
+        }
       }
     }
     return;
@@ -456,7 +532,8 @@ struct Plan {
 // Columns of one wavefront's share of a configuration's tile.
 constexpr int wave_cols(const Config& c) { return c.nw == 4 ? c.tbn / 2 : (c.tbn == 256 ? c.tbn / 4 : c.tbn / 2); }
 
-Plan plan_for(int64_t m, int64_t n, int64_t k, bool a_kc, bool b_kc, int rope_head_dim = 0) {
+Plan plan_for(int64_t m, int64_t n, int64_t k, bool a_kc, bool b_kc, int rope_head_dim = 0,
+              bool whole_k = false) {
   constexpr int64_t kCUs = 256;
   constexpr double kBytesPerS = 5e12;
   const int64_t big_tiles = ((m + 255) / 256) * ((n + 127) / 128);
@@ -475,7 +552,7 @@ Plan plan_for(int64_t m, int64_t n, int64_t k, bool a_kc, bool b_kc, int rope_he
       const int64_t slots = cf.nw == 4 ? 2 * kCUs : kCUs;
       const int64_t tiles = ((m + cf.tbm - 1) / cf.tbm) * ((n + cf.tbn - 1) / cf.tbn);
       const int64_t kt = std::max<int64_t>((k + cf.bkt - 1) / cf.bkt, 1);  // K tiles
-      for (int64_t s = 1; s <= (small && rope_head_dim == 0 ? 16 : 1); ++s) {
+      for (int64_t s = 1; s <= (small && rope_head_dim == 0 && !whole_k ? 16 : 1); ++s) {
         const int64_t tps = (kt + s - 1) / s;  // K tiles per split
         const int64_t splits = (kt + tps - 1) / tps;
         if (splits != s || (s > 1 && tps * cf.bkt < 512)) continue;
@@ -494,7 +571,7 @@ Plan plan_for(int64_t m, int64_t n, int64_t k, bool a_kc, bool b_kc, int rope_he
   // deep; its per-workgroup rate on this layout was measured at ~5.8e12 FLOP/s
   // (the 16-tile-row 32-deep tiles of the other family read twice the LDS
   // bytes per MFMA through the transposing reads).
-  if (!a_kc && !b_kc && rope_head_dim == 0) {
+  if (!a_kc && !b_kc && rope_head_dim == 0 && !whole_k) {
     constexpr double kRateMN = 5.8e12;
     const Config& cf = kConfigs[0];
     const int64_t tiles = ((m + cf.tbm - 1) / cf.tbm) * ((n + cf.tbn - 1) / cf.tbn);
@@ -514,17 +591,17 @@ Plan plan_for(int64_t m, int64_t n, int64_t k, bool a_kc, bool b_kc, int rope_he
   return best;
 }
 
-template <int TBM, int TBN, int NW, int BKT, bool A_KC, bool B_KC, int RD = 0>
+template <int TBM, int TBN, int NW, int BKT, bool A_KC, bool B_KC, int RD = 0, bool SWI = false>
 int launch(GemmArgs g, hipStream_t stream) {
   const int tiles_m = (g.M + TBM - 1) / TBM;
-  g.tiles_n = (g.N + TBN - 1) / TBN;
+  g.tiles_n = (g.N + out_cols<TBN, SWI>() - 1) / out_cols<TBN, SWI>();
   const int64_t tiles = static_cast<int64_t>(tiles_m) * g.tiles_n;
   const int64_t items = tiles * g.splits;
   NMB_REQUIRE(items < (int64_t{1} << 30), "gemm: too many tiles");
   g.tiles = static_cast<int>(tiles);
   g.items = static_cast<int>(items);
   g.per_xcd = static_cast<int>((items + 7) / 8);
-  hipLaunchKernelGGL((gemm_kernel<TBM, TBN, NW, BKT, A_KC, B_KC, RD>),
+  hipLaunchKernelGGL((gemm_kernel<TBM, TBN, NW, BKT, A_KC, B_KC, RD, SWI>),
                      dim3(static_cast<unsigned>(g.per_xcd * 8)), dim3(NW * 64), 0, stream, g);
   NMB_CHECK_LAUNCH("gemm");
   if (g.splits > 1) {
@@ -555,6 +632,15 @@ int dispatch_rope(int config, bool b_kc, const GemmArgs& g, hipStream_t s) {
     }
   }
   return b_kc ? launch<128, 256, 4, 32, true, true, RD>(g, s) : launch<128, 256, 4, 32, true, false, RD>(g, s);
+}
+
+int dispatch_swiglu(int config, const GemmArgs& g, hipStream_t s) {
+  switch (config) {
+    case 0: return launch<256, 256, 8, 64, true, true, 0, true>(g, s);
+    case 1: return launch<256, 128, 8, 64, true, true, 0, true>(g, s);
+    case 2: return launch<128, 128, 4, 32, true, true, 0, true>(g, s);
+    default: return launch<128, 256, 4, 32, true, true, 0, true>(g, s);
+  }
 }
 
 int64_t workspace_for(const Plan& p, int64_t m, int64_t n) {
@@ -689,4 +775,26 @@ extern "C" int nmb_gemm_bf16_rope(int b_layout, int64_t m, int64_t n, int64_t k,
   g.rope_cols = static_cast<int>(rope_cols);
   return head_dim == 64 ? nmb::dispatch_rope<64>(p.config, b_layout == 0, g, stream)
                         : nmb::dispatch_rope<128>(p.config, b_layout == 0, g, stream);
+}
+
+extern "C" int nmb_gemm_bf16_swiglu(int64_t m, int64_t f, int64_t k, const void* a, int64_t lda,
+                                    const void* b, int64_t ldb, void* d, int64_t ldd, void* gu,
+                                    int64_t ldgu, hipStream_t stream) {
+  NMB_REQUIRE(d != nullptr || gu != nullptr, "gemm_swiglu: neither d nor gu given");
+  // B is [2F, K]; D is [M, F]; gu is [M, 2F]
+  const int st = nmb::check_gemm(0, 0, m, f, k, a, lda, b, ldb, false, nullptr, 0,
+                                 d != nullptr ? d : gu, d != nullptr ? ldd : ldgu);
+  if (st != NMB_OK) return st;
+  NMB_REQUIRE_SUPPORTED(f % 8 == 0, "gemm_swiglu: F (%lld) must be a multiple of 8", (long long)f);
+  NMB_REQUIRE(gu == nullptr || (ldgu >= 2 * f && ldgu % 8 == 0 && nmb::aligned16(gu)),
+              "gemm_swiglu: gu must be 16-byte aligned with a leading dimension >= 2F, a multiple of 8");
+  // the paired loads address the whole [2F, K] weight with 32-bit byte offsets
+  NMB_REQUIRE_SUPPORTED(2 * (2 * f * ldb) < (int64_t{1} << 31),
+                        "gemm_swiglu: the gate/up weight spans more than 2 GiB");
+  if (m == 0 || f == 0) return NMB_OK;
+  const nmb::Plan p = nmb::plan_for(m, 2 * f, k, true, true, 0, true);
+  nmb::GemmArgs g = nmb::make_args(m, f, k, 1.f, a, lda, b, ldb, 0.f, nullptr, 0, d, ldd, nullptr, p);
+  g.gu = static_cast<nmb::bf16*>(gu);
+  g.ldgu = ldgu;
+  return nmb::dispatch_swiglu(p.config, g, stream);
 }

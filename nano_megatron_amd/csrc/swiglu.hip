@@ -10,39 +10,11 @@
 // d_gate uses the fast sigmoid below (a few fp32 ulps before its bf16
 // rounding); the activation itself rounds exactly as the exact formula does.
 #include "common.h"
+#include "swiglu_math.h"
 #include "vec.h"
 
 namespace nmb {
 namespace {
-
-// sigmoid(g) = 1 / (1 + 2^(-g log2 e)) from the hardware exp2 and reciprocal
-// (v_exp_f32, v_rcp_f32), against ~25 VALU instructions for expf plus an IEEE
-// division, which made these kernels VALU-bound.  Relative error: the rounded
-// argument t = -g log2 e contributes |t| ln2 / 2 fp32 ulps (<= 45 for |t| <=
-// 128, beyond which 2^t saturates to inf or 0), exp2, rcp and the final
-// product ~3 more.  Limits: g -> -inf: 2^+inf = inf, 1/inf = 0; g -> +inf:
-// sigmoid 1; NaN propagates.
-__device__ __forceinline__ float sigmoid_f(float g) {
-  constexpr float kLog2e = 1.4426950408889634f;
-  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * kLog2e));
-}
-
-// silu(g) = g sigmoid(g), rounded to T where the reference's F.silu output is
-// rounded.  For bf16 the result equals that of the exact formula the reference
-// evaluates in fp32 (g / (1 + exp(-g)), IEEE division): the fast product is
-// used unless it lies within 64 fp32 ulps of a bf16 rounding tie (low 16 bits
-// near 0x8000; the fast error bound above plus expf's own error is below 64),
-// or g < -87 (2^t near the fp32 range end, where the reciprocal's result is
-// subnormal); there the exact formula is evaluated (~0.2% of elements).
-template <typename T>
-__device__ __forceinline__ float silu_t(float g, float sig) {
-  float s = mul_rn(g, sig);
-  if constexpr (sizeof(T) == 2) {
-    const uint32_t b = __float_as_uint(s);
-    if (((b - 0x8000u + 64u) & 0xFFFFu) <= 128u || g < -87.0f) s = __fdiv_rn(g, 1.0f + expf(-g));
-  }
-  return round_as<T>(s);
-}
 
 struct SwigluArgs {
   int64_t g_ld, u_ld, d_ld, dg_ld, du_ld, o_ld;
@@ -104,7 +76,7 @@ __global__ __launch_bounds__(256) void swiglu_fwd_kernel(const T* __restrict__ g
     unpack<T>(graw[k], gv);
     unpack<T>(uraw[k], uv);
 #pragma unroll
-    for (int e = 0; e < V; ++e) ov[k][e] = mul_rn(silu_t<T>(gv[e], sigmoid_f(gv[e])), uv[e]);
+    for (int e = 0; e < V; ++e) ov[k][e] = swiglu_t<T>(gv[e], uv[e]);
   }
 #pragma unroll
   for (int k = 0; k < kVec; ++k)

@@ -1,0 +1,45 @@
+// The SwiGLU activation's fp32 math, shared by the SwiGLU kernels and the
+// gate/up GEMM's fused epilogue (both must round identically).
+#pragma once
+
+#include "common.h"
+
+namespace nmb {
+
+// sigmoid(g) = 1 / (1 + 2^(-g log2 e)) from the hardware exp2 and reciprocal
+// (v_exp_f32, v_rcp_f32), against ~25 VALU instructions for expf plus an IEEE
+// division, which made these kernels VALU-bound.  Relative error: the rounded
+// argument t = -g log2 e contributes |t| ln2 / 2 fp32 ulps (<= 45 for |t| <=
+// 128, beyond which 2^t saturates to inf or 0), exp2, rcp and the final
+// product ~3 more.  Limits: g -> -inf: 2^+inf = inf, 1/inf = 0; g -> +inf:
+// sigmoid 1; NaN propagates.
+__device__ __forceinline__ float sigmoid_f(float g) {
+  constexpr float kLog2e = 1.4426950408889634f;
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * kLog2e));
+}
+
+// silu(g) = g sigmoid(g), rounded to T where the reference's F.silu output is
+// rounded.  For bf16 the result equals that of the exact formula the reference
+// evaluates in fp32 (g / (1 + exp(-g)), IEEE division): the fast product is
+// used unless it lies within 64 fp32 ulps of a bf16 rounding tie (low 16 bits
+// near 0x8000; the fast error bound above plus expf's own error is below 64),
+// or g < -87 (2^t near the fp32 range end, where the reciprocal's result is
+// subnormal); there the exact formula is evaluated (~0.2% of elements).
+template <typename T>
+__device__ __forceinline__ float silu_t(float g, float sig) {
+  float s = mul_rn(g, sig);
+  if constexpr (sizeof(T) == 2) {
+    const uint32_t b = __float_as_uint(s);
+    if (((b - 0x8000u + 64u) & 0xFFFFu) <= 128u || g < -87.0f) s = __fdiv_rn(g, 1.0f + expf(-g));
+  }
+  return round_as<T>(s);
+}
+
+// out = bf16-or-fp32 rounding of silu(g) * u (reference models/gpt/mlp.py:77:
+// F.silu(gate) * up, each operation rounded to the tensor dtype)
+template <typename T>
+__device__ __forceinline__ float swiglu_t(float g, float u) {
+  return mul_rn(silu_t<T>(g, sigmoid_f(g)), u);
+}
+
+}  // namespace nmb

@@ -362,6 +362,52 @@ def swiglu_fwd(g: Tensor, u: Tensor, out: Tensor | None = None) -> Tensor:
     return out
 
 
+def mm_gate_up(a: Tensor, w_gu: Tensor, *, act: bool = True, gu: bool = False,
+               act_out: Tensor | None = None, gu_out: Tensor | None = None
+               ) -> tuple[Tensor | None, Tensor | None]:
+    """The gate/up projections of GPTMLP.forward (models/gpt/mlp.py:72-78) with
+    ``w_gu`` = [Wg; Wu] ([2F, K], row-major): returns (``silu(a Wg^T) * (a Wu^T)``
+    if act, the product ``a [Wg; Wu]^T`` [M, 2F] if gu).  bf16 runs one GEMM
+    with the activation as its epilogue (``nmb_gemm_bf16_swiglu``: one plan per
+    shape, so the product is the same bits with or without the activation, and
+    the activation equals ``swiglu_fwd`` of it); other dtypes run the GEMM and
+    then ``swiglu_fwd``."""
+    if not (act or gu):
+        raise ValueError("mm_gate_up: nothing requested")
+    m, k = a.shape
+    f2, k2 = w_gu.shape
+    if k != k2 or f2 % 2:
+        raise ValueError("mm_gate_up: w_gu must be [2F, K] with a = [M, K]")
+    f = f2 // 2
+    if a.dtype != torch.bfloat16:
+        p = mm(a, w_gu.t(), out=gu_out)
+        s = swiglu_fwd(p[:, :f], p[:, f:], out=act_out) if act else None
+        return s, (p if gu else None)
+    _require_gpu(a, w_gu)
+    if a.stride(1) != 1 or w_gu.stride(1) != 1 or w_gu.dtype != a.dtype:
+        raise ValueError("mm_gate_up: a and w_gu must be row-major and of one dtype")
+    s = p = None
+    if act:
+        s = act_out if act_out is not None else torch.empty(m, f, dtype=a.dtype, device=a.device)
+        if s.shape != (m, f) or s.dtype != a.dtype or s.stride(1) != 1:
+            raise ValueError("mm_gate_up: act_out must be a row-major [M, F] tensor of a's dtype")
+    if gu:
+        p = gu_out if gu_out is not None else torch.empty(m, f2, dtype=a.dtype, device=a.device)
+        if p.shape != (m, f2) or p.dtype != a.dtype or p.stride(1) != 1:
+            raise ValueError("mm_gate_up: gu_out must be a row-major [M, 2F] tensor of a's dtype")
+    _lib.call(
+        "nmb_gemm_bf16_swiglu", m, f, k, a.data_ptr(), max(a.stride(0), k), w_gu.data_ptr(),
+        max(w_gu.stride(0), k), _lib.ptr(s), s.stride(0) if s is not None else 0, _lib.ptr(p),
+        p.stride(0) if p is not None else 0, _lib.stream_of(a),
+    )
+    return s, p
+
+
+def mm_swiglu(a: Tensor, w_gu: Tensor, out: Tensor | None = None) -> Tensor:
+    """``silu(a Wg^T) * (a Wu^T)`` with ``w_gu`` = [Wg; Wu] (see ``mm_gate_up``)."""
+    return mm_gate_up(a, w_gu, act=True, act_out=out)[0]
+
+
 def swiglu_bwd(
     g: Tensor, u: Tensor, dout: Tensor, dg: Tensor, du: Tensor, out: Tensor | None = None
 ) -> None:

@@ -90,6 +90,18 @@ def test_rope_and_swiglu_and_ce_reject_bad_arguments() -> None:
     assert st == _lib.NMB_EUNSUPPORTED
     st = lib.nmb_ce_fwd(FAKE, 4, FAKE, 2, 8, -100, FAKE, FAKE, _lib.NMB_F32, None)
     assert st == _lib.NMB_EINVAL
+    # fused gate/up + SwiGLU: F a multiple of 8, the [2F, K] weight under 2 GiB
+    st = lib.nmb_gemm_bf16_swiglu(64, 12, 64, FAKE, 64, FAKE, 64, FAKE, 64, None, 0, None)
+    assert st == _lib.NMB_EUNSUPPORTED and b"of 8" in lib.nmb_last_error()
+    st = lib.nmb_gemm_bf16_swiglu(64, 1 << 20, 1024, FAKE, 1024, FAKE, 1024, FAKE, 1 << 20, None, 0,
+                                  None)
+    assert st == _lib.NMB_EUNSUPPORTED and b"2 GiB" in lib.nmb_last_error()
+    st = lib.nmb_gemm_bf16_swiglu(64, 64, 64, FAKE, 64, FAKE, 64, FAKE, 32, None, 0, None)
+    assert st == _lib.NMB_EINVAL and b"leading dimension" in lib.nmb_last_error()
+    st = lib.nmb_gemm_bf16_swiglu(64, 64, 64, FAKE, 64, FAKE, 64, None, 0, FAKE, 64, None)
+    assert st == _lib.NMB_EINVAL and b"2F" in lib.nmb_last_error()
+    st = lib.nmb_gemm_bf16_swiglu(64, 64, 64, FAKE, 64, FAKE, 64, None, 0, None, 0, None)
+    assert st == _lib.NMB_EINVAL and b"neither" in lib.nmb_last_error()
 
 
 def test_python_wrapper_maps_status_to_exceptions() -> None:

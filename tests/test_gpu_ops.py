@@ -357,6 +357,40 @@ def test_gemm_rope_equals_gemm_then_rope(device, batch, seq, hq, hkv, d, offset,
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("m,f,k,scale", [
+    (8192, 2736, 1024, 1.0),  # the config-3 gate/up shape (F not a multiple of 128)
+    (512, 2736, 1024, 1.0),
+    (300, 200, 256, 1.0),     # ragged rows and columns, small-tile configuration
+    (1000, 1032, 520, 8.0),   # ragged K; large gates reach silu's exact-formula branches
+])
+def test_gemm_swiglu_equals_gemm_then_swiglu(device, m, f, k, scale) -> None:
+    """nmb_gemm_bf16_swiglu: the activation equals nmb_swiglu_fwd of the product it
+    writes, bit for bit; the product is the same bits with or without the
+    activation; both match the fp32 expression."""
+    g = torch.Generator(device=device).manual_seed(m + f + k)
+    bf = torch.bfloat16
+    x = (scale * torch.randn(m, k, device=device, generator=g)).to(bf)
+    w = (0.05 * torch.randn(2 * f, k, device=device, generator=g)).to(bf)
+    act, _ = Fn.mm_gate_up(x, w, act=True, gu=False)
+    _, gu = Fn.mm_gate_up(x, w, act=False, gu=True)
+    act2, gu2 = Fn.mm_gate_up(x, w, act=True, gu=True)
+    ref = Fn.swiglu_fwd(gu[:, :f], gu[:, f:])
+    assert torch.equal(act, ref) and torch.equal(act2, ref) and torch.equal(gu2, gu)
+    if m >= 4096:  # unsplit plans on both sides: the plain GEMM gives the same product
+        assert torch.equal(gu, Fn.mm(x, w.t()))
+    p = x.float() @ w.float().t()
+    torch.testing.assert_close(gu.float(), p, rtol=1e-2, atol=1e-2 * scale)
+    exp = torch.nn.functional.silu(p[:, :f]) * p[:, f:]
+    torch.testing.assert_close(act.float(), exp, rtol=2e-2, atol=2e-2 * scale * scale)
+    # outputs with row strides wider than F and 2F
+    wide = torch.full((m, f + 24), 7.0, dtype=bf, device=device)
+    wide_gu = torch.full((m, 2 * f + 8), 7.0, dtype=bf, device=device)
+    Fn.mm_gate_up(x, w, act=True, gu=True, act_out=wide[:, :f], gu_out=wide_gu[:, :2 * f])
+    assert torch.equal(wide[:, :f], ref) and bool((wide[:, f:] == 7.0).all())
+    assert torch.equal(wide_gu[:, :2 * f], gu) and bool((wide_gu[:, 2 * f:] == 7.0).all())
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("batch,seq,hq,hkv,d,offset,explicit", [
     (2, 256, 4, 4, 64, 0, False),
     (2, 192, 4, 2, 64, 5, False),
