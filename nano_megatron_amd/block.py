@@ -126,6 +126,46 @@ def block_forward(x: Tensor, w: tuple[Tensor, ...], m: BlockMeta, *, recompute: 
     return acts
 
 
+_SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
+
+
+class _SideProducts:
+    """Weight-gradient products on a second stream of the device.
+
+    The four weight gradients of the block feed nothing else in its backward;
+    on their own stream (default priority, like every stream here) they fill
+    the CUs that the dX chain's launches leave idle (products of 128-176
+    workgroups, split-K tails).  Each product waits for the work queued so far
+    on the main stream, its operands are recorded on the side stream (the
+    allocator keeps them until it is done), and ``join`` makes the main stream
+    wait for all of them before the gradients are returned (autograd may read
+    them on the main stream: accumulation, hooks).  Every kernel is
+    deterministic, so the results do not depend on the overlap.  (Letting the
+    products run on under the next layers' backward, joined by a final
+    callback of the backward pass, measured no faster.)"""
+
+    def __init__(self, device: torch.device) -> None:
+        self.main = torch.cuda.current_stream(device)
+        side = _SIDE_STREAMS.get(device.index)
+        if side is None:
+            side = _SIDE_STREAMS[device.index] = torch.cuda.Stream(device)
+        self.side = side
+        self.used = False
+
+    def mm(self, a: Tensor, b: Tensor) -> Tensor:
+        self.side.wait_stream(self.main)
+        with torch.cuda.stream(self.side):
+            out = Fn.mm(a, b)
+        a.record_stream(self.side)
+        b.record_stream(self.side)
+        self.used = True
+        return out
+
+    def join(self) -> None:
+        if self.used:
+            self.main.wait_stream(self.side)
+
+
 def block_backward(acts: dict, dy: Tensor, w: tuple[Tensor, ...], m: BlockMeta, shape) -> tuple:
     """Gradients (dx, dw_in, dWq, dWk, dWv, dWo, dw_post, dWg, dWu, dWd) of the block."""
     w_in, wq, wk, wv, wo, w_post, wg, wu, wd = w
@@ -135,20 +175,21 @@ def block_backward(acts: dict, dy: Tensor, w: tuple[Tensor, ...], m: BlockMeta, 
     if not dy2.is_contiguous():
         dy2 = dy2.contiguous()
     x2, n1, qkv, o2, lse, h, n2, gu = (acts[k] for k in ("x2", "n1", "qkv", "o2", "lse", "h", "n2", "gu"))
+    side = _SideProducts(dy2.device)
 
     # MLP: y = h + s Wd^T, s = silu(g) * u, [g|u] = n2 [Wg;Wu]^T
     ds = Fn.mm(dy2, wd)
     dgu = torch.empty_like(gu)
     act = torch.empty(b * s, f, dtype=gu.dtype, device=gu.device)
     Fn.swiglu_bwd(gu[:, :f], gu[:, f:], ds, dgu[:, :f], dgu[:, f:], act)
-    dwd = Fn.mm(dy2.t(), act)
+    dwd = side.mm(dy2.t(), act)
     dn2 = Fn.mm(dgu, joined((wg, wu)))
-    dwgu = Fn.mm(dgu.t(), n2)
+    dwgu = side.mm(dgu.t(), n2)
     dh, dw_post = Fn.rmsnorm_bwd(h, w_post, dn2, m.eps, residual_grad=dy2)
 
     # attention: h = x + o Wo^T
     do2 = Fn.mm(dh, wo)
-    dwo = Fn.mm(dh.t(), o2)
+    dwo = side.mm(dh.t(), o2)
     q, k, v = _qkv_views(qkv, b, s, m)
     dqkv = torch.empty_like(qkv)
     dq, dk, dv = _qkv_views(dqkv, b, s, m)
@@ -159,8 +200,9 @@ def block_backward(acts: dict, dy: Tensor, w: tuple[Tensor, ...], m: BlockMeta, 
                           scale=None, cos=m.cos, sin=m.sin, pos_offset=m.sequence_offset,
                           positions=m.positions)
     dn1 = Fn.mm(dqkv, joined((wq, wk, wv)))
-    dwqkv = Fn.mm(dqkv.t(), n1)
+    dwqkv = side.mm(dqkv.t(), n1)
     dx, dw_in = Fn.rmsnorm_bwd(x2, w_in, dn1, m.eps, residual_grad=dh)
+    side.join()
 
     qd = m.heads * m.head_dim
     kd = m.kv_heads * m.head_dim
