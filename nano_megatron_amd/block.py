@@ -132,10 +132,12 @@ _SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
 class _SideProducts:
     """Weight-gradient products on a second stream of the device.
 
-    The four weight gradients of the block feed nothing else in its backward;
-    on their own stream (default priority, like every stream here) they fill
-    the CUs that the dX chain's launches leave idle (products of 128-176
-    workgroups, split-K tails).  Each product waits for the work queued so far
+    The weight gradients of the block feed nothing else in its backward; on
+    their own stream (default priority, like every stream here) they fill the
+    CUs that the dX chain's launches leave idle (products of 128-176
+    workgroups, split-K tails).  The out-projection's stays on the main stream:
+    its overlap would fall on the attention backward, whose workgroups it then
+    displaces (measured slower).  Each product waits for the work queued so far
     on the main stream, its operands are recorded on the side stream (the
     allocator keeps them until it is done), and ``join`` makes the main stream
     wait for all of them before the gradients are returned (autograd may read
@@ -189,7 +191,8 @@ def block_backward(acts: dict, dy: Tensor, w: tuple[Tensor, ...], m: BlockMeta, 
 
     # attention: h = x + o Wo^T
     do2 = Fn.mm(dh, wo)
-    dwo = side.mm(dh.t(), o2)
+    # on the main stream: beside the attention backward it measured slower
+    dwo = Fn.mm(dh.t(), o2)
     q, k, v = _qkv_views(qkv, b, s, m)
     dqkv = torch.empty_like(qkv)
     dq, dk, dv = _qkv_views(dqkv, b, s, m)
