@@ -338,6 +338,50 @@ def measured_traffic(kernel: str) -> int | None:
     return None
 
 
+def measured_ceilings(device) -> dict:
+    """Achievable ceilings on this box, beside the datasheet peaks: a plain
+    256 MiB device copy (256 MiB read + 256 MiB written) and an 8192^3 bf16
+    product (A row-major, B = W^T of a row-major W) by this library's GEMM and
+    by torch (hipBLASLt).  Best of three rounds of ten launches each."""
+    import torch
+
+    from nano_megatron_amd import functional as Fn
+
+    def best_ms(fn, reps=10, rounds=3):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(rounds):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            for _ in range(reps):
+                fn()
+            end.record()
+            end.synchronize()
+            best = min(best, start.elapsed_time(end) / reps)
+        return best
+
+    bf = torch.bfloat16
+    n = 128 << 20  # bf16 elements: 256 MiB
+    src = torch.ones(n, dtype=bf, device=device)
+    dst = torch.empty_like(src)
+    copy_ms = best_ms(lambda: dst.copy_(src))
+    copy_gbs = 2 * n * 2 / (copy_ms * 1e-3) / 1e9
+    del src, dst
+    g = torch.Generator(device=device).manual_seed(7)
+    m = 8192
+    a = torch.randn(m, m, device=device, dtype=bf, generator=g)
+    w = torch.randn(m, m, device=device, dtype=bf, generator=g)
+    out = torch.empty(m, m, device=device, dtype=bf)
+    flops = 2.0 * m * m * m
+    ours = flops / (best_ms(lambda: Fn.mm(a, w.t(), out=out)) * 1e-3) / 1e12
+    lt = flops / (best_ms(lambda: torch.mm(a, w.t(), out=out)) * 1e-3) / 1e12
+    return dict(copy_256mib_gbs=round(copy_gbs, 1), copy_hbm_frac=round(copy_gbs / HBM_PEAK_GBS, 3),
+                gemm_8192_tflops=round(ours, 1), gemm_8192_mfma_frac=round(ours / BF16_PEAK_TFLOPS, 3),
+                hipblaslt_gemm_8192_tflops=round(lt, 1))
+
+
 def copy_calibration(device) -> None:
     """A plain device copy of 256 MiB (read 256 MiB, write 256 MiB), run once so
     that a counter pass sees the HBM bytes one such copy reports."""
@@ -535,10 +579,13 @@ def main() -> None:
         run_c5(args, device)
         return
 
-    kernels = None
+    kernels = ceilings = None
     if not args.no_kernels:
         kernels = kernel_rooflines(device, args.kernel if args.only_kernels else None)
         print("kernels: " + json.dumps(kernels), file=sys.stderr, flush=True)
+        if not args.kernel:
+            ceilings = measured_ceilings(device)
+            print("ceilings: " + json.dumps(ceilings), file=sys.stderr, flush=True)
     if args.only_kernels:
         if args.kernel:
             copy_calibration(device)
@@ -593,6 +640,7 @@ def main() -> None:
         loss=round(full["loss"], 4),
         roofline=roofline,
         cpu_baseline=cpu,
+        ceilings=ceilings,
         kernels=kernels,
     )
     if eager:

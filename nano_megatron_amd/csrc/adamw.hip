@@ -83,7 +83,20 @@ __global__ __launch_bounds__(256) void sumsq_kernel(const uint64_t* __restrict__
     const G* g = reinterpret_cast<const G*>(grads[t]) - offsets[t];
     int64_t a, b;
     vector_span(g, lo, hi, &a, &b);
-    for (int64_t i = a + 8 * threadIdx.x; i < b; i += 8 * 256) {
+    // four vectors per thread and iteration, loaded before any is summed (one
+    // load in flight per thread left the kernel latency-bound); the sum runs
+    // in the same order as one vector at a time
+    int64_t i = a + 8 * threadIdx.x;
+    for (; i + 3 * 8 * 256 < b; i += 4 * 8 * 256) {
+      float v[4][8];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) load8(g + i + u * 8 * 256, v[u]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc += v[u][e] * v[u][e];
+    }
+    for (; i < b; i += 8 * 256) {
       float v[8];
       load8(g + i, v);
 #pragma unroll
