@@ -131,6 +131,24 @@ def test_full_recompute_grads_bit_identical_to_eager(device) -> None:
         assert torch.equal(a, b)
 
 
+def test_block_grads_accumulate_over_two_backward_passes(device) -> None:
+    """The weight gradients (some computed on a second stream) are complete when
+    the block's backward returns: a second pass accumulating into existing
+    .grad tensors gives the bf16 sum of the two single-pass gradients."""
+    x, w, meta = _block_inputs(device)
+    dys = [torch.randn_like(x), torch.randn_like(x)]
+    single = []
+    for dy in dys:
+        ws = [t.clone().requires_grad_(True) for t in w]
+        B.CheckpointedBlockFunction.apply(x, meta, *ws).backward(dy)
+        single.append([t.grad.clone() for t in ws])
+    ws = [t.clone().requires_grad_(True) for t in w]
+    for dy in dys:
+        B.CheckpointedBlockFunction.apply(x, meta, *ws).backward(dy)
+    for t, g1, g2 in zip(ws, *single):
+        assert torch.equal(t.grad, g1 + g2)
+
+
 def test_full_recompute_keeps_only_block_input_and_lse(device) -> None:
     """Peak activation memory per checkpointed layer is the bf16 input plus the lse."""
     cfg = nm.GPTConfig(layers=4, hidden_size=512, ffn_hidden_size=1376, heads=8, seq_length=256,
