@@ -447,9 +447,9 @@ def cpu_baseline() -> dict:
 
 
 def model_step_flops(cfg: dict, batch: int, seq: int, recompute: bool) -> float:
-    """FLOPs of one training step (GEMMs, causal attention, LM head), the
-    arithmetic of the block's survey: per layer 3x the forward GEMMs and 3.5x the
-    causal attention forward, plus 3x the LM head; recompute adds one forward
+    """FLOPs of one training step (GEMMs, causal attention, LM head): per layer
+    3x the forward GEMMs (forward, dX, dW) and 3.5x the causal attention forward
+    (forward 1x, backward 2.5x), plus 3x the LM head; recompute adds one forward
     without the down projection."""
     t, h, f, v = batch * seq, cfg["hidden_size"], cfg["ffn_hidden_size"], cfg["vocab_size"]
     hq = cfg["heads"]
@@ -495,7 +495,8 @@ def run_c5(args, device) -> None:
     """One ring rank's attention share: rank 3 of 4 (queries 24576..32767) over the
     four K/V blocks in ring order 3, 2, 1, 0 (context_parallel/ring.py:104-250),
     causal by absolute position, forward then backward (P recomputed from the
-    LSE); FLOPs as the survey counts them: visible scores only, backward 2.5x."""
+    LSE); FLOPs count the visible (causally unmasked) scores only, backward 2.5x
+    the forward."""
     import torch
 
     from nano_megatron_amd import functional as Fn
