@@ -518,9 +518,10 @@ constexpr Config kConfigs[] = {
 };
 
 struct Plan {
-  int config;  // index into kConfigs
-  int splits;  // 1: no split K
-  int kps;     // K per split (multiple of the config's K tile)
+  int config;     // index into kConfigs
+  int splits;     // 1: no split K
+  int kps;        // K per split (multiple of the config's K tile)
+  double time;    // the estimate the plan was chosen by (seconds)
 };
 
 // Configuration and K split for an M x N x K product on 256 CUs.  Products
@@ -538,7 +539,7 @@ Plan plan_for(int64_t m, int64_t n, int64_t k, bool a_kc, bool b_kc, int rope_he
   constexpr double kBytesPerS = 5e12;
   const int64_t big_tiles = ((m + 255) / 256) * ((n + 127) / 128);
   const bool small = (!a_kc && !b_kc) || big_tiles < kCUs;
-  Plan best{small ? 2 : 1, 1, 0};
+  Plan best{small ? 2 : 1, 1, 0, 0.0};
   double best_t = -1.0;
   // pass 0: the configurations of the problem's size class; pass 1 (RoPE only,
   // when none of those fits the head): any configuration that fits
@@ -561,7 +562,7 @@ Plan plan_for(int64_t m, int64_t n, int64_t k, bool a_kc, bool b_kc, int rope_he
         if (splits > 1) t += static_cast<double>(splits) * m * n * 8 / kBytesPerS;
         if (best_t < 0 || t < best_t * 0.999) {
           best_t = t;
-          best = Plan{c, static_cast<int>(splits), static_cast<int>(tps * cf.bkt)};
+          best = Plan{c, static_cast<int>(splits), static_cast<int>(tps * cf.bkt), t};
         }
       }
     }
@@ -584,7 +585,7 @@ Plan plan_for(int64_t m, int64_t n, int64_t k, bool a_kc, bool b_kc, int rope_he
       if (splits > 1) t += static_cast<double>(splits) * m * n * 8 / kBytesPerS;
       if (t < best_t * 0.999) {
         best_t = t;
-        best = Plan{0, static_cast<int>(splits), static_cast<int>(tps * cf.bkt)};
+        best = Plan{0, static_cast<int>(splits), static_cast<int>(tps * cf.bkt), t};
       }
     }
   }
@@ -763,8 +764,35 @@ extern "C" int nmb_gemm_bf16_rope(int b_layout, int64_t m, int64_t n, int64_t k,
     NMB_REQUIRE(pos_batch_stride >= 0, "gemm_rope: negative position batch stride");
   }
   if (m == 0 || n == 0) return NMB_OK;
-  const nmb::Plan p = nmb::plan_for(m, n, k, true, b_layout == 0, static_cast<int>(head_dim));
-  nmb::GemmArgs g = nmb::make_args(m, n, k, 1.f, a, lda, b, ldb, 0.f, nullptr, 0, d, ldd, nullptr, p);
+  const bool b_kc = b_layout == 0;
+  nmb::Plan p = nmb::plan_for(m, n, k, true, b_kc, static_cast<int>(head_dim));
+  int64_t n_rope = n;
+  if (rope_cols > 0 && rope_cols < n) {
+    // The columns past rope_cols (v) need no rotation: as a plain product of
+    // their own they can take a tile shape that fills the CUs in whole rounds
+    // where the full width cannot (8192 x 3072: 1.5 rounds of 256 x 256 tiles
+    // or three short ones of 256 x 128; split: one round of each).  Every tile
+    // shape accumulates K in the same order, so the bits do not change.
+    const nmb::Plan pr = nmb::plan_for(m, rope_cols, k, true, b_kc, static_cast<int>(head_dim));
+    const nmb::Plan pv = nmb::plan_for(m, n - rope_cols, k, true, b_kc, 0, true);
+    if (pr.time + pv.time < p.time) {
+      const nmb::bf16* bv = static_cast<const nmb::bf16*>(b) + (b_kc ? rope_cols * ldb : rope_cols);
+      nmb::bf16* dv = static_cast<nmb::bf16*>(d) + rope_cols;
+      const nmb::GemmArgs gv = nmb::make_args(m, n - rope_cols, k, 1.f, a, lda, bv, ldb, 0.f, nullptr, 0,
+                                              dv, ldd, nullptr, pv);
+      int st2 = NMB_OK;
+      switch (pv.config) {
+        case 0: st2 = nmb::dispatch_layout<256, 256, 8, 64>(true, b_kc, gv, stream); break;
+        case 1: st2 = nmb::dispatch_layout<256, 128, 8, 64>(true, b_kc, gv, stream); break;
+        case 2: st2 = nmb::dispatch_layout<128, 128, 4, 32>(true, b_kc, gv, stream); break;
+        default: st2 = nmb::dispatch_layout<128, 256, 4, 32>(true, b_kc, gv, stream); break;
+      }
+      if (st2 != NMB_OK) return st2;
+      p = pr;
+      n_rope = rope_cols;
+    }
+  }
+  nmb::GemmArgs g = nmb::make_args(m, n_rope, k, 1.f, a, lda, b, ldb, 0.f, nullptr, 0, d, ldd, nullptr, p);
   g.rope_cos = cos_table;
   g.rope_sin = sin_table;
   g.rope_pos = positions;

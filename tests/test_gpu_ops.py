@@ -357,6 +357,29 @@ def test_gemm_rope_equals_gemm_then_rope(device, batch, seq, hq, hkv, d, offset,
 
 
 @pytest.mark.gpu
+# config-3 rows: neither the fused entry nor the reference GEMM splits K there
+@pytest.mark.parametrize("batch,seq,heads,hidden", [(16, 512, 16, 1024)])
+def test_gemm_rope_split_launch_equals_gemm_then_rope(device, batch, seq, heads, hidden) -> None:
+    """At the config-3 Q/K/V shape the entry point runs the q/k columns (RoPE) and
+    the v columns (plain product) as two launches with different tile shapes;
+    the result still equals one GEMM followed by the rotary kernel, bit for bit."""
+    import nano_megatron_amd as nm
+
+    g = torch.Generator(device=device).manual_seed(11)
+    bf = torch.bfloat16
+    d = hidden // heads
+    n = 3 * hidden
+    x = torch.randn(batch * seq, hidden, device=device, generator=g).to(bf)
+    w = (0.05 * torch.randn(n, hidden, device=device, generator=g)).to(bf)
+    tab = nm.RotaryEmbedding(d).tables(device, seq)
+    fused = Fn.mm_rope(x, w.t(), seq=seq, head_dim=d, rope_cols=2 * hidden, cos=tab.cos, sin=tab.sin)
+    ref = Fn.mm(x, w.t())
+    qk = ref.view(batch, seq, n)[:, :, :2 * hidden].unflatten(2, (2 * heads, d))
+    Fn.rope_apply(qk, qk, tab.cos, tab.sin)
+    assert torch.equal(fused, ref)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("m,f,k,scale", [
     (8192, 2736, 1024, 1.0),  # the config-3 gate/up shape (F not a multiple of 128)
     (512, 2736, 1024, 1.0),
