@@ -823,6 +823,33 @@ class LMHeadCrossEntropyFunction(torch.autograd.Function):
         return dx, dw, None, None, None, None
 
 
+class TargetCheck:
+    """The cross entropy's target-range check (tensor_parallel/cross_entropy.py:
+    109-114: a ValueError for ids outside [0, vocab) other than ignore_index),
+    enqueued when constructed: the flag ``any(invalid)`` is copied to pinned
+    host memory behind an event.  ``raise_if_invalid`` waits for that event
+    only, so a check made at the start of the forward costs the host no wait
+    for the layers enqueued after it (as ``torch.any`` at the loss would)."""
+
+    def __init__(self, targets: Tensor, vocab: int, ignore_index: int = IGNORE_INDEX) -> None:
+        invalid = (targets != ignore_index) & ((targets < 0) | (targets >= vocab))
+        self._bad: bool | None = None
+        if targets.device.type == "cuda":
+            self._flag = torch.empty((), dtype=torch.bool, pin_memory=True)
+            self._flag.copy_(invalid.any(), non_blocking=True)
+            self._event = torch.cuda.Event()
+            self._event.record(torch.cuda.current_stream(targets.device))
+        else:
+            self._bad = bool(invalid.any())
+
+    def raise_if_invalid(self) -> None:
+        if self._bad is None:
+            self._event.synchronize()
+            self._bad = bool(self._flag)
+        if self._bad:
+            raise ValueError("targets contain ids outside the original (unpadded) vocabulary")
+
+
 def lm_head_cross_entropy(
     hidden: Tensor,
     weight: Tensor,
@@ -831,7 +858,7 @@ def lm_head_cross_entropy(
     ignore_index: int = IGNORE_INDEX,
     reduction: str = "mean",
     chunk: int = 2048,
-    validate: bool = True,
+    validate: "bool | TargetCheck" = True,
     tie: TiedGrad | None = None,
 ) -> Tensor:
     """Loss of ``F.linear(hidden, weight)`` under VocabParallelCrossEntropy
@@ -844,10 +871,10 @@ def lm_head_cross_entropy(
             f"hidden={tuple(hidden.shape)}, targets={tuple(targets.shape)}"
         )
     vocab = weight.shape[0]
-    if validate:
-        invalid = (targets != ignore_index) & ((targets < 0) | (targets >= vocab))
-        if torch.any(invalid):
-            raise ValueError("targets contain ids outside the original (unpadded) vocabulary")
+    if isinstance(validate, TargetCheck):
+        validate.raise_if_invalid()
+    elif validate:
+        TargetCheck(targets, vocab, ignore_index).raise_if_invalid()
     x2 = hidden.reshape(-1, hidden.shape[-1]).contiguous()
     t1 = targets.reshape(-1).to(torch.int64).contiguous()
     loss = LMHeadCrossEntropyFunction.apply(x2, weight, t1, int(ignore_index), int(chunk), tie)

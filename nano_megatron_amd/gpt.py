@@ -532,6 +532,10 @@ class GPTModel(nn.Module):
     def forward(self, input_ids: Tensor | None = None, *, labels: Tensor | None = None,
                 position_ids: Tensor | None = None, hidden_states: Tensor | None = None,
                 microbatch_index: int = 0) -> GPTOutput:
+        # the loss's target-range check, enqueued before the layers (see TargetCheck)
+        check = None
+        if labels is not None and self.lm_head is not None:
+            check = Fn.TargetCheck(labels, self.lm_head.weight.shape[0], Fn.IGNORE_INDEX)
         # the tied LM head passes its table gradient to the embedding's backward
         tie = None
         if (labels is not None and self.embedding is not None and self.lm_head is not None
@@ -584,7 +588,8 @@ class GPTModel(nn.Module):
             if self.lm_head is None:
                 raise ValueError("labels may only be supplied to a stage that owns the LM head")
             loss = Fn.lm_head_cross_entropy(hidden_states, self.lm_head.weight, labels,
-                                            reduction="mean", chunk=self.ce_chunk, tie=tie)
+                                            reduction="mean", chunk=self.ce_chunk, tie=tie,
+                                            validate=check)
         elif self.lm_head is not None:
             logits = self.lm_head(hidden_states)
         return GPTOutput(logits=logits, loss=loss, hidden_states=hidden_states)

@@ -131,6 +131,23 @@ def test_full_recompute_grads_bit_identical_to_eager(device) -> None:
         assert torch.equal(a, b)
 
 
+def test_model_rejects_out_of_range_labels(device) -> None:
+    """The target-range check enqueued at the start of the forward still raises
+    at the loss (tensor_parallel/cross_entropy.py:109-114); ignored ids pass."""
+    cfg = c1_config(layers=2)
+    model = nm.GPTModel(cfg, activation_checkpoint_config=nm.ActivationCheckpointConfig(mode="full"))
+    model = model.to(device=device, dtype=torch.bfloat16).train()
+    ids = torch.randint(0, cfg.vocab_size, (2, 64), device=device)
+    for bad in (cfg.vocab_size, -5):
+        labels = ids.clone()
+        labels[1, 7] = bad
+        with pytest.raises(ValueError, match="outside the original"):
+            model(ids, labels=labels)
+    labels = ids.clone()
+    labels[0, :5] = -100
+    assert torch.isfinite(model(ids, labels=labels).loss)
+
+
 def test_block_grads_accumulate_over_two_backward_passes(device) -> None:
     """The weight gradients (some computed on a second stream) are complete when
     the block's backward returns: a second pass accumulating into existing
