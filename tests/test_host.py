@@ -66,6 +66,22 @@ def test_kernels_refuse_cpu_tensors() -> None:
                                  torch.zeros(2, 3, dtype=torch.long))
 
 
+def test_target_check_rules() -> None:
+    """The cross entropy's target-range rule (tensor_parallel/cross_entropy.py:
+    109-114): ids in [0, vocab) or ignore_index pass; anything else raises."""
+    from nano_megatron_amd import functional as Fn
+
+    ok = torch.tensor([[0, 15, -100], [3, 7, 1]])
+    Fn.TargetCheck(ok, 16).raise_if_invalid()
+    Fn.TargetCheck(torch.tensor([[-1, 3]]), 16, ignore_index=-1).raise_if_invalid()
+    for bad in (16, -5, -100):
+        t = ok.clone()
+        t[1, 2] = bad
+        check = Fn.TargetCheck(t, 16, ignore_index=-100 if bad != -100 else -1)
+        with pytest.raises(ValueError, match="outside the original"):
+            check.raise_if_invalid()
+
+
 def test_model_structure_matches_reference_keys_and_rejects_parallel() -> None:
     cfg = nm.GPTConfig(layers=2, hidden_size=64, ffn_hidden_size=96, heads=2, kv_heads=1,
                        seq_length=16, vocab_size=128)
