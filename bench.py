@@ -50,6 +50,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-kernels", action="store_true", help="skip the per-kernel roofline timing")
     p.add_argument("--no-eager", action="store_true", help="skip the no-checkpoint comparison run")
+    p.add_argument("--no-legs", action="store_true", help="skip the config-4 and config-5 legs of the default line")
     p.add_argument("--only-kernels", action="store_true", help="time the kernels only (for profiling)")
     p.add_argument("--kernel", default=None, help="with --only-kernels: time just this kernel")
     p.add_argument("--config", default="c3", choices=("c3", "c4", "c5"),
@@ -163,14 +164,27 @@ def block_saved_mib(mode: str, device, model_cfg: dict = C3, batch: int = BATCH,
     return (saved[1] - saved[0]) / 2**20
 
 
+INFINITY_CACHE_BYTES = 256 << 20  # MI355X last-level (MALL) cache
+
+
+def _input_sets(nbytes: int) -> int:
+    """How many input sets an HBM-bound kernel's timing rotates through: enough
+    that between two launches on one set the others touch more than twice the
+    256 MB Infinity Cache, so each launch reads its inputs from HBM."""
+    return max(2, min(24, math.ceil(2 * INFINITY_CACHE_BYTES / max(nbytes, 1)) + 1))
+
+
 def kernel_rooflines(device, only: str | None = None) -> list[dict]:
     """Average launch time (HIP events on the launch stream) of each hand-written
     kernel at the config-3 shapes, with algorithmic bytes / FLOPs per launch
-    (``only``: just the named one)."""
+    (``only``: just the named one).  HBM-bound kernels rotate through input
+    sets larger than the Infinity Cache (``_input_sets``); MFMA-bound ones run
+    on one set, as in the step, where their operands were just written."""
     import torch
 
     import nano_megatron_amd as nm
     from nano_megatron_amd import functional as Fn
+    from nano_megatron_amd.optim import MasterAdamW
 
     T, H, F, V = BATCH * SEQ, C3["hidden_size"], C3["ffn_hidden_size"], C3["vocab_size"]
     nh, d = C3["heads"], C3["hidden_size"] // C3["heads"]
@@ -181,68 +195,113 @@ def kernel_rooflines(device, only: str | None = None) -> list[dict]:
     def randn(*shape, scale=1.0):
         return (scale * torch.randn(*shape, device=device, generator=g)).to(bf)
 
-    x = randn(T, H)
-    w = (1 + randn(H, scale=0.02).float()).to(bf)
-    dy = randn(T, H)
-    dres = randn(T, H)
+    tab = nm.RotaryEmbedding(d).tables(device, SEQ)
+    causal_flops = 2 * 2 * BATCH * nh * SEQ * SEQ * d / 2
+    E = 2  # bytes per bf16 element
+    chunk = 2048
+
+    # --- HBM-bound kernels: make() allocates one input set and returns its launch
+    def mk_rms_fwd():
+        x, w = randn(T, H), (1 + randn(H, scale=0.02).float()).to(bf)
+        y = torch.empty_like(x)
+        return lambda: Fn._lib.call("nmb_rmsnorm_fwd", x.data_ptr(), w.data_ptr(), y.data_ptr(), None, T, H,
+                                    1e-5, Fn._lib.NMB_BF16, Fn._lib.stream_of(x))
+
+    def mk_rms_bwd():
+        x, w, dy, dres = randn(T, H), (1 + randn(H, scale=0.02).float()).to(bf), randn(T, H), randn(T, H)
+        dx, dw = torch.empty_like(x), torch.empty_like(w)
+        nb = Fn._lib.ctypes.c_size_t(0)
+        Fn._lib.call("nmb_rmsnorm_bwd_workspace_bytes", T, H, Fn._lib.ctypes.byref(nb))
+        ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=device)
+        return lambda: Fn._lib.call("nmb_rmsnorm_bwd", x.data_ptr(), w.data_ptr(), dy.data_ptr(), dres.data_ptr(),
+                                    dx.data_ptr(), dw.data_ptr(), ws.data_ptr(), ws.numel(), T, H, 1e-5,
+                                    Fn._lib.NMB_BF16, Fn._lib.stream_of(x))
+
+    def mk_rope():
+        q = randn(BATCH, SEQ, nh, d)
+        out = torch.empty_like(q)
+        return lambda: Fn.rope_apply(q, out, tab.cos, tab.sin)
+
+    def mk_swiglu_fwd():
+        gu, act = randn(T, 2 * F), torch.empty(T, F, dtype=bf, device=device)
+        return lambda: Fn.swiglu_fwd(gu[:, :F], gu[:, F:], act)
+
+    def mk_swiglu_bwd():
+        gu, dh = randn(T, 2 * F), randn(T, F)
+        dgu, act = torch.empty_like(gu), torch.empty(T, F, dtype=bf, device=device)
+        return lambda: Fn.swiglu_bwd(gu[:, :F], gu[:, F:], dh, dgu[:, :F], dgu[:, F:], act)
+
+    def mk_ce_fwd():
+        logits = randn(chunk, V)
+        targets = torch.randint(0, V, (chunk,), device=device, generator=g)
+        loss = torch.empty(chunk, dtype=torch.float32, device=device)
+        lse_c = torch.empty_like(loss)
+        return lambda: Fn.ce_fwd(logits, targets, -100, loss, lse_c)
+
+    def mk_ce_bwd():
+        logits = randn(chunk, V)
+        targets = torch.randint(0, V, (chunk,), device=device, generator=g)
+        loss = torch.empty(chunk, dtype=torch.float32, device=device)
+        lse_c = torch.empty_like(loss)
+        Fn.ce_fwd(logits, targets, -100, loss, lse_c)
+        grad_c = torch.full((chunk,), 1.0 / T, device=device)
+        # in place: the values drift over launches, the work per launch does not
+        return lambda: Fn.ce_bwd_(logits, targets, -100, lse_c, grad_c)
+
+    def mk_emb_fwd():
+        table = randn(V, H, scale=0.02)
+        ids = torch.randint(0, V, (T,), device=device, generator=g)
+        out = torch.empty(T, H, dtype=bf, device=device)
+        return lambda: Fn._lib.call("nmb_embedding_fwd", table.data_ptr(), ids.data_ptr(), out.data_ptr(), T, V,
+                                    H, Fn._lib.NMB_BF16, Fn._lib.stream_of(table))
+
+    def mk_emb_bwd():
+        dout = randn(T, H)
+        ids = torch.randint(0, V, (T,), device=device, generator=g)
+        lm_grad, grad = randn(V, H), torch.empty(V, H, dtype=bf, device=device)
+        return lambda: Fn._lib.call("nmb_embedding_bwd", dout.data_ptr(), ids.data_ptr(), lm_grad.data_ptr(),
+                                    grad.data_ptr(), T, V, H, Fn._lib.NMB_BF16, Fn._lib.stream_of(dout))
+
+    # --- MFMA-bound kernels: one input set
     qkv = randn(T, 3 * H)
     q = qkv[:, :H].view(BATCH, SEQ, nh, d)
     k = qkv[:, H:2 * H].view(BATCH, SEQ, nh, d)
     v = qkv[:, 2 * H:].view(BATCH, SEQ, nh, d)
-    gu = randn(T, 2 * F)
-    gate, up = gu[:, :F], gu[:, F:]
-    dh = randn(T, F)
-    dgu = torch.empty_like(gu)
-    act = torch.empty(T, F, dtype=bf, device=device)
-    tab = nm.RotaryEmbedding(d).tables(device, SEQ)
     o, lse = Fn.attn_fwd_bshd(q, [k], [v], (0,), causal=True, q_offset=0, scale=None)
     do = randn(BATCH, SEQ, nh, d)
     dqkv = torch.empty_like(qkv)
     dq = dqkv[:, :H].view(BATCH, SEQ, nh, d)
     dk = dqkv[:, H:2 * H].view(BATCH, SEQ, nh, d)
     dv = dqkv[:, 2 * H:].view(BATCH, SEQ, nh, d)
-    chunk = chunk_rows = 2048
-    logits = randn(chunk, V)
-    targets = torch.randint(0, V, (chunk,), device=device, generator=g)
-    loss = torch.empty(chunk, dtype=torch.float32, device=device)
-    lse_c = torch.empty_like(loss)
-    grad_c = torch.full((chunk,), 1.0 / T, device=device)
-    Fn.ce_fwd(logits, targets, -100, loss, lse_c)
-    rope_out = torch.empty_like(q)
+    x = randn(T, H)
+    act = torch.empty(T, F, dtype=bf, device=device)
 
-    causal_flops = 2 * 2 * BATCH * nh * SEQ * SEQ * d / 2
-    E = 2  # bytes per bf16 element
-
-    # the step's GEMM shapes (fwd, recompute, backward, LM head chunks)
-    def gemm_case(name, m, n, k, a_t, b_t, per_step, residual=False):
-        a = randn(k, m).t() if a_t else randn(m, k)
-        b = randn(k, n) if b_t else randn(n, k).t()
+    def gemm_case(name, m, n, k_, a_t, b_t, per_step, residual=False):
+        a = randn(k_, m).t() if a_t else randn(m, k_)
+        b = randn(k_, n) if b_t else randn(n, k_).t()
         c = randn(m, n) if residual else None
         out = torch.empty(m, n, dtype=bf, device=device)
         fn = (lambda: Fn.mm(a, b, out=out, c=c, beta=1.0)) if residual else (lambda: Fn.mm(a, b, out=out))
-        nbytes = (m * k + k * n + m * n * (2 if residual else 1)) * E
-        return (name, fn, nbytes, 2.0 * m * n * k, "mfma", per_step)
+        nbytes = (m * k_ + k_ * n + m * n * (2 if residual else 1)) * E
+        return (name, fn, nbytes, 2.0 * m * n * k_, "mfma", per_step)
 
-    # the Q/K/V projection with RoPE of q and k in its epilogue, as the block runs it
     w_qkv = randn(3 * H, H)
     qkv_out = torch.empty(T, 3 * H, dtype=bf, device=device)
-    qkv_rope = ("gemm_qkv_rope",
-                lambda: Fn.mm_rope(x, w_qkv.t(), seq=SEQ, head_dim=d, rope_cols=2 * H, cos=tab.cos, sin=tab.sin,
-                                   out=qkv_out),
-                (T * H + 3 * H * H + 3 * T * H) * E, 2.0 * T * 3 * H * H, "mfma", 2 * L)
-    # the gate/up projection: the forward's applies the SwiGLU activation in its
-    # epilogue; the recompute's writes the product [g|u] (same kernel and plan)
     w_gu = randn(2 * F, H)
     gu_buf = torch.empty(T, 2 * F, dtype=bf, device=device)
-    gu_swiglu = ("gemm_gate_up_swiglu", lambda: Fn.mm_gate_up(x, w_gu, act=True, act_out=act),
-                 (T * H + 2 * F * H + T * F) * E, 2.0 * T * 2 * F * H, "mfma", L)
-    gu_product = ("gemm_gate_up", lambda: Fn.mm_gate_up(x, w_gu, act=False, gu=True, gu_out=gu_buf),
-                  (T * H + 2 * F * H + 2 * T * F) * E, 2.0 * T * 2 * F * H, "mfma", L)
     gemms = [
-        qkv_rope,
+        # the Q/K/V projection with RoPE of q and k in its epilogue, as the block runs it
+        ("gemm_qkv_rope",
+         lambda: Fn.mm_rope(x, w_qkv.t(), seq=SEQ, head_dim=d, rope_cols=2 * H, cos=tab.cos, sin=tab.sin,
+                            out=qkv_out),
+         (T * H + 3 * H * H + 3 * T * H) * E, 2.0 * T * 3 * H * H, "mfma", 2 * L),
         gemm_case("gemm_o_residual", T, H, H, False, False, 2 * L, residual=True),
-        gu_product,
-        gu_swiglu,
+        # the gate/up projection: the forward's applies SwiGLU in its epilogue; the
+        # recompute's writes the product [g|u] (same kernel and plan)
+        ("gemm_gate_up", lambda: Fn.mm_gate_up(x, w_gu, act=False, gu=True, gu_out=gu_buf),
+         (T * H + 2 * F * H + 2 * T * F) * E, 2.0 * T * 2 * F * H, "mfma", L),
+        ("gemm_gate_up_swiglu", lambda: Fn.mm_gate_up(x, w_gu, act=True, act_out=act),
+         (T * H + 2 * F * H + T * F) * E, 2.0 * T * 2 * F * H, "mfma", L),
         gemm_case("gemm_down_residual", T, H, F, False, False, L, residual=True),
         gemm_case("gemm_d_swiglu", T, F, H, False, True, L),
         gemm_case("gemm_dw_down", H, F, T, True, True, L),
@@ -252,54 +311,80 @@ def kernel_rooflines(device, only: str | None = None) -> list[dict]:
         gemm_case("gemm_dw_o", H, H, T, True, True, L),
         gemm_case("gemm_d_norm1", T, H, 3 * H, False, True, L),
         gemm_case("gemm_dw_qkv", 3 * H, H, T, True, True, L),
-        gemm_case("gemm_lm_logits", chunk_rows, V, H, False, False, 2 * T // chunk_rows),
-        gemm_case("gemm_lm_dx", chunk_rows, H, V, False, True, T // chunk_rows),
-        gemm_case("gemm_lm_dE", V, H, chunk_rows, True, True, T // chunk_rows, residual=True),
+        gemm_case("gemm_lm_logits", chunk, V, H, False, False, 2 * T // chunk),
+        gemm_case("gemm_lm_dx", chunk, H, V, False, True, T // chunk),
+        gemm_case("gemm_lm_dE", V, H, chunk, True, True, T // chunk, residual=True),
     ]
-    cases = [
-        # name, fn, algorithmic bytes, flops, bound, launches per training step (full recompute)
-        ("rmsnorm_fwd", lambda: Fn.rmsnorm_fwd(x, w, 1e-5), 2 * T * H * E + H * E, 0, "hbm", 4 * L + 1),
-        # in the block the norm backward also adds the residual branch's gradient
-        ("rmsnorm_bwd", lambda: Fn.rmsnorm_bwd(x, w, dy, 1e-5, residual_grad=dres), 4 * T * H * E + 2 * H * E, 0,
-         "hbm", 2 * L + 1),
+    hbm = [
+        # name, make, algorithmic bytes, launches per training step (full recompute)
+        ("rmsnorm_fwd", mk_rms_fwd, 2 * T * H * E + H * E, 4 * L + 1),
+        # in the block the norm backward also adds the residual branch's gradient;
+        # the launch includes the dw column sum
+        ("rmsnorm_bwd", mk_rms_bwd, 4 * T * H * E + 2 * H * E, 2 * L + 1),
         # the standalone rotary kernel; the step fuses RoPE into the QKV GEMM and the attention backward
-        ("rope_apply", lambda: Fn.rope_apply(q, rope_out, tab.cos, tab.sin), 2 * T * H * E, 0, "hbm", 0),
+        ("rope_apply", mk_rope, 2 * T * H * E, 0),
         # the standalone activation; the checkpointed step fuses it into the gate/up GEMM
-        ("swiglu_fwd", lambda: Fn.swiglu_fwd(gate, up, act), 3 * T * F * E, 0, "hbm", 0),
-        ("swiglu_bwd", lambda: Fn.swiglu_bwd(gate, up, dh, dgu[:, :F], dgu[:, F:], act), 6 * T * F * E, 0, "hbm", L),
-        ("attn_fwd", lambda: Fn.attn_fwd_bshd(q, [k], [v], (0,), causal=True, q_offset=0, scale=None, out=o, lse=lse),
+        ("swiglu_fwd", mk_swiglu_fwd, 3 * T * F * E, 0),
+        ("swiglu_bwd", mk_swiglu_bwd, 6 * T * F * E, L),
+        ("ce_fwd", mk_ce_fwd, chunk * V * E + chunk * 16, T // chunk),
+        ("ce_bwd", mk_ce_bwd, 2 * chunk * V * E + chunk * 16, T // chunk),
+        # token rows gathered and written; the backward reads the output gradient and the
+        # tied LM head's table gradient once and writes the table gradient once
+        ("embedding_fwd", mk_emb_fwd, 2 * T * H * E + T * 8, 1),
+        ("embedding_bwd", mk_emb_bwd, T * H * E + 2 * V * H * E + T * 8, 1),
+    ]
+    cases = [(name, make, nbytes, 0, "hbm", per) for name, make, nbytes, per in hbm]
+    cases += [
+        ("attn_fwd", lambda: Fn.attn_fwd_bshd(q, [k], [v], (0,), causal=True, q_offset=0, scale=None, out=o,
+                                              lse=lse),
          4 * T * H * E + BATCH * nh * SEQ * 4, causal_flops, "mfma", 2 * L),
-        ("attn_fwd_from_lse", lambda: Fn.attn_fwd_from_lse_bshd(q, [k], [v], (0,), lse, causal=True, q_offset=0, scale=None, out=o),
+        ("attn_fwd_from_lse", lambda: Fn.attn_fwd_from_lse_bshd(q, [k], [v], (0,), lse, causal=True, q_offset=0,
+                                                                scale=None, out=o),
          4 * T * H * E + BATCH * nh * SEQ * 4, causal_flops, "mfma", 0),
         # the backward with the inverse RoPE of dq and dk in its stores, as the block runs it
         ("attn_bwd_rope", lambda: Fn.attn_bwd_rope_bshd(q, k, v, o, do, lse, dq, dk, dv, causal=True, q_offset=0,
                                                         scale=None, cos=tab.cos, sin=tab.sin),
          8 * T * H * E + BATCH * nh * SEQ * 4, 2.5 * causal_flops, "mfma", L),
-        ("ce_fwd", lambda: Fn.ce_fwd(logits, targets, -100, loss, lse_c), chunk * V * E + chunk * 16, 0, "hbm", T // chunk),
-        ("ce_bwd", lambda: Fn.ce_bwd_(logits, targets, -100, lse_c, grad_c), 2 * chunk * V * E + chunk * 16, 0, "hbm", T // chunk),
     ] + gemms
-    if only is not None:
-        cases = [c_ for c_ in cases if c_[0] == only]
-        if not cases:
-            raise SystemExit(f"bench.py: no kernel named {only!r}")
+    names = [c_[0] for c_ in cases] + ["adamw_step"]
+    if only is not None and only not in names:
+        raise SystemExit(f"bench.py: no kernel named {only!r}")
     out = []
     side = torch.cuda.Stream(device)
+    stream = torch.cuda.current_stream(device)
+
+    def record(name, us, nbytes, flops, bound, per_step, sets):
+        gbs = nbytes / us / 1e3
+        entry = dict(kernel=name, us=round(us, 2), bytes=int(nbytes), gbs=round(gbs, 1),
+                     hbm_frac=round(gbs / HBM_PEAK_GBS, 3), bound=bound,
+                     us_per_step=round(us * per_step, 1), launches_per_step=per_step, input_sets=sets)
+        if flops:
+            tf = flops / us / 1e6
+            entry.update(flops=int(flops), tflops=round(tf, 1), mfma_frac=round(tf / BF16_PEAK_TFLOPS, 4))
+        out.append(entry)
+
     for name, fn, nbytes, flops, bound, per_step in cases:
-        # n launches captured in a HIP graph and replayed: the events then time
-        # GPU work only, not the host cost of issuing each launch.
-        n = 20
-        side.wait_stream(torch.cuda.current_stream(device))
+        if only is not None and name != only:
+            continue
+        sets = 1
+        fns = [fn]
+        if bound == "hbm":
+            sets = _input_sets(nbytes)
+            fns = [fn() for _ in range(sets)]
+        # launches captured in a HIP graph and replayed: the events then time GPU
+        # work only, not the host cost of issuing each launch
+        n = sets * max(1, math.ceil(20 / sets))
+        side.wait_stream(stream)
         with torch.cuda.stream(side):
-            for _ in range(3):
-                fn()
-        torch.cuda.current_stream(device).wait_stream(side)
+            for f in fns:
+                f()
+        stream.wait_stream(side)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            for _ in range(n):
-                fn()
+            for i in range(n):
+                fns[i % sets]()
         graph.replay()
         torch.cuda.synchronize()
-        stream = torch.cuda.current_stream(device)
         # three rounds of five replays; the best round's average per launch
         # (the clocks of a box vary between rounds by up to ~15%)
         reps, rounds = 5, 3
@@ -312,15 +397,36 @@ def kernel_rooflines(device, only: str | None = None) -> list[dict]:
             end.record(stream)
             end.synchronize()
             us = min(us, start.elapsed_time(end) * 1e3 / (n * reps))
-        del graph
-        gbs = nbytes / us / 1e3
-        entry = dict(kernel=name, us=round(us, 2), bytes=int(nbytes), gbs=round(gbs, 1),
-                     hbm_frac=round(gbs / HBM_PEAK_GBS, 3), bound=bound,
-                     us_per_step=round(us * per_step, 1), launches_per_step=per_step)
-        if flops:
-            tf = flops / us / 1e6
-            entry.update(flops=int(flops), tflops=round(tf, 1), mfma_frac=round(tf / BF16_PEAK_TFLOPS, 4))
-        out.append(entry)
+        del graph, fns
+        record(name, us, nbytes, flops, bound, per_step, sets)
+
+    if only is None or only == "adamw_step":
+        # the optimizer of the step: global grad-norm clip + fp32-master AdamW over the
+        # 310.8M parameters of config 3 in the model's tensor shapes (8.7 GB per launch,
+        # far beyond the cache); timed eagerly (each launch is ~1.7 ms)
+        shapes = [(V, H)] + [(H,), (3 * H, H), (H, H), (H,), (2 * F, H), (H, F)] * L + [(H,)]
+        params = [torch.nn.Parameter(randn(*sh, scale=0.02)) for sh in shapes]
+        for p_ in params:
+            p_.grad = randn(*p_.shape, scale=1e-3)
+        opt = MasterAdamW(params, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, clip_grad_norm=1.0)
+        n_el = sum(p_.numel() for p_ in params)
+        for _ in range(3):
+            opt.step()
+        torch.cuda.synchronize()
+        us = float("inf")
+        for _ in range(3):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            for _ in range(5):
+                opt.step()
+            end.record(stream)
+            end.synchronize()
+            us = min(us, start.elapsed_time(end) * 1e3 / 5)
+        # 28 B per parameter: bf16 grad read, bf16 param written, fp32 master and two
+        # moments read and written (the norm pass's second read of the grads not counted)
+        record("adamw_step", us, 28 * n_el, 0, "hbm", 1, 1)
+        del opt, params
+        torch.cuda.empty_cache()
     return out
 
 
@@ -394,10 +500,25 @@ def copy_calibration(device) -> None:
     torch.cuda.synchronize()
 
 
-def cpu_baseline() -> dict:
-    """The CPU oracle on a bounded sample of the config-3 step: 2 of the 24 layers
-    plus embedding/final norm/LM head/CE, one 512-token sequence, full recompute,
-    fp32 on the host cores; scaled to tokens/s of the 24-layer step."""
+def _host_cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(seconds: float = 25.0) -> dict:
+    """The repo's own CPU path (the oracle's PyTorch-CPU restatement of the
+    reference modules, fp32) running the full 24-layer config-3 training step
+    on one 512-token sequence: forward with per-layer recompute, backward,
+    global-norm clip and AdamW (torch.optim.AdamW, the reference's fp32 mode,
+    data_parallel/_common.py:242-252), timed with perf_counter after one
+    warm-up step; the median of at least three steps, or as many as fit in
+    ``seconds``.  Reported with the threads used and the implied FLOP rate."""
     import torch
 
     from oracle import reference as R
@@ -408,41 +529,47 @@ def cpu_baseline() -> dict:
         mode = "full"
         block_interval = 1
 
-    def time_layers(n_layers: int, reps: int) -> float:
-        cfg = dict(C3, layers=n_layers)
+    class Cfg:
+        pass
 
-        class Cfg:
-            pass
+    for k_, v_ in C3.items():
+        setattr(Cfg, k_, v_)
+    torch.manual_seed(0)
+    model = R.OracleGPTModel(Cfg(), activation_checkpoint_config=Ck()).train()
+    opt = torch.optim.AdamW(model.parameters(), lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+    g = torch.Generator().manual_seed(1234)
+    ids = torch.randint(0, C3["vocab_size"], (1, SEQ + 1), generator=g)
+    x, y = ids[:, :SEQ], ids[:, 1:]
 
-        for k_, v_ in cfg.items():
-            setattr(Cfg, k_, v_)
-        torch.manual_seed(0)
-        model = R.OracleGPTModel(Cfg(), activation_checkpoint_config=Ck()).train()
-        ids = torch.randint(0, C3["vocab_size"], (1, SEQ + 1))
-        x, y = ids[:, :SEQ], ids[:, 1:]
-        model(x, labels=y).loss.backward()  # warm-up
-        ts = []
-        for _ in range(reps):
-            model.zero_grad(set_to_none=True)
-            t0 = time.perf_counter()
-            model(x, labels=y).loss.backward()
-            ts.append(time.perf_counter() - t0)
-        ts.sort()
-        return ts[len(ts) // 2]
+    def step() -> float:
+        t0 = time.perf_counter()
+        opt.zero_grad(set_to_none=True)
+        model(x, labels=y).loss.backward()
+        torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0)
+        opt.step()
+        return time.perf_counter() - t0
 
-    t1 = time_layers(1, 3)
-    t2 = time_layers(2, 3)
-    per_layer = max(t2 - t1, 1e-9)
-    base = max(t1 - per_layer, 0.0)
-    t_step = base + C3["layers"] * per_layer
+    warm = step()
+    times = []
+    while len(times) < 3 or (sum(times) + warm < seconds and len(times) < 9):
+        times.append(step())
+    times.sort()
+    t_step = times[len(times) // 2]
+    flops = model_step_flops(C3, 1, SEQ, recompute=True)
+    del model, opt
     return dict(
         value=round(SEQ / t_step, 1),
         unit="tokens/s",
         cores=threads,
         kind="port",
-        sample=(f"CPU oracle (PyTorch fp32, {threads} threads), one 512-token sequence, 1- and "
-                f"2-layer models with full recompute; per-layer time {per_layer:.3f} s "
-                f"extrapolated to 24 layers + head ({t_step:.2f} s per 512 tokens)"),
+        sample=(f"CPU oracle (PyTorch fp32, {threads} threads on {_host_cpu_model()}): the full 24-layer "
+                f"config-3 step (forward with per-layer recompute, backward, clip, AdamW) on one "
+                f"512-token sequence, median of {len(times)} steps after one warm-up: "
+                f"{t_step:.2f} s per step ({min(times):.2f}-{max(times):.2f} s), "
+                f"{flops / t_step / 1e9:.0f} GFLOP/s implied"),
+        step_s=round(t_step, 3),
+        steps_timed=len(times),
+        implied_gflops=round(flops / t_step / 1e9, 1),
     )
 
 
@@ -463,40 +590,39 @@ def model_step_flops(cfg: dict, batch: int, seq: int, recompute: bool) -> float:
     return total
 
 
-def run_c4(args, device) -> None:
+def c4_leg(args, device, eager: bool = True) -> dict:
+    """Config 4: the GQA step, full recompute and none."""
     full = run_steps("full", args.steps, args.warmup, device, None, C4, C4_BATCH, C4_SEQ)
-    print("full: " + json.dumps(full), file=sys.stderr, flush=True)
-    eager = run_steps("none", args.steps, args.warmup, device, None, C4, C4_BATCH, C4_SEQ) if not args.no_eager else None
+    print("c4 full: " + json.dumps(full), file=sys.stderr, flush=True)
     fl = model_step_flops(C4, C4_BATCH, C4_SEQ, recompute=True)
     tf = fl / (full["ms_per_step"] * 1e-3) / 1e12
-    line = dict(
-        metric="train tokens/s, GQA 32q/8kv seq2048 full recompute, 1 MI355X",
-        value=round(full["tokens_per_s"], 1), unit="tokens/s", n_gpus=1, steps=args.steps,
-        warmup=args.warmup, ms_per_step=round(full["ms_per_step"], 3), higher_is_better=True,
-        scaling="weak", vs_baseline=None, dtype="bf16", data="synthetic",
-        config=dict(workload="C4: GQA GPT (16L, H2048, 32 query / 8 KV heads D64, ffn 5632, vocab 8192 "
-                             "tied) training step, full per-layer recompute, bf16 + fp32-master AdamW",
-                    global_batch=C4_BATCH, seq_len=C4_SEQ, parallelism="single GPU"),
+    leg = dict(
+        workload="C4: GQA GPT (16L, H2048, 32 query / 8 KV heads D64, ffn 5632, vocab 8192 tied) training "
+                 "step, B4 x S2048, full per-layer recompute, bf16 + fp32-master AdamW",
+        tokens_per_s=round(full["tokens_per_s"], 1), ms_per_step=round(full["ms_per_step"], 3),
         model_tflops=round(tf, 1), mfma_frac=round(tf / BF16_PEAK_TFLOPS, 4),
         peak_act_gib_per_layer=round(full["peak_act_gib_per_layer"], 4),
         # one block's saved activation (2-layer minus 1-layer model); the
         # whole-model figure spreads the head's saved state over the layers
         saved_act_mib_per_layer=round(block_saved_mib("full", device, C4, C4_BATCH, C4_SEQ), 2),
-        act_floor_mib_per_layer=33.0,
+        act_floor_mib_per_layer=32.0,
         saved_act_mib_whole_model_per_layer=round(full["saved_act_mib_per_layer"], 2),
+        loss=round(full["loss"], 4),
     )
     if eager:
-        line["no_checkpoint_tokens_per_s"] = round(eager["tokens_per_s"], 1)
-        line["recompute_overhead"] = round(full["ms_per_step"] / eager["ms_per_step"] - 1.0, 4)
-    print(json.dumps(line), flush=True)
+        none = run_steps("none", args.steps, args.warmup, device, None, C4, C4_BATCH, C4_SEQ)
+        print("c4 none: " + json.dumps(none), file=sys.stderr, flush=True)
+        leg["no_checkpoint_tokens_per_s"] = round(none["tokens_per_s"], 1)
+        leg["recompute_overhead"] = round(full["ms_per_step"] / none["ms_per_step"] - 1.0, 4)
+    return leg
 
 
-def run_c5(args, device) -> None:
-    """One ring rank's attention share: rank 3 of 4 (queries 24576..32767) over the
-    four K/V blocks in ring order 3, 2, 1, 0 (context_parallel/ring.py:104-250),
-    causal by absolute position, forward then backward (P recomputed from the
-    LSE); FLOPs count the visible (causally unmasked) scores only, backward 2.5x
-    the forward."""
+def c5_leg(args, device) -> dict:
+    """One ring rank's attention share: rank 3 of 4
+    (queries 24576..32767) over the four K/V blocks in ring order 3, 2, 1, 0
+    (context_parallel/ring.py:104-250), causal by absolute position, forward
+    then backward (P recomputed from the LSE); FLOPs count the visible
+    (causally unmasked) scores only, backward 2.5x the forward."""
     import torch
 
     from nano_megatron_amd import functional as Fn
@@ -527,11 +653,12 @@ def run_c5(args, device) -> None:
         for _ in range(max(args.warmup, 1)):
             fn()
         torch.cuda.synchronize()
+        stream = torch.cuda.current_stream(device)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
+        e0.record(stream)
         for _ in range(n):
             fn()
-        e1.record()
+        e1.record(stream)
         e1.synchronize()
         return e0.elapsed_time(e1) / n  # ms
 
@@ -541,18 +668,42 @@ def run_c5(args, device) -> None:
     t_f, t_b = timed(fwd, args.steps), timed(bwd, args.steps)
     tf_f, tf_b = fwd_flops / t_f / 1e9, bwd_flops / t_b / 1e9
     total = (fwd_flops + bwd_flops) / (t_f + t_b) / 1e9
-    line = dict(
-        metric="ring-share attention fwd+bwd TFLOP/s, 8192 queries x 4 K/V blocks, D128, 1 MI355X",
-        value=round(total, 1), unit="TFLOP/s", n_gpus=1, steps=args.steps, warmup=args.warmup,
-        ms_per_step=round(t_f + t_b, 3), higher_is_better=True, scaling="weak", vs_baseline=None,
-        dtype="bf16", data="synthetic",
-        config=dict(workload="C5: rank 3 of a 4-way ring, local Q [1, 8192, 16, 128], K/V blocks "
-                             "visited 3, 2, 1, 0, causal by absolute position", global_batch=1,
-                    seq_len=s, parallelism="single GPU (one ring rank's share)"),
+    del q, ks, vs, do, dq, dks, dvs, o, lse
+    torch.cuda.empty_cache()
+    return dict(
+        workload="C5: rank 3 of a 4-way ring, local Q [1, 8192, 16, 128] bf16, K/V blocks visited 3, 2, 1, 0, "
+                 "causal by absolute position, forward + backward",
+        tflops=round(total, 1), mfma_frac=round(total / BF16_PEAK_TFLOPS, 4), ms=round(t_f + t_b, 3),
         fwd_ms=round(t_f, 3), bwd_ms=round(t_b, 3), fwd_tflops=round(tf_f, 1), bwd_tflops=round(tf_b, 1),
         fwd_gflop=round(fwd_flops / 1e9, 1), bwd_gflop=round(bwd_flops / 1e9, 1),
-        roofline=dict(bound="mfma", achieved=round(total, 1), peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
-                      frac=round(total / BF16_PEAK_TFLOPS, 4), traffic=None, kernel="attn_fwd + attn_bwd"),
+    )
+
+
+def run_c4(args, device) -> None:
+    leg = c4_leg(args, device, eager=not args.no_eager)
+    line = dict(
+        metric="train tokens/s, GQA 32q/8kv seq2048 full recompute, 1 MI355X",
+        value=leg["tokens_per_s"], unit="tokens/s", n_gpus=1, steps=args.steps,
+        warmup=args.warmup, ms_per_step=leg["ms_per_step"], higher_is_better=True,
+        scaling="weak", vs_baseline=None, dtype="bf16", data="synthetic",
+        config=dict(workload=leg["workload"], global_batch=C4_BATCH, seq_len=C4_SEQ, parallelism="single GPU"),
+        **{k: v for k, v in leg.items() if k not in ("workload", "tokens_per_s", "ms_per_step")},
+    )
+    print(json.dumps(line), flush=True)
+
+
+def run_c5(args, device) -> None:
+    leg = c5_leg(args, device)
+    line = dict(
+        metric="ring-share attention fwd+bwd TFLOP/s, 8192 queries x 4 K/V blocks, D128, 1 MI355X",
+        value=leg["tflops"], unit="TFLOP/s", n_gpus=1, steps=args.steps, warmup=args.warmup,
+        ms_per_step=leg["ms"], higher_is_better=True, scaling="weak", vs_baseline=None,
+        dtype="bf16", data="synthetic",
+        config=dict(workload=leg["workload"], global_batch=1, seq_len=8192,
+                    parallelism="single GPU (one ring rank's share)"),
+        roofline=dict(bound="mfma", achieved=leg["tflops"], peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
+                      frac=leg["mfma_frac"], traffic=None, kernel="attn_fwd + attn_bwd"),
+        **{k: v for k, v in leg.items() if k not in ("workload", "tflops", "mfma_frac", "ms")},
     )
     print(json.dumps(line), flush=True)
 
@@ -598,6 +749,12 @@ def main() -> None:
         eager = run_steps("none", args.steps, args.warmup, device)
         print("none: " + json.dumps(eager), file=sys.stderr, flush=True)
 
+    c4 = c5 = None
+    if not args.no_legs:
+        c4 = c4_leg(args, device, eager=not args.no_eager)
+        c5 = c5_leg(args, device)
+        print("c4: " + json.dumps(c4) + "\nc5: " + json.dumps(c5), file=sys.stderr, flush=True)
+
     roofline = None
     if kernels:
         # the kernel with the most time per training step
@@ -635,7 +792,7 @@ def main() -> None:
         # one block's saved activation (2-layer minus 1-layer model); the
         # whole-model figure spreads the head's saved state over the layers
         saved_act_mib_per_layer=round(block_saved_mib("full", device), 2),
-        act_floor_mib_per_layer=16.5,
+        act_floor_mib_per_layer=16.0,
         saved_act_mib_whole_model_per_layer=round(full["saved_act_mib_per_layer"], 2),
         model_tflops=round(model_step_flops(C3, BATCH, SEQ, recompute=True) / (full["ms_per_step"] * 1e-3) / 1e12, 1),
         loss=round(full["loss"], 4),
@@ -643,6 +800,8 @@ def main() -> None:
         cpu_baseline=cpu,
         ceilings=ceilings,
         kernels=kernels,
+        c4=c4,
+        c5=c5,
     )
     if eager:
         line["no_checkpoint_tokens_per_s"] = round(eager["tokens_per_s"], 1)

@@ -168,7 +168,9 @@ int nmb_attn_bwd_rope(const void* q, const void* k, const void* v, const void* o
  * replaces VocabParallelEmbedding.forward at TP=1 (tensor_parallel/
  * embedding.py:60-74, F.embedding) and its backward.
  * table / out / dout / grads: row-major [vocab, hidden] and [n_tokens, hidden]
- * of dtype; ids: int64 [n_tokens].  An id outside [0, vocab) gives a NaN row.
+ * of dtype; ids: int64 [n_tokens].  An id outside [0, vocab) gives a zero row
+ * and contributes nothing to the table gradient (the reference masks ids
+ * outside its partition to zero rows, tensor_parallel/embedding.py:63-68).
  * Backward: grad_out = grad_in + sum over tokens of dout rows (fp32 sums in
  * token order, rounded to dtype, then added to grad_in, as autograd adds the
  * tied LM head's gradient: models/gpt/model.py:125-142); grad_in may be null

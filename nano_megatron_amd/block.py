@@ -13,12 +13,15 @@ models/gpt/layer.py:91-137):
 
 ``CheckpointedBlockFunction`` is the full-recompute policy of
 ``activation_checkpoint`` (nn/activation_checkpoint.py:73-100, selected by
-models/gpt/model.py:162-170, 215-233): it saves only the block input x and
-the attention lse.  Its backward re-runs the sequence above with the same
-kernels and shapes (so the recomputed tensors are bit-identical to the
-forward's), except that the gate/up GEMM writes the product [g|u] instead of
-s (same plan, same bits), and never re-runs the down projection, whose output
-the backward does not need; ``nmb_swiglu_bwd`` re-emits s for the Wd gradient.
+models/gpt/model.py:162-170, 215-233): it saves only the block input x.  Its
+backward re-runs the sequence above with the same kernels and shapes (so the
+recomputed tensors, the attention output and its lse included, are
+bit-identical to the forward's), except that the gate/up GEMM writes the
+product [g|u] instead of s (same plan, same bits), and never re-runs the down
+projection, whose output the backward does not need; ``nmb_swiglu_bwd``
+re-emits s for the Wd gradient.  With ``offload`` the saved input goes to
+pinned host memory (the reference's saved-tensor offload,
+nn/activation_checkpoint.py:24-41); the weights are parameters, never copied.
 ``EagerBlockFunction`` (activation_checkpoint.mode = "none") keeps the
 intermediates instead and shares the backward.
 """
@@ -40,10 +43,15 @@ class BlockMeta:
     kv_heads: int
     head_dim: int
     eps: float
-    sequence_offset: int
+    sequence_offset: int  # query offset of the causal mask (models/gpt/attention.py:199-206)
     cos: Tensor          # fp32 [n_pos, head_dim/2]
     sin: Tensor
-    positions: Tensor | None  # int32 [S] or [B,S], or None for offset + arange
+    positions: Tensor | None  # int32 [S] or [B,S], or None for rope_offset + arange
+    rope_offset: int | None = None  # RoPE position of token 0 without positions (default: sequence_offset)
+
+    @property
+    def pos_offset(self) -> int:
+        return self.sequence_offset if self.rope_offset is None else self.rope_offset
 
 
 def _adjacent(ws: tuple[Tensor, ...]) -> bool:
@@ -107,7 +115,7 @@ def block_forward(x: Tensor, w: tuple[Tensor, ...], m: BlockMeta, *, recompute: 
     # Q/K/V projection with RoPE of q and k as the GEMM epilogue
     qkv = Fn.mm_rope(n1, joined((wq, wk, wv)).t(), seq=s, head_dim=m.head_dim,
                      rope_cols=(m.heads + m.kv_heads) * m.head_dim, cos=m.cos, sin=m.sin,
-                     pos_offset=m.sequence_offset, positions=m.positions)
+                     pos_offset=m.pos_offset, positions=m.positions)
     q, k, v = _qkv_views(qkv, b, s, m)
     o, lse = Fn.attn_fwd_bshd(q, [k], [v], (0,), causal=True, q_offset=m.sequence_offset, scale=None)
     o2 = o.view(b * s, m.heads * m.head_dim)
@@ -200,7 +208,7 @@ def block_backward(acts: dict, dy: Tensor, w: tuple[Tensor, ...], m: BlockMeta, 
     do4 = do2.view(b, s, m.heads, m.head_dim)
     # attention backward with the RoPE backward of q and k fused into the dq/dk stores
     Fn.attn_bwd_rope_bshd(q, k, v, o4, do4, lse, dq, dk, dv, causal=True, q_offset=m.sequence_offset,
-                          scale=None, cos=m.cos, sin=m.sin, pos_offset=m.sequence_offset,
+                          scale=None, cos=m.cos, sin=m.sin, pos_offset=m.pos_offset,
                           positions=m.positions)
     dn1 = Fn.mm(dqkv, joined((wq, wk, wv)))
     dwqkv = side.mm(dqkv.t(), n1)
@@ -217,25 +225,42 @@ def block_backward(acts: dict, dy: Tensor, w: tuple[Tensor, ...], m: BlockMeta, 
 
 
 class CheckpointedBlockFunction(torch.autograd.Function):
-    """Full per-layer recompute: saves x (the block input) and the lse only."""
+    """Full per-layer recompute: saves x (the block input) only; with
+    ``offload`` x waits for the backward in pinned host memory."""
 
     @staticmethod
-    def forward(ctx: Any, x: Tensor, meta: BlockMeta, *weights: Tensor) -> Tensor:
+    def forward(ctx: Any, x: Tensor, meta: BlockMeta, offload: bool, *weights: Tensor) -> Tensor:
+        x = x.contiguous()
         with torch.no_grad():
-            acts = block_forward(x.contiguous(), weights, meta, recompute=False, keep_gu=False)
+            acts = block_forward(x, weights, meta, recompute=False, keep_gu=False)
         ctx.meta = meta
         ctx.shape = tuple(x.shape)
-        ctx.save_for_backward(x, acts["lse"], *weights)
+        ctx.offloaded = None
+        if offload:
+            # enqueued after the block's kernels on the same stream, which read x first
+            host = torch.empty(x.shape, dtype=x.dtype, pin_memory=True)
+            host.copy_(x, non_blocking=True)
+            ctx.offloaded = (host, x.device)
+            ctx.save_for_backward(*weights)
+        else:
+            ctx.save_for_backward(x, *weights)
         return acts["y"]
 
     @staticmethod
     def backward(ctx: Any, dy: Tensor):
-        x, lse, *weights = ctx.saved_tensors
+        saved = ctx.saved_tensors
+        if ctx.offloaded is not None:
+            host, device = ctx.offloaded
+            x, weights = host.to(device, non_blocking=True), saved
+            ctx.offloaded = None
+        else:
+            x, weights = saved[0], saved[1:]
         with torch.no_grad():
-            acts = block_forward(x.contiguous(), tuple(weights), ctx.meta, recompute=True)
-            acts["lse"] = lse
+            # the recompute re-runs the forward's attention kernel: o and lse come
+            # out bit-identical to the forward's, so the lse needs no saving
+            acts = block_forward(x, tuple(weights), ctx.meta, recompute=True)
             grads = block_backward(acts, dy, tuple(weights), ctx.meta, ctx.shape)
-        return (grads[0], None, *grads[1:])
+        return (grads[0], None, None, *grads[1:])
 
 
 class EagerBlockFunction(torch.autograd.Function):

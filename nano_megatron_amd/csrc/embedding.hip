@@ -3,7 +3,8 @@
 // Follows VocabParallelEmbedding.forward at TP=1 (reference
 // tensor_parallel/embedding.py:60-74: F.embedding, a row gather of the [V, H]
 // table) and its backward, the scatter-add of the output gradient rows into
-// the table gradient.  The table is tied to the LM head (models/gpt/model.py:
+// the table gradient.  An id outside [0, V) yields a zero row and adds nothing
+// to the table gradient (embedding.py:63-68 masks ids outside the partition).  The table is tied to the LM head (models/gpt/model.py:
 // 125-142), so the backward can take the LM head's table gradient and return
 // the sum, in the order autograd accumulates them: bf16(lm + bf16(rows)).
 //
@@ -40,9 +41,11 @@ __global__ __launch_bounds__(256) void embedding_fwd_kernel(const T* __restrict_
     if (id >= 0 && id < vocab) {
       load_vec<T>(table + id * hidden + c, v);
     } else {
-      // an id outside the table is a caller error: poison the row, read nothing
+      // an id outside the table's [0, vocab) gives a zero row and reads
+      // nothing, as the reference masks ids outside its partition
+      // (tensor_parallel/embedding.py:63-68; at TP=1 the partition is the table)
 #pragma unroll
-      for (int e = 0; e < V; ++e) v[e] = __builtin_nanf("");
+      for (int e = 0; e < V; ++e) v[e] = 0.f;
     }
     store_vec<T>(out + t * hidden + c, v);
   }

@@ -765,8 +765,9 @@ class EmbeddingFunction(torch.autograd.Function):
 
 
 def embedding(weight: Tensor, ids: Tensor, tie: TiedGrad | None = None) -> Tensor:
-    """``F.embedding(ids, weight)`` on the GPU kernels (an id outside the table
-    yields a NaN row)."""
+    """VocabParallelEmbedding's lookup at TP=1 on the GPU kernels
+    (tensor_parallel/embedding.py:60-68): ``F.embedding(ids, weight)`` for ids in
+    [0, V); an id outside the table gives a zero row and no table gradient."""
     if ids.dtype not in (torch.int32, torch.int64):
         raise TypeError(f"input_ids must be an integer tensor, got {ids.dtype}")
     return EmbeddingFunction.apply(weight, ids.to(torch.int64).contiguous(), tie)

@@ -12,8 +12,9 @@ reference's collectives are identities there).  ``GPTModel.forward`` runs each
 standard layer as one fused block Function:
 
 * ``activation_checkpoint.mode == "full"`` and ``layer_index % block_interval
-  == 0`` -> ``CheckpointedBlockFunction`` (saves the block input and the
-  attention lse; recomputes the rest inside backward);
+  == 0`` -> ``CheckpointedBlockFunction`` (saves the block input only, in
+  pinned host memory under ``offload_saved_tensors``; recomputes the rest
+  inside backward);
 * otherwise -> ``EagerBlockFunction`` (same kernels, intermediates kept).
 
 ``"selective"`` runs the layer module by module with the chosen sub-blocks
@@ -41,7 +42,7 @@ from nano_megatron_amd.block import (
     pack_adjacent,
 )
 from nano_megatron_amd.kernels import HipKernelBackend, KernelBackend
-from nano_megatron_amd.nn import RotaryEmbedding, _offload_context, activation_checkpoint
+from nano_megatron_amd.nn import RotaryEmbedding, activation_checkpoint
 
 _MISSING = object()
 
@@ -291,20 +292,51 @@ class GPTAttention(nn.Module):
         return output
 
 
-def _rope_inputs(rope: RotaryEmbedding, device: torch.device, sequence: int,
-                 position_ids: Tensor | None, sequence_offset: int):
-    """(tables, int32 positions or None, offset) for the RoPE kernel.
+@dataclass(frozen=True)
+class PositionPlan:
+    """RoPE positions of one forward, worked out once for all its layers:
+    ``positions`` (int32 [S] or [B, S]) or None for ``offset + arange(S)``, and
+    the number of table rows they need; ``first`` is the first position, the
+    causal mask's query offset (models/gpt/model.py:199-200)."""
 
-    Default positions arange(offset, offset + S) use the offset form (no
-    position tensor); explicit ids are passed through (one host sync sizes the
-    table)."""
+    positions: Tensor | None
+    offset: int
+    n_pos: int
+    first: int
+
+
+def position_plan(device: torch.device, sequence: int, position_ids: Tensor | None,
+                  sequence_offset: int) -> PositionPlan:
+    """Default positions arange(offset, offset + S) (models/gpt/model.py:193-198)
+    use the offset form (no position tensor), as does a 1-D ``position_ids``
+    equal to such a range.  Other ids pass through as an int32 tensor; one host
+    read validates and sizes them.  The RoPE tables are indexed by position,
+    so a negative position is a ValueError (the reference's rotary embedding
+    would accept it, nn/rotary.py:55-70)."""
     if position_ids is None:
-        return rope.tables(device, sequence_offset + sequence), None, int(sequence_offset)
+        offset = int(sequence_offset)
+        if offset < 0:
+            raise ValueError(f"sequence_offset must be non-negative, got {offset}")
+        return PositionPlan(None, offset, offset + sequence, offset)
     if position_ids.ndim not in (1, 2) or position_ids.shape[-1] != sequence:
         raise ValueError("position_ids sequence length must match the gathered sequence")
+    host = position_ids.detach().to("cpu", torch.int64)
+    if host.numel() == 0:
+        return PositionPlan(None, 0, 1, 0)
+    if int(host.min()) < 0:
+        raise ValueError("position_ids must be non-negative (the RoPE tables are indexed by position)")
+    first = int(host.reshape(-1)[0])
+    if host.ndim == 1 and torch.equal(host, torch.arange(first, first + sequence)):
+        return PositionPlan(None, first, first + sequence, first)
     pos = position_ids.to(device=device, dtype=torch.int32).contiguous()
-    n_pos = int(pos.max().item()) + 1 if pos.numel() else 1
-    return rope.tables(device, n_pos), pos, 0
+    return PositionPlan(pos, 0, int(host.max()) + 1, first)
+
+
+def _rope_inputs(rope: RotaryEmbedding, device: torch.device, sequence: int,
+                 position_ids: Tensor | None, sequence_offset: int):
+    """(tables, int32 positions or None, offset) for the RoPE kernel."""
+    plan = position_plan(device, sequence, position_ids, sequence_offset)
+    return rope.tables(device, plan.n_pos), plan.positions, plan.offset
 
 
 class GPTMLP(nn.Module):
@@ -399,14 +431,16 @@ class GPTLayer(nn.Module):
             m.up_proj.weight, m.down_proj.weight,
         )
 
-    def block_meta(self, device: torch.device, sequence: int, position_ids: Tensor | None,
-                   sequence_offset: int) -> BlockMeta:
+    def block_meta(self, device: torch.device, plan: PositionPlan, sequence_offset: int) -> BlockMeta:
+        """The fused block's parameters: ``sequence_offset`` is the causal mask's
+        query offset (the reference passes position_ids[0], models/gpt/model.py:
+        199-200), ``plan`` the RoPE positions."""
         a = self.attention
-        tab, positions, offset = _rope_inputs(a.rope, device, sequence, position_ids, sequence_offset)
+        tab = a.rope.tables(device, plan.n_pos)
         return BlockMeta(
             heads=a.num_heads, kv_heads=a.num_kv_heads, head_dim=a.head_dim,
-            eps=float(self.input_norm.eps), sequence_offset=offset, cos=tab.cos, sin=tab.sin,
-            positions=positions,
+            eps=float(self.input_norm.eps), sequence_offset=int(sequence_offset), cos=tab.cos,
+            sin=tab.sin, positions=plan.positions, rope_offset=plan.offset,
         )
 
     # -- module path (reference semantics, used by selective checkpointing)
@@ -549,12 +583,11 @@ class GPTModel(nn.Module):
             raise ValueError("a non-first pipeline stage requires hidden_states")
         Fn._require_gpu(hidden_states)
         sequence = hidden_states.shape[1]
-        offset = 0
-        if position_ids is not None:
-            offset = int(position_ids.reshape(-1)[0].item())
-            if torch.equal(position_ids.reshape(-1)[:sequence].cpu(),
-                           torch.arange(offset, offset + sequence)) and position_ids.ndim == 1:
-                position_ids = None  # the default arange: offset form, no position tensor
+        # positions and the causal offset once per forward (models/gpt/model.py:193-200)
+        plan = position_plan(hidden_states.device, sequence, position_ids, 0)
+        offset = plan.first
+        if plan.positions is None:
+            position_ids = None  # the offset form: the module path builds the same range
 
         self._pack_block_weights()
         mode = getattr(self.activation_checkpoint_config, "mode", "none")
@@ -567,14 +600,9 @@ class GPTModel(nn.Module):
                         "the fused block computes in the parameter dtype: parameters "
                         f"{weights[1].dtype} vs activations {hidden_states.dtype}"
                     )
-                meta = layer.block_meta(hidden_states.device, sequence, position_ids, offset)
+                meta = layer.block_meta(hidden_states.device, plan, offset)
                 if self._checkpoint_layer(layer):
-                    ctx = _offload_context(pin_memory=True, non_blocking=True) if offload else None
-                    if ctx is None:
-                        hidden_states = CheckpointedBlockFunction.apply(hidden_states, meta, *weights)
-                    else:
-                        with ctx:
-                            hidden_states = CheckpointedBlockFunction.apply(hidden_states, meta, *weights)
+                    hidden_states = CheckpointedBlockFunction.apply(hidden_states, meta, offload, *weights)
                 else:
                     hidden_states = EagerBlockFunction.apply(hidden_states, meta, *weights)
             else:

@@ -424,6 +424,20 @@ class GPTOutput:
     hidden_states: Tensor
 
 
+def embedding_lookup(input_ids: Tensor, weight: Tensor) -> Tensor:
+    """``VocabParallelEmbedding.forward`` at TP=1 (tensor_parallel/embedding.py:60-68).
+
+    The partition is the whole table [0, V): ids outside it are replaced by 0
+    for the gather and their rows masked to zero afterwards, so they read
+    nothing and pass no gradient to the table.
+    """
+    if input_ids.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"input_ids must be an integer tensor, got {input_ids.dtype}")
+    outside = (input_ids < 0) | (input_ids >= weight.shape[0])
+    local_ids = input_ids.masked_fill(outside, 0)
+    return F.embedding(local_ids, weight).masked_fill(outside.unsqueeze(-1), 0.0)
+
+
 class _Embedding(nn.Module):
     """VocabParallelEmbedding at TP=1 (tensor_parallel/embedding.py:22-75): N(0, init_std)."""
 
@@ -433,9 +447,7 @@ class _Embedding(nn.Module):
         nn.init.normal_(self.weight, mean=0.0, std=init_std)
 
     def forward(self, input_ids: Tensor) -> Tensor:
-        if input_ids.dtype not in (torch.int32, torch.int64):
-            raise TypeError(f"input_ids must be an integer tensor, got {input_ids.dtype}")
-        return F.embedding(input_ids, self.weight)
+        return embedding_lookup(input_ids, self.weight)
 
 
 class _LMHead(nn.Module):
@@ -493,20 +505,28 @@ class OracleGPTModel(nn.Module):
             raise ValueError("activation checkpoint block_interval must be positive")
         return layer.layer_index % interval == 0
 
-    def forward(self, input_ids: Tensor, *, labels: Tensor | None = None) -> GPTOutput:
+    def forward(self, input_ids: Tensor, *, labels: Tensor | None = None,
+                position_ids: Tensor | None = None) -> GPTOutput:
+        """model.py:171-250 at CP=TP=1: default positions arange(S) with offset 0,
+        else the given ids with offset position_ids[0] (:193-200), passed to every
+        layer as RoPE positions and the causal mask's query offset."""
         hidden = self.embedding(input_ids)
         seq = input_ids.shape[1]
-        position_ids = torch.arange(0, seq)
+        if position_ids is None:
+            offset = 0
+            position_ids = torch.arange(0, seq)
+        else:
+            offset = int(position_ids.reshape(-1)[0].item())
         for layer in self.layers:
             if self._checkpoint_layer(layer):
                 hidden = torch_checkpoint(
-                    lambda x, cur=layer: cur(x, position_ids=position_ids, sequence_offset=0),
+                    lambda x, cur=layer: cur(x, position_ids=position_ids, sequence_offset=offset),
                     hidden,
                     use_reentrant=False,
                     preserve_rng_state=True,
                 )
             else:
-                hidden = layer(hidden, position_ids=position_ids, sequence_offset=0)
+                hidden = layer(hidden, position_ids=position_ids, sequence_offset=offset)
         hidden = self.final_norm(hidden)
         logits = self.lm_head(hidden)
         loss = None

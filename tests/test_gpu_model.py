@@ -121,14 +121,18 @@ def test_full_recompute_grads_bit_identical_to_eager(device) -> None:
     x, w, meta = _block_inputs(device)
     dy = torch.randn_like(x)
     results = []
-    for fn in (B.CheckpointedBlockFunction, B.EagerBlockFunction):
+    for fn in (B.CheckpointedBlockFunction, B.EagerBlockFunction, "offload"):
         xs = x.clone().requires_grad_(True)
         ws = [t.clone().requires_grad_(True) for t in w]
-        y = fn.apply(xs, meta, *ws)
+        if fn is B.EagerBlockFunction:
+            y = fn.apply(xs, meta, *ws)
+        else:
+            y = B.CheckpointedBlockFunction.apply(xs, meta, fn == "offload", *ws)
         y.backward(dy)
         results.append((y.detach(), xs.grad, *[t.grad for t in ws]))
-    for a, b in zip(*results):
-        assert torch.equal(a, b)
+    for other in results[1:]:
+        for a, b in zip(results[0], other):
+            assert torch.equal(a, b)
 
 
 def test_model_rejects_out_of_range_labels(device) -> None:
@@ -157,33 +161,167 @@ def test_block_grads_accumulate_over_two_backward_passes(device) -> None:
     single = []
     for dy in dys:
         ws = [t.clone().requires_grad_(True) for t in w]
-        B.CheckpointedBlockFunction.apply(x, meta, *ws).backward(dy)
+        B.CheckpointedBlockFunction.apply(x, meta, False, *ws).backward(dy)
         single.append([t.grad.clone() for t in ws])
     ws = [t.clone().requires_grad_(True) for t in w]
     for dy in dys:
-        B.CheckpointedBlockFunction.apply(x, meta, *ws).backward(dy)
+        B.CheckpointedBlockFunction.apply(x, meta, False, *ws).backward(dy)
     for t, g1, g2 in zip(ws, *single):
         assert torch.equal(t.grad, g1 + g2)
 
 
-def test_full_recompute_keeps_only_block_input_and_lse(device) -> None:
-    """Peak activation memory per checkpointed layer is the bf16 input plus the lse."""
-    cfg = nm.GPTConfig(layers=4, hidden_size=512, ffn_hidden_size=1376, heads=8, seq_length=256,
-                       vocab_size=4096)
-    ids = torch.randint(0, 4096, (4, 256), device=device)
-    saved = {}
-    for mode in ("full", "none"):
-        model = nm.GPTModel(cfg, activation_checkpoint_config=nm.ActivationCheckpointConfig(mode=mode))
-        model = model.to(device=device, dtype=torch.bfloat16).train()
+def _block_saved_bytes(device, cfg, ids, ck) -> int:
+    """Device memory one block leaves saved after the forward: a 2-layer minus a
+    1-layer model's (embedding, final norm and LM-head state cancel)."""
+    saved = []
+    for layers in (1, 2):
+        c = nm.GPTConfig(**{**cfg, "layers": layers})
+        torch.manual_seed(0)
+        model = nm.GPTModel(c, activation_checkpoint_config=ck).to(device=device, dtype=torch.bfloat16).train()
+        model(ids, labels=ids)  # packs the block weights (new storage, old freed)
         torch.cuda.synchronize()
         base = torch.cuda.memory_allocated()
         out = model(ids, labels=ids)
         torch.cuda.synchronize()
-        saved[mode] = torch.cuda.memory_allocated() - base
+        saved.append(torch.cuda.memory_allocated() - base)
         out.loss.backward()
         del out, model
         torch.cuda.empty_cache()
-    per_layer_floor = 4 * 256 * 512 * 2 + 4 * 8 * 256 * 4
-    # embedding output + final norm + lse/CE state are outside the layers
-    assert saved["full"] <= 4 * per_layer_floor + 8 * 4 * 256 * 512 * 2, saved
-    assert saved["none"] > 3 * saved["full"], saved
+    return saved[1] - saved[0]
+
+
+def test_full_recompute_keeps_only_block_input(device) -> None:
+    """A checkpointed block keeps exactly its bf16 input on the device; with
+    offload_saved_tensors it keeps nothing there (the input waits in pinned host
+    memory, the weights are never copied); without checkpointing it keeps every
+    intermediate."""
+    cfg = dict(hidden_size=512, ffn_hidden_size=1376, heads=8, seq_length=256, vocab_size=4096)
+    ids = torch.randint(0, 4096, (4, 256), device=device)
+    x_bytes = 4 * 256 * 512 * 2
+    full = _block_saved_bytes(device, cfg, ids, nm.ActivationCheckpointConfig(mode="full"))
+    off = _block_saved_bytes(device, cfg, ids, nm.ActivationCheckpointConfig(mode="full", offload_saved_tensors=True))
+    none = _block_saved_bytes(device, cfg, ids, nm.ActivationCheckpointConfig(mode="none"))
+    assert full == x_bytes, full
+    assert off == 0, off
+    assert none > 8 * x_bytes, none
+
+
+def test_offload_and_block_interval_match_oracle_and_full_recompute(device) -> None:
+    """offload_saved_tensors=True and block_interval=2 (layers 0 and 2
+    checkpointed, 1 and 3 eager; models/gpt/model.py:162-170) give the loss and
+    gradients of plain full recompute bit for bit, and match the oracle run with
+    the same switch (bf16 tolerance)."""
+    cfg = c1_config(layers=4, kv_heads=2)
+    ids, labels = c1_batch()
+    results = {}
+    for name, ck in (("full", nm.ActivationCheckpointConfig(mode="full")),
+                     ("offload", nm.ActivationCheckpointConfig(mode="full", offload_saved_tensors=True)),
+                     ("interval2", nm.ActivationCheckpointConfig(mode="full", block_interval=2))):
+        torch.manual_seed(0)
+        ours = nm.GPTModel(cfg, activation_checkpoint_config=ck).to(device=device, dtype=torch.bfloat16).train()
+        lo = ours(ids.to(device), labels=labels.to(device)).loss
+        lo.backward()
+        results[name] = (lo.detach(), {n: p.grad.clone() for n, p in ours.named_parameters()})
+        if name == "interval2":
+            torch.manual_seed(0)
+            ref = R.OracleGPTModel(cfg, activation_checkpoint_config=ck).to(dtype=torch.bfloat16).train()
+            ref.load_state_dict({k: v.cpu() for k, v in ours.state_dict().items()})
+            lr = ref(ids, labels=labels).loss
+            lr.backward()
+            torch.testing.assert_close(lo.detach().float().cpu(), lr.detach().float(), rtol=2e-2, atol=1e-2)
+            assert_grads(ours, ref, rtol=2e-2, atol=1e-2)
+            assert [layer.forward_calls for layer in ref.layers] == [2, 1, 2, 1]
+    base_loss, base_grads = results["full"]
+    for name in ("offload", "interval2"):
+        loss, grads = results[name]
+        assert torch.equal(loss, base_loss), name
+        for n, g in grads.items():
+            assert torch.equal(g, base_grads[n]), (name, n)
+
+
+def test_explicit_position_ids_match_oracle(device) -> None:
+    """position_ids given as [B, S] ids (not a range): RoPE at those positions and
+    the causal mask's query offset position_ids[0] (models/gpt/model.py:193-200,
+    attention.py:180-206), against the oracle; a range given as 1-D ids takes the
+    offset form and equals the default; negative ids raise."""
+    cfg = c1_config(layers=2, kv_heads=2)
+    ours, ref = build_pair(cfg, "full", torch.bfloat16, device)
+    ids, labels = c1_batch()
+    g = torch.Generator().manual_seed(4)
+    pos = torch.stack([torch.randperm(600, generator=g)[:128] for _ in range(4)])
+    pos[0, 0] = 3
+    lo = ours(ids.to(device), labels=labels.to(device), position_ids=pos.to(device)).loss
+    lr = ref(ids, labels=labels, position_ids=pos).loss
+    lo.backward()
+    lr.backward()
+    torch.testing.assert_close(lo.detach().float().cpu(), lr.detach().float(), rtol=2e-2, atol=1e-2)
+    assert_grads(ours, ref, rtol=2e-2, atol=1e-2)
+    with torch.no_grad():
+        a = ours(ids.to(device), labels=labels.to(device)).loss
+        b = ours(ids.to(device), labels=labels.to(device), position_ids=torch.arange(128, device=device)).loss
+        assert torch.equal(a, b)
+        with pytest.raises(ValueError, match="non-negative"):
+            ours(ids.to(device), labels=labels.to(device), position_ids=pos.to(device) - 5)
+
+
+def test_c4_width_block_matches_oracle_layer(device) -> None:
+    """One config-4 block (hidden 2048, 32 query / 8 KV heads of 64, SwiGLU 5632)
+    at B1 S2048 in bf16, checkpointed, against the oracle's GPTLayer: the output,
+    a loss made of it and every gradient (input and the nine weights)."""
+    cfg = nm.GPTConfig(layers=1, hidden_size=2048, ffn_hidden_size=5632, heads=32, kv_heads=8,
+                       seq_length=2048, vocab_size=8192, norm_epsilon=1e-5, rope_theta=1e4)
+    torch.manual_seed(0)
+    layer = R.OracleLayer(cfg, 0, dtype=torch.bfloat16)
+    with torch.no_grad():  # norms away from 1 so their gradients are exercised
+        layer.input_norm.weight.add_(0.1 * torch.randn(2048).bfloat16())
+        layer.post_attention_norm.weight.add_(0.1 * torch.randn(2048).bfloat16())
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(1, 2048, 2048, generator=g).bfloat16()
+    dy = torch.randn(1, 2048, 2048, generator=g).bfloat16()
+    xr = x.clone().requires_grad_(True)
+    yr = layer(xr, position_ids=torch.arange(2048), sequence_offset=0)
+    loss_r = (yr.float() * dy.float()).sum()
+    loss_r.backward()
+    names = ("input_norm.weight", "attention.q_proj.linear.weight", "attention.k_proj.linear.weight",
+             "attention.v_proj.linear.weight", "attention.out_proj.linear.weight",
+             "post_attention_norm.weight", "mlp.gate_proj.linear.weight", "mlp.up_proj.linear.weight",
+             "mlp.down_proj.linear.weight")
+    params = dict(layer.named_parameters())
+    ws = [params[n].detach().to(device).requires_grad_(True) for n in names]
+    tab = nm.RotaryEmbedding(64).tables(device, 2048)
+    meta = B.BlockMeta(heads=32, kv_heads=8, head_dim=64, eps=1e-5, sequence_offset=0, cos=tab.cos,
+                       sin=tab.sin, positions=None)
+    xd = x.to(device).requires_grad_(True)
+    yd = B.CheckpointedBlockFunction.apply(xd, meta, False, *ws)
+    loss_d = (yd.float() * dy.to(device).float()).sum()
+    loss_d.backward()
+    torch.testing.assert_close(yd.detach().float().cpu(), yr.detach().float(), rtol=2e-2, atol=1e-2)
+    torch.testing.assert_close(loss_d.detach().cpu(), loss_r.detach(), rtol=2e-2, atol=1e-2)
+    for name, got, exp in (("x", xd.grad, xr.grad), *((n, w.grad, params[n].grad) for n, w in zip(names, ws))):
+        scale = max(1.0, float(exp.abs().max()))
+        torch.testing.assert_close(got.float().cpu(), exp.float(), rtol=2e-2, atol=1e-2 * scale, msg=name)
+
+
+def test_c3_model_step_full_and_none_bit_identical(device) -> None:
+    """The 24-layer config-3 model (310.8M parameters, B16 S512, bf16) with full
+    recompute and without checkpointing: the same loss and every gradient bit
+    for bit, all finite."""
+    cfg = nm.GPTConfig(layers=24, hidden_size=1024, ffn_hidden_size=2736, heads=16, seq_length=512,
+                       vocab_size=8192, norm_epsilon=1e-5, rope_theta=1e4)
+    g = torch.Generator(device=device).manual_seed(1234)
+    ids = torch.randint(0, 8192, (16, 513), device=device, generator=g)
+    x, y = ids[:, :512].contiguous(), ids[:, 1:].contiguous()
+    results = []
+    for mode in ("full", "none"):
+        torch.manual_seed(1234)
+        model = nm.GPTModel(cfg, activation_checkpoint_config=nm.ActivationCheckpointConfig(mode=mode))
+        model = model.to(device=device, dtype=torch.bfloat16).train()
+        loss = model(x, labels=y).loss
+        loss.backward()
+        results.append((loss.detach(), [p.grad for p in model.parameters()]))
+        del model
+    (l0, g0), (l1, g1) = results
+    assert torch.isfinite(l0) and torch.equal(l0, l1)
+    assert len(g0) == len(g1) == 24 * 9 + 2
+    for a, b in zip(g0, g1):
+        assert bool(torch.isfinite(a).all()) and torch.equal(a, b)

@@ -163,6 +163,11 @@ ATTN_CASES = [
     # head dim 64 from 1024 queries (two column tiles per wave, three workgroups per CU),
     # ragged last tile
     (1, 2, 2, 1100, 1100, 64, torch.bfloat16, 0, True),
+    # config-4 attention: GQA 4:1 at head dim 64 over 2048 queries (the C4 heads,
+    # 32 query / 8 KV, at batch 1), and the same ratio with a ragged tail
+    (1, 8, 2, 2048, 2048, 64, torch.bfloat16, 0, True),
+    (1, 32, 8, 2048, 2048, 64, torch.bfloat16, 0, True),
+    (1, 8, 2, 1100, 1100, 64, torch.bfloat16, 0, True),
 ]
 
 
@@ -190,16 +195,28 @@ def test_attention_matches_oracle(device, b, hq, hkv, sq, sk, d, dtype, offset, 
 
 
 def test_attention_c3_shape_and_lse(device) -> None:
-    """Config 3 attention shape [16,16,512,64] bf16; lse == logsumexp of masked scores."""
+    """Config 3 attention shape [16,16,512,64] bf16, forward and backward against
+    the oracle; lse == logsumexp of masked scores."""
     g = gen(1)
     b, h, s, d = 16, 16, 512, 64
     q = torch.randn(b, s, h, d, generator=g).bfloat16()
     k = torch.randn(b, s, h, d, generator=g).bfloat16()
     v = torch.randn(b, s, h, d, generator=g).bfloat16()
+    do = torch.randn(b, s, h, d, generator=g).bfloat16()
     o, lse = Fn.attn_fwd_bshd(q.to(device), [k.to(device)], [v.to(device)], (0,), causal=True,
                               q_offset=0, scale=None)
-    ref = R.local_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2))
+    qr, kr, vr = (t.transpose(1, 2).clone().requires_grad_(True) for t in (q, k, v))
+    ref = R.local_attention(qr, kr, vr)
+    ref.backward(do.transpose(1, 2))
     close(o.transpose(1, 2), ref, torch.bfloat16)
+    # the backward as the model runs it (delta fused in the dQ kernel, then dK/dV)
+    qd, kd, vd = (t.to(device).transpose(1, 2).requires_grad_(True) for t in (q, k, v))
+    od = nm.attention(qd, kd, vd)
+    od.backward(do.to(device).transpose(1, 2))
+    assert torch.equal(od.detach().transpose(1, 2), o)
+    close(qd.grad, qr.grad, torch.bfloat16, scale_atol=True, msg="dq")
+    close(kd.grad, kr.grad, torch.bfloat16, scale_atol=True, msg="dk")
+    close(vd.grad, vr.grad, torch.bfloat16, scale_atol=True, msg="dv")
     qf, kf = q[:2].float().transpose(1, 2), k[:2].float().transpose(1, 2)
     scores = qf @ kf.transpose(-1, -2) / math.sqrt(d)
     mask = torch.ones(s, s, dtype=torch.bool).tril()
@@ -524,3 +541,92 @@ def test_tied_embedding_gradient_merge(device) -> None:
     loss = Fn.lm_head_cross_entropy(h * 1.5, w, tgt)
     loss.backward()  # autograd adds the two gradients
     assert torch.equal(merged, w.grad)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_embedding_out_of_range_ids_match_oracle(device, dtype) -> None:
+    """Ids outside [0, V) (negative, V, far beyond V, the ignore value -100) give
+    zero rows and no table gradient, as the reference's TP=1 lookup masks them
+    (tensor_parallel/embedding.py:63-68): output and table gradient bit-equal to
+    the oracle.  The in-range ids are distinct, so every table-gradient row is
+    one token's row (or zero) and no summation order enters."""
+    g = torch.Generator().manual_seed(9)
+    vocab, hidden, b, s = 1000, 256, 4, 64
+    table = torch.randn(vocab, hidden, generator=g).to(dtype)
+    ids = torch.randperm(vocab, generator=g)[: b * s].view(b, s).clone()
+    ids[0, :4] = torch.tensor([-1, vocab, vocab + 5, -100])
+    ids[2, 10] = 2**40
+    ids[3, 63] = -(2**40)
+    dout = torch.randn(b, s, hidden, generator=g).to(dtype)
+    wr = table.clone().requires_grad_(True)
+    ref = R.embedding_lookup(ids, wr)
+    ref.backward(dout)
+    wd = table.to(device).requires_grad_(True)
+    out = Fn.embedding(wd, ids.to(device))
+    out.backward(dout.to(device))
+    assert torch.equal(out.cpu(), ref)
+    assert not bool(out[0, :4].any()) and not bool(out[2, 10].any())
+    assert torch.equal(wd.grad.cpu(), wr.grad)
+
+
+@pytest.mark.gpu
+def test_ring_share_c5_full_size_sampled_rows(device) -> None:
+    """Config 5 at full size: rank 3 of a 4-way ring, local queries 24576..32767
+    ([1, 8192, 16, 128] bf16) over four 8192-key blocks visited 3, 2, 1, 0
+    (context_parallel/ring.py:104-250).  The kernel runs the whole share; the
+    oracle checks windows of query rows of two heads (o, lse and dq of a row
+    depend on that row alone, over all 32768 keys) and, for one head, dk / dv of
+    key windows in the diagonal and a fully visible block (a key's gradient sums
+    over every query: the oracle forward over all queries supplies their lse)."""
+    s, h, d, nb, rank = 8192, 16, 128, 4, 3
+    g = gen(41)
+    q = torch.randn(1, s, h, d, generator=g).bfloat16()
+    ks = [torch.randn(1, s, h, d, generator=g).bfloat16() for _ in range(nb)]
+    vs = [torch.randn(1, s, h, d, generator=g).bfloat16() for _ in range(nb)]
+    do = torch.randn(1, s, h, d, generator=g).bfloat16()
+    order = [(rank - step) % nb for step in range(nb)]
+    offs = [r * s for r in order]
+    q_off = rank * s
+    kb, vb = [ks[r] for r in order], [vs[r] for r in order]
+    qd = q.to(device)
+    kbd, vbd = [t.to(device) for t in kb], [t.to(device) for t in vb]
+    o, lse = Fn.attn_fwd_bshd(qd, kbd, vbd, offs, causal=True, q_offset=q_off, scale=None)
+    dq = torch.empty_like(qd)
+    dks = [torch.empty_like(t) for t in kbd]
+    dvs = [torch.empty_like(t) for t in vbd]
+    Fn.attn_bwd_bshd(qd, kbd, vbd, offs, o, do.to(device), lse, dq, dks, dvs, causal=True,
+                     q_offset=q_off, scale=None)
+    torch.cuda.synchronize()
+    o, lse, dq = o.cpu(), lse.cpu(), dq.cpu()
+    dks, dvs = [t.cpu() for t in dks], [t.cpu() for t in dvs]
+
+    def bhsd(t, heads, rows=slice(None)):
+        return t[:, rows][:, :, heads].transpose(1, 2).contiguous()
+
+    heads = [0, 9]
+    bf = torch.bfloat16
+    for start, n in ((0, 48), (4000, 32), (s - 40, 40)):
+        rows = slice(start, start + n)
+        qr = bhsd(q, heads, rows)
+        blocks = [(bhsd(k, heads), bhsd(v, heads)) for k, v in zip(kb, vb)]
+        out_ref, lse_ref = R.ring_attention_forward(qr, blocks, offs, causal=True, query_offset=q_off + start)
+        dq_ref, _, _ = R.ring_attention_backward(bhsd(do, heads, rows), qr, blocks, offs, out_ref, lse_ref,
+                                                 causal=True, query_offset=q_off + start)
+        close(bhsd(o, heads, rows), out_ref, bf, msg=f"o rows {start}")
+        torch.testing.assert_close(lse[:, heads, rows], lse_ref.squeeze(-1), rtol=1e-3, atol=2e-3)
+        close(bhsd(dq, heads, rows), dq_ref, bf, scale_atol=True, msg=f"dq rows {start}")
+
+    head = [9]
+    qh = bhsd(q, head)
+    blocks = [(bhsd(k, head), bhsd(v, head)) for k, v in zip(kb, vb)]
+    out_all, lse_all = R.ring_attention_forward(qh, blocks, offs, causal=True, query_offset=q_off)
+    do_h = bhsd(do, head)
+    # block index 0 in ring order is the diagonal block (key positions 24576..), 2 is fully visible
+    for bi, kstart, n in ((0, 0, 64), (0, s - 64, 64), (2, 1000, 64)):
+        keys = slice(kstart, kstart + n)
+        kv = [(bhsd(kb[bi], head, keys), bhsd(vb[bi], head, keys))]
+        _, dk_ref, dv_ref = R.ring_attention_backward(do_h, qh, kv, [offs[bi] + kstart], out_all, lse_all,
+                                                      causal=True, query_offset=q_off)
+        close(bhsd(dks[bi], head, keys), dk_ref[0], bf, scale_atol=True, msg=f"dk block {bi} keys {kstart}")
+        close(bhsd(dvs[bi], head, keys), dv_ref[0], bf, scale_atol=True, msg=f"dv block {bi} keys {kstart}")

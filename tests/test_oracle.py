@@ -250,6 +250,82 @@ def test_adamw_master_step_matches_torch_adamw() -> None:
     torch.testing.assert_close(master, ref.detach(), rtol=1e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("scale,max_norm", [(3.0, 1.0), (1e-2, 1.0), (1e-7, 1e-6), (0.0, 1.0)])
+def test_clip_coefficient_matches_torch_clip_grad_norm(scale, max_norm) -> None:
+    """The factor ``torch.nn.utils.clip_grad_norm_`` multiplies the gradients by
+    (max_norm / (norm + 1e-6), clamped at 1) equals the oracle's coefficient
+    (data_parallel/_zero.py:160-163).  The 1e-7 case makes the 1e-6 term decide
+    the result (dropping it or moving it would change the coefficient by ~2x);
+    the 1e-2 and 0 cases sit under the clamp."""
+    g = torch.Generator().manual_seed(17)
+    grads = [torch.randn(*s, generator=g, dtype=torch.float64) * scale for s in ((7, 5), (11,), (3, 2, 4))]
+    params = [torch.nn.Parameter(torch.zeros_like(t)) for t in grads]
+    for p, t in zip(params, grads):
+        p.grad = t.clone()
+    norm = torch.nn.utils.clip_grad_norm_(params, max_norm)
+    coef = R.clip_coefficient(norm, max_norm)
+    for p, t in zip(params, grads):
+        torch.testing.assert_close(p.grad, t * coef, rtol=1e-12, atol=0)
+    if scale == 3.0:
+        assert coef < 0.2
+    if scale <= 1e-2 and scale != 1e-7:
+        assert coef == 1.0
+    if scale == 1e-7:
+        expected_no_eps = max_norm / float(norm)
+        assert abs(float(coef) - expected_no_eps) > 0.05 * expected_no_eps
+
+
+def test_clip_then_adamw_master_step_matches_torch() -> None:
+    """One ZeRO optimizer step at DP=1 (_zero.py:130-199): the global-norm clip
+    followed by the fp32-master AdamW, against clip_grad_norm_ + torch AdamW."""
+    g = torch.Generator().manual_seed(23)
+    shapes = ((40,), (6, 9))
+    init = [torch.randn(*s, generator=g) for s in shapes]
+    params = [torch.nn.Parameter(t.clone()) for t in init]
+    opt = torch.optim.AdamW(params, lr=1e-2, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+    master = [t.clone() for t in init]
+    m = [torch.zeros_like(t) for t in init]
+    v = [torch.zeros_like(t) for t in init]
+    for step in range(1, 4):
+        grads = [torch.randn(*s, generator=g) * 2.0 for s in shapes]
+        for p, t in zip(params, grads):
+            p.grad = t.clone()
+        torch.nn.utils.clip_grad_norm_(params, 1.0)
+        opt.step()
+        norm = torch.sqrt(sum((t * t).sum() for t in grads))
+        coef = R.clip_coefficient(norm, 1.0)
+        for w, mm, vv, t in zip(master, m, v, grads):
+            R.adamw_master_step(w, mm, vv, t * coef, step=step, lr=1e-2, weight_decay=0.1)
+    for p, w in zip(params, master):
+        torch.testing.assert_close(w, p.detach(), rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------- embedding
+def test_embedding_lookup_masks_ids_outside_the_table() -> None:
+    """VocabParallelEmbedding at TP=1 (tensor_parallel/embedding.py:63-68): ids in
+    [0, V) gather their row, ids outside give zero rows and pass no gradient;
+    checked against an explicit per-token loop and an index_add of the in-range
+    rows only."""
+    g = torch.Generator().manual_seed(3)
+    vocab, hidden = 10, 4
+    w = torch.randn(vocab, hidden, generator=g, dtype=torch.float64, requires_grad=True)
+    ids = torch.tensor([[0, 9, -1, 10, 3], [3, -100, 7, 25, 0]])
+    out = R.embedding_lookup(ids, w)
+    for b in range(ids.shape[0]):
+        for t in range(ids.shape[1]):
+            i = int(ids[b, t])
+            exp = w[i] if 0 <= i < vocab else torch.zeros(hidden, dtype=torch.float64)
+            assert torch.equal(out[b, t], exp)
+    dout = torch.randn(*ids.shape, hidden, generator=g, dtype=torch.float64)
+    out.backward(dout)
+    inside = (ids >= 0) & (ids < vocab)
+    exp_grad = torch.zeros(vocab, hidden, dtype=torch.float64).index_add_(
+        0, ids[inside], dout[inside])
+    torch.testing.assert_close(w.grad, exp_grad, rtol=0, atol=1e-15)
+    with pytest.raises(TypeError):
+        R.embedding_lookup(ids.float(), w)
+
+
 # ---------------------------------------------------------------- model
 class _Cfg:
     layers = 2
