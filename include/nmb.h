@@ -148,6 +148,24 @@ int nmb_attn_bwd(const void* q, const void* const* k_blocks, const void* const* 
                  const int64_t* q_strides, const int64_t* kv_strides, const int64_t* o_strides,
                  int causal, int64_t q_offset, float scale, int dtype, hipStream_t stream);
 
+/* nmb_attn_bwd without a workspace argument and without any allocation: no
+ * counterpart in the reference; for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Its scratch (delta and the base-2 LSE, fp32
+ * [batch, q_heads, seq_q] each) lives in a fixed 8 MiB device array, one per
+ * device, held until the process ends: batch x q_heads x seq_q must be at
+ * most 1,048,576 (EINVAL beyond).  Every call on a device uses that device's
+ * array, so calls that overlap on one device (two streams or threads) race;
+ * the stream must belong to the current device.  Same results as
+ * nmb_attn_bwd, bit for bit. */
+int nmb_attn_bwd_noalloc(const void* q, const void* const* k_blocks, const void* const* v_blocks,
+                         const int64_t* k_offsets, int n_blocks, const void* o, const void* dout,
+                         const float* lse, void* dq, void* const* dk_blocks, void* const* dv_blocks,
+                         int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                         int64_t seq_k, int64_t head_dim, const int64_t* q_strides,
+                         const int64_t* kv_strides, const int64_t* o_strides, int causal,
+                         int64_t q_offset, float scale, int dtype, hipStream_t stream);
+
 /* nmb_attn_bwd for one K/V block that holds the queries' own tokens (the
  * block's self-attention; reference models/gpt/attention.py:180-206) with the
  * RoPE backward of q and k fused into the dQ / dK stores (replaces

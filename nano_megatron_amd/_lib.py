@@ -61,6 +61,10 @@ SIGNATURES: dict[str, list] = {
         _p, _p, _p, _pi64, _i32, _p, _p, _p, _p, _p, _p, _p, _sz, _i64, _i64, _i64, _i64, _i64,
         _i64, _pi64, _pi64, _pi64, _i32, _i64, _f32, _i32, _p,
     ],
+    "nmb_attn_bwd_noalloc": [
+        _p, _p, _p, _pi64, _i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
+        _pi64, _pi64, _pi64, _i32, _i64, _f32, _i32, _p,
+    ],
     "nmb_attn_bwd_rope": [
         _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _i64, _i64, _i64, _i64, _i64, _pi64, _pi64,
         _pi64, _i32, _i64, _f32, _p, _p, _i64, _p, _i64, _i64, _p,

@@ -24,6 +24,9 @@
 //   parity configuration.
 #include <math.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "common.h"
 #include "lds_dma.h"
 
@@ -1603,4 +1606,90 @@ extern "C" int nmb_attn_bwd_rope(const void* q, const void* k, const void* v, co
   return nmb::attn_bwd_impl(q, kb, vb, koff, 1, o, dout, lse, dq, dkb, dvb, workspace,
                             workspace_bytes, batch, q_heads, kv_heads, seq, seq, head_dim, q_strides,
                             kv_strides, o_strides, causal, q_offset, scale, NMB_BF16, stream, &rg);
+}
+
+// ---------------------------------------------------------------- backward without allocation
+// nmb_attn_bwd_noalloc: nmb_attn_bwd with its workspace (delta and the base-2
+// lse, fp32 [B, Hq, Sq] each) in a fixed device array instead of a caller
+// buffer, for callers that cannot allocate.  Each device holds its own copy of
+// the array until the process ends; every call on a device uses that copy, so
+// calls that overlap on one device (two streams, two threads) race.  Nothing
+// in it needs clearing: the dQ kernel writes every delta and lse entry of the
+// call before the dK/dV kernel reads them (same stream).
+namespace {
+
+constexpr size_t kNoAllocScratchBytes = size_t{8} << 20;  // B x Hq x Sq <= 1M query rows
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+// device address of `scratch` per device, looked up once with that device current
+std::atomic<void*> g_scratch_address[kMaxDevices];
+std::mutex g_scratch_mutex;
+
+int scratch_for_stream(hipStream_t stream, void** out) {
+  int current = -1;
+  hipError_t e = hipGetDevice(&current);
+  if (e != hipSuccess) {
+    nmb::set_error("attn_bwd_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+    return NMB_EHIP;
+  }
+  if (stream != nullptr) {
+    int dev = -1;
+    e = hipStreamGetDevice(stream, &dev);
+    if (e != hipSuccess) {
+      nmb::set_error("attn_bwd_noalloc: hipStreamGetDevice failed: %s", hipGetErrorString(e));
+      return NMB_EHIP;
+    }
+    NMB_REQUIRE(dev == current,
+                "attn_bwd_noalloc: the stream belongs to device %d but device %d is current", dev,
+                current);
+  }
+  NMB_REQUIRE(current >= 0 && current < kMaxDevices, "attn_bwd_noalloc: device %d out of range",
+              current);
+  void* p = g_scratch_address[current].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    p = g_scratch_address[current].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      // the array's name is a host-side stand-in: kernels get this address
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || p == nullptr) {
+        nmb::set_error("attn_bwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                       current, hipGetErrorString(e));
+        return NMB_EHIP;
+      }
+      g_scratch_address[current].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return NMB_OK;
+}
+
+}  // namespace
+
+extern "C" int nmb_attn_bwd_noalloc(const void* q, const void* const* k_blocks,
+                                    const void* const* v_blocks, const int64_t* k_offsets,
+                                    int n_blocks, const void* o, const void* dout, const float* lse,
+                                    void* dq, void* const* dk_blocks, void* const* dv_blocks,
+                                    int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                    int64_t seq_q, int64_t seq_k, int64_t head_dim,
+                                    const int64_t* q_strides, const int64_t* kv_strides,
+                                    const int64_t* o_strides, int causal, int64_t q_offset,
+                                    float scale, int dtype, hipStream_t stream) {
+  NMB_REQUIRE(batch >= 0 && q_heads >= 0 && seq_q >= 0 && batch <= 65535 && q_heads <= 65535 &&
+                  seq_q <= 0x3fffffff,
+              "attn_bwd_noalloc: invalid shape");
+  const size_t need = 2 * static_cast<size_t>(batch * q_heads * seq_q) * sizeof(float);
+  NMB_REQUIRE(need <= kNoAllocScratchBytes,
+              "attn_bwd_noalloc: %zu bytes of scratch needed, at most %zu available "
+              "(batch x q_heads x seq_q <= %zu)",
+              need, kNoAllocScratchBytes, kNoAllocScratchBytes / (2 * sizeof(float)));
+  void* ws = nullptr;
+  const int st = scratch_for_stream(stream, &ws);
+  if (st != NMB_OK) return st;
+  return nmb::attn_bwd_impl(q, k_blocks, v_blocks, k_offsets, n_blocks, o, dout, lse, dq, dk_blocks,
+                            dv_blocks, ws, kNoAllocScratchBytes, batch, q_heads, kv_heads, seq_q,
+                            seq_k, head_dim, q_strides, kv_strides, o_strides, causal, q_offset,
+                            scale, dtype, stream, nullptr);
 }
