@@ -235,6 +235,16 @@ int nmb_gemm_bf16(int a_layout, int b_layout, int64_t m, int64_t n, int64_t k, f
                   const void* c, int64_t ldc, void* d, int64_t ldd, void* workspace,
                   int64_t workspace_bytes, hipStream_t stream);
 
+/* fp32 GEMM on the fp32 matrix cores, for the fp32 parity configuration
+ * (replaces the same nn.Linear / F.linear products in fp32):
+ *   D[M, N] = alpha * op(A) * op(B) + beta * C, layouts as nmb_gemm_bf16
+ * (a_layout 0: A [M, K], 1: [K, M]; b_layout 0: B [N, K], 1: [K, N]); any
+ * shape, leading dimension and alignment; C may alias D; exact fp32 products
+ * accumulated in fp32. */
+int nmb_gemm_f32(int a_layout, int b_layout, int64_t m, int64_t n, int64_t k, float alpha,
+                 const float* a, int64_t lda, const float* b, int64_t ldb, float beta,
+                 const float* c, int64_t ldc, float* d, int64_t ldd, hipStream_t stream);
+
 /* GEMM with the rotary embedding as its epilogue: the Q/K/V projection and
  * RoPE of q and k in one pass (reference models/gpt/attention.py:172-181 with
  * nn/rotary.py:27-38, 55-70; replaces nmb_gemm_bf16 + two nmb_rope_apply).

@@ -55,25 +55,24 @@ def _operand_layout(t: Tensor, rows_dim: int) -> tuple[int, int]:
 
 def mm(a: Tensor, b: Tensor, *, out: Tensor | None = None, c: Tensor | None = None,
        alpha: float = 1.0, beta: float = 0.0) -> Tensor:
-    """``out = alpha * a @ b + beta * c`` for 2-D tensors.
+    """``out = alpha * a @ b + beta * c`` for 2-D tensors (``c`` may be ``out``).
 
-    bf16 runs the gfx950 MFMA kernel ``nmb_gemm_bf16`` (any mix of row/column
-    major operands); fp32 (the parity configuration) uses the library GEMM.
+    bf16 runs the gfx950 MFMA kernel ``nmb_gemm_bf16``, fp32 (the parity
+    configuration) the fp32-MFMA kernel ``nmb_gemm_f32``; both take any mix of
+    row/column-major operands.  Other dtypes are a ValueError.
     """
     m, k = a.shape
     k2, n = b.shape
     if k != k2:
         raise ValueError(f"gemm: inner dimensions differ ({k} vs {k2})")
+    if a.dtype != b.dtype or (c is not None and c.dtype != a.dtype):
+        raise ValueError(f"gemm: operands of one dtype needed, got {a.dtype}, {b.dtype}")
     if out is None:
         out = torch.empty(m, n, dtype=a.dtype, device=a.device)
+    if a.dtype == torch.float32:
+        return _mm_f32(a, b, out, c, alpha, beta)
     if a.dtype != torch.bfloat16:
-        if beta != 0.0 and c is out:
-            out.addmm_(a, b, beta=beta, alpha=alpha)
-        elif beta != 0.0:
-            torch.addmm(c, a, b, beta=beta, alpha=alpha, out=out)
-        else:
-            torch.mm(a, b, out=out) if alpha == 1.0 else torch.mm(a, b, out=out).mul_(alpha)
-        return out
+        raise ValueError(f"nano_megatron_amd GEMMs support float32 and bfloat16, got {a.dtype}")
     _require_gpu(a, b, out)
     la, lda = _operand_layout(a, 0)
     # B is [K, N]: layout 0 means stored [N, K] (dim 0 = K contiguous)
@@ -96,6 +95,73 @@ def mm(a: Tensor, b: Tensor, *, out: Tensor | None = None, c: Tensor | None = No
         out.stride(0), _lib.ptr(ws), ws.numel() if ws is not None else 0, _lib.stream_of(a),
     )
     return out
+
+
+def _any_layout(t: Tensor) -> tuple[Tensor, int, int]:
+    """(t or a contiguous copy, layout, ld) for an fp32 operand (layout as _operand_layout)."""
+    try:
+        la, ld = _operand_layout(t, 0)
+    except ValueError:
+        t = t.contiguous()
+        la, ld = _operand_layout(t, 0)
+    return t, la, ld
+
+
+def _mm_f32(a: Tensor, b: Tensor, out: Tensor, c: Tensor | None, alpha: float, beta: float) -> Tensor:
+    _require_gpu(a, b, out)
+    m, k = a.shape
+    n = b.shape[1]
+    a, la, lda = _any_layout(a)
+    b, lb_rowmajor, ldb = _any_layout(b)
+    if out.stride(1) != 1 and out.numel() > 1:
+        raise ValueError("gemm: the output must be row-major")
+    if beta != 0.0 and (c is None or (c.stride(1) != 1 and c.numel() > 1)):
+        raise ValueError("gemm: beta != 0 needs a row-major C")
+    _lib.call(
+        "nmb_gemm_f32", la, 1 - lb_rowmajor, m, n, k, float(alpha), a.data_ptr(), lda, b.data_ptr(),
+        ldb, float(beta), _lib.ptr(c) if beta != 0.0 else None,
+        max(c.stride(0), n) if (c is not None and beta != 0.0) else n, out.data_ptr(),
+        max(out.stride(0), n), _lib.stream_of(a),
+    )
+    return out
+
+
+class LinearFunction(torch.autograd.Function):
+    """``F.linear(x, weight)`` (nn/kernels/torch_backend.py:19-20,
+    tensor_parallel/layers.py:214) on the library's GEMMs: y = x W^T,
+    dX = dY W, dW = dY^T X."""
+
+    @staticmethod
+    def forward(ctx: Any, x: Tensor, weight: Tensor) -> Tensor:
+        if x.shape[-1] != weight.shape[1]:
+            raise ValueError(f"linear: input features {x.shape[-1]} != weight {weight.shape[1]}")
+        x2 = x.reshape(-1, x.shape[-1])
+        if not x2.is_contiguous():
+            x2 = x2.contiguous()
+        y = mm(x2, weight.t())
+        ctx.save_for_backward(x2, weight)
+        ctx.shape = x.shape
+        return y.view(*x.shape[:-1], weight.shape[0])
+
+    @staticmethod
+    def backward(ctx: Any, dy: Tensor):
+        x2, weight = ctx.saved_tensors
+        dy2 = dy.reshape(-1, weight.shape[0])
+        if not dy2.is_contiguous():
+            dy2 = dy2.contiguous()
+        dx = dw = None
+        if ctx.needs_input_grad[0]:
+            dx = mm(dy2, weight).view(ctx.shape)
+        if ctx.needs_input_grad[1]:
+            dw = mm(dy2.t(), x2)
+        return dx, dw
+
+
+def linear(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
+    """``F.linear`` with the GEMM on this library's kernels (the bias, when a
+    module has one, is added by a broadcast tensor add)."""
+    y = LinearFunction.apply(x, weight)
+    return y if bias is None else y + bias
 
 
 def mm_rope(a: Tensor, b: Tensor, *, seq: int, head_dim: int, rope_cols: int, cos: Tensor,

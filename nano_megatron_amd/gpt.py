@@ -177,7 +177,7 @@ class VocabParallelLinear(nn.Module):
     def forward(self, x: Tensor) -> Tensor:
         if x.shape[-1] != self.hidden_size:
             raise ValueError(f"expected input hidden size {self.hidden_size}, got {x.shape[-1]}")
-        return F.linear(x, self.weight)
+        return Fn.linear(x, self.weight)
 
 
 class VocabParallelCrossEntropy(nn.Module):

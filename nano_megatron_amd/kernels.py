@@ -26,16 +26,22 @@ class KernelBackend(Protocol):
     def local_attention(self, q: Tensor, k: Tensor, v: Tensor, **kwargs: Any) -> Tensor: ...
 
 
+class Linear(nn.Linear):
+    """``nn.Linear`` (same parameters, attribute names and kaiming-uniform init,
+    so seeded weights equal the reference's) whose product runs on this
+    library's GEMM kernels (bf16 and fp32 MFMA) instead of the vendor GEMM."""
+
+    def forward(self, x: Tensor) -> Tensor:
+        return Fn.linear(x, self.weight, self.bias)
+
+
 class HipKernelBackend:
-    """gfx950 kernels: fused RMSNorm, MFMA attention; library GEMMs for ``linear``."""
+    """gfx950 kernels: MFMA GEMMs for ``linear``, fused RMSNorm, MFMA attention."""
 
     name = "hip"
 
     def linear(self, in_features: int, out_features: int, **kwargs: Any) -> nn.Module:
-        # A plain dense projection: the module (and its kaiming-uniform init, so
-        # seeded weights equal the reference's) is nn.Linear, whose GEMM runs on
-        # MFMA through hipBLASLt.
-        return nn.Linear(in_features, out_features, **kwargs)
+        return Linear(in_features, out_features, **kwargs)
 
     def rms_norm(self, hidden_size: int, eps: float, **kwargs: Any) -> nn.Module:
         return RMSNorm(hidden_size, eps, **kwargs)

@@ -104,6 +104,16 @@ def test_rope_and_swiglu_and_ce_reject_bad_arguments() -> None:
     assert st == _lib.NMB_EINVAL and b"neither" in lib.nmb_last_error()
 
 
+def test_gemm_f32_rejects_bad_arguments() -> None:
+    lib = _lib.load()
+    st = lib.nmb_gemm_f32(2, 0, 4, 4, 4, 1.0, FAKE, 4, FAKE, 4, 0.0, None, 4, FAKE, 4, None)
+    assert st == _lib.NMB_EINVAL and b"a_layout" in lib.nmb_last_error()
+    st = lib.nmb_gemm_f32(0, 0, 4, 4, 4, 1.0, FAKE, 3, FAKE, 4, 0.0, None, 4, FAKE, 4, None)
+    assert st == _lib.NMB_EINVAL and b"leading dimension" in lib.nmb_last_error()
+    st = lib.nmb_gemm_f32(0, 0, 4, 4, 4, 1.0, FAKE, 4, FAKE, 4, 1.0, None, 4, FAKE, 4, None)
+    assert st == _lib.NMB_EINVAL and b"needs C" in lib.nmb_last_error()
+
+
 def test_python_wrapper_maps_status_to_exceptions() -> None:
     with pytest.raises(ValueError, match="multiple of 8"):
         _lib.call("nmb_rmsnorm_fwd", FAKE, FAKE, FAKE, None, 4, 12, 1e-5, _lib.NMB_BF16, None)

@@ -630,3 +630,50 @@ def test_ring_share_c5_full_size_sampled_rows(device) -> None:
                                                       causal=True, query_offset=q_off)
         close(bhsd(dks[bi], head, keys), dk_ref[0], bf, scale_atol=True, msg=f"dk block {bi} keys {kstart}")
         close(bhsd(dvs[bi], head, keys), dv_ref[0], bf, scale_atol=True, msg=f"dv block {bi} keys {kstart}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m,n,k,layout", [
+    (512, 256, 256, "NT"), (333, 130, 77, "NN"), (65, 1000, 513, "TN"), (128, 64, 8192, "TT"), (1, 7, 3, "NT"),
+])
+def test_gemm_f32_matches_fp64_product(device, m, n, k, layout) -> None:
+    """nmb_gemm_f32 (fp32 MFMA) for every operand layout, ragged tiles, alpha,
+    beta and an aliased C, against the fp64 product at the fp32 parity
+    tolerance (rtol 1e-5)."""
+    g = torch.Generator(device=device).manual_seed(m * 3 + n + k)
+    a = torch.randn(m, k, device=device, generator=g) if layout[0] == "N" else torch.randn(k, m, device=device, generator=g).t()
+    b = torch.randn(k, n, device=device, generator=g) if layout[1] == "N" else torch.randn(n, k, device=device, generator=g).t()
+    c = torch.randn(m, n, device=device, generator=g)
+    exp = 0.75 * (a.double() @ b.double()) + 1.5 * c.double()
+    out = Fn.mm(a, b, c=c, alpha=0.75, beta=1.5)
+    scale = float((a.double().abs() @ b.double().abs()).max())
+    torch.testing.assert_close(out.double(), exp, rtol=1e-5, atol=1e-6 * scale)
+    acc = c.clone()
+    Fn.mm(a, b, out=acc, c=acc, beta=1.0)  # the in-place accumulation the LM head uses
+    torch.testing.assert_close(acc.double(), a.double() @ b.double() + c.double(), rtol=1e-5, atol=1e-6 * scale)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_backend_linear_matches_torch_linear(device, dtype) -> None:
+    """HipKernelBackend.linear: the nn.Linear parameters and seeded init, with
+    the product and its gradients on this library's GEMMs."""
+    from nano_megatron_amd.kernels import HipKernelBackend
+
+    torch.manual_seed(3)
+    ours = HipKernelBackend().linear(256, 384, bias=False).to(device=device, dtype=dtype)
+    torch.manual_seed(3)
+    ref = torch.nn.Linear(256, 384, bias=False).to(dtype=dtype)
+    assert torch.equal(ours.weight.detach().cpu(), ref.weight.detach())
+    g = gen(4)
+    x = torch.randn(2, 100, 256, generator=g).to(dtype)
+    dy = torch.randn(2, 100, 384, generator=g).to(dtype)
+    xr = x.clone().requires_grad_(True)
+    yr = ref(xr)
+    yr.backward(dy)
+    xd = x.to(device).requires_grad_(True)
+    yd = ours(xd)
+    yd.backward(dy.to(device))
+    close(yd, yr, dtype)
+    close(xd.grad, xr.grad, dtype, scale_atol=True)
+    close(ours.weight.grad, ref.weight.grad, dtype, scale_atol=True)
