@@ -15,7 +15,6 @@ constexpr uint32_t kOOB = 0x80000000u;  // offset past every num_records: the lo
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef short v4s __attribute__((ext_vector_type(4)));
-using lds_void = __attribute__((address_space(3))) void;
 using lds_v4s = __attribute__((address_space(3))) v4s;
 
 // Buffer descriptor of a raw (untyped) byte range: base, stride 0, num_records
@@ -27,6 +26,13 @@ __device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
                __builtin_amdgcn_readfirstlane(static_cast<int>(bytes)), 0x00020000};
 }
 
+// Byte offset in LDS of a generic pointer to shared memory: the shared
+// aperture keeps the LDS offset in the low 32 bits of a generic address, so a
+// truncation gives it (an address-space cast would add a null-pointer select).
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
+}
+
 // 16 bytes per lane from buffer offset voff into LDS at byte address
 // lds + 16 * lane (lds is wave-uniform; it goes to M0).  Written as inline asm
 // so that the compiler does not treat the LDS written in flight as a pending
@@ -34,8 +40,7 @@ __device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
 // the kernel waits for these loads itself with s_waitcnt vmcnt.
 __device__ __forceinline__ void load_lds16(const i32x4& r, const bf16* lds, uint32_t voff) {
   // the address is uniform across the wave; readfirstlane makes it scalar
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)(const_cast<bf16*>(lds)))));
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds));
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
                : "s"(m0), "v"(voff), "s"(r)
@@ -45,8 +50,7 @@ __device__ __forceinline__ void load_lds16(const i32x4& r, const bf16* lds, uint
 // 4 bytes per lane from buffer offset voff into LDS at byte address
 // lds + 4 * lane (as load_lds16).
 __device__ __forceinline__ void load_lds4(const i32x4& r, const void* lds, uint32_t voff) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)(const_cast<void*>(lds)))));
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds));
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
                :
                : "s"(m0), "v"(voff), "s"(r)
