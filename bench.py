@@ -51,6 +51,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-kernels", action="store_true", help="skip the per-kernel roofline timing")
     p.add_argument("--no-eager", action="store_true", help="skip the no-checkpoint comparison run")
     p.add_argument("--no-legs", action="store_true", help="skip the config-4 and config-5 legs of the default line")
+    p.add_argument("--host-launch", action="store_true",
+                   help="time the steps with every kernel launched from the host (no HIP graph)")
     p.add_argument("--only-kernels", action="store_true", help="time the kernels only (for profiling)")
     p.add_argument("--kernel", default=None, help="with --only-kernels: time just this kernel")
     p.add_argument("--config", default="c3", choices=("c3", "c4", "c5"),
@@ -61,7 +63,9 @@ def parse() -> argparse.Namespace:
 
 
 def run_steps(mode: str, steps: int, warmup: int, device, metrics_jsonl: str | None = None,
-              model_cfg: dict = C3, batch: int = BATCH, seq: int = SEQ) -> dict:
+              model_cfg: dict = C3, batch: int = BATCH, seq: int = SEQ, graph: bool = True) -> dict:
+    """Eager steps, then (``graph``) the same step captured as a HIP graph and
+    replayed (``CapturedTrainStep``): both timed, the graph's time reported."""
     import torch
 
     import nano_megatron_amd as nm
@@ -83,7 +87,7 @@ def run_steps(mode: str, steps: int, warmup: int, device, metrics_jsonl: str | N
         loss = model(x, labels=y).loss
         loss.backward()
         opt.step()
-        return loss
+        return loss.detach()  # no reference to the step's autograd graph outlives it
 
     for _ in range(warmup):
         step()
@@ -110,7 +114,21 @@ def run_steps(mode: str, steps: int, warmup: int, device, metrics_jsonl: str | N
     for _ in range(steps):
         loss = step()
     torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+    elapsed = eager_elapsed = time.perf_counter() - t0
+    launch = "eager"
+    if graph:
+        from nano_megatron_amd.graph import CapturedTrainStep
+
+        cap = CapturedTrainStep(model, opt, x, y)
+        for _ in range(2):
+            cap.step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            loss = cap.step()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        launch = "hip_graph"
     if metrics_jsonl:
         from nano_megatron_amd import metrics as M
 
@@ -124,6 +142,9 @@ def run_steps(mode: str, steps: int, warmup: int, device, metrics_jsonl: str | N
     result = dict(
         ms_per_step=1e3 * elapsed / steps,
         tokens_per_s=batch * seq * steps / elapsed,
+        launch=launch,
+        eager_ms_per_step=1e3 * eager_elapsed / steps,
+        eager_tokens_per_s=batch * seq * steps / eager_elapsed,
         loss=float(loss.item()),
         peak_act_gib_per_layer=peak / cfg.layers / 2**30,
         saved_act_mib_per_layer=saved_after_fwd / cfg.layers / 2**20,
@@ -592,7 +613,8 @@ def model_step_flops(cfg: dict, batch: int, seq: int, recompute: bool) -> float:
 
 def c4_leg(args, device, eager: bool = True) -> dict:
     """Config 4: the GQA step, full recompute and none."""
-    full = run_steps("full", args.steps, args.warmup, device, None, C4, C4_BATCH, C4_SEQ)
+    full = run_steps("full", args.steps, args.warmup, device, None, C4, C4_BATCH, C4_SEQ,
+                     graph=not args.host_launch)
     print("c4 full: " + json.dumps(full), file=sys.stderr, flush=True)
     fl = model_step_flops(C4, C4_BATCH, C4_SEQ, recompute=True)
     tf = fl / (full["ms_per_step"] * 1e-3) / 1e12
@@ -600,6 +622,7 @@ def c4_leg(args, device, eager: bool = True) -> dict:
         workload="C4: GQA GPT (16L, H2048, 32 query / 8 KV heads D64, ffn 5632, vocab 8192 tied) training "
                  "step, B4 x S2048, full per-layer recompute, bf16 + fp32-master AdamW",
         tokens_per_s=round(full["tokens_per_s"], 1), ms_per_step=round(full["ms_per_step"], 3),
+        launch=full["launch"], host_launched_tokens_per_s=round(full["eager_tokens_per_s"], 1),
         model_tflops=round(tf, 1), mfma_frac=round(tf / BF16_PEAK_TFLOPS, 4),
         peak_act_gib_per_layer=round(full["peak_act_gib_per_layer"], 4),
         # one block's saved activation (2-layer minus 1-layer model); the
@@ -610,7 +633,8 @@ def c4_leg(args, device, eager: bool = True) -> dict:
         loss=round(full["loss"], 4),
     )
     if eager:
-        none = run_steps("none", args.steps, args.warmup, device, None, C4, C4_BATCH, C4_SEQ)
+        none = run_steps("none", args.steps, args.warmup, device, None, C4, C4_BATCH, C4_SEQ,
+                         graph=not args.host_launch)
         print("c4 none: " + json.dumps(none), file=sys.stderr, flush=True)
         leg["no_checkpoint_tokens_per_s"] = round(none["tokens_per_s"], 1)
         leg["recompute_overhead"] = round(full["ms_per_step"] / none["ms_per_step"] - 1.0, 4)
@@ -742,11 +766,11 @@ def main() -> None:
         if args.kernel:
             copy_calibration(device)
         return
-    full = run_steps("full", args.steps, args.warmup, device, args.metrics_jsonl)
+    full = run_steps("full", args.steps, args.warmup, device, args.metrics_jsonl, graph=not args.host_launch)
     print("full: " + json.dumps(full), file=sys.stderr, flush=True)
     eager = None
     if not args.no_eager:
-        eager = run_steps("none", args.steps, args.warmup, device)
+        eager = run_steps("none", args.steps, args.warmup, device, graph=not args.host_launch)
         print("none: " + json.dumps(eager), file=sys.stderr, flush=True)
 
     c4 = c5 = None
@@ -778,6 +802,11 @@ def main() -> None:
         steps=args.steps,
         warmup=args.warmup,
         ms_per_step=round(full["ms_per_step"], 3),
+        # "hip_graph": the step captured once (CapturedTrainStep) and replayed;
+        # the same step with every kernel launched from the host, same process:
+        launch=full["launch"],
+        host_launched_tokens_per_s=round(full["eager_tokens_per_s"], 1),
+        host_launched_ms_per_step=round(full["eager_ms_per_step"], 3),
         higher_is_better=True,
         scaling="weak",
         vs_baseline=None,

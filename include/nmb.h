@@ -301,6 +301,24 @@ int nmb_adamw_step(const uint64_t* params, const uint64_t* grads, const int64_t*
                    double beta2, double eps, double weight_decay, int64_t step, float max_norm,
                    float* norm_out, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* nmb_adamw_step with the update's scalars read from device memory, so that a
+ * captured HIP graph of the training step (one capture of the trainer's step,
+ * training/trainer.py:424-474, replayed every step) picks up each step's bias
+ * corrections and learning rate: the launch arguments of a graph are fixed
+ * when it is captured.  The record (nmb_adamw_hyper_bytes bytes, 4-byte
+ * aligned, in device memory) is what nmb_adamw_hyper writes into host memory
+ * for (lr, beta1, beta2, eps, weight_decay, step): the same fp32 scalars
+ * nmb_adamw_step forms, so both entry points update bit-identically.  The
+ * caller copies the record to the device before each replay. */
+int nmb_adamw_hyper_bytes(size_t* bytes);
+int nmb_adamw_hyper(double lr, double beta1, double beta2, double eps, double weight_decay,
+                    int64_t step, void* record);
+int nmb_adamw_step_hyper(const uint64_t* params, const uint64_t* grads, const int64_t* offsets,
+                         int n_tensors, int64_t total_elements, float* master, float* exp_avg,
+                         float* exp_avg_sq, int param_dtype, int grad_dtype, const void* hyper,
+                         float max_norm, float* norm_out, void* workspace, size_t workspace_bytes,
+                         hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -91,6 +91,11 @@ SIGNATURES: dict[str, list] = {
         _p, _p, _p, _i32, _i64, _p, _p, _p, _i32, _i32, _f64, _f64, _f64, _f64, _f64, _i64, _f32,
         _p, _p, _sz, _p,
     ],
+    "nmb_adamw_hyper_bytes": [_psz],
+    "nmb_adamw_hyper": [_f64, _f64, _f64, _f64, _f64, _i64, _p],
+    "nmb_adamw_step_hyper": [
+        _p, _p, _p, _i32, _i64, _p, _p, _p, _i32, _i32, _p, _f32, _p, _p, _sz, _p,
+    ],
 }
 _RESTYPES = {"nmb_last_error": ctypes.c_char_p}
 

@@ -143,6 +143,25 @@ struct AdamArgs {
   int has_decay;
 };
 
+// The update's fp32 scalars from the reference's Python scalars
+// (_zero.py:176-189), each formed in double and rounded once.
+AdamArgs make_args(double lr, double beta1, double beta2, double eps, double weight_decay,
+                   int64_t step) {
+  const double bc1 = 1.0 - pow(beta1, static_cast<double>(step));
+  const double bc2 = 1.0 - pow(beta2, static_cast<double>(step));
+  AdamArgs a;
+  a.b1 = static_cast<float>(beta1);
+  a.one_minus_b1 = static_cast<float>(1.0 - beta1);
+  a.b2 = static_cast<float>(beta2);
+  a.one_minus_b2 = static_cast<float>(1.0 - beta2);
+  a.has_decay = weight_decay != 0.0;
+  a.decay = static_cast<float>(1.0 - lr * weight_decay);
+  a.eps = static_cast<float>(eps);
+  a.sqrt_bc2 = static_cast<float>(pow(bc2, 0.5));
+  a.neg_step = static_cast<float>(-(lr / bc1));
+  return a;
+}
+
 // One element of the update, the reference's tensor operations in their order
 // (data_parallel/_zero.py:184-189), rounded as torch's kernels round them:
 //   m.mul_(b1).add_(g, alpha=1-b1)       m = fma(1-b1, g, m*b1)  (add with alpha is a fused multiply-add)
@@ -172,7 +191,10 @@ __global__ __launch_bounds__(256) void adamw_kernel(const uint64_t* __restrict__
                                                     float* __restrict__ exp_avg,
                                                     float* __restrict__ exp_avg_sq,
                                                     const float* __restrict__ scalars,
-                                                    AdamArgs a) {
+                                                    AdamArgs a_arg,
+                                                    const AdamArgs* __restrict__ a_dev) {
+  // the scalars by value, or (a replayed graph) from device memory
+  const AdamArgs a = a_dev != nullptr ? *a_dev : a_arg;
   const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kChunk;
   const int64_t c1 = min(total, c0 + kChunk);
   const float coef = scalars[1];
@@ -239,60 +261,105 @@ extern "C" int nmb_adamw_workspace_bytes(int64_t total_elements, size_t* bytes) 
   return NMB_OK;
 }
 
+namespace nmb {
+namespace {
+
+int check_hyper(double lr, double beta1, double beta2, double eps, int64_t step) {
+  NMB_REQUIRE(step >= 1, "adamw_step: step must be >= 1, got %lld", (long long)step);
+  NMB_REQUIRE(lr > 0.0 && eps > 0.0 && beta1 >= 0.0 && beta1 < 1.0 && beta2 >= 0.0 && beta2 < 1.0,
+              "adamw_step: invalid hyper-parameters");
+  return NMB_OK;
+}
+
+// sumsq, clip coefficient, update; the update's scalars are a_val, or *a_dev
+// when a_dev is given
+int step_impl(const uint64_t* params, const uint64_t* grads, const int64_t* offsets, int n_tensors,
+              int64_t total_elements, float* master, float* exp_avg, float* exp_avg_sq,
+              int param_dtype, int grad_dtype, const AdamArgs& a_val, const AdamArgs* a_dev,
+              float max_norm, float* norm_out, void* workspace, size_t workspace_bytes,
+              hipStream_t stream) {
+  NMB_REQUIRE(params && grads && offsets && master && exp_avg && exp_avg_sq,
+              "adamw_step: null argument");
+  NMB_REQUIRE(n_tensors > 0 && total_elements > 0, "adamw_step: empty parameter set");
+  const int64_t nblocks = (total_elements + kChunk - 1) / kChunk;
+  NMB_REQUIRE(nblocks < (int64_t{1} << 30), "adamw_step: too many elements");
+  const size_t need = static_cast<size_t>(nblocks + 4) * sizeof(float);
+  NMB_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+              "adamw_step: workspace of %zu bytes is smaller than the %zu required",
+              workspace_bytes, need);
+  NMB_REQUIRE_SUPPORTED((param_dtype == NMB_BF16 && grad_dtype == NMB_BF16) ||
+                            (param_dtype == NMB_F32 && grad_dtype == NMB_F32) ||
+                            (param_dtype == NMB_BF16 && grad_dtype == NMB_F32),
+                        "adamw_step: unsupported dtype pair %d/%d", param_dtype, grad_dtype);
+  float* partial = static_cast<float*>(workspace);
+  float* scalars = norm_out != nullptr ? norm_out : partial + nblocks;
+  const unsigned grid = static_cast<unsigned>(nblocks);
+  if (grad_dtype == NMB_BF16)
+    hipLaunchKernelGGL(sumsq_kernel<bf16>, dim3(grid), dim3(256), 0, stream, grads, offsets,
+                       n_tensors, total_elements, partial);
+  else
+    hipLaunchKernelGGL(sumsq_kernel<float>, dim3(grid), dim3(256), 0, stream, grads, offsets,
+                       n_tensors, total_elements, partial);
+  NMB_CHECK_LAUNCH("adamw_step(sumsq)");
+  hipLaunchKernelGGL(clip_coef_kernel, dim3(1), dim3(256), 0, stream, partial,
+                     static_cast<int>(nblocks), max_norm, scalars);
+  NMB_CHECK_LAUNCH("adamw_step(clip)");
+#define NMB_ADAM(P, G)                                                                        \
+  hipLaunchKernelGGL((adamw_kernel<P, G>), dim3(grid), dim3(256), 0, stream, params, grads,   \
+                     offsets, n_tensors, total_elements, master, exp_avg, exp_avg_sq, scalars, \
+                     a_val, a_dev)
+  if (param_dtype == NMB_BF16 && grad_dtype == NMB_BF16) NMB_ADAM(bf16, bf16);
+  else if (param_dtype == NMB_F32) NMB_ADAM(float, float);
+  else NMB_ADAM(bf16, float);
+#undef NMB_ADAM
+  NMB_CHECK_LAUNCH("adamw_step(update)");
+  return NMB_OK;
+}
+
+}  // namespace
+}  // namespace nmb
+
 extern "C" int nmb_adamw_step(const uint64_t* params, const uint64_t* grads,
                               const int64_t* offsets, int n_tensors, int64_t total_elements,
                               float* master, float* exp_avg, float* exp_avg_sq, int param_dtype,
                               int grad_dtype, double lr, double beta1, double beta2, double eps,
                               double weight_decay, int64_t step, float max_norm, float* norm_out,
                               void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  NMB_REQUIRE(params && grads && offsets && master && exp_avg && exp_avg_sq,
-              "adamw_step: null argument");
-  NMB_REQUIRE(n_tensors > 0 && total_elements > 0, "adamw_step: empty parameter set");
-  NMB_REQUIRE(step >= 1, "adamw_step: step must be >= 1, got %lld", (long long)step);
-  NMB_REQUIRE(lr > 0.0 && eps > 0.0 && beta1 >= 0.0 && beta1 < 1.0 && beta2 >= 0.0 && beta2 < 1.0,
-              "adamw_step: invalid hyper-parameters");
-  const int64_t nblocks = (total_elements + nmb::kChunk - 1) / nmb::kChunk;
-  NMB_REQUIRE(nblocks < (int64_t{1} << 30), "adamw_step: too many elements");
-  const size_t need = static_cast<size_t>(nblocks + 4) * sizeof(float);
-  NMB_REQUIRE(workspace != nullptr && workspace_bytes >= need,
-              "adamw_step: workspace of %zu bytes is smaller than the %zu required",
-              workspace_bytes, need);
-  float* partial = static_cast<float*>(workspace);
-  float* scalars = norm_out != nullptr ? norm_out : partial + nblocks;
-  const unsigned grid = static_cast<unsigned>(nblocks);
-  if (grad_dtype == NMB_BF16)
-    hipLaunchKernelGGL(nmb::sumsq_kernel<nmb::bf16>, dim3(grid), dim3(256), 0, stream, grads,
-                       offsets, n_tensors, total_elements, partial);
-  else if (grad_dtype == NMB_F32)
-    hipLaunchKernelGGL(nmb::sumsq_kernel<float>, dim3(grid), dim3(256), 0, stream, grads, offsets,
-                       n_tensors, total_elements, partial);
-  else
-    NMB_REQUIRE_SUPPORTED(false, "adamw_step: unsupported grad dtype %d", grad_dtype);
-  NMB_CHECK_LAUNCH("adamw_step(sumsq)");
-  hipLaunchKernelGGL(nmb::clip_coef_kernel, dim3(1), dim3(256), 0, stream, partial,
-                     static_cast<int>(nblocks), max_norm, scalars);
-  NMB_CHECK_LAUNCH("adamw_step(clip)");
-  // the reference's Python scalars (_zero.py:176-189), in double
-  const double bc1 = 1.0 - pow(beta1, static_cast<double>(step));
-  const double bc2 = 1.0 - pow(beta2, static_cast<double>(step));
-  nmb::AdamArgs a;
-  a.b1 = static_cast<float>(beta1);
-  a.one_minus_b1 = static_cast<float>(1.0 - beta1);
-  a.b2 = static_cast<float>(beta2);
-  a.one_minus_b2 = static_cast<float>(1.0 - beta2);
-  a.has_decay = weight_decay != 0.0;
-  a.decay = static_cast<float>(1.0 - lr * weight_decay);
-  a.eps = static_cast<float>(eps);
-  a.sqrt_bc2 = static_cast<float>(pow(bc2, 0.5));
-  a.neg_step = static_cast<float>(-(lr / bc1));
-#define NMB_ADAM(P, G)                                                                        \
-  hipLaunchKernelGGL((nmb::adamw_kernel<P, G>), dim3(grid), dim3(256), 0, stream, params, grads, \
-                     offsets, n_tensors, total_elements, master, exp_avg, exp_avg_sq, scalars, a)
-  if (param_dtype == NMB_BF16 && grad_dtype == NMB_BF16) NMB_ADAM(nmb::bf16, nmb::bf16);
-  else if (param_dtype == NMB_F32 && grad_dtype == NMB_F32) NMB_ADAM(float, float);
-  else if (param_dtype == NMB_BF16 && grad_dtype == NMB_F32) NMB_ADAM(nmb::bf16, float);
-  else NMB_REQUIRE_SUPPORTED(false, "adamw_step: unsupported dtype pair %d/%d", param_dtype, grad_dtype);
-#undef NMB_ADAM
-  NMB_CHECK_LAUNCH("adamw_step(update)");
+  const int st = nmb::check_hyper(lr, beta1, beta2, eps, step);
+  if (st != NMB_OK) return st;
+  return nmb::step_impl(params, grads, offsets, n_tensors, total_elements, master, exp_avg,
+                        exp_avg_sq, param_dtype, grad_dtype,
+                        nmb::make_args(lr, beta1, beta2, eps, weight_decay, step), nullptr,
+                        max_norm, norm_out, workspace, workspace_bytes, stream);
+}
+
+extern "C" int nmb_adamw_hyper_bytes(size_t* bytes) {
+  NMB_REQUIRE(bytes != nullptr, "adamw_hyper_bytes: null argument");
+  *bytes = sizeof(nmb::AdamArgs);
   return NMB_OK;
+}
+
+extern "C" int nmb_adamw_hyper(double lr, double beta1, double beta2, double eps,
+                               double weight_decay, int64_t step, void* record) {
+  NMB_REQUIRE(record != nullptr, "adamw_hyper: null record");
+  const int st = nmb::check_hyper(lr, beta1, beta2, eps, step);
+  if (st != NMB_OK) return st;
+  const nmb::AdamArgs a = nmb::make_args(lr, beta1, beta2, eps, weight_decay, step);
+  __builtin_memcpy(record, &a, sizeof(a));
+  return NMB_OK;
+}
+
+extern "C" int nmb_adamw_step_hyper(const uint64_t* params, const uint64_t* grads,
+                                    const int64_t* offsets, int n_tensors, int64_t total_elements,
+                                    float* master, float* exp_avg, float* exp_avg_sq,
+                                    int param_dtype, int grad_dtype, const void* hyper,
+                                    float max_norm, float* norm_out, void* workspace,
+                                    size_t workspace_bytes, hipStream_t stream) {
+  NMB_REQUIRE(hyper != nullptr, "adamw_step_hyper: null hyper-parameter record");
+  NMB_REQUIRE((reinterpret_cast<uintptr_t>(hyper) & 3) == 0,
+              "adamw_step_hyper: the record must be 4-byte aligned");
+  return nmb::step_impl(params, grads, offsets, n_tensors, total_elements, master, exp_avg,
+                        exp_avg_sq, param_dtype, grad_dtype, nmb::AdamArgs{},
+                        static_cast<const nmb::AdamArgs*>(hyper), max_norm, norm_out, workspace,
+                        workspace_bytes, stream);
 }

@@ -566,10 +566,15 @@ class GPTModel(nn.Module):
     def forward(self, input_ids: Tensor | None = None, *, labels: Tensor | None = None,
                 position_ids: Tensor | None = None, hidden_states: Tensor | None = None,
                 microbatch_index: int = 0) -> GPTOutput:
-        # the loss's target-range check, enqueued before the layers (see TargetCheck)
+        # the loss's target-range check, enqueued before the layers (see TargetCheck);
+        # a host wait cannot be captured in a HIP graph, so under capture the
+        # caller validates the targets before each replay (CapturedTrainStep)
         check = None
         if labels is not None and self.lm_head is not None:
-            check = Fn.TargetCheck(labels, self.lm_head.weight.shape[0], Fn.IGNORE_INDEX)
+            if labels.is_cuda and torch.cuda.is_current_stream_capturing():
+                check = False
+            else:
+                check = Fn.TargetCheck(labels, self.lm_head.weight.shape[0], Fn.IGNORE_INDEX)
         # the tied LM head passes its table gradient to the embedding's backward
         tie = None
         if (labels is not None and self.embedding is not None and self.lm_head is not None

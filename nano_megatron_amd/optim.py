@@ -50,6 +50,7 @@ class MasterAdamW:
         self._param_table = torch.tensor([p.data_ptr() for p in self.params], dtype=torch.int64,
                                          device=device)
         self._param_ptrs = [p.data_ptr() for p in self.params]
+        self._graph: dict | None = None  # buffers of a captured step (prepare_graph)
 
     @property
     def last_grad_norm(self) -> Tensor:
@@ -61,6 +62,40 @@ class MasterAdamW:
                 p.grad = None
             elif p.grad is not None:
                 p.grad.zero_()
+
+    def prepare_graph(self) -> None:
+        """Buffers a step captured in a HIP graph needs, allocated before the
+        capture: a device record of the update's scalars (``advance_graph_step``
+        refreshes it before each replay; the launch arguments of a graph are
+        fixed) and a pinned staging copy of the gradient pointer table, which
+        the captured step copies to the device.  Refreshes the parameter table
+        if the parameters moved."""
+        ptrs = [p.data_ptr() for p in self.params]
+        if ptrs != self._param_ptrs:
+            self._param_table = torch.tensor(ptrs, dtype=torch.int64, device=self.device)
+            self._param_ptrs = ptrs
+        nb = _lib.ctypes.c_size_t(0)
+        _lib.call("nmb_adamw_hyper_bytes", _lib.ctypes.byref(nb))
+        n = len(self.params)
+        self._graph = dict(
+            hyper_host=torch.empty(nb.value, dtype=torch.uint8, pin_memory=True),
+            hyper_dev=torch.empty(nb.value, dtype=torch.uint8, device=self.device),
+            table_host=torch.empty(n, dtype=torch.int64, pin_memory=True),
+            table_dev=torch.empty(n, dtype=torch.int64, device=self.device),
+        )
+
+    def advance_graph_step(self) -> None:
+        """Before a replay of a captured step: the step count advances as an
+        eager ``step`` would advance it, and the update's scalars for that
+        step go to the device on the current stream.  The caller has waited
+        for the previous replay (the host record is reused)."""
+        if self._graph is None:
+            raise ValueError("MasterAdamW.advance_graph_step: call prepare_graph() before capturing")
+        self.step_count += 1
+        host = self._graph["hyper_host"]
+        _lib.call("nmb_adamw_hyper", self.lr, self.betas[0], self.betas[1], self.eps,
+                  self.weight_decay, self.step_count, host.data_ptr())
+        self._graph["hyper_dev"].copy_(host, non_blocking=True)
 
     @torch.no_grad()
     def step(self) -> None:
@@ -76,6 +111,9 @@ class MasterAdamW:
         if len(gdt) != 1:
             raise ValueError("MasterAdamW.step: gradients must share one dtype")
         ptrs = [p.data_ptr() for p in self.params]
+        if self.device.type == "cuda" and torch.cuda.is_current_stream_capturing():
+            self._captured_step(grads, gdt.pop(), ptrs)
+            return
         if ptrs != self._param_ptrs:  # parameters were moved or repacked
             self._param_table = torch.tensor(ptrs, dtype=torch.int64, device=self.device)
             self._param_ptrs = ptrs
@@ -92,3 +130,25 @@ class MasterAdamW:
             _lib.stream_of(self.master),
         )
         self._keep = (grads, grad_table)  # alive until the next step's kernels are enqueued
+
+    def _captured_step(self, grads: list[Tensor], gdtype: torch.dtype, ptrs: list[int]) -> None:
+        """The step as a graph records it: the gradient table is copied from the
+        pinned staging buffer (a copy node), the scalars come from the device
+        record; the step count advances per replay (``advance_graph_step``)."""
+        if self._graph is None:
+            raise ValueError("MasterAdamW.step under HIP graph capture needs prepare_graph() first")
+        if ptrs != self._param_ptrs:
+            raise ValueError("MasterAdamW.step under HIP graph capture: the parameters moved since "
+                             "prepare_graph()")
+        table_host, table_dev = self._graph["table_host"], self._graph["table_dev"]
+        table_host.copy_(torch.tensor([g.data_ptr() for g in grads], dtype=torch.int64))
+        table_dev.copy_(table_host, non_blocking=True)
+        _lib.call(
+            "nmb_adamw_step_hyper", self._param_table.data_ptr(), table_dev.data_ptr(),
+            self.offsets.data_ptr(), len(self.params), self.total, self.master.data_ptr(),
+            self.exp_avg.data_ptr(), self.exp_avg_sq.data_ptr(),
+            _lib.dtype_code(self.params[0].dtype), _lib.dtype_code(gdtype),
+            self._graph["hyper_dev"].data_ptr(), self.max_norm, self.stats.data_ptr(),
+            self.workspace.data_ptr(), self.workspace.numel(), _lib.stream_of(self.master),
+        )
+        self._keep = (grads, table_dev)

@@ -114,6 +114,37 @@ def test_gemm_f32_rejects_bad_arguments() -> None:
     assert st == _lib.NMB_EINVAL and b"needs C" in lib.nmb_last_error()
 
 
+def test_adamw_hyper_record_holds_the_double_formed_scalars() -> None:
+    """nmb_adamw_hyper (host arithmetic only) writes the fp32 scalars of the
+    update, each formed in double from the Python-float hyper-parameters and
+    rounded once (data_parallel/_zero.py:176-189): checked against numpy."""
+    import numpy as np
+
+    lib = _lib.load()
+    nb = ctypes.c_size_t(0)
+    assert lib.nmb_adamw_hyper_bytes(ctypes.byref(nb)) == _lib.NMB_OK and nb.value == 36
+    rec = (ctypes.c_uint8 * nb.value)()
+    lr, b1, b2, eps, wd = 3e-4, 0.9, 0.95, 1e-8, 0.1
+    for step in (1, 2, 7, 1000):
+        assert lib.nmb_adamw_hyper(lr, b1, b2, eps, wd, step, rec) == _lib.NMB_OK
+        got = np.frombuffer(bytes(rec), dtype=np.float32, count=8)
+        has_decay = np.frombuffer(bytes(rec), dtype=np.int32, count=1, offset=32)[0]
+        bc1, bc2 = 1.0 - b1**step, 1.0 - b2**step
+        want = np.array([b1, 1.0 - b1, b2, 1.0 - b2, 1.0 - lr * wd, eps, bc2**0.5, -(lr / bc1)],
+                        dtype=np.float64).astype(np.float32)
+        assert np.array_equal(got, want), (step, got, want)
+        assert has_decay == 1
+    assert lib.nmb_adamw_hyper(lr, b1, b2, eps, 0.0, 1, rec) == _lib.NMB_OK
+    assert np.frombuffer(bytes(rec), dtype=np.int32, count=1, offset=32)[0] == 0
+    assert lib.nmb_adamw_hyper(lr, b1, b2, eps, wd, 0, rec) == _lib.NMB_EINVAL
+    assert b"step" in lib.nmb_last_error()
+    assert lib.nmb_adamw_hyper(lr, 1.0, b2, eps, wd, 1, rec) == _lib.NMB_EINVAL
+    assert lib.nmb_adamw_hyper(lr, b1, b2, eps, wd, 1, None) == _lib.NMB_EINVAL
+    st = lib.nmb_adamw_step_hyper(FAKE, FAKE, FAKE, 1, 16, FAKE, FAKE, FAKE, _lib.NMB_BF16,
+                                  _lib.NMB_BF16, None, 1.0, None, FAKE, 1 << 20, None)
+    assert st == _lib.NMB_EINVAL and b"hyper" in lib.nmb_last_error()
+
+
 def test_python_wrapper_maps_status_to_exceptions() -> None:
     with pytest.raises(ValueError, match="multiple of 8"):
         _lib.call("nmb_rmsnorm_fwd", FAKE, FAKE, FAKE, None, 4, 12, 1e-5, _lib.NMB_BF16, None)

@@ -1,0 +1,103 @@
+"""The training step captured as a HIP graph (CapturedTrainStep) against eager
+steps: replays give the eager losses, parameters and optimizer state bit for
+bit, with eager work and a synchronisation between replays; out-of-range
+targets raise before any update, as in the eager forward."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import nano_megatron_amd as nm
+from nano_megatron_amd.graph import CapturedTrainStep
+from nano_megatron_amd.optim import MasterAdamW
+
+pytestmark = pytest.mark.gpu
+
+VOCAB = 1024
+
+
+def small_model(device, mode: str, offload: bool = False):
+    cfg = nm.GPTConfig(layers=2, hidden_size=256, ffn_hidden_size=688, heads=4, seq_length=128,
+                       vocab_size=VOCAB, norm_epsilon=1e-5, rope_theta=1e4)
+    ck = nm.ActivationCheckpointConfig(mode=mode, offload_saved_tensors=offload)
+    torch.manual_seed(0)
+    return nm.GPTModel(cfg, activation_checkpoint_config=ck).to(device=device, dtype=torch.bfloat16).train()
+
+
+def batches(device, n: int):
+    g = torch.Generator(device=device).manual_seed(7)
+    out = []
+    for _ in range(n):
+        ids = torch.randint(0, VOCAB, (2, 129), device=device, generator=g)
+        out.append((ids[:, :128].contiguous(), ids[:, 1:].contiguous()))
+    return out
+
+
+def optimizer(model):
+    return MasterAdamW(model.parameters(), lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1,
+                       clip_grad_norm=1.0)
+
+
+@pytest.mark.parametrize("mode", ["full", "none"])
+def test_captured_step_replays_match_eager_steps(device, mode) -> None:
+    data = batches(device, 4)
+    eager = small_model(device, mode)
+    opt_e = optimizer(eager)
+    losses_e = []
+    for x, y in data:
+        opt_e.zero_grad()
+        loss = eager(x, labels=y).loss
+        loss.backward()
+        opt_e.step()
+        losses_e.append(loss.detach().clone())
+
+    model = small_model(device, mode)
+    opt = optimizer(model)
+    cap = CapturedTrainStep(model, opt, data[0][0], data[0][1])
+    losses_g = []
+    for x, y in data:
+        losses_g.append(cap.step(x, y).clone())
+        # the program's own work and a synchronisation between replays
+        a = torch.randn(256, 256, device=device)
+        (a @ a).sum().item()
+        torch.cuda.synchronize()
+
+    for i, (le, lg) in enumerate(zip(losses_e, losses_g)):
+        assert torch.isfinite(le) and torch.equal(le, lg), f"step {i}: {le.item()} vs {lg.item()}"
+    assert opt.step_count == opt_e.step_count == len(data)
+    for (name, p), q in zip(eager.named_parameters(), model.parameters()):
+        assert torch.equal(p, q), name
+    for attr in ("master", "exp_avg", "exp_avg_sq"):
+        assert torch.equal(getattr(opt_e, attr), getattr(opt, attr)), attr
+    assert torch.equal(opt_e.last_grad_norm, opt.last_grad_norm)
+
+
+def test_captured_step_rejects_out_of_range_labels(device) -> None:
+    (x, y), = batches(device, 1)
+    model = small_model(device, "full")
+    opt = optimizer(model)
+    cap = CapturedTrainStep(model, opt, x, y)
+    before = [p.detach().clone() for p in model.parameters()]
+    bad = y.clone()
+    bad[1, 5] = VOCAB
+    with pytest.raises(ValueError, match="outside"):
+        cap.step(x, bad)
+    torch.cuda.synchronize()
+    assert opt.step_count == 0
+    for a, p in zip(before, model.parameters()):
+        assert torch.equal(a, p)
+    # a valid batch afterwards still steps
+    loss = cap.step(x, y)
+    assert torch.isfinite(loss) and opt.step_count == 1
+
+
+def test_captured_step_refuses_offload_and_shape_changes(device) -> None:
+    (x, y), = batches(device, 1)
+    model = small_model(device, "full", offload=True)
+    with pytest.raises(ValueError, match="offload_saved_tensors"):
+        CapturedTrainStep(model, optimizer(model), x, y)
+    model = small_model(device, "full")
+    cap = CapturedTrainStep(model, optimizer(model), x, y)
+    with pytest.raises(ValueError, match="shape"):
+        cap.step(x[:1], y[:1])

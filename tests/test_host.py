@@ -66,6 +66,14 @@ def test_kernels_refuse_cpu_tensors() -> None:
                                  torch.zeros(2, 3, dtype=torch.long))
 
 
+def test_captured_step_refuses_cpu_tensors() -> None:
+    from nano_megatron_amd.graph import CapturedTrainStep
+
+    x = torch.zeros(2, 8, dtype=torch.long)
+    with pytest.raises(ValueError, match="GPU"):
+        CapturedTrainStep(torch.nn.Linear(2, 2), None, x, x)
+
+
 def test_target_check_rules() -> None:
     """The cross entropy's target-range rule (tensor_parallel/cross_entropy.py:
     109-114): ids in [0, vocab) or ignore_index pass; anything else raises."""
