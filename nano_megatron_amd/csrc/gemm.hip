@@ -355,6 +355,53 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void gemm_kernel(GemmArgs
     // the product only (the recompute): no activation math in this epilogue,
     // whose time adds to the kernel's (every workgroup reaches it together)
     const bool act = g.d != nullptr;
+    if constexpr (TBN == 256 && NW == 8) {
+      // The product only: through LDS, as the plain epilogue below, the
+      // [gate | up] tile (256 x 256: the tile's 128 gate columns, then its 128
+      // up columns) stored as whole rows (3.9% faster at 8192 x 5472 x 1024;
+      // with the activation, whose 128-column tile gains less than the extra
+      // pass costs, the stores stay direct).
+      if (!act) {
+        constexpr int H = TBN / 2;
+        constexpr int RPA = (S * TBM * BKT) / TBN;
+        auto at = [&](int r, int c) -> bf16* {
+          bf16* rp = r < RPA ? &sA[0][0] + r * TBN : &sB[0][0] + (r - RPA) * TBN;
+          return rp + 8 * ((c >> 3) ^ (r & 15)) + (c & 4);
+        };
+        __syncthreads();  // every wave is done with the operand stages
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            if (j & 2) continue;
+            const int r = wm + 16 * i + l16;
+            const int oc = 32 * ((wn + 16 * j) >> 6) + 16 * (j & 1) + 4 * q4;
+            bf16x4 gv, uv;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              gv[e] = static_cast<bf16>(acc[i][j][e]);
+              uv[e] = static_cast<bf16>(acc[i][j + 2][e]);
+            }
+            *reinterpret_cast<bf16x4*>(at(r, oc)) = gv;
+            *reinterpret_cast<bf16x4*>(at(r, H + oc)) = uv;
+          }
+        }
+        __syncthreads();
+        constexpr int LPR = TBN / 8, RPI = 64 / LPR;  // 32 lanes per row: 16 gate, 16 up
+        constexpr int ROWS_PER_WAVE = TBM / NW;
+        const int sl = lane % LPR;
+        const int half = sl / (LPR / 2), col = 8 * (sl % (LPR / 2));
+#pragma unroll
+        for (int it = 0; it < ROWS_PER_WAVE / RPI; ++it) {
+          const int r = wave * ROWS_PER_WAVE + it * RPI + lane / LPR;
+          const bf16x8 v = *reinterpret_cast<const bf16x8*>(at(r, 8 * sl));
+          const int m = m0 + r, n = n0 + col;
+          if (m < g.M && n < g.N && g.gu != nullptr)
+            *reinterpret_cast<bf16x8*>(g.gu + static_cast<int64_t>(m) * g.ldgu + half * g.N + n) = v;
+        }
+        return;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int m = m0 + wm + 16 * i + l16;
