@@ -333,15 +333,42 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void gemm_kernel(GemmArgs
   // acc[i][j][e] = D[m0 + wm + 16 i + l16][n0 + wn + 16 j + 4 q4 + e]
   const int l16 = lane & 15, q4 = lane >> 4;
   if (g.splits > 1) {
+    // fp32 partials through LDS in passes of PR tile rows (as many as the
+    // operand stages hold), each row then stored by whole 16-byte slots; the
+    // row's slot s sits at s ^ (r & 15), so a fragment's 16 rows hit distinct
+    // banks
     float* part = g.partial + static_cast<int64_t>(split) * g.M * g.N;
+    constexpr int ROW_BYTES = TBN * 4;
+    constexpr int RA = (S * TBM * BKT * 2) / ROW_BYTES;  // rows in sA, the rest in sB
+    constexpr int CAP = RA + (S * TBN * BKT * 2) / ROW_BYTES;
+    constexpr int PR = CAP >= TBM ? TBM : (CAP >= 128 ? 128 : (CAP >= 64 ? 64 : 32));
+    static_assert(PR <= CAP && PR % 16 == 0 && TBM % PR == 0, "partial rows per pass");
+    auto slot_at = [&](int lr, int slot) -> float* {
+      float* rp = lr < RA ? reinterpret_cast<float*>(&sA[0][0]) + lr * TBN
+                          : reinterpret_cast<float*>(&sB[0][0]) + (lr - RA) * TBN;
+      return rp + 4 * (slot ^ (lr & 15));
+    };
+    constexpr int LPR = TBN / 4, RPI = 64 / LPR, ROWS_PER_WAVE = PR / NW;
+    static_assert(ROWS_PER_WAVE % RPI == 0, "whole store instructions per wave");
+    const int sl = lane % LPR;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int m = m0 + wm + 16 * i + l16;
-      if (m >= g.M) continue;
+    for (int p0 = 0; p0 < TBM; p0 += PR) {
+      __syncthreads();  // the operand stages (first pass) or the last pass's rows are free
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int n = n0 + wn + 16 * j + 4 * q4;
-        if (n < g.N) *reinterpret_cast<f32x4*>(part + static_cast<int64_t>(m) * g.N + n) = acc[i][j];
+      for (int i = 0; i < TM; ++i) {
+        const int lr = wm + 16 * i + l16 - p0;
+        if (lr < 0 || lr >= PR) continue;  // uniform over the 16 rows of a fragment
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          *reinterpret_cast<f32x4*>(slot_at(lr, (wn + 16 * j + 4 * q4) >> 2)) = acc[i][j];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int it = 0; it < ROWS_PER_WAVE / RPI; ++it) {
+        const int lr = wave * ROWS_PER_WAVE + it * RPI + lane / LPR;
+        const f32x4 v = *reinterpret_cast<const f32x4*>(slot_at(lr, sl));
+        const int m = m0 + p0 + lr, n = n0 + 4 * sl;
+        if (m < g.M && n < g.N) *reinterpret_cast<f32x4*>(part + static_cast<int64_t>(m) * g.N + n) = v;
       }
     }
     return;
