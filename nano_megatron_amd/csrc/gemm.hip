@@ -332,36 +332,41 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void gemm_kernel(GemmArgs
 
   // acc[i][j][e] = D[m0 + wm + 16 i + l16][n0 + wn + 16 j + 4 q4 + e]
   const int l16 = lane & 15, q4 = lane >> 4;
+  // fp32 rows of the tile through LDS in passes of PR tile rows (as many as
+  // the operand stages hold); the row's 16-byte slot s sits at s ^ (r & 15),
+  // so a fragment's 16 rows hit distinct banks.  stage_f32(p0) writes this
+  // wave's rows [p0, p0 + PR) of acc (alpha and beta are applied as the rows
+  // are stored).
+  constexpr int ROW_BYTES = TBN * 4;
+  constexpr int RA = (S * TBM * BKT * 2) / ROW_BYTES;  // rows in sA, the rest in sB
+  constexpr int CAP = RA + (S * TBN * BKT * 2) / ROW_BYTES;
+  constexpr int PR = CAP >= TBM ? TBM : (CAP >= 128 ? 128 : (CAP >= 64 ? 64 : 32));
+  static_assert(PR <= CAP && PR % 16 == 0 && TBM % PR == 0, "fp32 rows per pass");
+  auto slot_at = [&](int lr, int slot) -> float* {
+    float* rp = lr < RA ? reinterpret_cast<float*>(&sA[0][0]) + lr * TBN
+                        : reinterpret_cast<float*>(&sB[0][0]) + (lr - RA) * TBN;
+    return rp + 4 * (slot ^ (lr & 15));
+  };
+  auto stage_f32 = [&](int p0) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int lr = wm + 16 * i + l16 - p0;
+      if (lr < 0 || lr >= PR) continue;  // uniform over the 16 rows of a fragment
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        *reinterpret_cast<f32x4*>(slot_at(lr, (wn + 16 * j + 4 * q4) >> 2)) = acc[i][j];
+    }
+  };
   if (g.splits > 1) {
-    // fp32 partials through LDS in passes of PR tile rows (as many as the
-    // operand stages hold), each row then stored by whole 16-byte slots; the
-    // row's slot s sits at s ^ (r & 15), so a fragment's 16 rows hit distinct
-    // banks
+    // fp32 partials, each row stored by whole 16-byte slots
     float* part = g.partial + static_cast<int64_t>(split) * g.M * g.N;
-    constexpr int ROW_BYTES = TBN * 4;
-    constexpr int RA = (S * TBM * BKT * 2) / ROW_BYTES;  // rows in sA, the rest in sB
-    constexpr int CAP = RA + (S * TBN * BKT * 2) / ROW_BYTES;
-    constexpr int PR = CAP >= TBM ? TBM : (CAP >= 128 ? 128 : (CAP >= 64 ? 64 : 32));
-    static_assert(PR <= CAP && PR % 16 == 0 && TBM % PR == 0, "partial rows per pass");
-    auto slot_at = [&](int lr, int slot) -> float* {
-      float* rp = lr < RA ? reinterpret_cast<float*>(&sA[0][0]) + lr * TBN
-                          : reinterpret_cast<float*>(&sB[0][0]) + (lr - RA) * TBN;
-      return rp + 4 * (slot ^ (lr & 15));
-    };
     constexpr int LPR = TBN / 4, RPI = 64 / LPR, ROWS_PER_WAVE = PR / NW;
     static_assert(ROWS_PER_WAVE % RPI == 0, "whole store instructions per wave");
     const int sl = lane % LPR;
 #pragma unroll
     for (int p0 = 0; p0 < TBM; p0 += PR) {
       __syncthreads();  // the operand stages (first pass) or the last pass's rows are free
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int lr = wm + 16 * i + l16 - p0;
-        if (lr < 0 || lr >= PR) continue;  // uniform over the 16 rows of a fragment
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          *reinterpret_cast<f32x4*>(slot_at(lr, (wn + 16 * j + 4 * q4) >> 2)) = acc[i][j];
-      }
+      stage_f32(p0);
       __syncthreads();
 #pragma unroll
       for (int it = 0; it < ROWS_PER_WAVE / RPI; ++it) {
@@ -461,27 +466,38 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void gemm_kernel(GemmArgs
     return;
   }
   if constexpr (RD == 0) {
-    // with a residual add (beta != 0) C is read in the fragment layout anyway:
-    // stored straight from the fragments (the staged form below was slower)
+    // with a residual add (beta != 0): the fp32 products go through LDS, and
+    // each lane then reads 8 columns of C, adds and stores them as 16 bytes
+    // (D = bf16(alpha * acc + beta * C), one rounding)
     if (g.beta != 0.f) {
+      constexpr int LPR = TBN / 8, RPI = 64 / LPR, ROWS_PER_WAVE = PR / NW;
+      static_assert(ROWS_PER_WAVE % RPI == 0, "whole store instructions per wave");
+      const int sl = lane % LPR;
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int m = m0 + wm + 16 * i + l16;
-        if (m >= g.M) continue;
+      for (int p0 = 0; p0 < TBM; p0 += PR) {
+        __syncthreads();  // the operand stages (first pass) or the last pass's rows are free
+        stage_f32(p0);
+        __syncthreads();
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          const int n = n0 + wn + 16 * j + 4 * q4;
-          if (n >= g.N) continue;
-          float v[4];
+        for (int it = 0; it < ROWS_PER_WAVE / RPI; ++it) {
+          const int lr = wave * ROWS_PER_WAVE + it * RPI + lane / LPR;
+          const int m = m0 + p0 + lr, n = n0 + 8 * sl;
+          if (m >= g.M || n >= g.N) continue;
+          const f32x4 lo = *reinterpret_cast<const f32x4*>(slot_at(lr, 2 * sl));
+          const f32x4 hi = *reinterpret_cast<const f32x4*>(slot_at(lr, 2 * sl + 1));
+          const bf16x8 cv = *reinterpret_cast<const bf16x8*>(g.c + static_cast<int64_t>(m) * g.ldc + n);
+          float v[8];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = g.alpha * acc[i][j][e];
-          const bf16x4 cv = *reinterpret_cast<const bf16x4*>(g.c + static_cast<int64_t>(m) * g.ldc + n);
+          for (int e = 0; e < 4; ++e) {
+            v[e] = g.alpha * lo[e];
+            v[4 + e] = g.alpha * hi[e];
+          }
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] += g.beta * static_cast<float>(cv[e]);
-          bf16x4 ov;
+          for (int e = 0; e < 8; ++e) v[e] += g.beta * static_cast<float>(cv[e]);
+          bf16x8 ov;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) ov[e] = static_cast<bf16>(v[e]);
-          *reinterpret_cast<bf16x4*>(g.d + static_cast<int64_t>(m) * g.ldd + n) = ov;
+          for (int e = 0; e < 8; ++e) ov[e] = static_cast<bf16>(v[e]);
+          *reinterpret_cast<bf16x8*>(g.d + static_cast<int64_t>(m) * g.ldd + n) = ov;
         }
       }
       return;
