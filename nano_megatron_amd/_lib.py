@@ -69,6 +69,14 @@ SIGNATURES: dict[str, list] = {
         _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _i64, _i64, _i64, _i64, _i64, _pi64, _pi64,
         _pi64, _i32, _i64, _f32, _p, _p, _i64, _p, _i64, _i64, _p,
     ],
+    "nmb_attn_masked_fwd": [
+        _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _pi64, _pi64, _pi64, _p, _i32,
+        _pi64, _i32, _i64, _f32, _i32, _p,
+    ],
+    "nmb_attn_masked_bwd": [
+        _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _i64, _i64, _i64, _i64, _i64, _i64, _pi64,
+        _pi64, _pi64, _p, _i32, _pi64, _i32, _i64, _f32, _i32, _p,
+    ],
     "nmb_embedding_fwd": [_p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "nmb_embedding_bwd": [_p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "nmb_ce_fwd": [_p, _i64, _p, _i64, _i64, _i64, _p, _p, _i32, _p],

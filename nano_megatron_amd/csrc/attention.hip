@@ -1119,34 +1119,64 @@ __global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel
   finish();
 }
 
-// ---------------------------------------------------------------- fp32 path
-// One wavefront per query row; lane owns head_dim elements lane and lane + 64.
-__device__ __forceinline__ float dot_row(const float* a, const float* b, int D, int lane) {
+// ---------------------------------------------------------------- generic path
+// One wavefront per query row; lane owns head_dim elements lane and lane + 64
+// (head_dim <= 128).  The fp32 configuration's attention, and attention with
+// an explicit mask in any supported dtype (the reference passes attention_mask
+// to SDPA, nn/kernels/torch_backend.py:60-76): MK 0 no mask, 1 a boolean mask
+// (one byte per entry, nonzero = attend), 2 an additive mask in the attention
+// dtype (added to the scaled scores; -inf drops the key).  A query row with no
+// visible key gives zeros and lse = -inf, as the safe softmax of the
+// reference's SDPA does.
+struct MaskRef {
+  const void* p;
+  int64_t sb, sh, sq, sk;  // element strides of [batch, q_heads, seq_q, seq_k] (0: broadcast)
+};
+
+template <typename T, int MK>
+__device__ __forceinline__ bool visible(const MaskRef& mr, int b, int h, int64_t i, int64_t j, float& add) {
+  if constexpr (MK == 0) {
+    return true;
+  } else {
+    const int64_t off = b * mr.sb + h * mr.sh + i * mr.sq + j * mr.sk;
+    if constexpr (MK == 1) {
+      return static_cast<const uint8_t*>(mr.p)[off] != 0;
+    } else {
+      add = to_f32(static_cast<const T*>(mr.p)[off]);
+      return add != -__builtin_inff();
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ float dot_row(const T* a, const T* b, int D, int lane) {
   float s = 0.f;
-  for (int d = lane; d < D; d += 64) s += a[d] * b[d];
+  for (int d = lane; d < D; d += 64) s += to_f32(a[d]) * to_f32(b[d]);
   return wave_sum(s);
 }
 
-__global__ __launch_bounds__(64) void attn_fwd_f32_kernel(const float* __restrict__ q, KVBlocks kv,
-                                                          float* __restrict__ o,
-                                                          float* __restrict__ lse, AttnShape p,
-                                                          int D) {
+template <typename T, int MK>
+__global__ __launch_bounds__(64) void attn_fwd_generic_kernel(const T* __restrict__ q, KVBlocks kv,
+                                                              T* __restrict__ o, float* __restrict__ lse,
+                                                              AttnShape p, int D, MaskRef mr) {
   const int lane = threadIdx.x;
   const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int hk = h / (p.Hq / p.Hkv);
-  const float* qr = q + b * p.q_sb + static_cast<int64_t>(i) * p.q_ss + h * p.q_sh;
+  const T* qr = q + b * p.q_sb + static_cast<int64_t>(i) * p.q_ss + h * p.q_sh;
   const int64_t qa = p.q_offset + i;
   float m = -__builtin_inff(), l = 0.f;
   float acc[2] = {0.f, 0.f};
   for (int blk = 0; blk < p.nblk; ++blk) {
-    const float* kb = static_cast<const float*>(kv.k[blk]) + b * p.kv_sb + hk * p.kv_sh;
-    const float* vb = static_cast<const float*>(kv.v[blk]) + b * p.kv_sb + hk * p.kv_sh;
+    const T* kb = static_cast<const T*>(kv.k[blk]) + b * p.kv_sb + hk * p.kv_sh;
+    const T* vb = static_cast<const T*>(kv.v[blk]) + b * p.kv_sb + hk * p.kv_sh;
     const int64_t koff = kv.koff[blk];
     for (int j = 0; j < p.Sk; ++j) {
       if (p.causal && koff + j > qa) break;
-      const float* kr = kb + static_cast<int64_t>(j) * p.kv_ss;
-      const float* vr = vb + static_cast<int64_t>(j) * p.kv_ss;
-      const float sc = dot_row(qr, kr, D, lane) * p.scale;
+      float add = 0.f;
+      if (!visible<T, MK>(mr, b, h, i, j, add)) continue;
+      const T* kr = kb + static_cast<int64_t>(j) * p.kv_ss;
+      const T* vr = vb + static_cast<int64_t>(j) * p.kv_ss;
+      const float sc = dot_row(qr, kr, D, lane) * p.scale + add;
       const float mnew = fmaxf(m, sc);
       const float alpha = expf(m - mnew);
       const float pv = expf(sc - mnew);
@@ -1154,65 +1184,69 @@ __global__ __launch_bounds__(64) void attn_fwd_f32_kernel(const float* __restric
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         const int d = lane + 64 * c;
-        if (d < D) acc[c] = acc[c] * alpha + pv * vr[d];
+        if (d < D) acc[c] = acc[c] * alpha + pv * to_f32(vr[d]);
       }
       m = mnew;
     }
   }
-  float* orow = o + b * p.o_sb + static_cast<int64_t>(i) * p.o_ss + h * p.o_sh;
+  T* orow = o + b * p.o_sb + static_cast<int64_t>(i) * p.o_ss + h * p.o_sh;
   const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
     const int d = lane + 64 * c;
-    if (d < D) orow[d] = acc[c] * inv;
+    if (d < D) orow[d] = from_f32<T>(acc[c] * inv);
   }
   if (lane == 0)
     lse[(static_cast<int64_t>(b) * p.Hq + h) * p.Sq + i] = l > 0.f ? m + logf(l) : -__builtin_inff();
 }
 
-__global__ __launch_bounds__(64) void attn_bwd_dq_f32_kernel(
-    const float* __restrict__ q, KVBlocks kv, const float* __restrict__ dout,
-    const float* __restrict__ lse, const float* __restrict__ delta, float* __restrict__ dq,
-    AttnShape p, int D) {
+template <typename T, int MK>
+__global__ __launch_bounds__(64) void attn_bwd_dq_generic_kernel(
+    const T* __restrict__ q, KVBlocks kv, const T* __restrict__ dout,
+    const float* __restrict__ lse, const float* __restrict__ delta, T* __restrict__ dq,
+    AttnShape p, int D, MaskRef mr) {
   const int lane = threadIdx.x;
   const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int hk = h / (p.Hq / p.Hkv);
-  const float* qr = q + b * p.q_sb + static_cast<int64_t>(i) * p.q_ss + h * p.q_sh;
-  const float* dr = dout + b * p.o_sb + static_cast<int64_t>(i) * p.o_ss + h * p.o_sh;
+  const T* qr = q + b * p.q_sb + static_cast<int64_t>(i) * p.q_ss + h * p.q_sh;
+  const T* dr = dout + b * p.o_sb + static_cast<int64_t>(i) * p.o_ss + h * p.o_sh;
   const int64_t row = (static_cast<int64_t>(b) * p.Hq + h) * p.Sq + i;
   const float ls = lse[row], dl = delta[row];
   const int64_t qa = p.q_offset + i;
   float acc[2] = {0.f, 0.f};
   if (ls != -__builtin_inff()) {
     for (int blk = 0; blk < p.nblk; ++blk) {
-      const float* kb = static_cast<const float*>(kv.k[blk]) + b * p.kv_sb + hk * p.kv_sh;
-      const float* vb = static_cast<const float*>(kv.v[blk]) + b * p.kv_sb + hk * p.kv_sh;
+      const T* kb = static_cast<const T*>(kv.k[blk]) + b * p.kv_sb + hk * p.kv_sh;
+      const T* vb = static_cast<const T*>(kv.v[blk]) + b * p.kv_sb + hk * p.kv_sh;
       const int64_t koff = kv.koff[blk];
       for (int j = 0; j < p.Sk; ++j) {
         if (p.causal && koff + j > qa) break;
-        const float* kr = kb + static_cast<int64_t>(j) * p.kv_ss;
-        const float* vr = vb + static_cast<int64_t>(j) * p.kv_ss;
-        const float pv = expf(dot_row(qr, kr, D, lane) * p.scale - ls);
+        float add = 0.f;
+        if (!visible<T, MK>(mr, b, h, i, j, add)) continue;
+        const T* kr = kb + static_cast<int64_t>(j) * p.kv_ss;
+        const T* vr = vb + static_cast<int64_t>(j) * p.kv_ss;
+        const float pv = expf(dot_row(qr, kr, D, lane) * p.scale + add - ls);
         const float ds = pv * (dot_row(dr, vr, D, lane) - dl);
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
           const int d = lane + 64 * c;
-          if (d < D) acc[c] += ds * kr[d];
+          if (d < D) acc[c] += ds * to_f32(kr[d]);
         }
       }
     }
   }
-  float* out = dq + b * p.q_sb + static_cast<int64_t>(i) * p.q_ss + h * p.q_sh;
+  T* out = dq + b * p.q_sb + static_cast<int64_t>(i) * p.q_ss + h * p.q_sh;
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
     const int d = lane + 64 * c;
-    if (d < D) out[d] = acc[c] * p.scale;
+    if (d < D) out[d] = from_f32<T>(acc[c] * p.scale);
   }
 }
 
-__global__ __launch_bounds__(64) void attn_bwd_dkdv_f32_kernel(
-    const float* __restrict__ q, KVBlocks kv, const float* __restrict__ dout,
-    const float* __restrict__ lse, const float* __restrict__ delta, AttnShape p, int D) {
+template <typename T, int MK>
+__global__ __launch_bounds__(64) void attn_bwd_dkdv_generic_kernel(
+    const T* __restrict__ q, KVBlocks kv, const T* __restrict__ dout,
+    const float* __restrict__ lse, const float* __restrict__ delta, AttnShape p, int D, MaskRef mr) {
   const int lane = threadIdx.x;
   const int j = blockIdx.x, hk = blockIdx.y;
   const int blk = static_cast<int>(blockIdx.z) % p.nblk;
@@ -1220,8 +1254,8 @@ __global__ __launch_bounds__(64) void attn_bwd_dkdv_f32_kernel(
   const int group = p.Hq / p.Hkv;
   const int64_t koff = kv.koff[blk];
   const int64_t kvo = b * p.kv_sb + static_cast<int64_t>(j) * p.kv_ss + hk * p.kv_sh;
-  const float* kr = static_cast<const float*>(kv.k[blk]) + kvo;
-  const float* vr = static_cast<const float*>(kv.v[blk]) + kvo;
+  const T* kr = static_cast<const T*>(kv.k[blk]) + kvo;
+  const T* vr = static_cast<const T*>(kv.v[blk]) + kvo;
   float dk[2] = {0.f, 0.f}, dv[2] = {0.f, 0.f};
   int i0 = 0;
   if (p.causal) {
@@ -1234,28 +1268,30 @@ __global__ __launch_bounds__(64) void attn_bwd_dkdv_f32_kernel(
       const int64_t row = (static_cast<int64_t>(b) * p.Hq + h) * p.Sq + i;
       const float ls = lse[row];
       if (ls == -__builtin_inff()) continue;
-      const float* qr = q + b * p.q_sb + static_cast<int64_t>(i) * p.q_ss + h * p.q_sh;
-      const float* dr = dout + b * p.o_sb + static_cast<int64_t>(i) * p.o_ss + h * p.o_sh;
-      const float pv = expf(dot_row(qr, kr, D, lane) * p.scale - ls);
+      float add = 0.f;
+      if (!visible<T, MK>(mr, b, h, i, j, add)) continue;
+      const T* qr = q + b * p.q_sb + static_cast<int64_t>(i) * p.q_ss + h * p.q_sh;
+      const T* dr = dout + b * p.o_sb + static_cast<int64_t>(i) * p.o_ss + h * p.o_sh;
+      const float pv = expf(dot_row(qr, kr, D, lane) * p.scale + add - ls);
       const float ds = pv * (dot_row(dr, vr, D, lane) - delta[row]);
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         const int d = lane + 64 * c;
         if (d < D) {
-          dv[c] += pv * dr[d];
-          dk[c] += ds * qr[d];
+          dv[c] += pv * to_f32(dr[d]);
+          dk[c] += ds * to_f32(qr[d]);
         }
       }
     }
   }
-  float* dkr = static_cast<float*>(kv.dk[blk]) + kvo;
-  float* dvr = static_cast<float*>(kv.dv[blk]) + kvo;
+  T* dkr = static_cast<T*>(kv.dk[blk]) + kvo;
+  T* dvr = static_cast<T*>(kv.dv[blk]) + kvo;
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
     const int d = lane + 64 * c;
     if (d < D) {
-      dkr[d] = dk[c] * p.scale;
-      dvr[d] = dv[c];
+      dkr[d] = from_f32<T>(dk[c] * p.scale);
+      dvr[d] = from_f32<T>(dv[c]);
     }
   }
 }
@@ -1391,9 +1427,9 @@ int attn_fwd_impl(bool from_lse, const void* q, const void* const* k_blocks,
     NMB_REQUIRE_SUPPORTED(!from_lse, "attn_fwd_from_lse: bf16 only");
     const dim3 grid(static_cast<unsigned>(seq_q), static_cast<unsigned>(q_heads),
                     static_cast<unsigned>(batch));
-    hipLaunchKernelGGL(nmb::attn_fwd_f32_kernel, grid, dim3(64), 0, stream,
+    hipLaunchKernelGGL((nmb::attn_fwd_generic_kernel<float, 0>), grid, dim3(64), 0, stream,
                        static_cast<const float*>(q), kv, static_cast<float*>(o), lse, p,
-                       static_cast<int>(head_dim));
+                       static_cast<int>(head_dim), nmb::MaskRef{});
   }
   NMB_CHECK_LAUNCH("attn_fwd");
   return NMB_OK;
@@ -1541,15 +1577,15 @@ int attn_bwd_impl(const void* q, const void* const* k_blocks,
     if (seq_q > 0) {
       const dim3 grid(static_cast<unsigned>(seq_q), static_cast<unsigned>(q_heads),
                       static_cast<unsigned>(batch));
-      hipLaunchKernelGGL(nmb::attn_bwd_dq_f32_kernel, grid, dim3(64), 0, stream, qp, kv, dp, lse,
-                         delta, static_cast<float*>(dq), p, D);
+      hipLaunchKernelGGL((nmb::attn_bwd_dq_generic_kernel<float, 0>), grid, dim3(64), 0, stream, qp, kv,
+                         dp, lse, delta, static_cast<float*>(dq), p, D, nmb::MaskRef{});
       NMB_CHECK_LAUNCH("attn_bwd(dq,f32)");
     }
     if (seq_k > 0) {
       const dim3 grid(static_cast<unsigned>(seq_k), static_cast<unsigned>(kv_heads),
                       static_cast<unsigned>(batch * n_blocks));
-      hipLaunchKernelGGL(nmb::attn_bwd_dkdv_f32_kernel, grid, dim3(64), 0, stream, qp, kv, dp,
-                         lse, delta, p, D);
+      hipLaunchKernelGGL((nmb::attn_bwd_dkdv_generic_kernel<float, 0>), grid, dim3(64), 0, stream, qp,
+                         kv, dp, lse, delta, p, D, nmb::MaskRef{});
       NMB_CHECK_LAUNCH("attn_bwd(dkdv,f32)");
     }
   }
@@ -1572,6 +1608,139 @@ extern "C" int nmb_attn_bwd(const void* q, const void* const* k_blocks,
                             dv_blocks, workspace, workspace_bytes, batch, q_heads, kv_heads, seq_q,
                             seq_k, head_dim, q_strides, kv_strides, o_strides, causal, q_offset,
                             scale, dtype, stream, nullptr);
+}
+
+namespace nmb {
+namespace {
+
+// Shape and mask of the masked entry points: one K/V block at key offset 0;
+// the generic kernels load elements one at a time, so any head_dim <= 128 and
+// any strides (of bf16 or fp32 data) are accepted.
+int masked_setup(AttnShape* p, KVBlocks* kv, MaskRef* mr, const void* q, const void* k, const void* v,
+                 int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k,
+                 int64_t head_dim, const int64_t* qs, const int64_t* kvs, const int64_t* os,
+                 const void* mask, int mask_kind, const int64_t* ms, int causal, int64_t q_offset,
+                 float scale, int dtype) {
+  NMB_REQUIRE_SUPPORTED(dtype == NMB_BF16 || dtype == NMB_F32, "attention (masked): unsupported dtype code %d",
+                        dtype);
+  NMB_REQUIRE(mask_kind == 1 || mask_kind == 2,
+              "attention (masked): mask_kind must be 1 (boolean) or 2 (additive), got %d", mask_kind);
+  NMB_REQUIRE(mask != nullptr && ms != nullptr, "attention (masked): null mask");
+  NMB_REQUIRE(ms[0] >= 0 && ms[1] >= 0 && ms[2] >= 0 && ms[3] >= 0,
+              "attention (masked): mask strides must be non-negative");
+  const void* kb[1] = {k};
+  const void* vb[1] = {v};
+  const int64_t koff[1] = {0};
+  const int st = fill_shape(p, kv, q, kb, vb, koff, 1, batch, q_heads, kv_heads, seq_q, seq_k, head_dim,
+                            qs, kvs, os, causal, q_offset, scale, NMB_F32);
+  if (st != NMB_OK) return st;
+  *mr = MaskRef{mask, ms[0], ms[1], ms[2], ms[3]};
+  return NMB_OK;
+}
+
+template <typename T>
+void masked_fwd_launch(const AttnShape& p, const KVBlocks& kv, const MaskRef& mr, int kind, const void* q,
+                       void* o, float* lse, int D, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(p.Sq), static_cast<unsigned>(p.Hq), static_cast<unsigned>(p.B));
+  if (kind == 1)
+    hipLaunchKernelGGL((attn_fwd_generic_kernel<T, 1>), grid, dim3(64), 0, stream, static_cast<const T*>(q),
+                       kv, static_cast<T*>(o), lse, p, D, mr);
+  else
+    hipLaunchKernelGGL((attn_fwd_generic_kernel<T, 2>), grid, dim3(64), 0, stream, static_cast<const T*>(q),
+                       kv, static_cast<T*>(o), lse, p, D, mr);
+}
+
+template <typename T>
+void masked_bwd_launch(const AttnShape& p, const KVBlocks& kv, const MaskRef& mr, int kind, const void* q,
+                       const void* o, const void* dout, const float* lse, float* delta, void* dq, int D,
+                       hipStream_t stream) {
+  const T* qp = static_cast<const T*>(q);
+  const T* dp = static_cast<const T*>(dout);
+  const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
+  if (rows > 0) {
+    int64_t blocks = (rows + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(attn_delta_kernel<T>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                       static_cast<const T*>(o), dp, delta, p, D);
+    const dim3 grid(static_cast<unsigned>(p.Sq), static_cast<unsigned>(p.Hq), static_cast<unsigned>(p.B));
+    if (kind == 1)
+      hipLaunchKernelGGL((attn_bwd_dq_generic_kernel<T, 1>), grid, dim3(64), 0, stream, qp, kv, dp, lse, delta,
+                         static_cast<T*>(dq), p, D, mr);
+    else
+      hipLaunchKernelGGL((attn_bwd_dq_generic_kernel<T, 2>), grid, dim3(64), 0, stream, qp, kv, dp, lse, delta,
+                         static_cast<T*>(dq), p, D, mr);
+  }
+  if (p.Sk > 0 && p.B > 0) {
+    const dim3 grid(static_cast<unsigned>(p.Sk), static_cast<unsigned>(p.Hkv), static_cast<unsigned>(p.B));
+    if (kind == 1)
+      hipLaunchKernelGGL((attn_bwd_dkdv_generic_kernel<T, 1>), grid, dim3(64), 0, stream, qp, kv, dp, lse,
+                         delta, p, D, mr);
+    else
+      hipLaunchKernelGGL((attn_bwd_dkdv_generic_kernel<T, 2>), grid, dim3(64), 0, stream, qp, kv, dp, lse,
+                         delta, p, D, mr);
+  }
+}
+
+}  // namespace
+}  // namespace nmb
+
+extern "C" int nmb_attn_masked_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                                   int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                                   int64_t seq_k, int64_t head_dim, const int64_t* q_strides,
+                                   const int64_t* kv_strides, const int64_t* o_strides, const void* mask,
+                                   int mask_kind, const int64_t* mask_strides, int causal,
+                                   int64_t q_offset, float scale, int dtype, hipStream_t stream) {
+  AttnShape p;
+  KVBlocks kv;
+  nmb::MaskRef mr;
+  const int st = nmb::masked_setup(&p, &kv, &mr, q, k, v, batch, q_heads, kv_heads, seq_q, seq_k, head_dim,
+                                   q_strides, kv_strides, o_strides, mask, mask_kind, mask_strides, causal,
+                                   q_offset, scale, dtype);
+  if (st != NMB_OK) return st;
+  NMB_REQUIRE(o != nullptr && lse != nullptr, "attn_masked_fwd: null output");
+  if (batch == 0 || seq_q == 0) return NMB_OK;
+  if (dtype == NMB_BF16)
+    nmb::masked_fwd_launch<nmb::bf16>(p, kv, mr, mask_kind, q, o, lse, static_cast<int>(head_dim), stream);
+  else
+    nmb::masked_fwd_launch<float>(p, kv, mr, mask_kind, q, o, lse, static_cast<int>(head_dim), stream);
+  NMB_CHECK_LAUNCH("attn_masked_fwd");
+  return NMB_OK;
+}
+
+extern "C" int nmb_attn_masked_bwd(const void* q, const void* k, const void* v, const void* o,
+                                   const void* dout, const float* lse, void* dq, void* dk, void* dv,
+                                   void* workspace, size_t workspace_bytes, int64_t batch,
+                                   int64_t q_heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k,
+                                   int64_t head_dim, const int64_t* q_strides, const int64_t* kv_strides,
+                                   const int64_t* o_strides, const void* mask, int mask_kind,
+                                   const int64_t* mask_strides, int causal, int64_t q_offset, float scale,
+                                   int dtype, hipStream_t stream) {
+  AttnShape p;
+  KVBlocks kv;
+  nmb::MaskRef mr;
+  const int st = nmb::masked_setup(&p, &kv, &mr, q, k, v, batch, q_heads, kv_heads, seq_q, seq_k, head_dim,
+                                   q_strides, kv_strides, o_strides, mask, mask_kind, mask_strides, causal,
+                                   q_offset, scale, dtype);
+  if (st != NMB_OK) return st;
+  NMB_REQUIRE(o != nullptr && dout != nullptr && lse != nullptr && dq != nullptr && dk != nullptr &&
+                  dv != nullptr,
+              "attn_masked_bwd: null argument");
+  const size_t need = static_cast<size_t>(batch * q_heads * seq_q) * sizeof(float);
+  NMB_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+              "attn_masked_bwd: workspace of %zu bytes is smaller than the %zu required", workspace_bytes,
+              need);
+  kv.dk[0] = dk;
+  kv.dv[0] = dv;
+  if (batch == 0) return NMB_OK;
+  float* delta = static_cast<float*>(workspace);
+  if (dtype == NMB_BF16)
+    nmb::masked_bwd_launch<nmb::bf16>(p, kv, mr, mask_kind, q, o, dout, lse, delta, dq,
+                                      static_cast<int>(head_dim), stream);
+  else
+    nmb::masked_bwd_launch<float>(p, kv, mr, mask_kind, q, o, dout, lse, delta, dq,
+                                  static_cast<int>(head_dim), stream);
+  NMB_CHECK_LAUNCH("attn_masked_bwd");
+  return NMB_OK;
 }
 
 extern "C" int nmb_attn_bwd_rope(const void* q, const void* k, const void* v, const void* o,

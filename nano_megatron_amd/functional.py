@@ -740,6 +740,84 @@ def attention(
     return AttentionFunction.apply(q, causal, int(sequence_offset), scale, (0,), k, v)
 
 
+def _mask_args(mask: Tensor, q: Tensor, shape: tuple[int, int, int, int]) -> tuple[Tensor, int, tuple]:
+    """(mask tensor, kind, element strides over [B, Hq, Sq, Sk]) of an SDPA
+    attn_mask: broadcast like SDPA's (trailing dimensions), 0 strides where it
+    broadcasts; kind 1 boolean, 2 additive in q's dtype."""
+    if mask.dtype == torch.bool:
+        kind = 1
+    elif mask.dtype == q.dtype:
+        kind = 2
+    else:
+        raise ValueError(f"attention_mask must be boolean or of the query dtype {q.dtype}, got {mask.dtype}")
+    if mask.device != q.device:
+        raise ValueError("attention_mask must be on the query's device")
+    try:
+        full = torch.broadcast_to(mask, shape)
+    except RuntimeError as exc:
+        raise ValueError(f"attention_mask of shape {tuple(mask.shape)} does not broadcast to {shape}") from exc
+    return mask, kind, tuple(st if n > 1 else 0 for st, n in zip(full.stride(), shape))
+
+
+class MaskedAttentionFunction(torch.autograd.Function):
+    """``local_attention`` with ``attention_mask`` (nn/kernels/torch_backend.py:
+    60-76): the mask ANDed with the causal mask (boolean masks) or added to the
+    scores (masks of the query dtype), one K/V block; ``nmb_attn_masked_*``.
+    The mask itself gets no gradient."""
+
+    @staticmethod
+    def forward(ctx: Any, q: Tensor, k: Tensor, v: Tensor, mask: Tensor, causal: bool, q_offset: int,
+                scale: float | None) -> Tensor:
+        b, hq, hkv, sq, sk, d = _check_attn(q, [k], [v])
+        q, k, v = (_canonical_bhsd(t) for t in (q, k, v))
+        mask, kind, mstrides = _mask_args(mask, q, (b, hq, sq, sk))
+        o = _new_bhsd(q.shape, q)
+        lse = torch.empty(b, hq, sq, dtype=torch.float32, device=q.device)
+        qs, ks, os_ = (_eff_strides(_bshd_view(t)) for t in (q, k, o))
+        _lib.call(
+            "nmb_attn_masked_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+            b, hq, hkv, sq, sk, d, _lib.i64x3(qs), _lib.i64x3(ks), _lib.i64x3(os_), mask.data_ptr(), kind,
+            _lib.i64_array(mstrides), 1 if causal else 0, int(q_offset), float(scale) if scale else 0.0,
+            _lib.dtype_code(q.dtype), _lib.stream_of(q),
+        )
+        ctx.save_for_backward(q, k, v, o, lse, mask)
+        ctx.meta = (causal, q_offset, scale, kind, mstrides)
+        return o
+
+    @staticmethod
+    def backward(ctx: Any, grad: Tensor):
+        causal, q_offset, scale, kind, mstrides = ctx.meta
+        q, k, v, o, lse, mask = ctx.saved_tensors
+        b, hq, sq, d = q.shape
+        hkv, sk = k.shape[1], k.shape[2]
+        do = _canonical_bhsd(grad)
+        dq, dk, dv = _new_bhsd(q.shape, q), _new_bhsd(k.shape, k), _new_bhsd(v.shape, v)
+        nbytes = _lib.ctypes.c_size_t(0)
+        _lib.call("nmb_attn_bwd_workspace_bytes", b, hq, sq, _lib.ctypes.byref(nbytes))
+        ws = _workspace(nbytes.value, q.device)
+        if _eff_strides(_bshd_view(do)) != _eff_strides(_bshd_view(o)):
+            do = _canonical_bhsd(do.contiguous())
+        _lib.call(
+            "nmb_attn_masked_bwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
+            lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws.numel(),
+            b, hq, hkv, sq, sk, d, _lib.i64x3(_eff_strides(_bshd_view(q))),
+            _lib.i64x3(_eff_strides(_bshd_view(k))), _lib.i64x3(_eff_strides(_bshd_view(o))),
+            mask.data_ptr(), kind, _lib.i64_array(mstrides), 1 if causal else 0, int(q_offset),
+            float(scale) if scale else 0.0, _lib.dtype_code(q.dtype), _lib.stream_of(q),
+        )
+        return dq, dk, dv, None, None, None, None
+
+
+def masked_attention(q: Tensor, k: Tensor, v: Tensor, attention_mask: Tensor, *, causal: bool = True,
+                     sequence_offset: int = 0, scale: float | None = None) -> Tensor:
+    """``local_attention`` with ``attention_mask`` for [B,H,S,D] tensors."""
+    _require_gpu(q, k, v, attention_mask)
+    if causal and attention_mask.dtype != torch.bool:
+        # the reference combines the masks with `mask & causal_mask` (torch_backend.py:66)
+        raise ValueError("a causal attention_mask must be boolean (it is ANDed with the causal mask)")
+    return MaskedAttentionFunction.apply(q, k, v, attention_mask, bool(causal), int(sequence_offset), scale)
+
+
 def ring_attention(
     q: Tensor,
     kv_blocks: Sequence[tuple[Tensor, Tensor]],

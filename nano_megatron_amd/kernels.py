@@ -73,7 +73,8 @@ class HipKernelBackend:
         if dropout_p:
             raise ValueError("the hip backend implements attention dropout_p = 0 only")
         if attention_mask is not None:
-            raise ValueError("the hip backend implements the causal/offset mask, not arbitrary masks")
+            return Fn.masked_attention(q, k, v, attention_mask, causal=causal,
+                                       sequence_offset=sequence_offset, scale=scale)
         return Fn.attention(q, k, v, causal=causal, sequence_offset=sequence_offset, scale=scale)
 
 

@@ -145,12 +145,15 @@ def local_attention(
     causal: bool = True,
     sequence_offset: int = 0,
     scale: float | None = None,
+    attention_mask: Tensor | None = None,
 ) -> Tensor:
     """``TorchKernelBackend.local_attention`` (nn/kernels/torch_backend.py:25-76).
 
     GQA by ``repeat_interleave`` of K/V heads (:51-58); causal by ``is_causal``
-    at offset 0, else by an explicit ``key_pos <= offset + query_pos`` mask
-    (:60-66); then SDPA (:68-76).
+    when there is no mask and the offset is 0, else by an explicit
+    ``key_pos <= offset + query_pos`` mask, ANDed with ``attention_mask`` when
+    one is given (:60-66); then SDPA with that mask (:68-76): a boolean mask
+    keeps the True entries, a floating mask is added to the scores.
     """
     if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
         raise ValueError("q, k and v must have [batch, heads, sequence, head_dim] shape")
@@ -166,12 +169,13 @@ def local_attention(
         repeat = q.shape[1] // k.shape[1]
         k = k.repeat_interleave(repeat, dim=1)
         v = v.repeat_interleave(repeat, dim=1)
-    is_causal = causal and sequence_offset == 0
-    mask = None
+    is_causal = causal and attention_mask is None and sequence_offset == 0
+    mask = attention_mask
     if causal and not is_causal:
         query_positions = sequence_offset + torch.arange(q.shape[-2])
         key_positions = torch.arange(k.shape[-2])
-        mask = key_positions.unsqueeze(0) <= query_positions.unsqueeze(1)
+        causal_mask = key_positions.unsqueeze(0) <= query_positions.unsqueeze(1)
+        mask = causal_mask if mask is None else (mask & causal_mask)
     return F.scaled_dot_product_attention(q, k, v, attn_mask=mask, is_causal=is_causal, scale=scale)
 
 

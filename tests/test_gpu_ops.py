@@ -194,6 +194,64 @@ def test_attention_matches_oracle(device, b, hq, hkv, sq, sk, d, dtype, offset, 
     close(vd.grad, vr.grad, dtype, scale_atol=True, msg="dv")
 
 
+MASK_CASES = [
+    # (dtype, causal, offset, kind, hq, hkv, sq, sk, d)
+    (torch.bfloat16, True, 0, "bool", 4, 2, 64, 64, 64),
+    (torch.bfloat16, True, 7, "bool", 4, 4, 37, 45, 128),
+    (torch.bfloat16, False, 0, "add", 4, 1, 33, 50, 64),
+    (torch.float32, True, 0, "bool", 2, 2, 40, 40, 32),
+    (torch.float32, False, 0, "add", 4, 2, 29, 31, 80),
+]
+
+
+@pytest.mark.parametrize("dtype,causal,offset,kind,hq,hkv,sq,sk,d", MASK_CASES)
+def test_masked_attention_matches_oracle(device, dtype, causal, offset, kind, hq, hkv, sq, sk, d) -> None:
+    """local_attention with attention_mask through the HIP backend (nmb_attn_masked_*)
+    against the oracle (torch_backend.py:60-76): a boolean mask [B, 1, Sq, Sk]
+    ANDed with the causal mask, with one query row fully masked (zero output and
+    gradients), or an additive mask [Sq, Sk] of the query dtype with -inf
+    entries; GQA, head dims 32-128, ragged lengths; forward and q/k/v gradients."""
+    g = gen(7)
+    b = 2
+    q = torch.randn(b, hq, sq, d, generator=g).to(dtype)
+    k = torch.randn(b, hkv, sk, d, generator=g).to(dtype)
+    v = torch.randn(b, hkv, sk, d, generator=g).to(dtype)
+    do = torch.randn(b, hq, sq, d, generator=g).to(dtype)
+    if kind == "bool":
+        mask = torch.rand(b, 1, sq, sk, generator=g) > 0.3
+        mask[1, 0, 3] = False
+    else:
+        mask = torch.randn(sq, sk, generator=g).to(dtype)
+        mask[2, 1:9] = float("-inf")
+    qr, kr, vr = (t.float().clone().requires_grad_(True) for t in (q, k, v))
+    mr = mask if kind == "bool" else mask.float()
+    o_ref = R.local_attention(qr, kr, vr, causal=causal, sequence_offset=offset, attention_mask=mr)
+    o_ref.backward(do.float())
+    backend = nm.HipKernelBackend()
+    qd, kd, vd = (t.to(device).requires_grad_(True) for t in (q, k, v))
+    o = backend.local_attention(qd, kd, vd, causal=causal, sequence_offset=offset, attention_mask=mask.to(device))
+    o.backward(do.to(device))
+    close(o, o_ref, dtype)
+    close(qd.grad, qr.grad, dtype, scale_atol=True, msg="dq")
+    close(kd.grad, kr.grad, dtype, scale_atol=True, msg="dk")
+    close(vd.grad, vr.grad, dtype, scale_atol=True, msg="dv")
+    if kind == "bool":
+        assert torch.count_nonzero(o[1, :, 3]) == 0 and torch.count_nonzero(qd.grad[1, :, 3]) == 0
+
+
+def test_masked_attention_rejects_what_the_reference_rejects(device) -> None:
+    q = torch.randn(1, 2, 8, 64, device=device, dtype=torch.bfloat16)
+    backend = nm.HipKernelBackend()
+    with pytest.raises(ValueError, match="boolean"):  # `mask & causal_mask` needs a boolean mask
+        backend.local_attention(q, q, q, causal=True, attention_mask=torch.zeros(8, 8, device=device,
+                                                                                  dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="broadcast"):
+        backend.local_attention(q, q, q, causal=False, attention_mask=torch.ones(3, 8, 8, device=device,
+                                                                                  dtype=torch.bool))
+    with pytest.raises(ValueError, match="dtype"):
+        backend.local_attention(q, q, q, causal=False, attention_mask=torch.zeros(8, 8, device=device))
+
+
 def test_attention_c3_shape_and_lse(device) -> None:
     """Config 3 attention shape [16,16,512,64] bf16, forward and backward against
     the oracle; lse == logsumexp of masked scores."""

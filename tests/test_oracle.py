@@ -105,21 +105,35 @@ def test_rope_position_zero_is_identity_and_negative_sin_inverts() -> None:
 
 
 # ---------------------------------------------------------------- attention
-def _brute_attention(q, k, v, causal, q_off=0, k_off=0):
+def _brute_attention(q, k, v, causal, q_off=0, k_off=0, mask=None):
+    """Softmax attention by loops.  mask (broadcast to [b, h, sq, sk]): a
+    boolean mask drops the False keys, a floating one is added to the scores;
+    a row with no visible key gives zeros."""
     b, h, sq, d = q.shape
     rep = h // k.shape[1]
     out = torch.zeros_like(q)
+    if mask is not None:
+        mask = torch.broadcast_to(mask, (b, h, sq, k.shape[2]))
     for bi in range(b):
         for hi in range(h):
             kh = hi // rep
             for i in range(sq):
                 scores = []
                 for j in range(k.shape[2]):
-                    if causal and k_off + j > q_off + i:
-                        scores.append(-math.inf)
+                    visible = not (causal and k_off + j > q_off + i)
+                    extra = 0.0
+                    if mask is not None:
+                        if mask.dtype == torch.bool:
+                            visible = visible and bool(mask[bi, hi, i, j])
+                        else:
+                            extra = float(mask[bi, hi, i, j])
+                    if visible:
+                        scores.append(float(q[bi, hi, i] @ k[bi, kh, j]) / math.sqrt(d) + extra)
                     else:
-                        scores.append(float(q[bi, hi, i] @ k[bi, kh, j]) / math.sqrt(d))
+                        scores.append(-math.inf)
                 m = max(scores)
+                if m == -math.inf:
+                    continue
                 w = [math.exp(s - m) for s in scores]
                 tot = sum(w)
                 out[bi, hi, i] = sum(wj / tot * v[bi, kh, j] for j, wj in enumerate(w))
@@ -136,6 +150,27 @@ def test_local_attention_matches_bruteforce(causal, offset) -> None:
         k, v = k[:, :, :5], v[:, :, :5]
     got = R.local_attention(q, k, v, causal=causal, sequence_offset=offset)
     torch.testing.assert_close(got, _brute_attention(q, k, v, causal, q_off=offset))
+
+
+@pytest.mark.parametrize("causal,offset,kind", [(True, 0, "bool"), (True, 2, "bool"), (False, 0, "bool"),
+                                                (False, 0, "add")])
+def test_local_attention_with_mask_matches_bruteforce(causal, offset, kind) -> None:
+    """attention_mask as torch_backend.py:60-66 combines it: ANDed with the
+    causal mask (a boolean mask), or added to the scores (a floating mask,
+    without causal); a query row whose keys are all masked gives zeros (the
+    CPU SDPA's safe softmax), checked by loops."""
+    torch.manual_seed(5)
+    q = torch.randn(2, 4, 5, 8, dtype=torch.float64)
+    k = torch.randn(2, 2, 7, 8, dtype=torch.float64)
+    v = torch.randn(2, 2, 7, 8, dtype=torch.float64)
+    if kind == "bool":
+        mask = torch.rand(2, 1, 5, 7) > 0.3
+        mask[1, 0, 2] = False  # a fully masked row
+    else:
+        mask = torch.randn(5, 7, dtype=torch.float64)
+        mask[3, 1:5] = -math.inf
+    got = R.local_attention(q, k, v, causal=causal, sequence_offset=offset, attention_mask=mask)
+    torch.testing.assert_close(got, _brute_attention(q, k, v, causal, q_off=offset, mask=mask))
 
 
 def test_local_attention_is_causal_and_gqa_is_repeat() -> None:
