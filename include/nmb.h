@@ -305,6 +305,22 @@ int nmb_gemm_bf16_swiglu(int64_t m, int64_t f, int64_t k, const void* a, int64_t
                          int64_t ldb, void* d, int64_t ldd, void* gu, int64_t ldgu,
                          hipStream_t stream);
 
+/* The down projection's input gradient with the SwiGLU backward as its
+ * epilogue (autograd of models/gpt/mlp.py:77-78: ds = dY Wd, then the
+ * backward of silu(gate) * up; replaces nmb_gemm_bf16 + nmb_swiglu_bwd):
+ *   ds = bf16(A B), A row-major [M, K] (dY), b_layout as nmb_gemm_bf16
+ *   (Wd used as [K, F]: b_layout 1 for the row-major [K, F] weight);
+ *   gu [M, 2F] holds the gate/up product (gate columns 0..F-1, up F..2F-1);
+ *   dgu [M, 2F] receives (d gate | d up); act (nullable) [M, F] receives
+ *   silu(gate) * up for the down projection's weight gradient.
+ * Bit-identical to nmb_gemm_bf16 followed by nmb_swiglu_bwd (same element
+ * function, ds rounded to bf16 first); never split along K; F, K and the
+ * leading dimensions multiples of 8; no workspace; no intermediate ds in
+ * memory. */
+int nmb_gemm_bf16_swiglu_bwd(int b_layout, int64_t m, int64_t f, int64_t k, const void* a,
+                             int64_t lda, const void* b, int64_t ldb, const void* gu, int64_t ldgu,
+                             void* dgu, int64_t lddgu, void* act, int64_t ldact, hipStream_t stream);
+
 /* ------------------------------------------------------------ optimizer
  * replaces FlatShardZeROStrategy.clip_grad_norm + optimizer_step at DP=1
  * (data_parallel/_zero.py:130-199; defaults config/schema.py:439-445):

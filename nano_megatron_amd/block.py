@@ -18,8 +18,10 @@ backward re-runs the sequence above with the same kernels and shapes (so the
 recomputed tensors, the attention output and its lse included, are
 bit-identical to the forward's), except that the gate/up GEMM writes the
 product [g|u] instead of s (same plan, same bits), and never re-runs the down
-projection, whose output the backward does not need; ``nmb_swiglu_bwd``
-re-emits s for the Wd gradient.  With ``offload`` the saved input goes to
+projection, whose output the backward does not need.  The down projection's
+backward GEMM runs the SwiGLU backward as its epilogue
+(``nmb_gemm_bf16_swiglu_bwd``: no ds in memory) and re-emits s for the Wd
+gradient.  With ``offload`` the saved input goes to
 pinned host memory (the reference's saved-tensor offload,
 nn/activation_checkpoint.py:24-41); the weights are parameters, never copied.
 ``EagerBlockFunction`` (activation_checkpoint.mode = "none") keeps the
@@ -188,10 +190,8 @@ def block_backward(acts: dict, dy: Tensor, w: tuple[Tensor, ...], m: BlockMeta, 
     side = _SideProducts(dy2.device)
 
     # MLP: y = h + s Wd^T, s = silu(g) * u, [g|u] = n2 [Wg;Wu]^T
-    ds = Fn.mm(dy2, wd)
-    dgu = torch.empty_like(gu)
-    act = torch.empty(b * s, f, dtype=gu.dtype, device=gu.device)
-    Fn.swiglu_bwd(gu[:, :f], gu[:, f:], ds, dgu[:, :f], dgu[:, f:], act)
+    # ds = dY Wd and the SwiGLU backward in one GEMM (its epilogue); act feeds dWd
+    dgu, act = Fn.mm_swiglu_bwd(dy2, wd, gu)
     dwd = side.mm(dy2.t(), act)
     dn2 = Fn.mm(dgu, joined((wg, wu)))
     dwgu = side.mm(dgu.t(), n2)

@@ -192,6 +192,12 @@ struct GemmArgs {
   // SwiGLU epilogue: the [M, 2F] gate/up product (nullable; d nullable too)
   bf16* gu;
   int64_t ldgu;
+  // SwiGLU-backward epilogue: the forward's [M, 2F] gate/up product (read)
+  // and its gradient (written); D receives the re-emitted activation
+  const bf16* swb_gu;
+  int64_t swb_ldgu;
+  bf16* swb_dgu;
+  int64_t swb_lddgu;
 };
 
 // Columns of D covered by one TBN-wide tile: TBN, or TBN / 2 with the SwiGLU
@@ -203,7 +209,8 @@ constexpr int out_cols() { return SWI ? TBN / 2 : TBN; }
 // 8: 2 x 4 or 4 x 2, one workgroup per CU), BKT-deep K tiles.  RD > 0: RoPE
 // epilogue on heads of RD.  SWI: B is [2F, K] (gate rows, then up rows), N = F,
 // and D = swiglu(gate product, up product).
-template <int TBM, int TBN, int NW, int BKT, bool A_KC, bool B_KC, int RD, bool SWI = false>
+template <int TBM, int TBN, int NW, int BKT, bool A_KC, bool B_KC, int RD, bool SWI = false,
+          bool SWB = false>
 __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void gemm_kernel(GemmArgs g) {
   constexpr int WAVES_N = NW == 4 ? 2 : (TBN == 256 ? 4 : 2);
   constexpr int WAVES_M = NW / WAVES_N;
@@ -596,6 +603,59 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void gemm_kernel(GemmArgs
   constexpr int ROWS_PER_WAVE = TBM / NW;
   static_assert(ROWS_PER_WAVE % RPI == 0, "whole store instructions per wave");
   const int sl = lane % LPR;
+  if constexpr (SWB) {
+    // The SwiGLU backward on the tile (ds = bf16(acc), as the product would be
+    // stored): 8 columns of a row per lane, g and u read from the gate/up
+    // product (every load issued before any store: a wait after a store
+    // covers every outstanding load), dg and du written to its gradient and
+    // silu(g) u to D when it is given; bit-identical to the product followed
+    // by the SwiGLU backward kernel (same element function).
+    static_assert(RD == 0 && !SWI, "one epilogue at a time");
+    constexpr int IT = ROWS_PER_WAVE / RPI;
+    constexpr int CH = IT > 8 ? 8 : IT;  // rows in flight per lane (registers)
+    static_assert(IT % CH == 0, "whole chunks");
+#pragma unroll
+    for (int c0 = 0; c0 < IT; c0 += CH) {
+    uint4 graw[CH], uraw[CH];
+#pragma unroll
+    for (int ci = 0; ci < CH; ++ci) {
+      const int it = c0 + ci;
+      const int r = wave * ROWS_PER_WAVE + it * RPI + lane / LPR;
+      const int m = m0 + r, n = n0 + 8 * sl;
+      // out-of-range lanes read row m0, column 0 (in range; never used)
+      const bool ok = m < g.M && n < g.N;
+      const bf16* row = g.swb_gu + static_cast<int64_t>(ok ? m : m0) * g.swb_ldgu + (ok ? n : 0);
+      graw[ci] = *reinterpret_cast<const uint4*>(row);
+      uraw[ci] = *reinterpret_cast<const uint4*>(row + g.N);
+    }
+#pragma unroll
+    for (int ci = 0; ci < CH; ++ci) {
+      const int it = c0 + ci;
+      const int r = wave * ROWS_PER_WAVE + it * RPI + lane / LPR;
+      const int m = m0 + r, n = n0 + 8 * sl;
+      const bf16x8 dsv = *reinterpret_cast<const bf16x8*>(tile_at(r, 8 * sl));
+      bf16x8 gv, uv, dgo, duo, oo;
+      __builtin_memcpy(&gv, &graw[ci], 16);
+      __builtin_memcpy(&uv, &uraw[ci], 16);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float dgf, duf, of;
+        swiglu_bwd_elem<bf16>(static_cast<float>(gv[e]), static_cast<float>(uv[e]), static_cast<float>(dsv[e]),
+                              dgf, duf, of);
+        dgo[e] = static_cast<bf16>(dgf);
+        duo[e] = static_cast<bf16>(duf);
+        oo[e] = static_cast<bf16>(of);
+      }
+      if (m < g.M && n < g.N) {
+        bf16* drow = g.swb_dgu + static_cast<int64_t>(m) * g.swb_lddgu;
+        *reinterpret_cast<bf16x8*>(drow + n) = dgo;
+        *reinterpret_cast<bf16x8*>(drow + g.N + n) = duo;
+        if (g.d != nullptr) *reinterpret_cast<bf16x8*>(g.d + static_cast<int64_t>(m) * g.ldd + n) = oo;
+      }
+    }
+    }
+    return;
+  }
 #pragma unroll
   for (int it = 0; it < ROWS_PER_WAVE / RPI; ++it) {
     const int r = wave * ROWS_PER_WAVE + it * RPI + lane / LPR;
@@ -732,7 +792,8 @@ Plan plan_for(int64_t m, int64_t n, int64_t k, bool a_kc, bool b_kc, int rope_he
   return best;
 }
 
-template <int TBM, int TBN, int NW, int BKT, bool A_KC, bool B_KC, int RD = 0, bool SWI = false>
+template <int TBM, int TBN, int NW, int BKT, bool A_KC, bool B_KC, int RD = 0, bool SWI = false,
+          bool SWB = false>
 int launch(GemmArgs g, hipStream_t stream) {
   const int tiles_m = (g.M + TBM - 1) / TBM;
   g.tiles_n = (g.N + out_cols<TBN, SWI>() - 1) / out_cols<TBN, SWI>();
@@ -742,7 +803,7 @@ int launch(GemmArgs g, hipStream_t stream) {
   g.tiles = static_cast<int>(tiles);
   g.items = static_cast<int>(items);
   g.per_xcd = static_cast<int>((items + 7) / 8);
-  hipLaunchKernelGGL((gemm_kernel<TBM, TBN, NW, BKT, A_KC, B_KC, RD, SWI>),
+  hipLaunchKernelGGL((gemm_kernel<TBM, TBN, NW, BKT, A_KC, B_KC, RD, SWI, SWB>),
                      dim3(static_cast<unsigned>(g.per_xcd * 8)), dim3(NW * 64), 0, stream, g);
   NMB_CHECK_LAUNCH("gemm");
   if (g.splits > 1) {
@@ -773,6 +834,19 @@ int dispatch_rope(int config, bool b_kc, const GemmArgs& g, hipStream_t s) {
     }
   }
   return b_kc ? launch<128, 256, 4, 32, true, true, RD>(g, s) : launch<128, 256, 4, 32, true, false, RD>(g, s);
+}
+
+int dispatch_swiglu_bwd(int config, bool b_kc, const GemmArgs& g, hipStream_t s) {
+  switch (config) {
+    case 0: return b_kc ? launch<256, 256, 8, 64, true, true, 0, false, true>(g, s)
+                        : launch<256, 256, 8, 64, true, false, 0, false, true>(g, s);
+    case 1: return b_kc ? launch<256, 128, 8, 64, true, true, 0, false, true>(g, s)
+                        : launch<256, 128, 8, 64, true, false, 0, false, true>(g, s);
+    case 2: return b_kc ? launch<128, 128, 4, 32, true, true, 0, false, true>(g, s)
+                        : launch<128, 128, 4, 32, true, false, 0, false, true>(g, s);
+    default: return b_kc ? launch<128, 256, 4, 32, true, true, 0, false, true>(g, s)
+                         : launch<128, 256, 4, 32, true, false, 0, false, true>(g, s);
+  }
 }
 
 int dispatch_swiglu(int config, const GemmArgs& g, hipStream_t s) {
@@ -965,4 +1039,28 @@ extern "C" int nmb_gemm_bf16_swiglu(int64_t m, int64_t f, int64_t k, const void*
   g.gu = static_cast<nmb::bf16*>(gu);
   g.ldgu = ldgu;
   return nmb::dispatch_swiglu(p.config, g, stream);
+}
+
+extern "C" int nmb_gemm_bf16_swiglu_bwd(int b_layout, int64_t m, int64_t f, int64_t k, const void* a,
+                                        int64_t lda, const void* b, int64_t ldb, const void* gu, int64_t ldgu,
+                                        void* dgu, int64_t lddgu, void* act, int64_t ldact,
+                                        hipStream_t stream) {
+  // ds = A B is [M, F]; gu and dgu are [M, 2F]; act (nullable) is [M, F]
+  NMB_REQUIRE(dgu != nullptr && gu != nullptr, "gemm_swiglu_bwd: null gu or dgu");
+  const int st = nmb::check_gemm(0, b_layout, m, f, k, a, lda, b, ldb, false, nullptr, 0, dgu, lddgu);
+  if (st != NMB_OK) return st;
+  NMB_REQUIRE_SUPPORTED(f % 8 == 0, "gemm_swiglu_bwd: F (%lld) must be a multiple of 8", (long long)f);
+  NMB_REQUIRE(ldgu >= 2 * f && ldgu % 8 == 0 && nmb::aligned16(gu) && lddgu >= 2 * f && lddgu % 8 == 0,
+              "gemm_swiglu_bwd: gu and dgu must be 16-byte aligned [M, 2F] with leading dimensions multiples of 8");
+  NMB_REQUIRE(act == nullptr || (ldact >= f && ldact % 8 == 0 && nmb::aligned16(act)),
+              "gemm_swiglu_bwd: act must be 16-byte aligned [M, F] with a leading dimension multiple of 8");
+  if (m == 0 || f == 0) return NMB_OK;
+  const bool b_kc = b_layout == 0;
+  const nmb::Plan p = nmb::plan_for(m, f, k, true, b_kc, 0, true);
+  nmb::GemmArgs g = nmb::make_args(m, f, k, 1.f, a, lda, b, ldb, 0.f, nullptr, 0, act, ldact, nullptr, p);
+  g.swb_gu = static_cast<const nmb::bf16*>(gu);
+  g.swb_ldgu = ldgu;
+  g.swb_dgu = static_cast<nmb::bf16*>(dgu);
+  g.swb_lddgu = lddgu;
+  return nmb::dispatch_swiglu_bwd(p.config, b_kc, g, stream);
 }

@@ -111,14 +111,7 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const T* __restrict__ g
     unpack<T>(uraw[k], uv);
     unpack<T>(draw[k], dv);
 #pragma unroll
-    for (int e = 0; e < V; ++e) {
-      const float sig = sigmoid_f(gv[e]);
-      const float s = silu_t<T>(gv[e], sig);
-      ov[k][e] = mul_rn(s, uv[e]);
-      duv[k][e] = mul_rn(dv[e], s);
-      const float ds = round_as<T>(mul_rn(dv[e], uv[e]));
-      dgv[k][e] = ds * sig * (1.0f + gv[e] * (1.0f - sig));
-    }
+    for (int e = 0; e < V; ++e) swiglu_bwd_elem<T>(gv[e], uv[e], dv[e], dgv[k][e], duv[k][e], ov[k][e]);
   }
 #pragma unroll
   for (int k = 0; k < kVec; ++k) {

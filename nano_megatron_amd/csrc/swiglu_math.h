@@ -42,4 +42,19 @@ __device__ __forceinline__ float swiglu_t(float g, float u) {
   return mul_rn(silu_t<T>(g, sigmoid_f(g)), u);
 }
 
+// The backward of out = silu(g) * u for one element, given d = dL/dout
+// (autograd of models/gpt/mlp.py:77): du = d * silu(g); dg = bf16(d * u) *
+// sigmoid(g) (1 + g (1 - sigmoid(g))); o = silu(g) * u re-emitted for the
+// down projection's weight gradient.  Shared by the SwiGLU backward kernel and
+// the down projection's GEMM epilogue, which must agree bit for bit.
+template <typename T>
+__device__ __forceinline__ void swiglu_bwd_elem(float g, float u, float d, float& dg, float& du, float& o) {
+  const float sig = sigmoid_f(g);
+  const float s = silu_t<T>(g, sig);
+  o = mul_rn(s, u);
+  du = mul_rn(d, s);
+  const float ds = round_as<T>(mul_rn(d, u));
+  dg = ds * sig * (1.0f + g * (1.0f - sig));
+}
+
 }  // namespace nmb

@@ -428,6 +428,37 @@ def swiglu_fwd(g: Tensor, u: Tensor, out: Tensor | None = None) -> Tensor:
     return out
 
 
+def mm_swiglu_bwd(dy: Tensor, wd: Tensor, gu: Tensor, *, act: bool = True) -> tuple[Tensor, Tensor | None]:
+    """The MLP's backward through the down projection and SwiGLU (autograd of
+    models/gpt/mlp.py:77-78): ``ds = dy @ wd`` (``wd`` the down projection's
+    [H, F] weight), then the SwiGLU backward against the forward's gate/up
+    product ``gu`` [M, 2F].  Returns (``dgu`` [M, 2F] = (d gate | d up), the
+    activation ``silu(g) * u`` [M, F] if act).  bf16 runs one GEMM with the
+    SwiGLU backward as its epilogue (``nmb_gemm_bf16_swiglu_bwd``, bit-identical
+    to the product then ``swiglu_bwd``, without ds in memory); other dtypes run
+    the two."""
+    m, h = dy.shape
+    h2, f = wd.shape
+    if h != h2 or gu.shape != (m, 2 * f):
+        raise ValueError("mm_swiglu_bwd: dy [M, H], wd [H, F] and gu [M, 2F] expected")
+    dgu = torch.empty_like(gu)
+    out = torch.empty(m, f, dtype=gu.dtype, device=gu.device) if act else None
+    if dy.dtype != torch.bfloat16:
+        ds = mm(dy, wd)
+        o = out if out is not None else torch.empty(m, f, dtype=gu.dtype, device=gu.device)
+        swiglu_bwd(gu[:, :f], gu[:, f:], ds, dgu[:, :f], dgu[:, f:], o)
+        return dgu, out
+    _require_gpu(dy, wd, gu)
+    if dy.stride(1) != 1 or wd.stride(1) != 1 or gu.stride(1) != 1 or not (dy.dtype == wd.dtype == gu.dtype):
+        raise ValueError("mm_swiglu_bwd: dy, wd and gu must be row-major and of one dtype")
+    _lib.call(
+        "nmb_gemm_bf16_swiglu_bwd", 1, m, f, h, dy.data_ptr(), max(dy.stride(0), h), wd.data_ptr(),
+        max(wd.stride(0), f), gu.data_ptr(), gu.stride(0), dgu.data_ptr(), dgu.stride(0), _lib.ptr(out),
+        out.stride(0) if out is not None else 0, _lib.stream_of(dy),
+    )
+    return dgu, out
+
+
 def mm_gate_up(a: Tensor, w_gu: Tensor, *, act: bool = True, gu: bool = False,
                act_out: Tensor | None = None, gu_out: Tensor | None = None
                ) -> tuple[Tensor | None, Tensor | None]:

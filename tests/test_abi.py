@@ -104,6 +104,26 @@ def test_rope_and_swiglu_and_ce_reject_bad_arguments() -> None:
     assert st == _lib.NMB_EINVAL and b"neither" in lib.nmb_last_error()
 
 
+def test_gemm_swiglu_bwd_rejects_bad_arguments() -> None:
+    lib = _lib.load()
+    st = lib.nmb_gemm_bf16_swiglu_bwd(1, 64, 64, 64, FAKE, 64, FAKE, 64, None, 128, FAKE, 128, None,
+                                      0, None)
+    assert st == _lib.NMB_EINVAL and b"null" in lib.nmb_last_error()
+    st = lib.nmb_gemm_bf16_swiglu_bwd(2, 64, 64, 64, FAKE, 64, FAKE, 64, FAKE, 128, FAKE, 128, None,
+                                      0, None)
+    assert st == _lib.NMB_EINVAL and b"b_layout" in lib.nmb_last_error()
+    st = lib.nmb_gemm_bf16_swiglu_bwd(1, 64, 12, 64, FAKE, 64, FAKE, 16, FAKE, 24, FAKE, 24, None,
+                                      0, None)
+    assert st == _lib.NMB_EUNSUPPORTED and b"multiples of 8" in lib.nmb_last_error()
+    # gu narrower than [M, 2F]
+    st = lib.nmb_gemm_bf16_swiglu_bwd(1, 64, 64, 64, FAKE, 64, FAKE, 64, FAKE, 64, FAKE, 128, None,
+                                      0, None)
+    assert st == _lib.NMB_EINVAL and b"[M, 2F]" in lib.nmb_last_error()
+    st = lib.nmb_gemm_bf16_swiglu_bwd(1, 64, 64, 64, FAKE, 64, FAKE, 64, FAKE, 128, FAKE, 128, FAKE,
+                                      32, None)
+    assert st == _lib.NMB_EINVAL and b"act" in lib.nmb_last_error()
+
+
 def test_gemm_f32_rejects_bad_arguments() -> None:
     lib = _lib.load()
     st = lib.nmb_gemm_f32(2, 0, 4, 4, 4, 1.0, FAKE, 4, FAKE, 4, 0.0, None, 4, FAKE, 4, None)

@@ -391,6 +391,34 @@ def test_gemm_bf16_many_tiles_per_workgroup(device, m, n, k, layout) -> None:
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("m,f,h", [(8192, 2736, 1024), (4096, 5632, 2048), (300, 200, 136)])
+def test_gemm_swiglu_bwd_equals_gemm_then_swiglu_bwd(device, m, f, h) -> None:
+    """nmb_gemm_bf16_swiglu_bwd (ds = dY Wd with the SwiGLU backward as the
+    epilogue) against the product then nmb_swiglu_bwd: bit for bit where both
+    use unsplit plans (M >= 4096), and against the fp32 expression."""
+    g = torch.Generator(device=device).manual_seed(m + f + h)
+    bf = torch.bfloat16
+    dy = torch.randn(m, h, device=device, generator=g).to(bf)
+    wd = (0.05 * torch.randn(h, f, device=device, generator=g)).to(bf)
+    gu = torch.randn(m, 2 * f, device=device, generator=g).to(bf)
+    dgu, act = Fn.mm_swiglu_bwd(dy, wd, gu)
+    dgu2, none = Fn.mm_swiglu_bwd(dy, wd, gu, act=False)
+    assert none is None and torch.equal(dgu, dgu2)
+    ds = Fn.mm(dy, wd)
+    rdgu = torch.empty_like(gu)
+    ract = torch.empty(m, f, dtype=bf, device=device)
+    Fn.swiglu_bwd(gu[:, :f], gu[:, f:], ds, rdgu[:, :f], rdgu[:, f:], ract)
+    assert torch.equal(act, ract)
+    if m >= 4096:
+        assert torch.equal(dgu, rdgu)
+    gf, uf = gu[:, :f].float(), gu[:, f:].float()
+    dsf = dy.float() @ wd.float()
+    sig = torch.sigmoid(gf)
+    torch.testing.assert_close(dgu[:, f:].float(), dsf * gf * sig, rtol=2e-2, atol=2e-2)
+    torch.testing.assert_close(dgu[:, :f].float(), dsf * uf * sig * (1 + gf * (1 - sig)), rtol=2e-2, atol=2e-2)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("batch,seq,hq,hkv,d,offset,explicit", [
     (4, 128, 4, 2, 64, 0, False),
     (2, 256, 2, 1, 128, 0, True),
