@@ -54,12 +54,13 @@ __device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<
 
 // 16-byte chunk slots of the K-contiguous tile.  64-deep K tiles (128-byte
 // rows, 8 chunks): row r keeps chunk c in slot c ^ (r & 7).  32-deep K tiles
-// (64-byte rows, 4 chunks): slot c ^ (((r >> 1) & 3) ^ ((r >> 3) & 1)), so that
-// the 16 rows of a fragment read spread over all banks whether the hardware
-// serves 8 or 16 lanes per pass.
+// (64-byte rows, 4 chunks): slot c ^ ((r >> 1) & 3).  With these a fragment
+// read (16 rows x 16 bytes in each group of 16 lanes) has no LDS bank
+// conflicts on gfx950 (SQ_LDS_BANK_CONFLICT reads zero; c ^ (r & 3), no
+// swizzle, and ((r >> 1) & 3) ^ ((r >> 3) & 1) give two-way conflicts).
 template <int BKT>
 __device__ __forceinline__ int kc_swizzle(int r) {
-  return BKT == 64 ? (r & 7) : (((r >> 1) & 3) ^ ((r >> 3) & 1));
+  return BKT == 64 ? (r & 7) : ((r >> 1) & 3);
 }
 // 32-byte pair slots of the M/N-contiguous tile: k row k keeps pair p in slot
 // p ^ rc_swizzle(k), so that the 8 k rows of a half-wave transposed read
@@ -134,6 +135,23 @@ struct Loader {
     for (int j = 0; j < kPer; ++j) {
       const bool ok = off[j] != kOOB && k0 + kin[j] < k_end;
       load_lds16(rsrc, tile + 512 * (wave * kPer + j), ok ? off[j] + koff : kOOB);
+    }
+  }
+  // The same with scalar arithmetic only for a whole K tile: m0 is the LDS
+  // byte address of this wave's first 1 KB of the tile (uniform) and the K
+  // advance rides in the instruction's scalar offset; a partial last K tile
+  // zeroes its chunks past k_end per lane.
+  __device__ __forceinline__ void issue_s(uint32_t m0, int k0, int k_end) const {
+    const uint32_t koff = static_cast<uint32_t>(k0) * kstride;
+    if (k0 + BKT <= k_end) {
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) load_lds16s(rsrc, m0 + 1024u * j, off[j], koff);
+    } else {
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const bool ok = off[j] != kOOB && k0 + kin[j] < k_end;
+        load_lds16s(rsrc, m0 + 1024u * j, ok ? off[j] : kOOB, koff);
+      }
     }
   }
 };
@@ -283,10 +301,21 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void gemm_kernel(GemmArgs
   // then the MFMAs.
   constexpr int kLoads = Loader<TBM, A_KC, BKT, NW>::kPer + Loader<TBN, B_KC, BKT, NW>::kPer;
   const int nk = (k_end - k_begin + BKT - 1) / BKT;
+  // scalar load issue (fewer VALU instructions in the loop): 1-4% faster on
+  // the 256 x 128 and 128-row tiles, 2-4% slower on 256 x 256 (measured)
+  constexpr bool kScalarIssue = !(TBM == 256 && TBN == 256);
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t a_lds = lds_offset(&sA[0][0]) + 1024u * wave_u * Loader<TBM, A_KC, BKT, NW>::kPer;
+  const uint32_t b_lds = lds_offset(&sB[0][0]) + 1024u * wave_u * Loader<TBN, B_KC, BKT, NW>::kPer;
   auto issue = [&](int kt) {
     const int st = kt % S;
-    la.issue(&sA[st][0], k_begin + kt * BKT, k_end, wave);
-    lb.issue(&sB[st][0], k_begin + kt * BKT, k_end, wave);
+    if constexpr (kScalarIssue) {
+      la.issue_s(a_lds + st * (TBM * BKT * 2u), k_begin + kt * BKT, k_end);
+      lb.issue_s(b_lds + st * (TBN * BKT * 2u), k_begin + kt * BKT, k_end);
+    } else {
+      la.issue(&sA[st][0], k_begin + kt * BKT, k_end, wave);
+      lb.issue(&sB[st][0], k_begin + kt * BKT, k_end, wave);
+    }
   };
 #pragma unroll
   for (int p = 0; p < S - 1; ++p)

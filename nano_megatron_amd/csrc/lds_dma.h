@@ -47,6 +47,15 @@ __device__ __forceinline__ void load_lds16(const i32x4& r, const bf16* lds, uint
                : "memory");
 }
 
+// As load_lds16 with the LDS byte address m0 already wave-uniform (an SGPR
+// value) and a wave-uniform byte offset soff added to the lane offsets.
+__device__ __forceinline__ void load_lds16s(const i32x4& r, uint32_t m0, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(m0), "v"(voff), "s"(r), "s"(soff)
+               : "memory");
+}
+
 // 4 bytes per lane from buffer offset voff into LDS at byte address
 // lds + 4 * lane (as load_lds16).
 __device__ __forceinline__ void load_lds4(const i32x4& r, const void* lds, uint32_t voff) {
