@@ -145,9 +145,11 @@ class _SideProducts:
     The weight gradients of the block feed nothing else in its backward; on
     their own stream (default priority, like every stream here) they fill the
     CUs that the dX chain's launches leave idle (products of 128-176
-    workgroups, split-K tails).  The out-projection's stays on the main stream:
-    its overlap would fall on the attention backward, whose workgroups it then
-    displaces (measured slower).  Each product waits for the work queued so far
+    workgroups, split-K tails).  The MLP's two run there; the out-projection's
+    and the QKV projection's stay on the main stream: the first's overlap would
+    fall on the attention backward, whose workgroups it then displaces, the
+    second's on the norm backward only, with the join then holding the next
+    layer's recompute (each measured slower on the side).  Each product waits for the work queued so far
     on the main stream, its operands are recorded on the side stream (the
     allocator keeps them until it is done), and ``join`` makes the main stream
     wait for all of them before the gradients are returned (autograd may read
@@ -211,7 +213,9 @@ def block_backward(acts: dict, dy: Tensor, w: tuple[Tensor, ...], m: BlockMeta, 
                           scale=None, cos=m.cos, sin=m.sin, pos_offset=m.pos_offset,
                           positions=m.positions)
     dn1 = Fn.mm(dqkv, joined((wq, wk, wv)))
-    dwqkv = side.mm(dqkv.t(), n1)
+    # on the main stream too: on the side it only overlaps the norm backward,
+    # and the join then holds the next layer's recompute (measured slower)
+    dwqkv = Fn.mm(dqkv.t(), n1)
     dx, dw_in = Fn.rmsnorm_bwd(x2, w_in, dn1, m.eps, residual_grad=dh)
     side.join()
 
