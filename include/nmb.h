@@ -263,6 +263,19 @@ int nmb_gemm_bf16(int a_layout, int b_layout, int64_t m, int64_t n, int64_t k, f
                   const void* c, int64_t ldc, void* d, int64_t ldd, void* workspace,
                   int64_t workspace_bytes, hipStream_t stream);
 
+/* bf16 GEMM with an fp32 output, for sums of products rounded to bf16 once
+ * (the tied LM-head gradient dE = sum over token chunks of G_c^T x_c, which
+ * the reference forms as one product G^T X with one rounding:
+ * tensor_parallel/layers.py:207-214 under autograd):
+ *   D32[M, N] = alpha * op(A) * op(B) + beta * D32   (fp32, row-major)
+ * Operands, layouts, checks and workspace as nmb_gemm_bf16 (same plan, so
+ * nmb_gemm_bf16_workspace_bytes gives the size); ldd32 >= N, a multiple of 4,
+ * D32 16-byte aligned. */
+int nmb_gemm_bf16_f32out(int a_layout, int b_layout, int64_t m, int64_t n, int64_t k, float alpha,
+                         const void* a, int64_t lda, const void* b, int64_t ldb, float beta,
+                         float* d32, int64_t ldd32, void* workspace, int64_t workspace_bytes,
+                         hipStream_t stream);
+
 /* fp32 GEMM on the fp32 matrix cores, for the fp32 parity configuration
  * (replaces the same nn.Linear / F.linear products in fp32):
  *   D[M, N] = alpha * op(A) * op(B) + beta * C, layouts as nmb_gemm_bf16

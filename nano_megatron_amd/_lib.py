@@ -89,6 +89,9 @@ SIGNATURES: dict[str, list] = {
     "nmb_gemm_f32": [
         _i32, _i32, _i64, _i64, _i64, _f32, _p, _i64, _p, _i64, _f32, _p, _i64, _p, _i64, _p,
     ],
+    "nmb_gemm_bf16_f32out": [
+        _i32, _i32, _i64, _i64, _i64, _f32, _p, _i64, _p, _i64, _f32, _p, _i64, _p, _i64, _p,
+    ],
     "nmb_gemm_bf16_rope": [
         _i32, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i64,
         _i64, _i64, _p,

@@ -216,6 +216,11 @@ struct GemmArgs {
   int64_t swb_ldgu;
   bf16* swb_dgu;
   int64_t swb_lddgu;
+  // fp32 output (nullable): D32 = alpha A B + beta D32, written in place of D
+  // (C and D unused); unsplit plans store it from the tile, split ones from
+  // the reduction
+  float* d32;
+  int64_t ldd32;
 };
 
 // Columns of D covered by one TBN-wide tile: TBN, or TBN / 2 with the SwiGLU
@@ -393,9 +398,12 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void gemm_kernel(GemmArgs
         *reinterpret_cast<f32x4*>(slot_at(lr, (wn + 16 * j + 4 * q4) >> 2)) = acc[i][j];
     }
   };
-  if (g.splits > 1) {
-    // fp32 partials, each row stored by whole 16-byte slots
-    float* part = g.partial + static_cast<int64_t>(split) * g.M * g.N;
+  if (g.splits > 1 || g.d32 != nullptr) {
+    // fp32 partials, each row stored by whole 16-byte slots; or, unsplit with
+    // an fp32 output, D32 = alpha acc + beta D32 (as the reduction forms it)
+    const bool direct = g.splits == 1;
+    float* part = direct ? g.d32 : g.partial + static_cast<int64_t>(split) * g.M * g.N;
+    const int64_t ldp = direct ? g.ldd32 : g.N;
     constexpr int LPR = TBN / 4, RPI = 64 / LPR, ROWS_PER_WAVE = PR / NW;
     static_assert(ROWS_PER_WAVE % RPI == 0, "whole store instructions per wave");
     const int sl = lane % LPR;
@@ -407,9 +415,20 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void gemm_kernel(GemmArgs
 #pragma unroll
       for (int it = 0; it < ROWS_PER_WAVE / RPI; ++it) {
         const int lr = wave * ROWS_PER_WAVE + it * RPI + lane / LPR;
-        const f32x4 v = *reinterpret_cast<const f32x4*>(slot_at(lr, sl));
+        f32x4 v = *reinterpret_cast<const f32x4*>(slot_at(lr, sl));
         const int m = m0 + p0 + lr, n = n0 + 4 * sl;
-        if (m < g.M && n < g.N) *reinterpret_cast<f32x4*>(part + static_cast<int64_t>(m) * g.N + n) = v;
+        if (m < g.M && n < g.N) {
+          f32x4* dst = reinterpret_cast<f32x4*>(part + static_cast<int64_t>(m) * ldp + n);
+          if (direct) {
+            const f32x4 old = g.beta != 0.f ? *dst : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              v[e] = g.alpha * v[e];
+              if (g.beta != 0.f) v[e] += g.beta * old[e];
+            }
+          }
+          *dst = v;
+        }
       }
     }
     return;
@@ -720,6 +739,21 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
       v[e] = g.alpha * s0[e];
       v[4 + e] = g.alpha * s1[e];
     }
+    if (g.d32 != nullptr) {
+      // fp32 output: D32 = alpha sum + beta D32
+      f32x4* dst = reinterpret_cast<f32x4*>(g.d32 + static_cast<int64_t>(m) * g.ldd32 + n);
+      if (g.beta != 0.f) {
+        const f32x4 o0 = dst[0], o1 = dst[1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] += g.beta * o0[e];
+          v[4 + e] += g.beta * o1[e];
+        }
+      }
+      dst[0] = f32x4{v[0], v[1], v[2], v[3]};
+      dst[1] = f32x4{v[4], v[5], v[6], v[7]};
+      continue;
+    }
     if (g.beta != 0.f) {
       const bf16x8 cv = ld8(g.c + static_cast<int64_t>(m) * g.ldc + n);
 #pragma unroll
@@ -975,6 +1009,34 @@ extern "C" int nmb_gemm_bf16(int a_layout, int b_layout, int64_t m, int64_t n, i
               (long long)workspace_bytes);
   NMB_REQUIRE(need == 0 || nmb::aligned16(workspace), "gemm: workspace must be 16-byte aligned");
   const nmb::GemmArgs g = nmb::make_args(m, n, k, alpha, a, lda, b, ldb, beta, c, ldc, d, ldd, workspace, p);
+  switch (p.config) {
+    case 0: return nmb::dispatch_layout<256, 256, 8, 64>(a_kc, b_kc, g, stream);
+    case 1: return nmb::dispatch_layout<256, 128, 8, 64>(a_kc, b_kc, g, stream);
+    case 2: return nmb::dispatch_layout<128, 128, 4, 32>(a_kc, b_kc, g, stream);
+    default: return nmb::dispatch_layout<128, 256, 4, 32>(a_kc, b_kc, g, stream);
+  }
+}
+
+extern "C" int nmb_gemm_bf16_f32out(int a_layout, int b_layout, int64_t m, int64_t n, int64_t k,
+                                    float alpha, const void* a, int64_t lda, const void* b,
+                                    int64_t ldb, float beta, float* d32, int64_t ldd32,
+                                    void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  // the bf16 checks (D32 stands in for D: non-null, 16-byte aligned), then D32's leading dimension
+  const int st = nmb::check_gemm(a_layout, b_layout, m, n, k, a, lda, b, ldb, false, nullptr, 0, d32, n);
+  if (st != NMB_OK) return st;
+  NMB_REQUIRE(ldd32 >= n && ldd32 % 4 == 0,
+              "gemm_f32out: D32 leading dimension must be >= N and a multiple of 4");
+  if (m == 0 || n == 0) return NMB_OK;
+  const bool a_kc = a_layout == 0, b_kc = b_layout == 0;
+  const nmb::Plan p = nmb::plan_for(m, n, k, a_kc, b_kc);
+  const int64_t need = nmb::workspace_for(p, m, n);
+  NMB_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+              "gemm_f32out: workspace of %lld bytes needed, %lld given", (long long)need,
+              (long long)workspace_bytes);
+  NMB_REQUIRE(need == 0 || nmb::aligned16(workspace), "gemm_f32out: workspace must be 16-byte aligned");
+  nmb::GemmArgs g = nmb::make_args(m, n, k, alpha, a, lda, b, ldb, beta, nullptr, 0, nullptr, 0, workspace, p);
+  g.d32 = d32;
+  g.ldd32 = ldd32;
   switch (p.config) {
     case 0: return nmb::dispatch_layout<256, 256, 8, 64>(a_kc, b_kc, g, stream);
     case 1: return nmb::dispatch_layout<256, 128, 8, 64>(a_kc, b_kc, g, stream);

@@ -97,6 +97,37 @@ def mm(a: Tensor, b: Tensor, *, out: Tensor | None = None, c: Tensor | None = No
     return out
 
 
+def mm_f32out(a: Tensor, b: Tensor, out: Tensor, *, alpha: float = 1.0, beta: float = 0.0) -> Tensor:
+    """``out = alpha * a @ b + beta * out`` with bf16 ``a``, ``b`` and an fp32
+    row-major ``out`` (``nmb_gemm_bf16_f32out``): sums of bf16 products kept
+    in fp32, to be rounded once by the caller."""
+    m, k = a.shape
+    k2, n = b.shape
+    if k != k2 or out.shape != (m, n):
+        raise ValueError(f"gemm_f32out: shapes {tuple(a.shape)} x {tuple(b.shape)} -> {tuple(out.shape)}")
+    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16 or out.dtype != torch.float32:
+        raise ValueError("gemm_f32out: bf16 operands and an fp32 output needed")
+    _require_gpu(a, b, out)
+    if out.stride(1) != 1:
+        raise ValueError("gemm_f32out: the output must be row-major")
+    la, lda = _operand_layout(a, 0)
+    lb_rowmajor, ldb = _operand_layout(b, 0)
+    lb = 1 - lb_rowmajor
+    key = (la, lb, m, n, k)
+    nbytes = _GEMM_WS.get(key)
+    if nbytes is None:
+        q = _lib.ctypes.c_int64()
+        _lib.call("nmb_gemm_bf16_workspace_bytes", la, lb, m, n, k, _lib.ctypes.byref(q))
+        nbytes = _GEMM_WS[key] = q.value
+    ws = _workspace(nbytes, a.device) if nbytes else None
+    _lib.call(
+        "nmb_gemm_bf16_f32out", la, lb, m, n, k, float(alpha), a.data_ptr(), lda, b.data_ptr(), ldb,
+        float(beta), out.data_ptr(), out.stride(0), _lib.ptr(ws), ws.numel() if ws is not None else 0,
+        _lib.stream_of(a),
+    )
+    return out
+
+
 def _any_layout(t: Tensor) -> tuple[Tensor, int, int]:
     """(t or a contiguous copy, layout, ld) for an fp32 operand (layout as _operand_layout)."""
     try:
@@ -955,7 +986,8 @@ class LMHeadCrossEntropyFunction(torch.autograd.Function):
     buffer), then ``nmb_ce_fwd`` -> per-token loss and lse.  Only lse is kept.
     Backward, per chunk: recompute the chunk's logits, ``nmb_ce_bwd`` turns them
     in place into G = (softmax - onehot) * grad, then dx_c = G E and
-    dE += G^T x_c (fixed chunk order: deterministic).  Matches
+    dE += G^T x_c (fixed chunk order: deterministic), summed in fp32 and rounded
+    to bf16 once, as the reference's single product G^T X is.  Matches
     VocabParallelLinear + _VocabParallelCrossEntropy at TP=1
     (tensor_parallel/layers.py:207-214, cross_entropy.py:30-86).
     """
@@ -984,15 +1016,26 @@ class LMHeadCrossEntropyFunction(torch.autograd.Function):
         grad_loss = grad_loss.float().contiguous()
         rows = x2.shape[0]
         dx = torch.empty_like(x2)
-        dw = torch.zeros_like(weight)
+        f32 = weight.dtype == torch.float32
+        # the bf16 gradient accumulates over the chunks in fp32 (one rounding at the end)
+        if f32:
+            dw = torch.zeros_like(weight)
+        else:  # the first chunk writes it (beta 0)
+            dw = (torch.empty if rows > 0 else torch.zeros)(weight.shape, dtype=torch.float32,
+                                                             device=weight.device)
         buf = torch.empty(min(ctx.chunk, max(rows, 1)), weight.shape[0], dtype=x2.dtype,
                           device=x2.device)
-        for s, e in _chunks(rows, ctx.chunk):
+        for i, (s, e) in enumerate(_chunks(rows, ctx.chunk)):
             g = buf[: e - s]
             mm(x2[s:e], weight.t(), out=g)
             ce_bwd_(g, targets[s:e], ctx.ignore_index, lse[s:e], grad_loss[s:e])
             mm(g, weight, out=dx[s:e])
-            mm(g.t(), x2[s:e], out=dw, c=dw, beta=1.0)
+            if f32:
+                mm(g.t(), x2[s:e], out=dw, c=dw, beta=1.0)
+            else:
+                mm_f32out(g.t(), x2[s:e], dw, beta=0.0 if i == 0 else 1.0)
+        if not f32:
+            dw = dw.to(weight.dtype)
         if ctx.tie is not None:  # the embedding's backward adds it to its own gradient
             ctx.tie.grad = dw
             return dx, None, None, None, None, None

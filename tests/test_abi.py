@@ -104,6 +104,23 @@ def test_rope_and_swiglu_and_ce_reject_bad_arguments() -> None:
     assert st == _lib.NMB_EINVAL and b"neither" in lib.nmb_last_error()
 
 
+def test_gemm_f32out_rejects_bad_arguments() -> None:
+    lib = _lib.load()
+    st = lib.nmb_gemm_bf16_f32out(0, 0, 64, 64, 64, 1.0, FAKE, 64, FAKE, 64, 0.0, None, 64, None, 0,
+                                  None)
+    assert st == _lib.NMB_EINVAL and b"null" in lib.nmb_last_error()
+    st = lib.nmb_gemm_bf16_f32out(0, 0, 64, 64, 64, 1.0, FAKE, 64, FAKE, 64, 0.0, FAKE, 62, None, 0,
+                                  None)
+    assert st == _lib.NMB_EINVAL and b"multiple of 4" in lib.nmb_last_error()
+    st = lib.nmb_gemm_bf16_f32out(0, 0, 64, 64, 64, 1.0, FAKE, 64, FAKE, 64, 0.0, FAKE, 32, None, 0,
+                                  None)
+    assert st == _lib.NMB_EINVAL and b">= N" in lib.nmb_last_error()
+    # a split plan needs its workspace
+    st = lib.nmb_gemm_bf16_f32out(1, 1, 1024, 1024, 8192, 1.0, FAKE, 1024, FAKE, 1024, 0.0, FAKE,
+                                  1024, None, 0, None)
+    assert st == _lib.NMB_EINVAL and b"workspace" in lib.nmb_last_error()
+
+
 def test_gemm_swiglu_bwd_rejects_bad_arguments() -> None:
     lib = _lib.load()
     st = lib.nmb_gemm_bf16_swiglu_bwd(1, 64, 64, 64, FAKE, 64, FAKE, 64, None, 128, FAKE, 128, None,

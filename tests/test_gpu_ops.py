@@ -763,3 +763,63 @@ def test_backend_linear_matches_torch_linear(device, dtype) -> None:
     close(yd, yr, dtype)
     close(xd.grad, xr.grad, dtype, scale_atol=True)
     close(ours.weight.grad, ref.weight.grad, dtype, scale_atol=True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m,n,k,at,bt", [(8192, 1024, 2048, True, True), (1024, 1024, 8192, True, True),
+                                         (304, 520, 136, False, False), (2048, 3072, 1024, False, True)])
+def test_gemm_f32out_is_the_bf16_gemm_before_its_rounding(device, m, n, k, at, bt) -> None:
+    """nmb_gemm_bf16_f32out (beta 0) rounded to bf16 equals nmb_gemm_bf16 bit for
+    bit (same plan and sums, split along K or not); its fp32 values lie within
+    the fp32 summation bound of the exact product; alpha and beta apply in fp32."""
+    g = torch.Generator(device=device).manual_seed(m + n + k)
+    bf = torch.bfloat16
+    a = torch.randn(k, m, device=device, generator=g).to(bf).t() if at else \
+        torch.randn(m, k, device=device, generator=g).to(bf)
+    b = torch.randn(k, n, device=device, generator=g).to(bf) if bt else \
+        torch.randn(n, k, device=device, generator=g).to(bf).t()
+    out = torch.empty(m, n, dtype=torch.float32, device=device)
+    Fn.mm_f32out(a, b, out)
+    assert torch.equal(out.to(bf), Fn.mm(a, b))
+    exact = a.double() @ b.double()
+    bound = k * 2.0 ** -24 * (a.double().abs() @ b.double().abs())
+    assert bool(((out.double() - exact).abs() <= bound).all())
+    twice = out.clone()
+    Fn.mm_f32out(a, b, twice, beta=1.0)
+    assert torch.equal(twice, 2 * out)
+    half = torch.empty_like(out)
+    Fn.mm_f32out(a, b, half, alpha=0.5)
+    assert torch.equal(half, 0.5 * out)
+
+
+@pytest.mark.gpu
+def test_lm_head_table_gradient_is_rounded_once(device) -> None:
+    """The tied LM head's table gradient, accumulated over four 2048-token chunks,
+    is the bf16 rounding of a value within the fp32 summation bound of the exact
+    sum of G_c^T x_c (as the reference's single product G^T X is rounded once),
+    not the sum of four rounded chunk products."""
+    g = torch.Generator(device=device).manual_seed(11)
+    bf = torch.bfloat16
+    t, h, v, chunk = 8192, 1024, 8192, 2048
+    x = torch.randn(t, h, device=device, generator=g).to(bf)
+    w = (0.02 * torch.randn(v, h, device=device, generator=g)).to(bf).requires_grad_()
+    y = torch.randint(0, v, (t,), device=device, generator=g)
+    Fn.lm_head_cross_entropy(x, w, y, reduction="sum", chunk=chunk).backward()
+    # the chunks' G exactly as the backward forms them (same kernels, same inputs)
+    with torch.no_grad():
+        loss = torch.empty(t, dtype=torch.float32, device=device)
+        lse = torch.empty_like(loss)
+        ones = torch.ones(t, dtype=torch.float32, device=device)
+        exact = torch.zeros(v, h, dtype=torch.float64, device=device)
+        absum = torch.zeros_like(exact)
+        for s in range(0, t, chunk):
+            logits = Fn.mm(x[s:s + chunk], w.detach().t())
+            Fn.ce_fwd(logits, y[s:s + chunk], -100, loss[s:s + chunk], lse[s:s + chunk])
+            Fn.ce_bwd_(logits, y[s:s + chunk], -100, lse[s:s + chunk], ones[s:s + chunk])
+            exact += logits.double().t() @ x[s:s + chunk].double()
+            absum += logits.double().abs().t() @ x[s:s + chunk].double().abs()
+        bound = t * 2.0 ** -24 * absum
+        mag = exact.abs() + bound
+        half_ulp = torch.where(mag > 0, torch.exp2(torch.floor(torch.log2(mag)) - 8), torch.zeros_like(mag))
+        err = (w.grad.double() - exact).abs()
+        assert bool((err <= half_ulp + bound).all()), float((err - half_ulp - bound).max())
