@@ -309,6 +309,9 @@ def kernel_rooflines(device, only: str | None = None) -> list[dict]:
     w_qkv = randn(3 * H, H)
     qkv_out = torch.empty(T, 3 * H, dtype=bf, device=device)
     w_gu = randn(2 * F, H)
+    dy_swb, wd_swb, gu_swb = randn(T, H), randn(H, F), randn(T, 2 * F)
+    g_de, x_de = randn(chunk, V), randn(chunk, H)
+    de32 = torch.zeros(V, H, dtype=torch.float32, device=device)
     gu_buf = torch.empty(T, 2 * F, dtype=bf, device=device)
     gemms = [
         # the Q/K/V projection with RoPE of q and k in its epilogue, as the block runs it
@@ -324,7 +327,10 @@ def kernel_rooflines(device, only: str | None = None) -> list[dict]:
         ("gemm_gate_up_swiglu", lambda: Fn.mm_gate_up(x, w_gu, act=True, act_out=act),
          (T * H + 2 * F * H + T * F) * E, 2.0 * T * 2 * F * H, "mfma", L),
         gemm_case("gemm_down_residual", T, H, F, False, False, L, residual=True),
-        gemm_case("gemm_d_swiglu", T, F, H, False, True, L),
+        # ds = dY Wd with the SwiGLU backward as its epilogue (reads [g|u], writes
+        # [dg|du] and the re-emitted activation; ds never reaches memory)
+        ("gemm_d_swiglu_bwd", lambda: Fn.mm_swiglu_bwd(dy_swb, wd_swb, gu_swb),
+         (T * H + H * F + 5 * T * F) * E, 2.0 * T * F * H, "mfma", L),
         gemm_case("gemm_dw_down", H, F, T, True, True, L),
         gemm_case("gemm_d_norm2", T, H, 2 * F, False, True, L),
         gemm_case("gemm_dw_gate_up", 2 * F, H, T, True, True, L),
@@ -334,7 +340,9 @@ def kernel_rooflines(device, only: str | None = None) -> list[dict]:
         gemm_case("gemm_dw_qkv", 3 * H, H, T, True, True, L),
         gemm_case("gemm_lm_logits", chunk, V, H, False, False, 2 * T // chunk),
         gemm_case("gemm_lm_dx", chunk, H, V, False, True, T // chunk),
-        gemm_case("gemm_lm_dE", V, H, chunk, True, True, T // chunk, residual=True),
+        # the tied table gradient: dE += G^T x over the token chunks, summed in fp32
+        ("gemm_lm_dE", lambda: Fn.mm_f32out(g_de.t(), x_de, de32, beta=1.0),
+         (chunk * V + chunk * H) * E + 2 * V * H * 4, 2.0 * V * H * chunk, "mfma", T // chunk),
     ]
     hbm = [
         # name, make, algorithmic bytes, launches per training step (full recompute)
@@ -346,7 +354,8 @@ def kernel_rooflines(device, only: str | None = None) -> list[dict]:
         ("rope_apply", mk_rope, 2 * T * H * E, 0),
         # the standalone activation; the checkpointed step fuses it into the gate/up GEMM
         ("swiglu_fwd", mk_swiglu_fwd, 3 * T * F * E, 0),
-        ("swiglu_bwd", mk_swiglu_bwd, 6 * T * F * E, L),
+        # the standalone backward; the step runs it as the down projection's dX GEMM epilogue
+        ("swiglu_bwd", mk_swiglu_bwd, 6 * T * F * E, 0),
         ("ce_fwd", mk_ce_fwd, chunk * V * E + chunk * 16, T // chunk),
         ("ce_bwd", mk_ce_bwd, 2 * chunk * V * E + chunk * 16, T // chunk),
         # token rows gathered and written; the backward reads the output gradient and the
