@@ -7,18 +7,19 @@
 // with A stored K-contiguous ([M, K]) or M-contiguous ([K, M]) and B stored
 // K-contiguous ([N, K], a weight used as W^T) or N-contiguous ([K, N]).
 //
-// Workgroup tile 256 x 128, 128 x 256 or 128 x 128, K tile 32, 4 wavefronts in
-// a 2 x 2 arrangement, two workgroups per CU: a single wavefront per SIMD
-// issues MFMAs at about 60% of the peak rate, and two workgroups (unlike one of
-// 8 wavefronts) do not meet at the same barriers, so one's MFMAs fill the
-// other's barrier and LDS-latency stalls.
+// Configurations (a plan per shape picks one): 256 x 256 or 256 x 128 output
+// tiles of 8 wavefronts, one workgroup per CU, 64-deep K tiles; 128 x 128 or
+// 128 x 256 tiles of 4 wavefronts, two workgroups per CU, 32-deep K tiles.
+// Every one runs two wavefronts per SIMD: one wavefront per SIMD leaves the
+// MFMA unit idle through every LDS and barrier wait, and with the compiler's
+// accumulator allocation issues MFMAs at ~60% of the peak rate.
 //
 // Operands go from HBM straight into LDS (buffer_load ... lds, 16 bytes per
 // lane, no VGPR round trip), each in the layout it has in memory:
-//  * K-contiguous tile [rows][32 k]: 64-byte rows, the 16-byte k chunk c of
-//    row r stored in slot c ^ kc_swizzle(r).  An MFMA fragment (16 rows x 8 k
-//    per lane group) is one ds_read_b128 per lane.
-//  * M/N-contiguous tile [32 k][R]: 2R-byte k rows, the 32-byte chunk pair p
+//  * K-contiguous tile [rows][BKT k]: 2 BKT-byte rows, the 16-byte k chunk c
+//    of row r stored in slot c ^ kc_swizzle(r).  An MFMA fragment (16 rows x
+//    8 k per lane group) is one ds_read_b128 per lane.
+//  * M/N-contiguous tile [BKT k][R]: 2R-byte k rows, the 32-byte chunk pair p
 //    of k row k stored at pair slot p ^ rc_swizzle(k).  A fragment is two
 //    ds_read_b64_tr_b16 per lane: in each group of 16 lanes, lane i receives
 //    element i & 3 of the 8 bytes addressed by lane 4j + i/4 (j = 0..3), so
@@ -27,16 +28,19 @@
 // Row, column and k tails: the loads of invalid chunks get an offset past the
 // buffer's num_records, which the hardware returns as zeros.
 //
-// LDS holds two K tiles; the next tile's loads are issued right after the
-// barrier that publishes the current one (one barrier per K tile).  Each MFMA
-// computes a D^T tile (B fragment as the A operand), so a lane ends up with
-// four consecutive columns of one output row.  Blocks are mapped so that the
-// tiles an XCD (with its own L2) runs together form a 4 x 8 block of tiles.
+// LDS holds S = 2-4 K-tile stages (as many as fit the workgroup's share);
+// after the barrier that publishes tile kt, the loads of tile kt + S - 1 go
+// into the stage everyone has finished reading (one barrier per K tile).
+// Each MFMA computes a D^T tile (B fragment as the A operand), so a lane ends
+// up with four consecutive columns of one output row; the epilogues stage the
+// tile through LDS and store whole rows.  Blocks are mapped so that the tiles
+// an XCD (with its own L2) runs together form a 4 x 8 block of tiles.
 //
 // Split K (small M x N, long K -- the weight gradients): split s of a tile
 // covers K range [s * kps, (s + 1) * kps) and writes fp32 partials to the
 // caller's workspace; a second kernel sums the splits in a fixed order
-// (deterministic) and applies alpha, beta and the bf16 rounding.
+// (deterministic) and applies alpha, beta and the bf16 rounding (or writes
+// fp32, for nmb_gemm_bf16_f32out).
 #include <algorithm>
 
 #include "common.h"
