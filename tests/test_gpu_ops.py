@@ -461,11 +461,13 @@ def test_gemm_rope_equals_gemm_then_rope(device, batch, seq, hq, hkv, d, offset,
 
 @pytest.mark.gpu
 # config-3 rows: neither the fused entry nor the reference GEMM splits K there
-@pytest.mark.parametrize("batch,seq,heads,hidden", [(16, 512, 16, 1024)])
-def test_gemm_rope_split_launch_equals_gemm_then_rope(device, batch, seq, heads, hidden) -> None:
-    """At the config-3 Q/K/V shape the entry point runs the q/k columns (RoPE) and
-    the v columns (plain product) as two launches with different tile shapes;
-    the result still equals one GEMM followed by the rotary kernel, bit for bit."""
+@pytest.mark.parametrize("batch,seq,heads,hidden,explicit", [(16, 512, 16, 1024, False),
+                                                             (4, 2048, 16, 1024, True)])
+def test_gemm_rope_split_launch_equals_gemm_then_rope(device, batch, seq, heads, hidden, explicit) -> None:
+    """At the config-3 Q/K/V shape the entry point runs the q/k columns (RoPE, 256 x
+    256 tiles) and the v columns (plain product, 256 x 128 tiles) in one launch
+    (gemm_pair_kernel); the result still equals one GEMM followed by the rotary
+    kernel, bit for bit, with offset or explicit per-token positions."""
     import nano_megatron_amd as nm
 
     g = torch.Generator(device=device).manual_seed(11)
@@ -474,11 +476,14 @@ def test_gemm_rope_split_launch_equals_gemm_then_rope(device, batch, seq, heads,
     n = 3 * hidden
     x = torch.randn(batch * seq, hidden, device=device, generator=g).to(bf)
     w = (0.05 * torch.randn(n, hidden, device=device, generator=g)).to(bf)
-    tab = nm.RotaryEmbedding(d).tables(device, seq)
-    fused = Fn.mm_rope(x, w.t(), seq=seq, head_dim=d, rope_cols=2 * hidden, cos=tab.cos, sin=tab.sin)
+    tab = nm.RotaryEmbedding(d).tables(device, 2 * seq)
+    pos = (torch.randint(0, 2 * seq, (batch, seq), device=device, generator=g).to(torch.int32)
+           if explicit else None)
+    fused = Fn.mm_rope(x, w.t(), seq=seq, head_dim=d, rope_cols=2 * hidden, cos=tab.cos, sin=tab.sin,
+                       positions=pos)
     ref = Fn.mm(x, w.t())
     qk = ref.view(batch, seq, n)[:, :, :2 * hidden].unflatten(2, (2 * heads, d))
-    Fn.rope_apply(qk, qk, tab.cos, tab.sin)
+    Fn.rope_apply(qk, qk, tab.cos, tab.sin, positions=pos)
     assert torch.equal(fused, ref)
 
 
