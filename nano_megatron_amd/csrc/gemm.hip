@@ -675,43 +675,43 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int L,
     static_assert(IT % CH == 0, "whole chunks");
 #pragma unroll
     for (int c0 = 0; c0 < IT; c0 += CH) {
-    uint4 graw[CH], uraw[CH];
+      uint4 graw[CH], uraw[CH];
 #pragma unroll
-    for (int ci = 0; ci < CH; ++ci) {
-      const int it = c0 + ci;
-      const int r = wave * ROWS_PER_WAVE + it * RPI + lane / LPR;
-      const int m = m0 + r, n = n0 + 8 * sl;
-      // out-of-range lanes read row m0, column 0 (in range; never used)
-      const bool ok = m < g.M && n < g.N;
-      const bf16* row = g.swb_gu + static_cast<int64_t>(ok ? m : m0) * g.swb_ldgu + (ok ? n : 0);
-      graw[ci] = *reinterpret_cast<const uint4*>(row);
-      uraw[ci] = *reinterpret_cast<const uint4*>(row + g.N);
-    }
-#pragma unroll
-    for (int ci = 0; ci < CH; ++ci) {
-      const int it = c0 + ci;
-      const int r = wave * ROWS_PER_WAVE + it * RPI + lane / LPR;
-      const int m = m0 + r, n = n0 + 8 * sl;
-      const bf16x8 dsv = *reinterpret_cast<const bf16x8*>(tile_at(r, 8 * sl));
-      bf16x8 gv, uv, dgo, duo, oo;
-      __builtin_memcpy(&gv, &graw[ci], 16);
-      __builtin_memcpy(&uv, &uraw[ci], 16);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float dgf, duf, of;
-        swiglu_bwd_elem<bf16>(static_cast<float>(gv[e]), static_cast<float>(uv[e]), static_cast<float>(dsv[e]),
-                              dgf, duf, of);
-        dgo[e] = static_cast<bf16>(dgf);
-        duo[e] = static_cast<bf16>(duf);
-        oo[e] = static_cast<bf16>(of);
+      for (int ci = 0; ci < CH; ++ci) {
+        const int it = c0 + ci;
+        const int r = wave * ROWS_PER_WAVE + it * RPI + lane / LPR;
+        const int m = m0 + r, n = n0 + 8 * sl;
+        // out-of-range lanes read row m0, column 0 (in range; never used)
+        const bool ok = m < g.M && n < g.N;
+        const bf16* row = g.swb_gu + static_cast<int64_t>(ok ? m : m0) * g.swb_ldgu + (ok ? n : 0);
+        graw[ci] = *reinterpret_cast<const uint4*>(row);
+        uraw[ci] = *reinterpret_cast<const uint4*>(row + g.N);
       }
-      if (m < g.M && n < g.N) {
-        bf16* drow = g.swb_dgu + static_cast<int64_t>(m) * g.swb_lddgu;
-        *reinterpret_cast<bf16x8*>(drow + n) = dgo;
-        *reinterpret_cast<bf16x8*>(drow + g.N + n) = duo;
-        if (g.d != nullptr) *reinterpret_cast<bf16x8*>(g.d + static_cast<int64_t>(m) * g.ldd + n) = oo;
+#pragma unroll
+      for (int ci = 0; ci < CH; ++ci) {
+        const int it = c0 + ci;
+        const int r = wave * ROWS_PER_WAVE + it * RPI + lane / LPR;
+        const int m = m0 + r, n = n0 + 8 * sl;
+        const bf16x8 dsv = *reinterpret_cast<const bf16x8*>(tile_at(r, 8 * sl));
+        bf16x8 gv, uv, dgo, duo, oo;
+        __builtin_memcpy(&gv, &graw[ci], 16);
+        __builtin_memcpy(&uv, &uraw[ci], 16);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float dgf, duf, of;
+          swiglu_bwd_elem<bf16>(static_cast<float>(gv[e]), static_cast<float>(uv[e]), static_cast<float>(dsv[e]),
+                                dgf, duf, of);
+          dgo[e] = static_cast<bf16>(dgf);
+          duo[e] = static_cast<bf16>(duf);
+          oo[e] = static_cast<bf16>(of);
+        }
+        if (m < g.M && n < g.N) {
+          bf16* drow = g.swb_dgu + static_cast<int64_t>(m) * g.swb_lddgu;
+          *reinterpret_cast<bf16x8*>(drow + n) = dgo;
+          *reinterpret_cast<bf16x8*>(drow + g.N + n) = duo;
+          if (g.d != nullptr) *reinterpret_cast<bf16x8*>(g.d + static_cast<int64_t>(m) * g.ldd + n) = oo;
+        }
       }
-    }
     }
     return;
   }
