@@ -461,9 +461,11 @@ def test_gemm_rope_equals_gemm_then_rope(device, batch, seq, hq, hkv, d, offset,
 
 @pytest.mark.gpu
 # config-3 rows: neither the fused entry nor the reference GEMM splits K there
-@pytest.mark.parametrize("batch,seq,heads,hidden,explicit", [(16, 512, 16, 1024, False),
-                                                             (4, 2048, 16, 1024, True)])
-def test_gemm_rope_split_launch_equals_gemm_then_rope(device, batch, seq, heads, hidden, explicit) -> None:
+@pytest.mark.parametrize("batch,seq,heads,hidden,explicit,b_rowmajor", [(16, 512, 16, 1024, False, False),
+                                                                        (4, 2048, 16, 1024, True, False),
+                                                                        (16, 512, 16, 1024, False, True)])
+def test_gemm_rope_split_launch_equals_gemm_then_rope(device, batch, seq, heads, hidden, explicit,
+                                                      b_rowmajor) -> None:
     """At the config-3 Q/K/V shape the entry point runs the q/k columns (RoPE, 256 x
     256 tiles) and the v columns (plain product, 256 x 128 tiles) in one launch
     (gemm_pair_kernel); the result still equals one GEMM followed by the rotary
@@ -479,9 +481,10 @@ def test_gemm_rope_split_launch_equals_gemm_then_rope(device, batch, seq, heads,
     tab = nm.RotaryEmbedding(d).tables(device, 2 * seq)
     pos = (torch.randint(0, 2 * seq, (batch, seq), device=device, generator=g).to(torch.int32)
            if explicit else None)
-    fused = Fn.mm_rope(x, w.t(), seq=seq, head_dim=d, rope_cols=2 * hidden, cos=tab.cos, sin=tab.sin,
+    wt = w.t().contiguous() if b_rowmajor else w.t()  # B as [K, N] row-major or the weight's W^T view
+    fused = Fn.mm_rope(x, wt, seq=seq, head_dim=d, rope_cols=2 * hidden, cos=tab.cos, sin=tab.sin,
                        positions=pos)
-    ref = Fn.mm(x, w.t())
+    ref = Fn.mm(x, wt)
     qk = ref.view(batch, seq, n)[:, :, :2 * hidden].unflatten(2, (2 * heads, d))
     Fn.rope_apply(qk, qk, tab.cos, tab.sin, positions=pos)
     assert torch.equal(fused, ref)
