@@ -182,25 +182,34 @@ int nmb_attn_bwd_rope(const void* q, const void* k, const void* v, const void* o
                       int64_t n_pos, const int32_t* positions, int64_t pos_batch_stride,
                       int64_t pos_offset, hipStream_t stream);
 
-/* Attention with an explicit mask: local_attention called with attention_mask
- * (reference nn/kernels/torch_backend.py:60-76: the mask goes to SDPA, ANDed
- * with the causal mask when causal).  One K/V block at key offset 0; layouts
- * and strides as nmb_attn_fwd / nmb_attn_bwd.  mask_kind 1: a boolean mask,
+/* Attention with an explicit mask and/or dropout: local_attention called
+ * with attention_mask or dropout_p > 0 (reference nn/kernels/torch_backend.py:
+ * 60-76: the mask goes to SDPA, ANDed with the causal mask when causal, and
+ * SDPA applies dropout_p to the normalised probabilities).  One K/V block at
+ * key offset 0; layouts and strides as nmb_attn_fwd / nmb_attn_bwd.
+ * mask_kind 0: no mask (mask and mask_strides ignored); 1: a boolean mask,
  * one byte per entry, nonzero = attend; 2: an additive mask of the attention
  * dtype, added to the scaled scores (-inf drops the key).  mask_strides: the
  * mask's element strides over [batch, q_heads, seq_q, seq_k], 0 for a
  * broadcast dimension.  A query row with no visible key gives a zero output
- * row, lse = -inf and zero gradients (SDPA's safe softmax).  bf16 or fp32,
- * head_dim <= 128, any strides; computed in fp32 one query row per
- * wavefront (a parity path: no configuration of the reference uses a mask).
- * Backward workspace: nmb_attn_bwd_workspace_bytes (only its first half, the
- * delta rows, is used). */
+ * row, lse = -inf and zero gradients (SDPA's safe softmax).  dropout_p in
+ * [0, 1): probability (b, h, i, j) is kept iff bits >= floor(p * 2^32) and then
+ * scaled by 1 / (1 - p), with bits the 32-bit half (idx & 1) of SplitMix64's
+ * output for counter idx >> 1 under `seed` (SplitMix64: Steele, Lea and Flood,
+ * OOPSLA 2014) at idx = ((b * q_heads + h) * seq_q + i) * seq_k + j; lse is
+ * that of the undropped softmax, and the backward, given the same seed,
+ * regenerates the mask.  The mask cannot equal torch's Philox stream, so
+ * dropout matches the reference in distribution, not bit for bit.  bf16 or
+ * fp32, head_dim <= 128, any strides; computed in fp32 one query row per
+ * wavefront (a parity path: no configuration of the reference uses a mask
+ * or attention dropout).  Backward workspace: nmb_attn_bwd_workspace_bytes
+ * (only its first half, the delta rows, is used). */
 int nmb_attn_masked_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
                         int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
                         int64_t seq_k, int64_t head_dim, const int64_t* q_strides,
                         const int64_t* kv_strides, const int64_t* o_strides, const void* mask,
                         int mask_kind, const int64_t* mask_strides, int causal, int64_t q_offset,
-                        float scale, int dtype, hipStream_t stream);
+                        float scale, float dropout_p, uint64_t seed, int dtype, hipStream_t stream);
 int nmb_attn_masked_bwd(const void* q, const void* k, const void* v, const void* o,
                         const void* dout, const float* lse, void* dq, void* dk, void* dv,
                         void* workspace, size_t workspace_bytes, int64_t batch, int64_t q_heads,
@@ -208,7 +217,19 @@ int nmb_attn_masked_bwd(const void* q, const void* k, const void* v, const void*
                         const int64_t* q_strides, const int64_t* kv_strides,
                         const int64_t* o_strides, const void* mask, int mask_kind,
                         const int64_t* mask_strides, int causal, int64_t q_offset, float scale,
-                        int dtype, hipStream_t stream);
+                        float dropout_p, uint64_t seed, int dtype, hipStream_t stream);
+
+/* ------------------------------------------------------------ dropout
+ * replaces parallel_dropout (nn/dropout.py:47-70, F.dropout) and the residual
+ * add around it in GPTLayer.forward (models/gpt/layer.py:114-137) and after
+ * the embedding (models/gpt/model.py:203-212).
+ * out[i] = cast(residual[i] + cast(keep(i) ? x[i] / (1 - p) : 0)) over n
+ * contiguous elements of dtype, residual nullable (then 0); keep(i) is the
+ * SplitMix64 mask of nmb_attn_masked_fwd at idx = i.  Without a residual the
+ * call is also the dropout's backward (dx = dropout(dout), same seed).  out
+ * may alias x or residual.  p in [0, 1); p = 0 is the identity. */
+int nmb_dropout_add(const void* x, const void* residual, void* out, int64_t n, float p, uint64_t seed,
+                    int dtype, hipStream_t stream);
 
 /* ------------------------------------------------------------ embedding
  * replaces VocabParallelEmbedding.forward at TP=1 (tensor_parallel/

@@ -23,7 +23,15 @@ from nano_megatron_amd.gpt import (
     GPTOutput,
 )
 from nano_megatron_amd.kernels import HipKernelBackend, KernelBackend, build_kernel_backend
-from nano_megatron_amd.nn import RMSNorm, RotaryEmbedding, activation_checkpoint, apply_rotary_pos_emb
+from nano_megatron_amd.nn import (
+    ActivationCheckpoint,
+    RMSNorm,
+    RotaryEmbedding,
+    activation_checkpoint,
+    activation_rng_context,
+    apply_rotary_pos_emb,
+    parallel_dropout,
+)
 
 __all__ = [
     "ActivationCheckpointConfig",
@@ -40,6 +48,9 @@ __all__ = [
     "RMSNorm",
     "RotaryEmbedding",
     "activation_checkpoint",
+    "activation_rng_context",
+    "parallel_dropout",
+    "ActivationCheckpoint",
     "apply_rotary_pos_emb",
     "attention",
     "build_kernel_backend",

@@ -24,11 +24,15 @@ NMB_EHIP = 3
 NMB_F32 = 0
 NMB_BF16 = 1
 
+# nmb_abi_version() of the sources these signatures follow
+ABI_VERSION = 2
+
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int
 _f32 = ctypes.c_float
 _f64 = ctypes.c_double
+_u64 = ctypes.c_uint64
 _sz = ctypes.c_size_t
 _pi64 = ctypes.POINTER(ctypes.c_int64)
 _psz = ctypes.POINTER(ctypes.c_size_t)
@@ -71,12 +75,13 @@ SIGNATURES: dict[str, list] = {
     ],
     "nmb_attn_masked_fwd": [
         _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _pi64, _pi64, _pi64, _p, _i32,
-        _pi64, _i32, _i64, _f32, _i32, _p,
+        _pi64, _i32, _i64, _f32, _f32, _u64, _i32, _p,
     ],
     "nmb_attn_masked_bwd": [
         _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _i64, _i64, _i64, _i64, _i64, _i64, _pi64,
-        _pi64, _pi64, _p, _i32, _pi64, _i32, _i64, _f32, _i32, _p,
+        _pi64, _pi64, _p, _i32, _pi64, _i32, _i64, _f32, _f32, _u64, _i32, _p,
     ],
+    "nmb_dropout_add": [_p, _p, _p, _i64, _f32, _u64, _i32, _p],
     "nmb_embedding_fwd": [_p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "nmb_embedding_bwd": [_p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "nmb_ce_fwd": [_p, _i64, _p, _i64, _i64, _i64, _p, _p, _i32, _p],
@@ -128,6 +133,12 @@ def load() -> ctypes.CDLL:
                     "(nano_megatron_amd has no CPU fallback)"
                 )
             lib = ctypes.CDLL(str(LIB_PATH))
+            lib.nmb_abi_version.restype = ctypes.c_int
+            if lib.nmb_abi_version() != ABI_VERSION:
+                raise RuntimeError(
+                    f"{LIB_PATH} has ABI version {lib.nmb_abi_version()}, these bindings expect "
+                    f"{ABI_VERSION}; rebuild it with `python -m nano_megatron_amd.build`"
+                )
             for name, args in SIGNATURES.items():
                 fn = getattr(lib, name)
                 fn.argtypes = args

@@ -28,6 +28,7 @@
 #include <mutex>
 
 #include "common.h"
+#include "dropout_math.h"
 #include "lds_dma.h"
 
 namespace nmb {
@@ -1127,7 +1128,10 @@ __global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel
 // (one byte per entry, nonzero = attend), 2 an additive mask in the attention
 // dtype (added to the scaled scores; -inf drops the key).  A query row with no
 // visible key gives zeros and lse = -inf, as the safe softmax of the
-// reference's SDPA does.
+// reference's SDPA does.  Attention dropout (SDPA's dropout_p, applied to the
+// normalised probabilities): probability (b, h, i, j) is multiplied by the
+// dropout_math.h factor of index ((b * Hq + h) * Sq + i) * Sk + j; l and the
+// lse stay those of the undropped softmax.
 struct MaskRef {
   const void* p;
   int64_t sb, sh, sq, sk;  // element strides of [batch, q_heads, seq_q, seq_k] (0: broadcast)
@@ -1158,12 +1162,14 @@ __device__ __forceinline__ float dot_row(const T* a, const T* b, int D, int lane
 template <typename T, int MK>
 __global__ __launch_bounds__(64) void attn_fwd_generic_kernel(const T* __restrict__ q, KVBlocks kv,
                                                               T* __restrict__ o, float* __restrict__ lse,
-                                                              AttnShape p, int D, MaskRef mr) {
+                                                              AttnShape p, int D, MaskRef mr,
+                                                              DropoutParams dp) {
   const int lane = threadIdx.x;
   const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int hk = h / (p.Hq / p.Hkv);
   const T* qr = q + b * p.q_sb + static_cast<int64_t>(i) * p.q_ss + h * p.q_sh;
   const int64_t qa = p.q_offset + i;
+  const uint64_t prow = ((static_cast<uint64_t>(b) * p.Hq + h) * p.Sq + i) * p.Sk;  // dropout index base
   float m = -__builtin_inff(), l = 0.f;
   float acc[2] = {0.f, 0.f};
   for (int blk = 0; blk < p.nblk; ++blk) {
@@ -1181,10 +1187,11 @@ __global__ __launch_bounds__(64) void attn_fwd_generic_kernel(const T* __restric
       const float alpha = expf(m - mnew);
       const float pv = expf(sc - mnew);
       l = l * alpha + pv;
+      const float pz = pv * drop_factor(dp, prow + j);  // dropout acts after the normalisation
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         const int d = lane + 64 * c;
-        if (d < D) acc[c] = acc[c] * alpha + pv * to_f32(vr[d]);
+        if (d < D) acc[c] = acc[c] * alpha + pz * to_f32(vr[d]);
       }
       m = mnew;
     }
@@ -1204,13 +1211,14 @@ template <typename T, int MK>
 __global__ __launch_bounds__(64) void attn_bwd_dq_generic_kernel(
     const T* __restrict__ q, KVBlocks kv, const T* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, T* __restrict__ dq,
-    AttnShape p, int D, MaskRef mr) {
+    AttnShape p, int D, MaskRef mr, DropoutParams dp) {
   const int lane = threadIdx.x;
   const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int hk = h / (p.Hq / p.Hkv);
   const T* qr = q + b * p.q_sb + static_cast<int64_t>(i) * p.q_ss + h * p.q_sh;
   const T* dr = dout + b * p.o_sb + static_cast<int64_t>(i) * p.o_ss + h * p.o_sh;
   const int64_t row = (static_cast<int64_t>(b) * p.Hq + h) * p.Sq + i;
+  const uint64_t prow = static_cast<uint64_t>(row) * p.Sk;
   const float ls = lse[row], dl = delta[row];
   const int64_t qa = p.q_offset + i;
   float acc[2] = {0.f, 0.f};
@@ -1226,7 +1234,9 @@ __global__ __launch_bounds__(64) void attn_bwd_dq_generic_kernel(
         const T* kr = kb + static_cast<int64_t>(j) * p.kv_ss;
         const T* vr = vb + static_cast<int64_t>(j) * p.kv_ss;
         const float pv = expf(dot_row(qr, kr, D, lane) * p.scale + add - ls);
-        const float ds = pv * (dot_row(dr, vr, D, lane) - dl);
+        // dropout: dP = Z (dO . V) with Z = keep / (1 - p); delta = rowsum(dO o O) still
+        // equals sum_j P Z (dO . V), so dS = P (dP - delta)
+        const float ds = pv * (drop_factor(dp, prow + j) * dot_row(dr, vr, D, lane) - dl);
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
           const int d = lane + 64 * c;
@@ -1246,7 +1256,8 @@ __global__ __launch_bounds__(64) void attn_bwd_dq_generic_kernel(
 template <typename T, int MK>
 __global__ __launch_bounds__(64) void attn_bwd_dkdv_generic_kernel(
     const T* __restrict__ q, KVBlocks kv, const T* __restrict__ dout,
-    const float* __restrict__ lse, const float* __restrict__ delta, AttnShape p, int D, MaskRef mr) {
+    const float* __restrict__ lse, const float* __restrict__ delta, AttnShape p, int D, MaskRef mr,
+    DropoutParams dp) {
   const int lane = threadIdx.x;
   const int j = blockIdx.x, hk = blockIdx.y;
   const int blk = static_cast<int>(blockIdx.z) % p.nblk;
@@ -1273,12 +1284,14 @@ __global__ __launch_bounds__(64) void attn_bwd_dkdv_generic_kernel(
       const T* qr = q + b * p.q_sb + static_cast<int64_t>(i) * p.q_ss + h * p.q_sh;
       const T* dr = dout + b * p.o_sb + static_cast<int64_t>(i) * p.o_ss + h * p.o_sh;
       const float pv = expf(dot_row(qr, kr, D, lane) * p.scale + add - ls);
-      const float ds = pv * (dot_row(dr, vr, D, lane) - delta[row]);
+      const float z = drop_factor(dp, static_cast<uint64_t>(row) * p.Sk + j);
+      const float ds = pv * (z * dot_row(dr, vr, D, lane) - delta[row]);
+      const float pz = pv * z;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         const int d = lane + 64 * c;
         if (d < D) {
-          dv[c] += pv * to_f32(dr[d]);
+          dv[c] += pz * to_f32(dr[d]);
           dk[c] += ds * to_f32(qr[d]);
         }
       }
@@ -1429,7 +1442,7 @@ int attn_fwd_impl(bool from_lse, const void* q, const void* const* k_blocks,
                     static_cast<unsigned>(batch));
     hipLaunchKernelGGL((nmb::attn_fwd_generic_kernel<float, 0>), grid, dim3(64), 0, stream,
                        static_cast<const float*>(q), kv, static_cast<float*>(o), lse, p,
-                       static_cast<int>(head_dim), nmb::MaskRef{});
+                       static_cast<int>(head_dim), nmb::MaskRef{}, nmb::DropoutParams{0, 0, 1.f});
   }
   NMB_CHECK_LAUNCH("attn_fwd");
   return NMB_OK;
@@ -1578,14 +1591,15 @@ int attn_bwd_impl(const void* q, const void* const* k_blocks,
       const dim3 grid(static_cast<unsigned>(seq_q), static_cast<unsigned>(q_heads),
                       static_cast<unsigned>(batch));
       hipLaunchKernelGGL((nmb::attn_bwd_dq_generic_kernel<float, 0>), grid, dim3(64), 0, stream, qp, kv,
-                         dp, lse, delta, static_cast<float*>(dq), p, D, nmb::MaskRef{});
+                         dp, lse, delta, static_cast<float*>(dq), p, D, nmb::MaskRef{},
+                         nmb::DropoutParams{0, 0, 1.f});
       NMB_CHECK_LAUNCH("attn_bwd(dq,f32)");
     }
     if (seq_k > 0) {
       const dim3 grid(static_cast<unsigned>(seq_k), static_cast<unsigned>(kv_heads),
                       static_cast<unsigned>(batch * n_blocks));
       hipLaunchKernelGGL((nmb::attn_bwd_dkdv_generic_kernel<float, 0>), grid, dim3(64), 0, stream, qp,
-                         kv, dp, lse, delta, p, D, nmb::MaskRef{});
+                         kv, dp, lse, delta, p, D, nmb::MaskRef{}, nmb::DropoutParams{0, 0, 1.f});
       NMB_CHECK_LAUNCH("attn_bwd(dkdv,f32)");
     }
   }
@@ -1613,47 +1627,56 @@ extern "C" int nmb_attn_bwd(const void* q, const void* const* k_blocks,
 namespace nmb {
 namespace {
 
-// Shape and mask of the masked entry points: one K/V block at key offset 0;
-// the generic kernels load elements one at a time, so any head_dim <= 128 and
-// any strides (of bf16 or fp32 data) are accepted.
-int masked_setup(AttnShape* p, KVBlocks* kv, MaskRef* mr, const void* q, const void* k, const void* v,
-                 int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k,
-                 int64_t head_dim, const int64_t* qs, const int64_t* kvs, const int64_t* os,
+// Shape, mask and dropout of the masked entry points: one K/V block at key
+// offset 0; the generic kernels load elements one at a time, so any head_dim
+// <= 128 and any strides (of bf16 or fp32 data) are accepted.  mask_kind 0
+// (no mask) serves attention with dropout alone.
+int masked_setup(AttnShape* p, KVBlocks* kv, MaskRef* mr, DropoutParams* dp, const void* q, const void* k,
+                 const void* v, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                 int64_t seq_k, int64_t head_dim, const int64_t* qs, const int64_t* kvs, const int64_t* os,
                  const void* mask, int mask_kind, const int64_t* ms, int causal, int64_t q_offset,
-                 float scale, int dtype) {
+                 float scale, float dropout_p, uint64_t seed, int dtype) {
   NMB_REQUIRE_SUPPORTED(dtype == NMB_BF16 || dtype == NMB_F32, "attention (masked): unsupported dtype code %d",
                         dtype);
-  NMB_REQUIRE(mask_kind == 1 || mask_kind == 2,
-              "attention (masked): mask_kind must be 1 (boolean) or 2 (additive), got %d", mask_kind);
-  NMB_REQUIRE(mask != nullptr && ms != nullptr, "attention (masked): null mask");
-  NMB_REQUIRE(ms[0] >= 0 && ms[1] >= 0 && ms[2] >= 0 && ms[3] >= 0,
-              "attention (masked): mask strides must be non-negative");
+  NMB_REQUIRE(mask_kind == 0 || mask_kind == 1 || mask_kind == 2,
+              "attention (masked): mask_kind must be 0 (none), 1 (boolean) or 2 (additive), got %d",
+              mask_kind);
+  NMB_REQUIRE(dropout_p >= 0.f && dropout_p < 1.f, "attention (masked): dropout_p must be in [0, 1), got %g",
+              static_cast<double>(dropout_p));
+  if (mask_kind != 0) {
+    NMB_REQUIRE(mask != nullptr && ms != nullptr, "attention (masked): null mask");
+    NMB_REQUIRE(ms[0] >= 0 && ms[1] >= 0 && ms[2] >= 0 && ms[3] >= 0,
+                "attention (masked): mask strides must be non-negative");
+  }
   const void* kb[1] = {k};
   const void* vb[1] = {v};
   const int64_t koff[1] = {0};
   const int st = fill_shape(p, kv, q, kb, vb, koff, 1, batch, q_heads, kv_heads, seq_q, seq_k, head_dim,
                             qs, kvs, os, causal, q_offset, scale, NMB_F32);
   if (st != NMB_OK) return st;
-  *mr = MaskRef{mask, ms[0], ms[1], ms[2], ms[3]};
+  *mr = mask_kind != 0 ? MaskRef{mask, ms[0], ms[1], ms[2], ms[3]} : MaskRef{};
+  *dp = make_dropout(static_cast<double>(dropout_p), seed);
   return NMB_OK;
 }
 
 template <typename T>
-void masked_fwd_launch(const AttnShape& p, const KVBlocks& kv, const MaskRef& mr, int kind, const void* q,
-                       void* o, float* lse, int D, hipStream_t stream) {
+void masked_fwd_launch(const AttnShape& p, const KVBlocks& kv, const MaskRef& mr, const DropoutParams& dp,
+                       int kind, const void* q, void* o, float* lse, int D, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(p.Sq), static_cast<unsigned>(p.Hq), static_cast<unsigned>(p.B));
-  if (kind == 1)
-    hipLaunchKernelGGL((attn_fwd_generic_kernel<T, 1>), grid, dim3(64), 0, stream, static_cast<const T*>(q),
-                       kv, static_cast<T*>(o), lse, p, D, mr);
+  const T* qp = static_cast<const T*>(q);
+  T* op = static_cast<T*>(o);
+  if (kind == 0)
+    hipLaunchKernelGGL((attn_fwd_generic_kernel<T, 0>), grid, dim3(64), 0, stream, qp, kv, op, lse, p, D, mr, dp);
+  else if (kind == 1)
+    hipLaunchKernelGGL((attn_fwd_generic_kernel<T, 1>), grid, dim3(64), 0, stream, qp, kv, op, lse, p, D, mr, dp);
   else
-    hipLaunchKernelGGL((attn_fwd_generic_kernel<T, 2>), grid, dim3(64), 0, stream, static_cast<const T*>(q),
-                       kv, static_cast<T*>(o), lse, p, D, mr);
+    hipLaunchKernelGGL((attn_fwd_generic_kernel<T, 2>), grid, dim3(64), 0, stream, qp, kv, op, lse, p, D, mr, dp);
 }
 
 template <typename T>
-void masked_bwd_launch(const AttnShape& p, const KVBlocks& kv, const MaskRef& mr, int kind, const void* q,
-                       const void* o, const void* dout, const float* lse, float* delta, void* dq, int D,
-                       hipStream_t stream) {
+void masked_bwd_launch(const AttnShape& p, const KVBlocks& kv, const MaskRef& mr, const DropoutParams& drop,
+                       int kind, const void* q, const void* o, const void* dout, const float* lse, float* delta,
+                       void* dq, int D, hipStream_t stream) {
   const T* qp = static_cast<const T*>(q);
   const T* dp = static_cast<const T*>(dout);
   const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
@@ -1663,21 +1686,28 @@ void masked_bwd_launch(const AttnShape& p, const KVBlocks& kv, const MaskRef& mr
     hipLaunchKernelGGL(attn_delta_kernel<T>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
                        static_cast<const T*>(o), dp, delta, p, D);
     const dim3 grid(static_cast<unsigned>(p.Sq), static_cast<unsigned>(p.Hq), static_cast<unsigned>(p.B));
-    if (kind == 1)
+    T* dqp = static_cast<T*>(dq);
+    if (kind == 0)
+      hipLaunchKernelGGL((attn_bwd_dq_generic_kernel<T, 0>), grid, dim3(64), 0, stream, qp, kv, dp, lse, delta,
+                         dqp, p, D, mr, drop);
+    else if (kind == 1)
       hipLaunchKernelGGL((attn_bwd_dq_generic_kernel<T, 1>), grid, dim3(64), 0, stream, qp, kv, dp, lse, delta,
-                         static_cast<T*>(dq), p, D, mr);
+                         dqp, p, D, mr, drop);
     else
       hipLaunchKernelGGL((attn_bwd_dq_generic_kernel<T, 2>), grid, dim3(64), 0, stream, qp, kv, dp, lse, delta,
-                         static_cast<T*>(dq), p, D, mr);
+                         dqp, p, D, mr, drop);
   }
   if (p.Sk > 0 && p.B > 0) {
     const dim3 grid(static_cast<unsigned>(p.Sk), static_cast<unsigned>(p.Hkv), static_cast<unsigned>(p.B));
-    if (kind == 1)
+    if (kind == 0)
+      hipLaunchKernelGGL((attn_bwd_dkdv_generic_kernel<T, 0>), grid, dim3(64), 0, stream, qp, kv, dp, lse,
+                         delta, p, D, mr, drop);
+    else if (kind == 1)
       hipLaunchKernelGGL((attn_bwd_dkdv_generic_kernel<T, 1>), grid, dim3(64), 0, stream, qp, kv, dp, lse,
-                         delta, p, D, mr);
+                         delta, p, D, mr, drop);
     else
       hipLaunchKernelGGL((attn_bwd_dkdv_generic_kernel<T, 2>), grid, dim3(64), 0, stream, qp, kv, dp, lse,
-                         delta, p, D, mr);
+                         delta, p, D, mr, drop);
   }
 }
 
@@ -1689,20 +1719,22 @@ extern "C" int nmb_attn_masked_fwd(const void* q, const void* k, const void* v, 
                                    int64_t seq_k, int64_t head_dim, const int64_t* q_strides,
                                    const int64_t* kv_strides, const int64_t* o_strides, const void* mask,
                                    int mask_kind, const int64_t* mask_strides, int causal,
-                                   int64_t q_offset, float scale, int dtype, hipStream_t stream) {
+                                   int64_t q_offset, float scale, float dropout_p, uint64_t seed, int dtype,
+                                   hipStream_t stream) {
   AttnShape p;
   KVBlocks kv;
   nmb::MaskRef mr;
-  const int st = nmb::masked_setup(&p, &kv, &mr, q, k, v, batch, q_heads, kv_heads, seq_q, seq_k, head_dim,
-                                   q_strides, kv_strides, o_strides, mask, mask_kind, mask_strides, causal,
-                                   q_offset, scale, dtype);
+  nmb::DropoutParams dp;
+  const int st = nmb::masked_setup(&p, &kv, &mr, &dp, q, k, v, batch, q_heads, kv_heads, seq_q, seq_k,
+                                   head_dim, q_strides, kv_strides, o_strides, mask, mask_kind, mask_strides,
+                                   causal, q_offset, scale, dropout_p, seed, dtype);
   if (st != NMB_OK) return st;
   NMB_REQUIRE(o != nullptr && lse != nullptr, "attn_masked_fwd: null output");
   if (batch == 0 || seq_q == 0) return NMB_OK;
   if (dtype == NMB_BF16)
-    nmb::masked_fwd_launch<nmb::bf16>(p, kv, mr, mask_kind, q, o, lse, static_cast<int>(head_dim), stream);
+    nmb::masked_fwd_launch<nmb::bf16>(p, kv, mr, dp, mask_kind, q, o, lse, static_cast<int>(head_dim), stream);
   else
-    nmb::masked_fwd_launch<float>(p, kv, mr, mask_kind, q, o, lse, static_cast<int>(head_dim), stream);
+    nmb::masked_fwd_launch<float>(p, kv, mr, dp, mask_kind, q, o, lse, static_cast<int>(head_dim), stream);
   NMB_CHECK_LAUNCH("attn_masked_fwd");
   return NMB_OK;
 }
@@ -1714,13 +1746,14 @@ extern "C" int nmb_attn_masked_bwd(const void* q, const void* k, const void* v, 
                                    int64_t head_dim, const int64_t* q_strides, const int64_t* kv_strides,
                                    const int64_t* o_strides, const void* mask, int mask_kind,
                                    const int64_t* mask_strides, int causal, int64_t q_offset, float scale,
-                                   int dtype, hipStream_t stream) {
+                                   float dropout_p, uint64_t seed, int dtype, hipStream_t stream) {
   AttnShape p;
   KVBlocks kv;
   nmb::MaskRef mr;
-  const int st = nmb::masked_setup(&p, &kv, &mr, q, k, v, batch, q_heads, kv_heads, seq_q, seq_k, head_dim,
-                                   q_strides, kv_strides, o_strides, mask, mask_kind, mask_strides, causal,
-                                   q_offset, scale, dtype);
+  nmb::DropoutParams dp;
+  const int st = nmb::masked_setup(&p, &kv, &mr, &dp, q, k, v, batch, q_heads, kv_heads, seq_q, seq_k,
+                                   head_dim, q_strides, kv_strides, o_strides, mask, mask_kind, mask_strides,
+                                   causal, q_offset, scale, dropout_p, seed, dtype);
   if (st != NMB_OK) return st;
   NMB_REQUIRE(o != nullptr && dout != nullptr && lse != nullptr && dq != nullptr && dk != nullptr &&
                   dv != nullptr,
@@ -1734,10 +1767,10 @@ extern "C" int nmb_attn_masked_bwd(const void* q, const void* k, const void* v, 
   if (batch == 0) return NMB_OK;
   float* delta = static_cast<float*>(workspace);
   if (dtype == NMB_BF16)
-    nmb::masked_bwd_launch<nmb::bf16>(p, kv, mr, mask_kind, q, o, dout, lse, delta, dq,
+    nmb::masked_bwd_launch<nmb::bf16>(p, kv, mr, dp, mask_kind, q, o, dout, lse, delta, dq,
                                       static_cast<int>(head_dim), stream);
   else
-    nmb::masked_bwd_launch<float>(p, kv, mr, mask_kind, q, o, dout, lse, delta, dq,
+    nmb::masked_bwd_launch<float>(p, kv, mr, dp, mask_kind, q, o, dout, lse, delta, dq,
                                   static_cast<int>(head_dim), stream);
   NMB_CHECK_LAUNCH("attn_masked_bwd");
   return NMB_OK;

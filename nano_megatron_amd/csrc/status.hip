@@ -21,4 +21,4 @@ void clear_error() { g_last_error[0] = '\0'; }
 
 extern "C" const char* nmb_last_error(void) { return nmb::g_last_error; }
 
-extern "C" int nmb_abi_version(void) { return 1; }
+extern "C" int nmb_abi_version(void) { return 2; }

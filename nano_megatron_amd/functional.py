@@ -822,33 +822,38 @@ def _mask_args(mask: Tensor, q: Tensor, shape: tuple[int, int, int, int]) -> tup
 
 
 class MaskedAttentionFunction(torch.autograd.Function):
-    """``local_attention`` with ``attention_mask`` (nn/kernels/torch_backend.py:
-    60-76): the mask ANDed with the causal mask (boolean masks) or added to the
-    scores (masks of the query dtype), one K/V block; ``nmb_attn_masked_*``.
-    The mask itself gets no gradient."""
+    """``local_attention`` with ``attention_mask`` and/or ``dropout_p``
+    (nn/kernels/torch_backend.py:60-76): the mask ANDed with the causal mask
+    (boolean masks) or added to the scores (masks of the query dtype), one K/V
+    block; dropout of the normalised probabilities with the counter-based mask
+    of ``seed``; ``nmb_attn_masked_*``.  The mask itself gets no gradient."""
 
     @staticmethod
-    def forward(ctx: Any, q: Tensor, k: Tensor, v: Tensor, mask: Tensor, causal: bool, q_offset: int,
-                scale: float | None) -> Tensor:
+    def forward(ctx: Any, q: Tensor, k: Tensor, v: Tensor, mask: Tensor | None, causal: bool,
+                q_offset: int, scale: float | None, dropout_p: float, seed: int) -> Tensor:
         b, hq, hkv, sq, sk, d = _check_attn(q, [k], [v])
         q, k, v = (_canonical_bhsd(t) for t in (q, k, v))
-        mask, kind, mstrides = _mask_args(mask, q, (b, hq, sq, sk))
+        if mask is None:
+            kind, mstrides = 0, (0, 0, 0, 0)
+        else:
+            mask, kind, mstrides = _mask_args(mask, q, (b, hq, sq, sk))
+        mask_ptr = mask.data_ptr() if mask is not None else None
         o = _new_bhsd(q.shape, q)
         lse = torch.empty(b, hq, sq, dtype=torch.float32, device=q.device)
         qs, ks, os_ = (_eff_strides(_bshd_view(t)) for t in (q, k, o))
         _lib.call(
             "nmb_attn_masked_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
-            b, hq, hkv, sq, sk, d, _lib.i64x3(qs), _lib.i64x3(ks), _lib.i64x3(os_), mask.data_ptr(), kind,
+            b, hq, hkv, sq, sk, d, _lib.i64x3(qs), _lib.i64x3(ks), _lib.i64x3(os_), mask_ptr, kind,
             _lib.i64_array(mstrides), 1 if causal else 0, int(q_offset), float(scale) if scale else 0.0,
-            _lib.dtype_code(q.dtype), _lib.stream_of(q),
+            float(dropout_p), int(seed), _lib.dtype_code(q.dtype), _lib.stream_of(q),
         )
         ctx.save_for_backward(q, k, v, o, lse, mask)
-        ctx.meta = (causal, q_offset, scale, kind, mstrides)
+        ctx.meta = (causal, q_offset, scale, kind, mstrides, dropout_p, seed)
         return o
 
     @staticmethod
     def backward(ctx: Any, grad: Tensor):
-        causal, q_offset, scale, kind, mstrides = ctx.meta
+        causal, q_offset, scale, kind, mstrides, dropout_p, seed = ctx.meta
         q, k, v, o, lse, mask = ctx.saved_tensors
         b, hq, sq, d = q.shape
         hkv, sk = k.shape[1], k.shape[2]
@@ -864,20 +869,42 @@ class MaskedAttentionFunction(torch.autograd.Function):
             lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws.numel(),
             b, hq, hkv, sq, sk, d, _lib.i64x3(_eff_strides(_bshd_view(q))),
             _lib.i64x3(_eff_strides(_bshd_view(k))), _lib.i64x3(_eff_strides(_bshd_view(o))),
-            mask.data_ptr(), kind, _lib.i64_array(mstrides), 1 if causal else 0, int(q_offset),
-            float(scale) if scale else 0.0, _lib.dtype_code(q.dtype), _lib.stream_of(q),
+            mask.data_ptr() if mask is not None else None, kind, _lib.i64_array(mstrides),
+            1 if causal else 0, int(q_offset), float(scale) if scale else 0.0, float(dropout_p), int(seed),
+            _lib.dtype_code(q.dtype), _lib.stream_of(q),
         )
-        return dq, dk, dv, None, None, None, None
+        return dq, dk, dv, None, None, None, None, None, None
 
 
-def masked_attention(q: Tensor, k: Tensor, v: Tensor, attention_mask: Tensor, *, causal: bool = True,
-                     sequence_offset: int = 0, scale: float | None = None) -> Tensor:
-    """``local_attention`` with ``attention_mask`` for [B,H,S,D] tensors."""
+def _check_dropout_p(p: float) -> float:
+    p = float(p)
+    if not 0.0 <= p < 1.0:
+        raise ValueError(f"dropout probability must be in [0, 1), got {p}")
+    return p
+
+
+def dropout_seed() -> int:
+    """A 63-bit key for the counter-based dropout masks, drawn from torch's
+    default CPU generator, so that whatever replays that generator replays the
+    mask: the recompute of a torch activation checkpoint (preserve_rng_state)
+    and a forked, explicitly seeded stream (nn.activation_rng_context)."""
+    return int(torch.randint(0, 2**63 - 1, (1,), dtype=torch.int64).item())
+
+
+def masked_attention(q: Tensor, k: Tensor, v: Tensor, attention_mask: Tensor | None, *,
+                     causal: bool = True, sequence_offset: int = 0, scale: float | None = None,
+                     dropout_p: float = 0.0, seed: int | None = None) -> Tensor:
+    """``local_attention`` with ``attention_mask`` and/or ``dropout_p`` for
+    [B,H,S,D] tensors; ``seed`` keys the dropout mask (default: dropout_seed())."""
+    dropout_p = _check_dropout_p(dropout_p)
     _require_gpu(q, k, v, attention_mask)
-    if causal and attention_mask.dtype != torch.bool:
+    if causal and attention_mask is not None and attention_mask.dtype != torch.bool:
         # the reference combines the masks with `mask & causal_mask` (torch_backend.py:66)
         raise ValueError("a causal attention_mask must be boolean (it is ANDed with the causal mask)")
-    return MaskedAttentionFunction.apply(q, k, v, attention_mask, bool(causal), int(sequence_offset), scale)
+    if dropout_p and seed is None:
+        seed = dropout_seed()
+    return MaskedAttentionFunction.apply(q, k, v, attention_mask, bool(causal), int(sequence_offset), scale,
+                                         dropout_p, int(seed or 0))
 
 
 def ring_attention(
@@ -899,6 +926,49 @@ def ring_attention(
     return AttentionFunction.apply(
         q, causal, int(query_offset), scale, tuple(int(o) for o in key_offsets), *ks, *vs
     )
+
+
+# ---------------------------------------------------------------- dropout
+class DropoutAddFunction(torch.autograd.Function):
+    """``residual + F.dropout(x, p)`` (models/gpt/layer.py:114-137, nn/dropout.py:
+    47-70) as one ``nmb_dropout_add`` pass, residual optional; the backward is
+    the same kernel on the gradient with the same seed (the mask is a function
+    of (seed, element index), nothing is saved)."""
+
+    @staticmethod
+    def forward(ctx: Any, x: Tensor, residual: Tensor | None, p: float, seed: int) -> Tensor:
+        xc = x.contiguous()
+        rc = residual.contiguous() if residual is not None else None
+        out = torch.empty_like(xc)
+        _lib.call("nmb_dropout_add", xc.data_ptr(), rc.data_ptr() if rc is not None else None,
+                  out.data_ptr(), xc.numel(), p, seed, _lib.dtype_code(x.dtype), _lib.stream_of(x))
+        ctx.meta = (p, seed, residual is not None)
+        return out
+
+    @staticmethod
+    def backward(ctx: Any, grad: Tensor):
+        p, seed, has_residual = ctx.meta
+        g = grad.contiguous()
+        dx = torch.empty_like(g)
+        _lib.call("nmb_dropout_add", g.data_ptr(), None, dx.data_ptr(), g.numel(), p, seed,
+                  _lib.dtype_code(g.dtype), _lib.stream_of(g))
+        return dx, (grad if has_residual else None), None, None
+
+
+def dropout_add(x: Tensor, p: float, *, seed: int | None = None, residual: Tensor | None = None) -> Tensor:
+    """``residual + dropout(x, p)`` (just the dropout without ``residual``) in the
+    training mode of F.dropout: kept elements scaled by 1 / (1 - p); ``seed``
+    keys the mask (default: dropout_seed())."""
+    p = _check_dropout_p(p)
+    _require_gpu(x, residual)
+    if residual is not None and (residual.shape != x.shape or residual.dtype != x.dtype
+                                 or residual.device != x.device):
+        raise ValueError(
+            f"residual {tuple(residual.shape)} {residual.dtype} does not match x {tuple(x.shape)} {x.dtype}"
+        )
+    if seed is None:
+        seed = dropout_seed()
+    return DropoutAddFunction.apply(x, residual, p, int(seed))
 
 
 # ---------------------------------------------------------------- LM head + CE

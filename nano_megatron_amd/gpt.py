@@ -42,7 +42,7 @@ from nano_megatron_amd.block import (
     pack_adjacent,
 )
 from nano_megatron_amd.kernels import HipKernelBackend, KernelBackend
-from nano_megatron_amd.nn import RotaryEmbedding, activation_checkpoint
+from nano_megatron_amd.nn import RotaryEmbedding, activation_checkpoint, activation_rng_context, parallel_dropout
 
 _MISSING = object()
 
@@ -271,7 +271,6 @@ class GPTAttention(nn.Module):
 
     def forward(self, hidden_states: Tensor, *, position_ids: Tensor | None = None,
                 sequence_offset: int = 0, microbatch_index: int = 0) -> Tensor:
-        del microbatch_index
         batch, sequence, _ = hidden_states.shape
         q, _ = self.q_proj(hidden_states)
         k, _ = self.k_proj(hidden_states)
@@ -283,10 +282,14 @@ class GPTAttention(nn.Module):
                                               position_ids, sequence_offset)
         q = Fn.RotaryFunction.apply(Fn._canonical_bhsd(q), tab.cos, tab.sin, positions, offset)
         k = Fn.RotaryFunction.apply(Fn._canonical_bhsd(k), tab.cos, tab.sin, positions, offset)
-        context = self.kernels.local_attention(
-            q, k, v, causal=True, sequence_offset=sequence_offset,
-            dropout_p=self.dropout if self.training else 0.0,
-        )
+        with activation_rng_context(
+            self.rng if self.training and self.dropout > 0.0 else None, q, layer=self.layer_index,
+            microbatch=microbatch_index, global_token_offset=sequence_offset, op="attention.tp=0",
+        ):
+            context = self.kernels.local_attention(
+                q, k, v, causal=True, sequence_offset=sequence_offset,
+                dropout_p=self.dropout if self.training else 0.0,
+            )
         context = context.transpose(1, 2).contiguous().view(batch, sequence, self.local_hidden_size)
         output, _ = self.out_proj(context)
         return output
@@ -468,10 +471,20 @@ class GPTLayer(nn.Module):
                                      microbatch_index=microbatch_index),
             normalized,
         )
-        hidden_states = residual + attention_output
+        # residual + dropout (models/gpt/layer.py:114-137) in one pass; the
+        # activation offset is the sequence offset (no sequence parallelism)
+        hidden_states = parallel_dropout(
+            attention_output, self.dropout, training=self.training, rng=self.rng, layer=self.layer_index,
+            microbatch=microbatch_index, global_token_offset=sequence_offset, op="attention_residual",
+            residual=residual,
+        )
         residual = hidden_states
         normalized = self.post_attention_norm(hidden_states)
-        return residual + self._run("mlp", self.mlp, normalized)
+        return parallel_dropout(
+            self._run("mlp", self.mlp, normalized), self.dropout, training=self.training, rng=self.rng,
+            layer=self.layer_index, microbatch=microbatch_index, global_token_offset=sequence_offset,
+            op="mlp_residual", residual=residual,
+        )
 
 
 @dataclass
@@ -507,8 +520,6 @@ class GPTModel(nn.Module):
         self.original_vocab_size = int(config_value(config, "vocab_size"))
         self.padded_vocab_size = self.original_vocab_size
         self.dropout = float(config_value(config, "embedding_dropout", "dropout", default=0.0))
-        if self.dropout:
-            raise ValueError("nano_megatron_amd implements dropout = 0 only")
         self.ce_chunk = int(ce_chunk)
         self.layer_start = layer_start
         self.layer_end = self.num_layers if layer_end is None else layer_end
@@ -594,6 +605,13 @@ class GPTModel(nn.Module):
         if plan.positions is None:
             position_ids = None  # the offset form: the module path builds the same range
 
+        if self.embedding is not None:
+            # models/gpt/model.py:203-212 (no sequence parallelism: the offset is the position)
+            hidden_states = parallel_dropout(
+                hidden_states, self.dropout, training=self.training, rng=self.rng, layer=0,
+                microbatch=microbatch_index, global_token_offset=offset, op="embedding",
+            )
+
         self._pack_block_weights()
         mode = getattr(self.activation_checkpoint_config, "mode", "none")
         offload = bool(getattr(self.activation_checkpoint_config, "offload_saved_tensors", False))
@@ -610,6 +628,15 @@ class GPTModel(nn.Module):
                     hidden_states = CheckpointedBlockFunction.apply(hidden_states, meta, offload, *weights)
                 else:
                     hidden_states = EagerBlockFunction.apply(hidden_states, meta, *weights)
+            elif self._checkpoint_layer(layer):
+                # a layer the fused block does not cover (dropout, biases, other
+                # components): torch's checkpoint of the module path
+                # (models/gpt/model.py:217-235)
+                hidden_states = activation_checkpoint(
+                    lambda x, current=layer: current(x, position_ids=position_ids, sequence_offset=offset,
+                                                     microbatch_index=microbatch_index),
+                    hidden_states, rng=self.rng, offload_saved_tensors=offload,
+                )
             else:
                 hidden_states = layer(hidden_states, position_ids=position_ids,
                                       sequence_offset=offset, microbatch_index=microbatch_index)

@@ -70,11 +70,11 @@ class HipKernelBackend:
             raise ValueError(
                 f"query heads ({q.shape[1]}) must be divisible by KV heads ({k.shape[1]})"
             )
-        if dropout_p:
-            raise ValueError("the hip backend implements attention dropout_p = 0 only")
-        if attention_mask is not None:
+        if attention_mask is not None or dropout_p:
+            # the seed comes from torch's default CPU generator, the stream the
+            # caller's activation_rng_context forks (models/gpt/attention.py:190-206)
             return Fn.masked_attention(q, k, v, attention_mask, causal=causal,
-                                       sequence_offset=sequence_offset, scale=scale)
+                                       sequence_offset=sequence_offset, scale=scale, dropout_p=dropout_p)
         return Fn.attention(q, k, v, causal=causal, sequence_offset=sequence_offset, scale=scale)
 
 

@@ -1,14 +1,15 @@
-"""RMSNorm, RoPE and the activation-checkpoint helper, backed by libnmb.so.
+"""RMSNorm, RoPE, dropout and the activation-checkpoint helper, backed by libnmb.so.
 
-Mirrors nn/norms.py:13-44, nn/rotary.py:9-73 and
-nn/activation_checkpoint.py:73-131 of the reference: same constructor
+Mirrors nn/norms.py:13-44, nn/rotary.py:9-73, nn/dropout.py:14-70 and
+nn/activation_checkpoint.py:44-131 of the reference: same constructor
 arguments, validation messages and outputs.
 """
 
 from __future__ import annotations
 
-from collections.abc import Callable
-from contextlib import nullcontext
+import copy
+from collections.abc import Callable, Iterator
+from contextlib import contextmanager, nullcontext
 from typing import Any, TypeVar
 
 import torch
@@ -135,6 +136,30 @@ def _offload_context(*, pin_memory: bool, non_blocking: bool):
     return torch.autograd.graph.saved_tensors_hooks(pack, unpack)
 
 
+def _rng_replaying(function: Callable[..., T], rng: Any | None) -> Callable[..., T]:
+    """nn/activation_checkpoint.py:44-70: a stateful RNG tracker (anything with
+    state_dict / load_state_dict) starts the first forward and the recompute
+    from the same state, and is left where the first forward left it.  torch's
+    own CPU generator, which the dropout seeds come from, is replayed by
+    torch's checkpoint itself (preserve_rng_state)."""
+    if rng is None or not hasattr(rng, "state_dict") or not hasattr(rng, "load_state_dict"):
+        return function
+    start = copy.deepcopy(rng.state_dict())
+    after_first: list[Any] = []
+
+    def replaying(*args: Any, **kwargs: Any) -> T:
+        rng.load_state_dict(copy.deepcopy(start))
+        try:
+            return function(*args, **kwargs)
+        finally:
+            if after_first:
+                rng.load_state_dict(copy.deepcopy(after_first[0]))
+            else:
+                after_first.append(copy.deepcopy(rng.state_dict()))
+
+    return replaying
+
+
 def activation_checkpoint(
     function: Callable[..., T],
     *args: Any,
@@ -146,11 +171,12 @@ def activation_checkpoint(
 ) -> T:
     """Non-reentrant checkpoint of an arbitrary function (nn/activation_checkpoint.py:73-100).
 
-    Used for the selective mode; the full mode of GPTModel uses the fused
-    CheckpointedBlockFunction instead.  ``rng`` is accepted for signature
-    compatibility: the hot path has no random ops at dropout 0.
+    Used for the selective mode and for layers the fused block does not cover
+    (dropout, biases); the full mode of fusable layers uses the fused
+    CheckpointedBlockFunction instead.  ``rng``: a stateful tracker replayed
+    across the recompute.
     """
-    del rng
+    function = _rng_replaying(function, rng)
     context = (
         _offload_context(pin_memory=pin_memory, non_blocking=non_blocking)
         if offload_saved_tensors
@@ -161,3 +187,55 @@ def activation_checkpoint(
             lambda *inputs: function(*inputs, **kwargs), *args, use_reentrant=False,
             preserve_rng_state=True,
         )
+
+
+class ActivationCheckpoint(nn.Module):
+    """nn/activation_checkpoint.py:103-131: a module whose forward runs the
+    wrapped module under activation_checkpoint with the stored options."""
+
+    def __init__(self, module: nn.Module, *, rng: Any | None = None, offload_saved_tensors: bool = False,
+                 pin_memory: bool = True, non_blocking: bool = True) -> None:
+        super().__init__()
+        self.module = module
+        self.rng = rng
+        self.offload_saved_tensors = offload_saved_tensors
+        self.pin_memory = pin_memory
+        self.non_blocking = non_blocking
+
+    def forward(self, *args: Any, **kwargs: Any) -> Any:
+        return activation_checkpoint(self.module, *args, rng=self.rng,
+                                     offload_saved_tensors=self.offload_saved_tensors,
+                                     pin_memory=self.pin_memory, non_blocking=self.non_blocking, **kwargs)
+
+
+@contextmanager
+def activation_rng_context(rng: Any | None, tensor: Tensor, *, layer: int, microbatch: int,
+                           global_token_offset: int, op: str) -> Iterator[None]:
+    """nn/dropout.py:14-44: run one logical random operation inside the stream
+    ``rng.fork`` derives from (layer, microbatch, global_token_offset, op), so
+    its dropout mask does not depend on what ran before it.  The kernels draw
+    their mask keys from torch's default CPU generator (functional.dropout_seed),
+    the generator the fork reseeds; no CUDA generator is involved, so none is
+    forked.  Without an rng (or one without ``fork``) the default generator's
+    running stream is used, as the reference's F.dropout then does."""
+    del tensor
+    if rng is None or not hasattr(rng, "fork"):
+        yield
+        return
+    with rng.fork("activation", components=(layer, microbatch, global_token_offset, op), cuda_devices=(),
+                  advance=False):
+        yield
+
+
+def parallel_dropout(tensor: Tensor, p: float, *, training: bool, rng: Any | None, layer: int,
+                     microbatch: int, global_token_offset: int, op: str,
+                     residual: Tensor | None = None) -> Tensor:
+    """nn/dropout.py:47-70 (``F.dropout`` in training mode under the forked
+    stream), plus the residual add that follows it in GPTLayer.forward
+    (models/gpt/layer.py:114-137) fused into the same pass when ``residual``
+    is given.  Identity (or the plain add) when not training or at p = 0."""
+    if not training or p == 0.0:
+        return tensor if residual is None else residual + tensor
+    with activation_rng_context(rng, tensor, layer=layer, microbatch=microbatch,
+                                global_token_offset=global_token_offset, op=op):
+        return Fn.dropout_add(tensor, p, residual=residual)

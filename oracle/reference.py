@@ -11,7 +11,10 @@ Tensor parallel, sequence parallel and context parallel all run at size 1 here,
 where every collective on the path is an identity
 (tensor_parallel/sequence_parallel.py:37-39, 46-48, 55-57).  Dropout is the
 identity at p = 0 (nn/dropout.py:60-61), which is the only value the configs
-use.
+use; for p > 0 the reference draws its masks from torch's Philox stream,
+which no other generator reproduces, so the functions below take the keep
+mask of the library's SplitMix64 stream (``dropout_keep``) and apply it with
+the reference's arithmetic.
 """
 
 from __future__ import annotations
@@ -20,6 +23,7 @@ import math
 from dataclasses import dataclass
 from typing import Any, Sequence
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
@@ -146,6 +150,8 @@ def local_attention(
     sequence_offset: int = 0,
     scale: float | None = None,
     attention_mask: Tensor | None = None,
+    dropout_p: float = 0.0,
+    dropout_seed: int = 0,
 ) -> Tensor:
     """``TorchKernelBackend.local_attention`` (nn/kernels/torch_backend.py:25-76).
 
@@ -153,7 +159,10 @@ def local_attention(
     when there is no mask and the offset is 0, else by an explicit
     ``key_pos <= offset + query_pos`` mask, ANDed with ``attention_mask`` when
     one is given (:60-66); then SDPA with that mask (:68-76): a boolean mask
-    keeps the True entries, a floating mask is added to the scores.
+    keeps the True entries, a floating mask is added to the scores.  With
+    ``dropout_p`` > 0 (:73), torch's math SDPA applies the keep mask
+    ``dropout_keep(dropout_seed, [B, Hq, Sq, Sk], dropout_p)`` to the
+    normalised probabilities and scales by 1 / (1 - p).
     """
     if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
         raise ValueError("q, k and v must have [batch, heads, sequence, head_dim] shape")
@@ -176,7 +185,72 @@ def local_attention(
         key_positions = torch.arange(k.shape[-2])
         causal_mask = key_positions.unsqueeze(0) <= query_positions.unsqueeze(1)
         mask = causal_mask if mask is None else (mask & causal_mask)
+    if dropout_p:
+        keep = dropout_keep(dropout_seed, (q.shape[0], q.shape[1], q.shape[2], k.shape[2]), dropout_p)
+        if mask is not None and mask.dtype == torch.bool:
+            # the math kernel takes additive masks: SDPA's own conversion (False -> -inf)
+            mask = torch.zeros(mask.shape, dtype=q.dtype).masked_fill(~mask, float("-inf"))
+        out, _ = torch.ops.aten._scaled_dot_product_attention_math(
+            q, k, v, mask, float(np.float32(dropout_p)), is_causal, keep, scale=scale)
+        return out
     return F.scaled_dot_product_attention(q, k, v, attn_mask=mask, is_causal=is_causal, scale=scale)
+
+
+# ---------------------------------------------------------------- dropout masks
+_SM_GAMMA = np.uint64(0x9E3779B97F4A7C15)
+_SM_MUL1 = np.uint64(0xBF58476D1CE4E5B9)
+_SM_MUL2 = np.uint64(0x94D049BB133111EB)
+
+
+def splitmix64(seed: int, counters: np.ndarray) -> np.ndarray:
+    """Output ``counter + 1`` of SplitMix64 seeded with ``seed`` (Steele, Lea
+    and Flood, OOPSLA 2014; the mixing of Vigna's splitmix64.c), for each
+    counter: z = seed + (counter + 1) * 0x9E3779B97F4A7C15, two
+    xor-shift-multiply rounds (30, 27) and a final xor-shift (31), mod 2^64."""
+    with np.errstate(over="ignore"):
+        z = np.uint64(seed) + (np.asarray(counters, dtype=np.uint64) + np.uint64(1)) * _SM_GAMMA
+        z = (z ^ (z >> np.uint64(30))) * _SM_MUL1
+        z = (z ^ (z >> np.uint64(27))) * _SM_MUL2
+        return z ^ (z >> np.uint64(31))
+
+
+def dropout_bits(seed: int, n: int) -> np.ndarray:
+    """The 32-bit draw of elements 0..n-1: the low (even index) or high (odd
+    index) half of splitmix64(seed, index >> 1)."""
+    idx = np.arange(n, dtype=np.uint64)
+    z = splitmix64(seed, idx >> np.uint64(1))
+    return np.where((idx & np.uint64(1)) == 1, z >> np.uint64(32), z & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+
+
+def dropout_keep(seed: int, shape: Sequence[int], p: float) -> Tensor:
+    """Boolean keep mask over ``shape`` (row-major element index): kept iff
+    the draw is >= floor(p * 2^32), p taken in float32 as the kernels take it."""
+    threshold = int(float(np.float32(p)) * 4294967296.0)
+    n = int(np.prod(shape)) if len(shape) else 1
+    return torch.from_numpy(dropout_bits(seed, n) >= threshold).reshape(tuple(shape))
+
+
+def dropout_scale(p: float) -> float:
+    """1 / (1 - p) rounded to float32, the kept elements' factor."""
+    return float(np.float32(1.0 / (1.0 - float(np.float32(p)))))
+
+
+def dropout_add(x: Tensor, p: float, seed: int, residual: Tensor | None = None) -> Tensor:
+    """``residual + F.dropout(x, p)`` with the keep mask of ``seed``
+    (nn/dropout.py:47-70; models/gpt/layer.py:114-137)."""
+    return dropout_apply(x, dropout_keep(seed, x.shape, p), p, residual)
+
+
+def dropout_apply(x: Tensor, keep: Tensor, p: float, residual: Tensor | None = None) -> Tensor:
+    """F.dropout's arithmetic on the GPU for a given keep mask: x * (1 / (1 - p))
+    in float32, rounded to x's dtype (0 where dropped); then ``residual +`` that,
+    rounded once more."""
+    keep = keep.to(x.device)
+    scaled = x.float() * torch.tensor(dropout_scale(p), dtype=torch.float32, device=x.device)
+    y = torch.where(keep, scaled, torch.zeros((), dtype=torch.float32, device=x.device)).to(x.dtype)
+    if residual is None:
+        return y
+    return (residual.float() + y.float()).to(x.dtype)
 
 
 def _ring_block_mask(sq: int, sk: int, query_offset: int, key_offset: int) -> Tensor:
@@ -371,15 +445,19 @@ class OracleAttention(nn.Module):
         self.v_proj = _ProjectedLinear(self.hidden_size, kv_hidden, dtype)
         self.out_proj = _ProjectedLinear(self.hidden_size, self.hidden_size, dtype)
         self.rope = OracleRotaryEmbedding(self.head_dim, float(_cfg(config, "rope_theta", default=1e4)))
+        self.dropout = float(_cfg(config, "attention_dropout", "dropout", default=0.0))
 
-    def forward(self, x: Tensor, *, position_ids: Tensor, sequence_offset: int = 0) -> Tensor:
+    def forward(self, x: Tensor, *, position_ids: Tensor, sequence_offset: int = 0,
+                dropout_seed: int = 0) -> Tensor:
         b, s, _ = x.shape
         q = self.q_proj(x).view(b, s, self.num_heads, self.head_dim).transpose(1, 2)
         k = self.k_proj(x).view(b, s, self.num_kv_heads, self.head_dim).transpose(1, 2)
         v = self.v_proj(x).view(b, s, self.num_kv_heads, self.head_dim).transpose(1, 2)
         cos, sin = self.rope(position_ids, dtype=q.dtype)
         q, k = apply_rotary_pos_emb(q, k, cos, sin)
-        ctx = local_attention(q, k, v, causal=True, sequence_offset=sequence_offset)
+        # attention.py:190-206: dropout_p only in training
+        ctx = local_attention(q, k, v, causal=True, sequence_offset=sequence_offset,
+                              dropout_p=self.dropout if self.training else 0.0, dropout_seed=dropout_seed)
         ctx = ctx.transpose(1, 2).contiguous().view(b, s, self.hidden_size)
         return self.out_proj(ctx)
 
@@ -400,7 +478,10 @@ class OracleMLP(nn.Module):
 
 
 class OracleLayer(nn.Module):
-    """GPTLayer (models/gpt/layer.py:22-137): pre-norm attention + SwiGLU with residuals."""
+    """GPTLayer (models/gpt/layer.py:22-137): pre-norm attention + SwiGLU with
+    residuals, each residual branch through dropout in training (:114-137).
+    ``dropout_seed(layer, op)`` gives the mask key of each random op ("attention.tp=0",
+    "attention_residual", "mlp_residual")."""
 
     def __init__(self, config: Any, layer_index: int, dtype: torch.dtype | None = None) -> None:
         super().__init__()
@@ -411,12 +492,22 @@ class OracleLayer(nn.Module):
         self.attention = OracleAttention(config, dtype)
         self.post_attention_norm = OracleRMSNorm(h, eps, dtype)
         self.mlp = OracleMLP(config, dtype)
+        self.dropout = float(_cfg(config, "hidden_dropout", "dropout", default=0.0))
         self.forward_calls = 0
 
-    def forward(self, x: Tensor, *, position_ids: Tensor, sequence_offset: int = 0) -> Tensor:
+    def _residual(self, residual: Tensor, branch: Tensor, seed: int) -> Tensor:
+        if not self.training or self.dropout == 0.0:
+            return residual + branch
+        return dropout_add(branch, self.dropout, seed, residual=residual)
+
+    def forward(self, x: Tensor, *, position_ids: Tensor, sequence_offset: int = 0,
+                dropout_seed: Any = None) -> Tensor:
         self.forward_calls += 1
-        h = x + self.attention(self.input_norm(x), position_ids=position_ids, sequence_offset=sequence_offset)
-        return h + self.mlp(self.post_attention_norm(h))
+        seed = dropout_seed if dropout_seed is not None else (lambda layer, op: 0)
+        a = self.attention(self.input_norm(x), position_ids=position_ids, sequence_offset=sequence_offset,
+                           dropout_seed=seed(self.layer_index, "attention.tp=0"))
+        h = self._residual(x, a, seed(self.layer_index, "attention_residual"))
+        return self._residual(h, self.mlp(self.post_attention_norm(h)), seed(self.layer_index, "mlp_residual"))
 
 
 @dataclass
@@ -486,10 +577,15 @@ class OracleGPTModel(nn.Module):
         *,
         activation_checkpoint_config: Any | None = None,
         dtype: torch.dtype | None = None,
+        dropout_seed: Any = None,
     ) -> None:
         super().__init__()
         self.config = config
         self.activation_checkpoint_config = activation_checkpoint_config
+        # dropout (models/gpt/model.py:72, 203-212; layer.py:114-137; attention.py:190-206):
+        # dropout_seed(layer, op) keys each random op's mask
+        self.dropout = float(_cfg(config, "embedding_dropout", "dropout", default=0.0))
+        self.dropout_seed = dropout_seed if dropout_seed is not None else (lambda layer, op: 0)
         h = int(_cfg(config, "hidden_size"))
         layers = int(_cfg(config, "layers", "num_layers"))
         vocab = int(_cfg(config, "vocab_size"))
@@ -521,16 +617,20 @@ class OracleGPTModel(nn.Module):
             position_ids = torch.arange(0, seq)
         else:
             offset = int(position_ids.reshape(-1)[0].item())
+        if self.training and self.dropout:
+            hidden = dropout_add(hidden, self.dropout, self.dropout_seed(0, "embedding"))
         for layer in self.layers:
             if self._checkpoint_layer(layer):
                 hidden = torch_checkpoint(
-                    lambda x, cur=layer: cur(x, position_ids=position_ids, sequence_offset=offset),
+                    lambda x, cur=layer: cur(x, position_ids=position_ids, sequence_offset=offset,
+                                             dropout_seed=self.dropout_seed),
                     hidden,
                     use_reentrant=False,
                     preserve_rng_state=True,
                 )
             else:
-                hidden = layer(hidden, position_ids=position_ids, sequence_offset=offset)
+                hidden = layer(hidden, position_ids=position_ids, sequence_offset=offset,
+                               dropout_seed=self.dropout_seed)
         hidden = self.final_norm(hidden)
         logits = self.lm_head(hidden)
         loss = None

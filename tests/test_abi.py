@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol() -> None:
     for name in declared_functions():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.nmb_abi_version() == 1
+    assert lib.nmb_abi_version() == 2
 
 
 FAKE = 256  # a non-null, 16-byte aligned address that is never dereferenced
@@ -187,3 +187,30 @@ def test_python_wrapper_maps_status_to_exceptions() -> None:
         _lib.call("nmb_rmsnorm_fwd", FAKE, FAKE, FAKE, None, 4, 12, 1e-5, _lib.NMB_BF16, None)
     with pytest.raises(ValueError):
         _lib.dtype_code(torch.float16)
+
+
+def test_dropout_add_rejects_bad_arguments() -> None:
+    lib = _lib.load()
+    st = lib.nmb_dropout_add(FAKE, None, FAKE, 64, 1.0, 1, _lib.NMB_BF16, None)
+    assert st == _lib.NMB_EINVAL and b"[0, 1)" in lib.nmb_last_error()
+    st = lib.nmb_dropout_add(FAKE, None, FAKE, 64, -0.5, 1, _lib.NMB_BF16, None)
+    assert st == _lib.NMB_EINVAL and b"[0, 1)" in lib.nmb_last_error()
+    st = lib.nmb_dropout_add(None, None, FAKE, 64, 0.1, 1, _lib.NMB_BF16, None)
+    assert st == _lib.NMB_EINVAL and b"null" in lib.nmb_last_error()
+    st = lib.nmb_dropout_add(FAKE, None, FAKE, -1, 0.1, 1, _lib.NMB_BF16, None)
+    assert st == _lib.NMB_EINVAL and b"negative" in lib.nmb_last_error()
+    st = lib.nmb_dropout_add(FAKE, None, FAKE, 64, 0.1, 1, 7, None)
+    assert st == _lib.NMB_EUNSUPPORTED and b"dtype" in lib.nmb_last_error()
+    # nothing to do: no launch, OK
+    assert lib.nmb_dropout_add(FAKE, None, FAKE, 0, 0.1, 1, _lib.NMB_BF16, None) == _lib.NMB_OK
+
+
+def test_masked_attention_rejects_bad_dropout_and_mask_kind() -> None:
+    lib = _lib.load()
+    args = (FAKE, FAKE, FAKE, FAKE, FAKE, 1, 2, 2, 4, 4, 64, None, None, None)
+    st = lib.nmb_attn_masked_fwd(*args, None, 0, None, 1, 0, 0.0, 1.0, 5, _lib.NMB_BF16, None)
+    assert st == _lib.NMB_EINVAL and b"dropout_p" in lib.nmb_last_error()
+    st = lib.nmb_attn_masked_fwd(*args, None, 3, None, 1, 0, 0.0, 0.1, 5, _lib.NMB_BF16, None)
+    assert st == _lib.NMB_EINVAL and b"mask_kind" in lib.nmb_last_error()
+    st = lib.nmb_attn_masked_fwd(*args, None, 1, None, 1, 0, 0.0, 0.1, 5, _lib.NMB_BF16, None)
+    assert st == _lib.NMB_EINVAL and b"null mask" in lib.nmb_last_error()

@@ -48,7 +48,10 @@ def test_local_attention_validates_like_the_reference() -> None:
         backend.local_attention(q, torch.randn(1, 4, 4, 8), torch.randn(1, 4, 4, 8))
     with pytest.raises(ValueError, match="identical shapes"):
         backend.local_attention(q, torch.randn(1, 2, 4, 8), torch.randn(1, 2, 5, 8))
-    with pytest.raises(ValueError, match="dropout"):
+    for p in (-0.1, 1.0):
+        with pytest.raises(ValueError, match="dropout probability"):
+            backend.local_attention(q, torch.randn(1, 2, 4, 8), torch.randn(1, 2, 4, 8), dropout_p=p)
+    with pytest.raises(ValueError, match="no CPU fallback"):
         backend.local_attention(q, torch.randn(1, 2, 4, 8), torch.randn(1, 2, 4, 8), dropout_p=0.1)
 
 

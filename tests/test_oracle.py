@@ -398,3 +398,95 @@ def test_checkpointed_model_grads_equal_eager_and_weights_are_tied() -> None:
     # full recompute runs each layer forward twice
     assert all(layer.forward_calls == 2 for layer in full.layers)
     assert all(layer.forward_calls == 1 for layer in eager.layers)
+
+
+# ---------------------------------------------------------------- dropout
+def test_splitmix64_known_answers() -> None:
+    """Published SplitMix64 outputs (Vigna's splitmix64.c): the first outputs of
+    the generator seeded with 0 and with 1234567."""
+    import numpy as np
+
+    assert [int(z) for z in R.splitmix64(0, np.arange(4))] == [
+        0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F, 0xF88BB8A8724C81EC]
+    assert [int(z) for z in R.splitmix64(1234567, np.arange(3))] == [
+        6457827717110365317, 3203168211198807973, 9817491932198370423]
+
+
+def test_dropout_bits_take_the_halves_of_one_draw_per_pair() -> None:
+    bits = R.dropout_bits(0, 5)
+    assert [int(b) for b in bits[:4]] == [0x7B1DCDAF, 0xE220A839, 0xA1B965F4, 0x6E789E6A]
+    assert int(bits[4]) == 0x8009454F
+
+
+@pytest.mark.parametrize("p", [0.1, 0.5, 0.9])
+def test_dropout_keep_rate_and_independence(p) -> None:
+    """Keep probability 1 - p within 5 sigma over 2^20 draws; neighbouring
+    elements (which share one SplitMix64 output) are uncorrelated; different
+    seeds give different masks."""
+    n = 1 << 20
+    keep = R.dropout_keep(123, (n,), p).float()
+    sigma = math.sqrt(p * (1 - p) / n)
+    assert abs(float(keep.mean()) - (1 - p)) < 5 * sigma
+    a, b = keep[0::2] - keep.mean(), keep[1::2] - keep.mean()
+    corr = float((a * b).mean() / (a.square().mean().sqrt() * b.square().mean().sqrt()))
+    assert abs(corr) < 5 / math.sqrt(n / 2)
+    other = R.dropout_keep(124, (n,), p).float()
+    assert float((keep != other).float().mean()) > p * (1 - p)
+    assert bool(R.dropout_keep(123, (64,), 0.0).all())
+
+
+def test_dropout_arithmetic_matches_torch_fp32() -> None:
+    """F.dropout's arithmetic: torch's own dropout (native_dropout returns its
+    mask) equals dropout_apply with that mask, bit for bit, in fp32."""
+    torch.manual_seed(3)
+    x = torch.randn(4096)
+    for p in (0.1, 0.3, 0.37):
+        out, mask = torch.ops.aten.native_dropout(x, p, True)
+        assert torch.equal(R.dropout_apply(x, mask, p), out)
+    r = torch.randn(4096)
+    out, mask = torch.ops.aten.native_dropout(x, 0.2, True)
+    assert torch.equal(R.dropout_apply(x, mask, 0.2, residual=r), r + out)
+
+
+def test_dropout_add_is_unbiased_and_its_own_backward() -> None:
+    """E[dropout(x)] = x over seeds (a wrong scale or an inverted mask moves the
+    mean by a factor); the backward of residual + dropout(x) through autograd
+    of the mask arithmetic is dropout(grad) with the same mask."""
+    x = torch.linspace(-2, 2, 64, dtype=torch.float64)
+    mean = torch.stack([R.dropout_add(x, 0.25, s) for s in range(4000)]).mean(0)
+    torch.testing.assert_close(mean, x, rtol=0.0, atol=0.06)
+    xg = x.clone().requires_grad_(True)
+    keep = R.dropout_keep(9, x.shape, 0.25)
+    (R.dropout_apply(xg, keep, 0.25) * torch.arange(64.0, dtype=torch.float64)).sum().backward()
+    expected = R.dropout_apply(torch.arange(64.0, dtype=torch.float64), keep, 0.25)
+    torch.testing.assert_close(xg.grad, expected, rtol=1e-12, atol=0.0)
+
+
+def test_attention_dropout_reduces_to_sdpa_and_is_unbiased() -> None:
+    """With a keep-everything mask the dropout path equals the plain SDPA path;
+    averaged over seeds it converges to the no-dropout output (unbiased)."""
+    torch.manual_seed(4)
+    q, k, v = (torch.randn(1, 2, 6, 8, dtype=torch.float64) for _ in range(3))
+    plain = R.local_attention(q, k, v, causal=True)
+    tiny = R.local_attention(q, k, v, causal=True, dropout_p=1e-12, dropout_seed=5)
+    torch.testing.assert_close(tiny, plain, rtol=1e-9, atol=1e-9)
+    # a boolean mask (with a fully masked row) and an offset: still the SDPA path's output
+    mask = torch.rand(1, 1, 6, 6, generator=torch.Generator().manual_seed(1)) > 0.4
+    mask[0, 0, 2] = False
+    for causal, offset in ((True, 3), (False, 0)):
+        plain_m = R.local_attention(q, k, v, causal=causal, sequence_offset=offset, attention_mask=mask)
+        tiny_m = R.local_attention(q, k, v, causal=causal, sequence_offset=offset, attention_mask=mask,
+                                   dropout_p=1e-12, dropout_seed=5)
+        torch.testing.assert_close(tiny_m, plain_m, rtol=1e-9, atol=1e-9)
+        assert torch.count_nonzero(tiny_m[0, :, 2]) == 0
+    mean = torch.stack([R.local_attention(q, k, v, causal=True, dropout_p=0.3, dropout_seed=s)
+                        for s in range(3000)]).mean(0)
+    torch.testing.assert_close(mean, plain, rtol=0.0, atol=0.08)
+    # the mask is indexed over [B, Hq, Sq, Sk]: a dropped (b, h, i, j) removes
+    # exactly that key's term from that query's output
+    keep = R.dropout_keep(11, (1, 2, 6, 6), 0.3)
+    probs = torch.softmax((q @ k.transpose(-1, -2)) / math.sqrt(8) + torch.full((6, 6), float("-inf"))
+                          .triu(1).to(torch.float64), dim=-1)
+    expected = (probs * keep / (1 - float(torch.tensor(0.3, dtype=torch.float32)))) @ v
+    got = R.local_attention(q, k, v, causal=True, dropout_p=0.3, dropout_seed=11)
+    torch.testing.assert_close(got, expected, rtol=1e-6, atol=1e-6)
