@@ -370,7 +370,9 @@ int nmb_gemm_bf16_swiglu_bwd(int b_layout, int64_t m, int64_t f, int64_t k, cons
  * derived scalars (1 - beta, 1 - lr wd, sqrt(bias correction 2), lr / bias
  * correction 1) are formed in double and rounded to fp32 once, as torch rounds
  * a Python scalar meeting an fp32 tensor; the update then runs the
- * reference's tensor operations in their order, each rounded once. */
+ * reference's tensor operations in their order, each rounded once.  Valid
+ * hyper-parameters: lr >= 0 (a schedule may end at 0), eps > 0, betas in
+ * [0, 1), step >= 1. */
 int nmb_adamw_workspace_bytes(int64_t total_elements, size_t* bytes);
 
 int nmb_adamw_step(const uint64_t* params, const uint64_t* grads, const int64_t* offsets,

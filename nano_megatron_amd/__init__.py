@@ -6,7 +6,13 @@ The package mirrors the reference's hot-path API (``nano_megatron.nn``,
 on one GPU and has no CPU fallback.
 """
 
-from nano_megatron_amd.config import ActivationCheckpointConfig, GPTConfig, KernelConfig
+from nano_megatron_amd.config import (
+    ActivationCheckpointConfig,
+    GPTConfig,
+    KernelConfig,
+    LearningRateSchedulerConfig,
+    OptimizerConfig,
+)
 from nano_megatron_amd.functional import (
     attention,
     lm_head_cross_entropy,
@@ -23,6 +29,7 @@ from nano_megatron_amd.gpt import (
     GPTOutput,
 )
 from nano_megatron_amd.kernels import HipKernelBackend, KernelBackend, build_kernel_backend
+from nano_megatron_amd.train import LearningRateScheduler, StepOutput, split_microbatches, train_step
 from nano_megatron_amd.nn import (
     ActivationCheckpoint,
     RMSNorm,
@@ -45,12 +52,18 @@ __all__ = [
     "HipKernelBackend",
     "KernelBackend",
     "KernelConfig",
+    "LearningRateSchedulerConfig",
+    "OptimizerConfig",
     "RMSNorm",
     "RotaryEmbedding",
     "activation_checkpoint",
     "activation_rng_context",
     "parallel_dropout",
     "ActivationCheckpoint",
+    "StepOutput",
+    "LearningRateScheduler",
+    "split_microbatches",
+    "train_step",
     "apply_rotary_pos_emb",
     "attention",
     "build_kernel_backend",

@@ -266,7 +266,9 @@ namespace {
 
 int check_hyper(double lr, double beta1, double beta2, double eps, int64_t step) {
   NMB_REQUIRE(step >= 1, "adamw_step: step must be >= 1, got %lld", (long long)step);
-  NMB_REQUIRE(lr > 0.0 && eps > 0.0 && beta1 >= 0.0 && beta1 < 1.0 && beta2 >= 0.0 && beta2 < 1.0,
+  // lr 0 is a valid rate (a cosine schedule ends at min_lr, which may be 0):
+  // the moments still advance and the weights stay
+  NMB_REQUIRE(lr >= 0.0 && eps > 0.0 && beta1 >= 0.0 && beta1 < 1.0 && beta2 >= 0.0 && beta2 < 1.0,
               "adamw_step: invalid hyper-parameters");
   return NMB_OK;
 }

@@ -52,6 +52,19 @@ class MasterAdamW:
         self._param_ptrs = [p.data_ptr() for p in self.params]
         self._graph: dict | None = None  # buffers of a captured step (prepare_graph)
 
+    @classmethod
+    def from_config(cls, params: Iterable[nn.Parameter], config) -> "MasterAdamW":
+        """From an OptimizerConfig (config/schema.py:438-463)."""
+        return cls(params, lr=config.lr, betas=tuple(config.betas), eps=config.eps,
+                   weight_decay=config.weight_decay, clip_grad_norm=config.clip_grad_norm)
+
+    def set_learning_rate(self, lr: float) -> None:
+        """The rate of the next update (what LearningRateScheduler installs,
+        training/lr_scheduler.py:119-122)."""
+        if isinstance(lr, bool) or not lr >= 0.0:
+            raise ValueError(f"learning rate must be >= 0, got {lr!r}")
+        self.lr = float(lr)
+
     @property
     def last_grad_norm(self) -> Tensor:
         return self.stats[0]

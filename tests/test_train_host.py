@@ -1,0 +1,211 @@
+"""The training step's host logic on the CPU: micro-batch splitting as the
+reference's (training/microbatches.py:56-86), the schedules' backward order
+and loss scaling (pipeline_parallel/schedules/gpipe.py, one_f_one_b.py,
+base.py:111-126), and the token-weighted loss metric (training/metrics.py:
+68-121), checked on a small CPU model against closed forms."""
+
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import pytest
+import torch
+from torch import nn
+
+import nano_megatron_amd as nm
+
+
+def test_split_microbatches_slices_every_batched_tensor() -> None:
+    ids = torch.arange(24).reshape(6, 4)
+    batch = {"input_ids": ids, "labels": ids + 1, "scale": torch.tensor(2.0), "name": "x"}
+    parts = nm.split_microbatches(batch, 2)
+    assert len(parts) == 3
+    for i, part in enumerate(parts):
+        assert torch.equal(part["input_ids"], ids[2 * i:2 * i + 2])
+        assert torch.equal(part["labels"], ids[2 * i:2 * i + 2] + 1)
+        assert part["scale"] is batch["scale"] and part["name"] == "x"
+        assert part["input_ids"].data_ptr() == ids[2 * i].data_ptr()  # views, no copies
+
+
+@pytest.mark.parametrize("batch,mbs,match", [
+    ({"input_ids": torch.zeros(4, 2)}, 0, "micro_batch_size must be positive"),
+    ({"input_ids": torch.zeros(4, 2)}, 3, "divisible by micro_batch_size"),
+    ({"input_ids": torch.zeros(4, 2), "labels": torch.zeros(5, 2)}, 2, "same leading dimension"),
+    ({"input_ids": torch.tensor(1.0)}, 1, "no tensor with a leading batch dimension"),
+])
+def test_split_microbatches_rejects_what_the_reference_rejects(batch, mbs, match) -> None:
+    with pytest.raises(ValueError, match=match):
+        nm.split_microbatches(batch, mbs)
+
+
+class TinyLM(nn.Module):
+    """Embedding + linear head with a mean token cross-entropy (ignore -100), in
+    fp64 so that the order of the gradient additions stays below the
+    tolerances: enough to exercise the step's host logic on the CPU."""
+
+    def __init__(self) -> None:
+        super().__init__()
+        torch.manual_seed(0)
+        self.emb = nn.Embedding(11, 8, dtype=torch.float64)
+        self.head = nn.Linear(8, 11, dtype=torch.float64)
+        self.calls: list[int] = []
+
+    def forward(self, input_ids, *, labels=None, position_ids=None, microbatch_index=0):
+        self.calls.append(microbatch_index)
+        logits = self.head(self.emb(input_ids))
+        loss = nn.functional.cross_entropy(logits.reshape(-1, 11), labels.reshape(-1), ignore_index=-100)
+        return SimpleNamespace(loss=loss)
+
+
+def _batch():
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, 11, (6, 5), generator=g)
+    labels = torch.randint(0, 11, (6, 5), generator=g)
+    labels[0, :4] = -100  # uneven token counts per micro-batch
+    labels[3, :2] = -100
+    return {"input_ids": ids, "labels": labels}
+
+
+@pytest.mark.parametrize("schedule", ["gpipe", "1f1b"])
+def test_train_step_accumulates_the_mean_of_microbatch_losses(schedule) -> None:
+    """Gradient = d/dw of the mean over micro-batches of each micro-batch's
+    mean loss (the schedules divide each by their number); the reported loss
+    is the token-weighted mean; micro-batches are numbered from step x
+    accumulation steps; the step applies clip and the optimizer."""
+    batch = _batch()
+    model = TinyLM()
+    ref = TinyLM()
+    opt = torch.optim.SGD(model.parameters(), lr=0.1)
+    out = nm.train_step(model, opt, batch, micro_batch_size=2, gradient_accumulation_steps=3,
+                        schedule=schedule, clip_grad_norm=None, step_index=4)
+    assert model.calls == [12, 13, 14]
+    parts = nm.split_microbatches(batch, 2)
+    losses = [ref(p["input_ids"], labels=p["labels"]).loss for p in parts]
+    (sum(losses) / 3).backward()
+    with torch.no_grad():
+        for p in ref.parameters():
+            p -= 0.1 * p.grad
+    for a, b in zip(model.parameters(), ref.parameters()):
+        torch.testing.assert_close(a, b, rtol=1e-12, atol=1e-12)
+    tokens = [(p["labels"] != -100).sum().item() for p in parts]
+    weighted = sum(float(l.detach()) * t for l, t in zip(losses, tokens)) / sum(tokens)
+    assert out.metrics["token_count"] == sum(tokens)
+    assert out.metrics["loss"] == pytest.approx(weighted, rel=1e-12)
+    assert out.metrics["learning_rate"] == pytest.approx(0.1)
+    assert float(out.loss) == pytest.approx(float(sum(losses).detach() / 3), rel=1e-12)
+
+
+def test_train_step_backward_order_per_schedule() -> None:
+    """GPipe runs every forward, then the backwards newest first; 1F1B at one
+    stage alternates forward and backward."""
+    order: list[str] = []
+
+    class Probe(TinyLM):
+        def forward(self, input_ids, *, labels=None, position_ids=None, microbatch_index=0):
+            out = super().forward(input_ids, labels=labels, microbatch_index=microbatch_index)
+            order.append(f"F{microbatch_index}")
+            out.loss.register_hook(lambda g, i=microbatch_index: order.append(f"B{i}"))
+            return out
+
+    for schedule, expected in (("gpipe", ["F0", "F1", "F2", "B2", "B1", "B0"]),
+                               ("1f1b", ["F0", "B0", "F1", "B1", "F2", "B2"])):
+        order.clear()
+        model = Probe()
+        nm.train_step(model, torch.optim.SGD(model.parameters(), lr=0.0), _batch(), micro_batch_size=2,
+                      schedule=schedule, clip_grad_norm=None)
+        assert order == expected, schedule
+
+
+def test_train_step_clips_and_follows_the_lr_scheduler() -> None:
+    class Sched:
+        def __init__(self) -> None:
+            self.learning_rate = 0.05
+            self.completed = None
+
+        def set_completed_steps(self, n: int) -> None:
+            self.completed = n
+
+    model, ref = TinyLM(), TinyLM()
+    sched = Sched()
+    opt = torch.optim.SGD(model.parameters(), lr=123.0)
+    out = nm.train_step(model, opt, _batch(), micro_batch_size=3, schedule="gpipe", clip_grad_norm=0.01,
+                        lr_scheduler=sched, step_index=7)
+    assert sched.completed == 8 and out.metrics["learning_rate"] == 0.05
+    parts = nm.split_microbatches(_batch(), 3)
+    (sum(ref(p["input_ids"], labels=p["labels"]).loss for p in parts) / 2).backward()
+    norm = torch.nn.utils.clip_grad_norm_(ref.parameters(), 0.01)
+    assert out.metrics["grad_norm"] == pytest.approx(float(norm), rel=1e-12)
+    with torch.no_grad():
+        for p in ref.parameters():
+            p -= 0.05 * p.grad
+    for a, b in zip(model.parameters(), ref.parameters()):
+        torch.testing.assert_close(a, b, rtol=1e-12, atol=1e-12)
+
+
+def test_train_step_rejects_bad_arguments() -> None:
+    model = TinyLM()
+    opt = torch.optim.SGD(model.parameters(), lr=0.1)
+    with pytest.raises(ValueError, match="exactly gradient_accumulation_steps"):
+        nm.train_step(model, opt, _batch(), micro_batch_size=2, gradient_accumulation_steps=2)
+    with pytest.raises(ValueError, match="unknown schedule"):
+        nm.train_step(model, opt, _batch(), micro_batch_size=2, schedule="interleaved")
+    with pytest.raises(ValueError, match="labels"):
+        nm.train_step(model, opt, {"input_ids": torch.zeros(2, 3, dtype=torch.long)}, micro_batch_size=1)
+
+
+class _Sink:
+    def __init__(self) -> None:
+        self.rates: list[float] = []
+
+    def set_learning_rate(self, lr: float) -> None:
+        self.rates.append(lr)
+
+
+def test_lr_scheduler_warmup_cosine_and_resume() -> None:
+    """training/lr_scheduler.py: warm-up base * (k + 1) / W, cosine from base
+    to min over [W, decay] (half-way = the mean, the end and after = min); the
+    rate for the next update is installed at every change; a state dict
+    restores it and refuses a changed configuration."""
+    cfg = nm.LearningRateSchedulerConfig(schedule="cosine", warmup_steps=4, decay_steps=20, min_lr=1e-5)
+    sink = _Sink()
+    s = nm.LearningRateScheduler(config=cfg, optimizer_config=nm.OptimizerConfig(lr=1e-3), data_parallel=sink,
+                                 max_steps=1000)
+    assert [s.rate_at(k) for k in range(4)] == pytest.approx([2.5e-4, 5e-4, 7.5e-4, 1e-3])
+    assert s.rate_at(4) == pytest.approx(1e-3)
+    assert s.rate_at(12) == pytest.approx((1e-3 + 1e-5) / 2)
+    assert s.rate_at(20) == pytest.approx(1e-5) and s.rate_at(500) == pytest.approx(1e-5)
+    assert sink.rates == [pytest.approx(2.5e-4)]
+    s.step()
+    s.step()
+    assert sink.rates[-1] == pytest.approx(7.5e-4) and s.completed_steps == 2
+    state = s.state_dict()
+    other = nm.LearningRateScheduler(config=cfg, optimizer_config=nm.OptimizerConfig(lr=1e-3),
+                                     data_parallel=_Sink(), max_steps=1000)
+    other.load_state_dict(state, expected_completed_steps=2)
+    assert other.learning_rate == s.learning_rate
+    changed = nm.LearningRateScheduler(config=cfg, optimizer_config=nm.OptimizerConfig(lr=2e-3),
+                                       data_parallel=_Sink(), max_steps=1000)
+    with pytest.raises(RuntimeError, match="changed across resume for base_lr"):
+        changed.load_state_dict(state)
+    const = nm.LearningRateScheduler(config=nm.LearningRateSchedulerConfig(schedule="constant"),
+                                     optimizer_config=nm.OptimizerConfig(lr=3e-4), data_parallel=_Sink(),
+                                     max_steps=10)
+    assert const.rate_at(0) == const.rate_at(9) == pytest.approx(3e-4)
+
+
+def test_optimizer_and_scheduler_configs_validate_like_the_reference() -> None:
+    with pytest.raises(ValueError, match="optimizer.lr must be > 0"):
+        nm.OptimizerConfig(lr=0.0)
+    with pytest.raises(ValueError, match="betas"):
+        nm.OptimizerConfig(betas=(0.9, 1.0))
+    with pytest.raises(ValueError, match="'adamw'"):
+        nm.OptimizerConfig(name="sgd")
+    with pytest.raises(ValueError, match="lr_scheduler.schedule must be one of"):
+        nm.LearningRateSchedulerConfig(schedule="linear")
+    with pytest.raises(ValueError, match="min_lr must be between"):
+        nm.LearningRateScheduler(config=nm.LearningRateSchedulerConfig(min_lr=1.0),
+                                 optimizer_config=nm.OptimizerConfig(lr=1e-3), data_parallel=_Sink(),
+                                 max_steps=10)
+    with pytest.raises(ValueError, match="warmup_steps cannot exceed decay_steps"):
+        nm.LearningRateScheduler(config=nm.LearningRateSchedulerConfig(warmup_steps=5, decay_steps=3),
+                                 optimizer_config=nm.OptimizerConfig(), data_parallel=_Sink(), max_steps=10)
