@@ -69,6 +69,39 @@ class MasterAdamW:
     def last_grad_norm(self) -> Tensor:
         return self.stats[0]
 
+    def state_dict(self) -> dict:
+        """The resumable state, as the ZeRO strategy keeps it at one rank
+        (data_parallel/_zero.py:234-251: the fp32 master and both moments,
+        the step count and the rate), as host tensors over the flat layout."""
+        return {
+            "mode": "master_adamw",
+            "step": self.step_count,
+            "learning_rate": self.lr,
+            "numels": [p.numel() for p in self.params],
+            "master_parameter": self.master.detach().cpu(),
+            "exp_avg": self.exp_avg.detach().cpu(),
+            "exp_avg_sq": self.exp_avg_sq.detach().cpu(),
+        }
+
+    @torch.no_grad()
+    def load_state_dict(self, state: dict) -> None:
+        """data_parallel/_zero.py:253-301: the layout must match the current
+        parameters; the master, both moments, the step and the rate are
+        restored (the parameters themselves come from the model's state dict)."""
+        if state.get("mode", "master_adamw") != "master_adamw":
+            raise ValueError(f"cannot load {state.get('mode')!r} state into MasterAdamW")
+        numels = [p.numel() for p in self.params]
+        if list(state.get("numels", numels)) != numels:
+            raise ValueError(f"parameter layout changed: saved={state.get('numels')}, current={numels}")
+        for key, target in (("master_parameter", self.master), ("exp_avg", self.exp_avg),
+                            ("exp_avg_sq", self.exp_avg_sq)):
+            full = state.get(key)
+            if not isinstance(full, Tensor) or full.numel() != self.total:
+                raise ValueError(f"{key} has an incompatible logical shape")
+            target.copy_(full.reshape(-1).to(device=self.device, dtype=torch.float32))
+        self.step_count = int(state.get("step", 0))
+        self.set_learning_rate(float(state.get("learning_rate", self.lr)))
+
     def zero_grad(self, set_to_none: bool = True) -> None:
         for p in self.params:
             if set_to_none:

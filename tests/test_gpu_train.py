@@ -186,3 +186,33 @@ def test_cosine_schedule_to_zero_drives_master_adamw(device) -> None:
     assert rates == pytest.approx([1e-3, 1e-3, 0.0])
     assert sched.completed_steps == 3 and opt.lr == 0.0
     assert not torch.equal(*masters[0]) and torch.equal(*masters[2])
+
+
+def test_master_adamw_resumes_from_its_state_dict(device) -> None:
+    """Two steps, save (model and optimizer), a third step; a fresh model and
+    optimizer loaded from the saved state take the same third step, bit for
+    bit (data_parallel/_zero.py:234-301)."""
+    cfg = config(layers=1)
+    b = {k: v.to(device) for k, v in batch(n=2).items()}
+
+    def fresh():
+        torch.manual_seed(0)
+        m = nm.GPTModel(cfg).to(device=device, dtype=torch.bfloat16)
+        return m, MasterAdamW(m.parameters(), lr=1e-3)
+
+    model, opt = fresh()
+    for step in range(2):
+        nm.train_step(model, opt, b, micro_batch_size=2, step_index=step)
+    saved_model = {k: v.clone() for k, v in model.state_dict().items()}
+    saved_opt = opt.state_dict()
+    third = nm.train_step(model, opt, b, micro_batch_size=2, step_index=2)
+    model2, opt2 = fresh()
+    model2.load_state_dict(saved_model)
+    opt2.load_state_dict(saved_opt)
+    again = nm.train_step(model2, opt2, b, micro_batch_size=2, step_index=2)
+    assert torch.equal(third.loss, again.loss)
+    assert torch.equal(opt.master, opt2.master) and torch.equal(opt.exp_avg_sq, opt2.exp_avg_sq)
+    assert opt2.step_count == 3
+    bad = dict(saved_opt, numels=saved_opt["numels"][:-1])
+    with pytest.raises(ValueError, match="layout changed"):
+        opt2.load_state_dict(bad)
