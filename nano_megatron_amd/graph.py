@@ -49,7 +49,8 @@ class CapturedTrainStep:
                              "replay cannot reuse: capture without it")
         if getattr(model, "lm_head", None) is None:
             raise ValueError("CapturedTrainStep needs the stage that owns the LM head (the loss)")
-        if any(float(getattr(m, "dropout", 0.0) or 0.0) > 0.0 for m in model.modules()):
+        rates = (getattr(m, "dropout", 0.0) for m in model.modules())
+        if any(isinstance(r, (int, float)) and not isinstance(r, bool) and r > 0.0 for r in rates):
             raise ValueError("dropout masks are keyed by seeds passed from the host at launch, which "
                              "every replay of a captured graph would repeat: capture with dropout 0")
         self.model, self.optimizer = model, optimizer
