@@ -18,8 +18,9 @@ What changes per replay and what does not:
   update, as in the eager forward, tensor_parallel/cross_entropy.py:109-114):
   made before each replay, since a host wait cannot be captured.
 The activation checkpoint options must not move tensors to the host
-(``offload_saved_tensors``), and explicit ``position_ids`` (read on the host) are
-not accepted; both raise ``ValueError``.  No reference to an earlier step's
+(``offload_saved_tensors``), explicit ``position_ids`` (read on the host) are
+not accepted, and neither is dropout > 0 (its masks are keyed by seeds passed
+at launch, which every replay would repeat); all raise ``ValueError``.  No reference to an earlier step's
 autograd graph (an undetached loss) may be alive when the step is captured:
 its gradient-accumulation nodes belong to the stream of that earlier step,
 and the backward under capture would synchronise with it, which invalidates
