@@ -420,14 +420,21 @@ def cross_entropy_tokens(
 
 # ---------------------------------------------------------------- modules
 class _ProjectedLinear(nn.Module):
-    """Column/RowParallelLinear at TP=1: ``self.linear = nn.Linear`` (tensor_parallel/layers.py:56-62)."""
+    """Column/RowParallelLinear at TP=1: ``self.linear = nn.Linear``
+    (tensor_parallel/layers.py:56-62).  With a bias, the column form keeps it in
+    the ``nn.Linear`` (its default init); the row form keeps a zero-initialised
+    ``self.bias`` beside a bias-free ``nn.Linear`` and adds it after the product
+    (layers.py:110-126, 153-155)."""
 
-    def __init__(self, in_features: int, out_features: int, dtype: torch.dtype | None) -> None:
+    def __init__(self, in_features: int, out_features: int, dtype: torch.dtype | None, *,
+                 bias: bool = False, row: bool = False) -> None:
         super().__init__()
-        self.linear = nn.Linear(in_features, out_features, bias=False, dtype=dtype)
+        self.linear = nn.Linear(in_features, out_features, bias=bias and not row, dtype=dtype)
+        self.bias = nn.Parameter(torch.zeros(out_features, dtype=dtype)) if bias and row else None
 
     def forward(self, x: Tensor) -> Tensor:
-        return self.linear(x)
+        y = self.linear(x)
+        return y + self.bias if self.bias is not None else y
 
 
 class OracleAttention(nn.Module):
@@ -440,10 +447,11 @@ class OracleAttention(nn.Module):
         self.num_kv_heads = int(_cfg(config, "num_kv_heads", "kv_heads", default=self.num_heads))
         self.head_dim = self.hidden_size // self.num_heads
         kv_hidden = self.num_kv_heads * self.head_dim
-        self.q_proj = _ProjectedLinear(self.hidden_size, self.hidden_size, dtype)
-        self.k_proj = _ProjectedLinear(self.hidden_size, kv_hidden, dtype)
-        self.v_proj = _ProjectedLinear(self.hidden_size, kv_hidden, dtype)
-        self.out_proj = _ProjectedLinear(self.hidden_size, self.hidden_size, dtype)
+        bias = bool(_cfg(config, "linear_bias", "bias", default=False))  # attention.py:78-117
+        self.q_proj = _ProjectedLinear(self.hidden_size, self.hidden_size, dtype, bias=bias)
+        self.k_proj = _ProjectedLinear(self.hidden_size, kv_hidden, dtype, bias=bias)
+        self.v_proj = _ProjectedLinear(self.hidden_size, kv_hidden, dtype, bias=bias)
+        self.out_proj = _ProjectedLinear(self.hidden_size, self.hidden_size, dtype, bias=bias, row=True)
         self.rope = OracleRotaryEmbedding(self.head_dim, float(_cfg(config, "rope_theta", default=1e4)))
         self.dropout = float(_cfg(config, "attention_dropout", "dropout", default=0.0))
 
@@ -469,9 +477,10 @@ class OracleMLP(nn.Module):
         super().__init__()
         h = int(_cfg(config, "hidden_size"))
         f = int(_cfg(config, "ffn_hidden_size"))
-        self.gate_proj = _ProjectedLinear(h, f, dtype)
-        self.up_proj = _ProjectedLinear(h, f, dtype)
-        self.down_proj = _ProjectedLinear(f, h, dtype)
+        bias = bool(_cfg(config, "linear_bias", "bias", default=False))  # mlp.py:40-70
+        self.gate_proj = _ProjectedLinear(h, f, dtype, bias=bias)
+        self.up_proj = _ProjectedLinear(h, f, dtype, bias=bias)
+        self.down_proj = _ProjectedLinear(f, h, dtype, bias=bias, row=True)
 
     def forward(self, x: Tensor) -> Tensor:
         return self.down_proj(swiglu(self.gate_proj(x), self.up_proj(x)))
@@ -546,7 +555,8 @@ class _Embedding(nn.Module):
 
 
 class _LMHead(nn.Module):
-    """VocabParallelLinear with a tied weight (tensor_parallel/layers.py:158-214)."""
+    """VocabParallelLinear (tensor_parallel/layers.py:158-214): the embedding's
+    weight when tied, else its own N(0, init_std) weight."""
 
     def __init__(self, weight: nn.Parameter) -> None:
         super().__init__()
@@ -594,7 +604,12 @@ class OracleGPTModel(nn.Module):
         self.embedding = _Embedding(vocab, h, init_std, dtype)
         self.layers = nn.ModuleList([OracleLayer(config, i, dtype) for i in range(layers)])
         self.final_norm = OracleRMSNorm(h, eps, dtype)
-        self.lm_head = _LMHead(self.embedding.weight)
+        if bool(_cfg(config, "tie_embeddings", default=True)):  # model.py:125-142
+            self.lm_head = _LMHead(self.embedding.weight)
+        else:
+            head = nn.Parameter(torch.empty(vocab, h, dtype=dtype))
+            nn.init.normal_(head, mean=0.0, std=init_std)
+            self.lm_head = _LMHead(head)
 
     def _checkpoint_layer(self, layer: OracleLayer) -> bool:
         cfg = self.activation_checkpoint_config

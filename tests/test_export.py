@@ -25,9 +25,12 @@ def reference_state_shapes(cfg: nm.GPTConfig) -> dict[str, tuple[int, ...]]:
     """Keys and shapes of the reference GPTModel's state_dict at TP=1, read off
     its modules: embedding / final_norm / tied lm_head (models/gpt/model.py:86-142),
     per layer input_norm, attention, post_attention_norm, mlp (layer.py:47-61), the
-    projections as ``<name>.linear.weight`` without bias (attention.py:82-117,
-    mlp.py:44-70, tensor_parallel/layers.py:56-70, 112-132), no persistent
-    buffers (the RoPE inv_freq is non-persistent, nn/rotary.py:53)."""
+    projections as ``<name>.linear.weight`` (attention.py:82-117, mlp.py:44-70,
+    tensor_parallel/layers.py:56-70, 112-132) with, under ``bias``, the column
+    projections' ``<name>.linear.bias`` and the row projections' ``<name>.bias``
+    (layers.py:110-126), no persistent buffers (the RoPE inv_freq is
+    non-persistent, nn/rotary.py:53); ``lm_head.weight`` is the embedding's
+    when tied, its own tensor otherwise (model.py:125-142)."""
     h, v, f = cfg.hidden_size, cfg.vocab_size, cfg.ffn_hidden_size
     hq = cfg.heads
     hkv = cfg.kv_heads or hq
@@ -44,6 +47,12 @@ def reference_state_shapes(cfg: nm.GPTConfig) -> dict[str, tuple[int, ...]]:
         shapes[p + "mlp.gate_proj.linear.weight"] = (f, h)
         shapes[p + "mlp.up_proj.linear.weight"] = (f, h)
         shapes[p + "mlp.down_proj.linear.weight"] = (h, f)
+        if cfg.bias:
+            for name, n in (("attention.q_proj", hq * d), ("attention.k_proj", hkv * d),
+                            ("attention.v_proj", hkv * d), ("mlp.gate_proj", f), ("mlp.up_proj", f)):
+                shapes[p + name + ".linear.bias"] = (n,)
+            shapes[p + "attention.out_proj.bias"] = (h,)
+            shapes[p + "mlp.down_proj.bias"] = (h,)
     shapes["final_norm.weight"] = (h,)
     shapes["lm_head.weight"] = (v, h)
     return shapes
@@ -52,6 +61,8 @@ def reference_state_shapes(cfg: nm.GPTConfig) -> dict[str, tuple[int, ...]]:
 CONFIGS = [
     dict(layers=2, hidden_size=128, ffn_hidden_size=352, heads=2, seq_length=32, vocab_size=256),
     dict(layers=3, hidden_size=256, ffn_hidden_size=688, heads=4, kv_heads=2, seq_length=32, vocab_size=512),
+    dict(layers=2, hidden_size=128, ffn_hidden_size=352, heads=2, seq_length=32, vocab_size=256, bias=True,
+         tie_embeddings=False),
 ]
 
 
@@ -64,7 +75,8 @@ def _validate_like_export(state: dict, cfg: nm.GPTConfig) -> None:
     floating = {t.dtype for t in state.values() if t.is_floating_point()}
     assert len(floating) == 1
     assert state["embedding.weight"].dtype == state["lm_head.weight"].dtype
-    assert torch.equal(state["embedding.weight"], state["lm_head.weight"])
+    if cfg.tie_embeddings:
+        assert torch.equal(state["embedding.weight"], state["lm_head.weight"])
 
 
 @pytest.mark.parametrize("kw", CONFIGS)
@@ -92,7 +104,7 @@ def test_export_round_trip_keeps_weights_and_tied_head(kw) -> None:
     _validate_like_export(loaded, cfg)
     fresh = nm.GPTModel(cfg).to(torch.bfloat16)
     fresh.load_state_dict(loaded, strict=True)
-    assert fresh.lm_head.weight is fresh.embedding.weight
+    assert (fresh.lm_head.weight is fresh.embedding.weight) == cfg.tie_embeddings
     for k, t in fresh.state_dict().items():
         assert torch.equal(t, state[k]), k
 

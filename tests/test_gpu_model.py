@@ -325,3 +325,26 @@ def test_c3_model_step_full_and_none_bit_identical(device) -> None:
     assert len(g0) == len(g1) == 24 * 9 + 2
     for a, b in zip(g0, g1):
         assert bool(torch.isfinite(a).all()) and torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype,bias,tie,mode", [
+    (torch.float32, True, True, "full"), (torch.float32, False, False, "full"),
+    (torch.bfloat16, True, False, "none"), (torch.bfloat16, False, False, "full"),
+])
+def test_bias_and_untied_head_match_oracle(device, dtype, bias, tie, mode) -> None:
+    """GPTConfig.bias (column biases in the nn.Linear, row biases added after
+    the product; tensor_parallel/layers.py:27-155) and tie_embeddings=False
+    (the LM head's own N(0, 0.02) weight; models/gpt/model.py:125-142): loss and
+    every gradient against the oracle (fp32 rtol 1e-5; bf16 2e-2 / 1e-2).
+    Layers with biases run the module path; an untied head keeps the fused one."""
+    cfg = c1_config(layers=2, bias=bias, tie_embeddings=tie)
+    ours, ref = build_pair(cfg, mode, dtype, device)
+    assert (ours.lm_head.weight is ours.embedding.weight) == tie
+    ids, labels = c1_batch()
+    lo = ours(ids.to(device), labels=labels.to(device)).loss
+    lr = ref(ids, labels=labels).loss
+    lo.backward()
+    lr.backward()
+    tol = dict(rtol=1e-5, atol=1e-5) if dtype == torch.float32 else dict(rtol=2e-2, atol=1e-2)
+    torch.testing.assert_close(lo.detach().float().cpu(), lr.detach().float(), rtol=tol["rtol"], atol=tol["atol"])
+    assert_grads(ours, ref, **tol)
