@@ -243,6 +243,12 @@ def kernel_rooflines(device, only: str | None = None) -> list[dict]:
         out = torch.empty_like(q)
         return lambda: Fn.rope_apply(q, out, tab.cos, tab.sin)
 
+    def mk_dropout_add():
+        x, r = randn(T, H), randn(T, H)
+        out = torch.empty_like(x)
+        return lambda: Fn._lib.call("nmb_dropout_add", x.data_ptr(), r.data_ptr(), out.data_ptr(), T * H, 0.1,
+                                    1234, Fn._lib.NMB_BF16, Fn._lib.stream_of(x))
+
     def mk_swiglu_fwd():
         gu, act = randn(T, 2 * F), torch.empty(T, F, dtype=bf, device=device)
         return lambda: Fn.swiglu_fwd(gu[:, :F], gu[:, F:], act)
@@ -352,6 +358,8 @@ def kernel_rooflines(device, only: str | None = None) -> list[dict]:
         ("rmsnorm_bwd", mk_rms_bwd, 4 * T * H * E + 2 * H * E, 2 * L + 1),
         # the standalone rotary kernel; the step fuses RoPE into the QKV GEMM and the attention backward
         ("rope_apply", mk_rope, 2 * T * H * E, 0),
+        # residual + dropout (p 0.1) on [T, H]; the configurations train at dropout 0
+        ("dropout_add", mk_dropout_add, 3 * T * H * E, 0),
         # the standalone activation; the checkpointed step fuses it into the gate/up GEMM
         ("swiglu_fwd", mk_swiglu_fwd, 3 * T * F * E, 0),
         # the standalone backward; the step runs it as the down projection's dX GEMM epilogue
