@@ -51,6 +51,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-kernels", action="store_true", help="skip the per-kernel roofline timing")
     p.add_argument("--no-eager", action="store_true", help="skip the no-checkpoint comparison run")
     p.add_argument("--no-legs", action="store_true", help="skip the config-4 and config-5 legs of the default line")
+    p.add_argument("--no-torch", action="store_true",
+                   help="skip the plain PyTorch-ROCm implementation of the same step (context)")
     p.add_argument("--host-launch", action="store_true",
                    help="time the steps with every kernel launched from the host (no HIP graph)")
     p.add_argument("--only-kernels", action="store_true", help="time the kernels only (for profiling)")
@@ -658,6 +660,98 @@ def c4_leg(args, device, eager: bool = True) -> dict:
     return leg
 
 
+def torch_eager_leg(device, steps: int = 10, warmup: int = 3) -> dict:
+    """The config-3 step written in plain PyTorch on the same GPU, for context:
+    the reference's modules as torch operations (F.rms_norm, RoPE by tensor
+    ops, SDPA causal attention, nn.Linear on hipBLASLt, SwiGLU, the full-logit
+    cross-entropy, torch's non-reentrant checkpoint per layer), bf16 parameters
+    with an fp32 master copy stepped by torch's fused AdamW after a global
+    clip (the ZeRO path's arithmetic at one rank), launched from the host.
+    Same shapes, same work per step; random weights of the same sizes."""
+    import torch
+    import torch.nn.functional as F
+    from torch import nn
+    from torch.utils.checkpoint import checkpoint
+
+    L, H, nh, ff, V = C3["layers"], C3["hidden_size"], C3["heads"], C3["ffn_hidden_size"], C3["vocab_size"]
+    B, S, d = BATCH, SEQ, C3["hidden_size"] // C3["heads"]
+
+    class Layer(nn.Module):
+        def __init__(self) -> None:
+            super().__init__()
+            self.n1, self.n2 = nn.Parameter(torch.ones(H)), nn.Parameter(torch.ones(H))
+            self.q, self.k, self.v, self.o = (nn.Linear(H, H, bias=False) for _ in range(4))
+            self.g, self.u = nn.Linear(H, ff, bias=False), nn.Linear(H, ff, bias=False)
+            self.d = nn.Linear(ff, H, bias=False)
+
+        def forward(self, x, cos, sin):
+            def rope(t):
+                a, b = t.chunk(2, -1)
+                return t * cos + torch.cat([-b, a], -1) * sin
+
+            h = F.rms_norm(x, (H,), self.n1, 1e-5)
+            q, k, v = (m(h).view(B, S, nh, d).transpose(1, 2) for m in (self.q, self.k, self.v))
+            a = F.scaled_dot_product_attention(rope(q), rope(k), v, is_causal=True)
+            x = x + self.o(a.transpose(1, 2).reshape(B, S, H))
+            h = F.rms_norm(x, (H,), self.n2, 1e-5)
+            return x + self.d(F.silu(self.g(h)) * self.u(h))
+
+    def run(mode: str) -> float:
+        torch.manual_seed(0)
+        emb = nn.Parameter(torch.randn(V, H) * 0.02)
+        layers = nn.ModuleList(Layer() for _ in range(L))
+        nf = nn.Parameter(torch.ones(H))
+        params = [emb, nf, *layers.parameters()]
+        with torch.no_grad():
+            for p_ in params:
+                p_.data = p_.data.to(device=device, dtype=torch.bfloat16)
+        master = [p_.detach().float().clone().requires_grad_(True) for p_ in params]
+        opt = torch.optim.AdamW(master, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, fused=True)
+        inv = 1.0 / (1e4 ** (torch.arange(0, d, 2, device=device, dtype=torch.float32) / d))
+        fr = torch.outer(torch.arange(S, device=device, dtype=torch.float32), inv)
+        cos, sin = (t.to(torch.bfloat16) for t in (torch.cat([fr, fr], -1).cos(), torch.cat([fr, fr], -1).sin()))
+        gen = torch.Generator(device=device).manual_seed(1)
+        ids = torch.randint(0, V, (B, S + 1), device=device, generator=gen)
+        x_ids, y = ids[:, :S], ids[:, 1:]
+
+        def step():
+            for p_ in params:
+                p_.grad = None
+            x = F.embedding(x_ids, emb)
+            for layer in layers:
+                x = checkpoint(layer, x, cos, sin, use_reentrant=False) if mode == "full" else layer(x, cos, sin)
+            logits = F.rms_norm(x, (H,), nf, 1e-5) @ emb.t()
+            F.cross_entropy(logits.float().reshape(-1, V), y.reshape(-1)).backward()
+            for m, p_ in zip(master, params):
+                m.grad = p_.grad.float()
+            torch.nn.utils.clip_grad_norm_(master, 1.0)
+            opt.step()
+            with torch.no_grad():
+                for m, p_ in zip(master, params):
+                    p_.copy_(m)
+
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize(device)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize(device)
+        return (time.perf_counter() - t0) / steps
+
+    try:
+        t_full = run("full")
+        t_none = run("none")
+    except Exception as exc:  # context only: never fail the benchmark line for it
+        return {"error": f"{type(exc).__name__}: {exc}"}
+    return dict(
+        workload="the config-3 step in plain PyTorch-ROCm (SDPA, hipBLASLt, F.rms_norm, torch checkpoint, "
+                 "fused AdamW on an fp32 master), host-launched, same GPU",
+        tokens_per_s=round(B * S / t_full, 1), ms_per_step=round(t_full * 1e3, 3),
+        no_checkpoint_tokens_per_s=round(B * S / t_none, 1), steps_timed=steps,
+    )
+
+
 def c5_leg(args, device) -> dict:
     """One ring rank's attention share: rank 3 of 4
     (queries 24576..32767) over the four K/V blocks in ring order 3, 2, 1, 0
@@ -796,6 +890,11 @@ def main() -> None:
         c5 = c5_leg(args, device)
         print("c4: " + json.dumps(c4) + "\nc5: " + json.dumps(c5), file=sys.stderr, flush=True)
 
+    torch_ref = None
+    if not args.no_torch:
+        torch_ref = torch_eager_leg(device)
+        print("torch_eager: " + json.dumps(torch_ref), file=sys.stderr, flush=True)
+
     roofline = None
     if kernels:
         # the kernel with the most time per training step
@@ -848,6 +947,7 @@ def main() -> None:
         kernels=kernels,
         c4=c4,
         c5=c5,
+        torch_eager=torch_ref,
     )
     if eager:
         line["no_checkpoint_tokens_per_s"] = round(eager["tokens_per_s"], 1)
