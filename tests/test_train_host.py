@@ -27,6 +27,20 @@ def test_split_microbatches_slices_every_batched_tensor() -> None:
         assert part["input_ids"].data_ptr() == ids[2 * i].data_ptr()  # views, no copies
 
 
+def test_split_microbatches_keeps_container_types() -> None:
+    from collections import namedtuple
+
+    Pair = namedtuple("Pair", "ids mask")
+    ids = torch.arange(8).reshape(4, 2)
+    # the batch size comes from the top-level tensors (the reference collects
+    # tensors from mappings only, microbatches.py:62-72); nested containers are sliced
+    batch = {"input_ids": ids, "pair": Pair(ids, ids > 3), "list": [ids, ids * 2], "tuple": (ids,)}
+    parts = nm.split_microbatches(batch, 2)
+    assert isinstance(parts[1]["pair"], Pair) and torch.equal(parts[1]["pair"].ids, ids[2:])
+    assert isinstance(parts[0]["list"], list) and torch.equal(parts[0]["list"][1], ids[:2] * 2)
+    assert isinstance(parts[1]["tuple"], tuple) and torch.equal(parts[1]["tuple"][0], ids[2:])
+
+
 @pytest.mark.parametrize("batch,mbs,match", [
     ({"input_ids": torch.zeros(4, 2)}, 0, "micro_batch_size must be positive"),
     ({"input_ids": torch.zeros(4, 2)}, 3, "divisible by micro_batch_size"),
