@@ -50,7 +50,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-kernels", action="store_true", help="skip the per-kernel roofline timing")
     p.add_argument("--no-eager", action="store_true", help="skip the no-checkpoint comparison run")
-    p.add_argument("--no-legs", action="store_true", help="skip the config-4 and config-5 legs of the default line")
+    p.add_argument("--no-legs", action="store_true",
+                   help="skip the config-4, config-5 and PyTorch legs of the default line")
     p.add_argument("--no-torch", action="store_true",
                    help="skip the plain PyTorch-ROCm implementation of the same step (context)")
     p.add_argument("--host-launch", action="store_true",
@@ -891,7 +892,7 @@ def main() -> None:
         print("c4: " + json.dumps(c4) + "\nc5: " + json.dumps(c5), file=sys.stderr, flush=True)
 
     torch_ref = None
-    if not args.no_torch:
+    if not args.no_legs and not args.no_torch:
         torch_ref = torch_eager_leg(device)
         print("torch_eager: " + json.dumps(torch_ref), file=sys.stderr, flush=True)
 
