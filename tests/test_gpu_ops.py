@@ -168,6 +168,13 @@ ATTN_CASES = [
     (1, 8, 2, 2048, 2048, 64, torch.bfloat16, 0, True),
     (1, 32, 8, 2048, 2048, 64, torch.bfloat16, 0, True),
     (1, 8, 2, 1100, 1100, 64, torch.bfloat16, 0, True),
+    # tiles mostly padding: one query and one key, a 17-token sequence; GQA 8:1;
+    # more queries than keys without the causal mask at head dim 128
+    (1, 2, 2, 1, 1, 64, torch.bfloat16, 0, True),
+    (2, 4, 4, 17, 17, 64, torch.bfloat16, 0, True),
+    (3, 2, 2, 33, 33, 128, torch.bfloat16, 0, True),
+    (1, 16, 2, 96, 96, 64, torch.bfloat16, 0, True),
+    (1, 2, 1, 200, 64, 128, torch.bfloat16, 0, False),
 ]
 
 
