@@ -157,10 +157,26 @@ def _mm_f32(a: Tensor, b: Tensor, out: Tensor, c: Tensor | None, alpha: float, b
     return out
 
 
+def _round8(n: int) -> int:
+    return (n + 7) // 8 * 8
+
+
+def _zero_padded(t: Tensor, rows: int, cols: int) -> Tensor:
+    """``t`` (2-D) in the top-left corner of a zero [rows, cols] tensor."""
+    if tuple(t.shape) == (rows, cols):
+        return t
+    out = torch.zeros(rows, cols, dtype=t.dtype, device=t.device)
+    out[: t.shape[0], : t.shape[1]].copy_(t)
+    return out
+
+
 class LinearFunction(torch.autograd.Function):
     """``F.linear(x, weight)`` (nn/kernels/torch_backend.py:19-20,
     tensor_parallel/layers.py:214) on the library's GEMMs: y = x W^T,
-    dX = dY W, dW = dY^T X."""
+    dX = dY W, dW = dY^T X.  The bf16 GEMM moves 16-byte chunks, so feature
+    counts that are not multiples of 8 (a 50257-token vocabulary, say) run on
+    copies zero-padded to the next multiple of 8: the extra terms are zero
+    products, so the results are those of the unpadded shapes."""
 
     @staticmethod
     def forward(ctx: Any, x: Tensor, weight: Tensor) -> Tensor:
@@ -169,18 +185,32 @@ class LinearFunction(torch.autograd.Function):
         x2 = x.reshape(-1, x.shape[-1])
         if not x2.is_contiguous():
             x2 = x2.contiguous()
-        y = mm(x2, weight.t())
+        n, k = weight.shape
         ctx.save_for_backward(x2, weight)
         ctx.shape = x.shape
-        return y.view(*x.shape[:-1], weight.shape[0])
+        if weight.dtype == torch.bfloat16 and (n % 8 or k % 8):
+            n8, k8 = _round8(n), _round8(k)
+            y = mm(_zero_padded(x2, x2.shape[0], k8), _zero_padded(weight, n8, k8).t())[:, :n].contiguous()
+        else:
+            y = mm(x2, weight.t())
+        return y.view(*x.shape[:-1], n)
 
     @staticmethod
     def backward(ctx: Any, dy: Tensor):
         x2, weight = ctx.saved_tensors
-        dy2 = dy.reshape(-1, weight.shape[0])
+        n, k = weight.shape
+        dy2 = dy.reshape(-1, n)
         if not dy2.is_contiguous():
             dy2 = dy2.contiguous()
         dx = dw = None
+        if weight.dtype == torch.bfloat16 and (n % 8 or k % 8):
+            n8, k8 = _round8(n), _round8(k)
+            dyp = _zero_padded(dy2, dy2.shape[0], n8)
+            if ctx.needs_input_grad[0]:
+                dx = mm(dyp, _zero_padded(weight, n8, k8))[:, :k].contiguous().view(ctx.shape)
+            if ctx.needs_input_grad[1]:
+                dw = mm(dyp.t(), _zero_padded(x2, x2.shape[0], k8))[:n, :k].contiguous()
+            return dx, dw
         if ctx.needs_input_grad[0]:
             dx = mm(dy2, weight).view(ctx.shape)
         if ctx.needs_input_grad[1]:
@@ -972,6 +1002,23 @@ def dropout_add(x: Tensor, p: float, *, seed: int | None = None, residual: Tenso
 
 
 # ---------------------------------------------------------------- LM head + CE
+def _padded_head(weight: Tensor) -> tuple[Tensor, int]:
+    """The LM-head table with its vocabulary rows zero-padded to a multiple of
+    8 (the GEMM and cross-entropy kernels move 16-byte chunks), and the true
+    vocabulary size; the table itself when no padding is needed."""
+    vocab = weight.shape[0]
+    if vocab % 8 == 0:
+        return weight, vocab
+    return _zero_padded(weight, _round8(vocab), weight.shape[1]), vocab
+
+
+def _mask_padding(logits: Tensor, vocab: int) -> None:
+    """-inf in the padded vocabulary columns: they add exp(-inf) = 0 to the
+    softmax and get a zero gradient."""
+    if logits.shape[1] > vocab:
+        logits[:, vocab:].fill_(float("-inf"))
+
+
 def ce_fwd(logits2: Tensor, targets: Tensor, ignore_index: int, loss: Tensor, lse: Tensor) -> None:
     rows, vocab = logits2.shape
     _lib.call(
@@ -1069,10 +1116,12 @@ class LMHeadCrossEntropyFunction(torch.autograd.Function):
         rows = x2.shape[0]
         loss = torch.empty(rows, dtype=torch.float32, device=x2.device)
         lse = torch.empty_like(loss)
-        buf = torch.empty(min(chunk, max(rows, 1)), weight.shape[0], dtype=x2.dtype, device=x2.device)
+        w, vocab = _padded_head(weight)
+        buf = torch.empty(min(chunk, max(rows, 1)), w.shape[0], dtype=x2.dtype, device=x2.device)
         for s, e in _chunks(rows, chunk):
             logits = buf[: e - s]
-            mm(x2[s:e], weight.t(), out=logits)
+            mm(x2[s:e], w.t(), out=logits)
+            _mask_padding(logits, vocab)
             ce_fwd(logits, targets[s:e], ignore_index, loss[s:e], lse[s:e])
         ctx.save_for_backward(x2, weight, targets, lse)
         ctx.ignore_index = ignore_index
@@ -1087,23 +1136,26 @@ class LMHeadCrossEntropyFunction(torch.autograd.Function):
         rows = x2.shape[0]
         dx = torch.empty_like(x2)
         f32 = weight.dtype == torch.float32
+        w, vocab = _padded_head(weight)
         # the bf16 gradient accumulates over the chunks in fp32 (one rounding at the end)
         if f32:
-            dw = torch.zeros_like(weight)
+            dw = torch.zeros_like(w)
         else:  # the first chunk writes it (beta 0)
-            dw = (torch.empty if rows > 0 else torch.zeros)(weight.shape, dtype=torch.float32,
+            dw = (torch.empty if rows > 0 else torch.zeros)(w.shape, dtype=torch.float32,
                                                              device=weight.device)
-        buf = torch.empty(min(ctx.chunk, max(rows, 1)), weight.shape[0], dtype=x2.dtype,
+        buf = torch.empty(min(ctx.chunk, max(rows, 1)), w.shape[0], dtype=x2.dtype,
                           device=x2.device)
         for i, (s, e) in enumerate(_chunks(rows, ctx.chunk)):
             g = buf[: e - s]
-            mm(x2[s:e], weight.t(), out=g)
+            mm(x2[s:e], w.t(), out=g)
+            _mask_padding(g, vocab)
             ce_bwd_(g, targets[s:e], ctx.ignore_index, lse[s:e], grad_loss[s:e])
-            mm(g, weight, out=dx[s:e])
+            mm(g, w, out=dx[s:e])
             if f32:
                 mm(g.t(), x2[s:e], out=dw, c=dw, beta=1.0)
             else:
                 mm_f32out(g.t(), x2[s:e], dw, beta=0.0 if i == 0 else 1.0)
+        dw = dw[:vocab]
         if not f32:
             dw = dw.to(weight.dtype)
         if ctx.tie is not None:  # the embedding's backward adds it to its own gradient

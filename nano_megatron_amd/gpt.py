@@ -217,14 +217,26 @@ class VocabParallelCrossEntropy(nn.Module):
 
 
 class _LogitsCrossEntropy(torch.autograd.Function):
+    """The kernels move 16-byte chunks: a vocabulary that is not a multiple of
+    8 runs on a copy padded with -inf columns (zero probability, zero
+    gradient)."""
+
     @staticmethod
     def forward(ctx: Any, logits2: Tensor, targets: Tensor, ignore_index: int) -> Tensor:
-        logits2 = logits2.contiguous()
+        vocab = logits2.shape[1]
+        if vocab % 8:
+            padded = torch.empty(logits2.shape[0], Fn._round8(vocab), dtype=logits2.dtype, device=logits2.device)
+            padded[:, :vocab].copy_(logits2)
+            Fn._mask_padding(padded, vocab)
+            logits2 = padded
+        else:
+            logits2 = logits2.contiguous()
         loss = torch.empty(logits2.shape[0], dtype=torch.float32, device=logits2.device)
         lse = torch.empty_like(loss)
         Fn.ce_fwd(logits2, targets, ignore_index, loss, lse)
         ctx.save_for_backward(logits2, targets, lse)
         ctx.ignore_index = ignore_index
+        ctx.vocab = vocab
         return loss
 
     @staticmethod
@@ -232,7 +244,7 @@ class _LogitsCrossEntropy(torch.autograd.Function):
         logits2, targets, lse = ctx.saved_tensors
         g = logits2.clone()
         Fn.ce_bwd_(g, targets, ctx.ignore_index, lse, grad.float().contiguous())
-        return g, None, None
+        return (g if g.shape[1] == ctx.vocab else g[:, : ctx.vocab].contiguous()), None, None
 
 
 # ---------------------------------------------------------------- attention / MLP

@@ -348,3 +348,31 @@ def test_bias_and_untied_head_match_oracle(device, dtype, bias, tie, mode) -> No
     tol = dict(rtol=1e-5, atol=1e-5) if dtype == torch.float32 else dict(rtol=2e-2, atol=1e-2)
     torch.testing.assert_close(lo.detach().float().cpu(), lr.detach().float(), rtol=tol["rtol"], atol=tol["atol"])
     assert_grads(ours, ref, **tol)
+
+
+@pytest.mark.parametrize("dtype,tie", [(torch.float32, True), (torch.bfloat16, True), (torch.bfloat16, False)])
+def test_vocabulary_not_a_multiple_of_8_matches_oracle(device, dtype, tie) -> None:
+    """A 1001-token vocabulary (the reference takes any size; the kernels move
+    16-byte chunks, so the LM head runs on a zero-padded table with -inf logits
+    in the padding): loss and every gradient, and the logits of the
+    label-free forward, against the oracle."""
+    cfg = c1_config(layers=2, vocab_size=1001, tie_embeddings=tie)
+    ours, ref = build_pair(cfg, "full", dtype, device)
+    g = torch.Generator().manual_seed(4)
+    ids = torch.randint(0, 1001, (2, 129), generator=g)
+    x, y = ids[:, :128].contiguous(), ids[:, 1:].contiguous()
+    y[0, :3] = -100
+    y[1, 5] = 1000  # the last real token
+    lo = ours(x.to(device), labels=y.to(device)).loss
+    lr = ref(x, labels=y).loss
+    lo.backward()
+    lr.backward()
+    tol = dict(rtol=1e-5, atol=1e-5) if dtype == torch.float32 else dict(rtol=2e-2, atol=1e-2)
+    torch.testing.assert_close(lo.detach().float().cpu(), lr.detach().float(), **tol)
+    assert_grads(ours, ref, **tol)
+    with torch.no_grad():
+        logits = ours(x.to(device)).logits
+        rlog = ref(x).logits
+    assert logits.shape == (2, 128, 1001)
+    torch.testing.assert_close(logits.float().cpu(), rlog.float(), rtol=tol["rtol"],
+                               atol=tol["atol"] * float(rlog.abs().max()))

@@ -358,6 +358,9 @@ def test_lm_head_cross_entropy_matches_oracle(device, rows, hidden, vocab, dtype
 @pytest.mark.parametrize("m,n,k,layout", [
     (512, 384, 256, "NT"), (1000, 264, 200, "NT"), (333, 520, 136, "NN"),
     (520, 88, 72, "TN"), (256, 1024, 4096, "TN"), (300, 256, 64, "NN"),
+    # one row, one 8-column group, the smallest K; 7 rows; a long K over a
+    # narrow product (K split into fp32 partials)
+    (1, 8, 8, "NT"), (7, 16, 24, "NT"), (64, 8, 4104, "TN"), (8, 40, 8200, "NN"),
 ])
 def test_gemm_bf16_matches_fp32_product(device, m, n, k, layout) -> None:
     """nmb_gemm_bf16 for row/column-major operand mixes, ragged tiles, alpha/beta."""
@@ -838,3 +841,25 @@ def test_lm_head_table_gradient_is_rounded_once(device) -> None:
         half_ulp = torch.where(mag > 0, torch.exp2(torch.floor(torch.log2(mag)) - 8), torch.zeros_like(mag))
         err = (w.grad.double() - exact).abs()
         assert bool((err <= half_ulp + bound).all()), float((err - half_ulp - bound).max())
+
+
+@pytest.mark.parametrize("n_in,n_out", [(100, 52), (96, 1001), (37, 8)])
+def test_linear_with_feature_counts_not_multiples_of_8(device, n_in, n_out) -> None:
+    """HipKernelBackend.linear for any feature counts (nn.Linear's contract):
+    the bf16 GEMM runs on zero-padded copies; forward and both gradients
+    against fp32 products."""
+    backend = nm.HipKernelBackend()
+    torch.manual_seed(n_in + n_out)
+    lin = backend.linear(n_in, n_out, bias=True).to(device=device, dtype=torch.bfloat16)
+    x = torch.randn(3, 41, n_in, device=device).bfloat16().requires_grad_(True)
+    dy = torch.randn(3, 41, n_out, device=device).bfloat16()
+    y = lin(x)
+    y.backward(dy)
+    xf, wf = x.detach().float(), lin.weight.detach().float()
+    ref = xf @ wf.t() + lin.bias.detach().float()
+    assert y.shape == (3, 41, n_out)
+    torch.testing.assert_close(y.float(), ref, rtol=2e-2, atol=2e-2 * float(ref.abs().max()))
+    dxr = dy.float() @ wf
+    dwr = dy.float().reshape(-1, n_out).t() @ xf.reshape(-1, n_in)
+    torch.testing.assert_close(x.grad.float(), dxr, rtol=2e-2, atol=2e-2 * float(dxr.abs().max()))
+    torch.testing.assert_close(lin.weight.grad.float(), dwr, rtol=2e-2, atol=2e-2 * float(dwr.abs().max()))
