@@ -827,8 +827,13 @@ def attention(
     sequence_offset: int = 0,
     scale: float | None = None,
 ) -> Tensor:
-    """``local_attention`` for [B,H,S,D] tensors, GQA without repeated K/V."""
+    """``local_attention`` for [B,H,S,D] tensors, GQA without repeated K/V.
+    The bf16 MFMA kernels take heads of 64 and 128; other head sizes (up to
+    128) run on the generic kernels of the masked entry points, without a
+    mask."""
     _check_attn(q, [k], [v])
+    if q.dtype == torch.bfloat16 and q.shape[-1] not in (64, 128):
+        return masked_attention(q, k, v, None, causal=causal, sequence_offset=sequence_offset, scale=scale)
     return AttentionFunction.apply(q, causal, int(sequence_offset), scale, (0,), k, v)
 
 

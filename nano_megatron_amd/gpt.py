@@ -430,6 +430,8 @@ class GPTLayer(nn.Module):
             and type(self.post_attention_norm).__name__ == "RMSNorm"
             and self.dropout == 0.0
             and self.attention.dropout == 0.0
+            # the fused block's bf16 attention kernels take heads of 64 and 128
+            and (self.attention.head_dim in (64, 128) or self.input_norm.weight.dtype == torch.float32)
             and all(
                 getattr(m, "bias", None) is None
                 for m in (self.attention.q_proj.linear, self.attention.k_proj.linear,

@@ -376,3 +376,19 @@ def test_vocabulary_not_a_multiple_of_8_matches_oracle(device, dtype, tie) -> No
     assert logits.shape == (2, 128, 1001)
     torch.testing.assert_close(logits.float().cpu(), rlog.float(), rtol=tol["rtol"],
                                atol=tol["atol"] * float(rlog.abs().max()))
+
+
+def test_head_size_96_model_matches_oracle(device) -> None:
+    """hidden 384 over 4 heads (head size 96) in bf16: the layers leave the
+    fused block (its attention kernels take 64 and 128) for the module path;
+    loss and every gradient against the oracle."""
+    cfg = c1_config(layers=2, hidden_size=384, ffn_hidden_size=1024, heads=4, kv_heads=2)
+    ours, ref = build_pair(cfg, "full", torch.bfloat16, device)
+    assert not any(layer.fusable() for layer in ours.layers)
+    ids, labels = c1_batch()
+    lo = ours(ids.to(device), labels=labels.to(device)).loss
+    lr = ref(ids, labels=labels).loss
+    lo.backward()
+    lr.backward()
+    torch.testing.assert_close(lo.detach().float().cpu(), lr.detach().float(), rtol=2e-2, atol=1e-2)
+    assert_grads(ours, ref, rtol=2e-2, atol=1e-2)

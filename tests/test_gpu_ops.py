@@ -863,3 +863,24 @@ def test_linear_with_feature_counts_not_multiples_of_8(device, n_in, n_out) -> N
     dwr = dy.float().reshape(-1, n_out).t() @ xf.reshape(-1, n_in)
     torch.testing.assert_close(x.grad.float(), dxr, rtol=2e-2, atol=2e-2 * float(dxr.abs().max()))
     torch.testing.assert_close(lin.weight.grad.float(), dwr, rtol=2e-2, atol=2e-2 * float(dwr.abs().max()))
+
+
+@pytest.mark.parametrize("d,hq,hkv,causal", [(96, 4, 2, True), (32, 2, 2, False), (80, 4, 1, True)])
+def test_attention_other_head_sizes_bf16(device, d, hq, hkv, causal) -> None:
+    """local_attention at head sizes other than 64 and 128 in bf16 (SDPA takes
+    any): the generic kernels, forward and gradients against the oracle."""
+    g = gen(d + hq)
+    q = torch.randn(2, hq, 70, d, generator=g).bfloat16()
+    k = torch.randn(2, hkv, 70, d, generator=g).bfloat16()
+    v = torch.randn(2, hkv, 70, d, generator=g).bfloat16()
+    do = torch.randn(2, hq, 70, d, generator=g).bfloat16()
+    qr, kr, vr = (t.float().clone().requires_grad_(True) for t in (q, k, v))
+    o_ref = R.local_attention(qr, kr, vr, causal=causal)
+    o_ref.backward(do.float())
+    qd, kd, vd = (t.to(device).requires_grad_(True) for t in (q, k, v))
+    o = nm.HipKernelBackend().local_attention(qd, kd, vd, causal=causal)
+    o.backward(do.to(device))
+    close(o, o_ref, torch.bfloat16)
+    close(qd.grad, qr.grad, torch.bfloat16, scale_atol=True, msg="dq")
+    close(kd.grad, kr.grad, torch.bfloat16, scale_atol=True, msg="dk")
+    close(vd.grad, vr.grad, torch.bfloat16, scale_atol=True, msg="dv")
