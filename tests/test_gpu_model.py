@@ -392,3 +392,44 @@ def test_head_size_96_model_matches_oracle(device) -> None:
     lr.backward()
     torch.testing.assert_close(lo.detach().float().cpu(), lr.detach().float(), rtol=2e-2, atol=1e-2)
     assert_grads(ours, ref, rtol=2e-2, atol=1e-2)
+
+
+def test_pipeline_stage_split_equals_the_whole_model(device) -> None:
+    """Two stages of one model (models/gpt/model.py:40-250 with layer_start /
+    layer_end and the owns_* flags, chained through hidden_states as a
+    pipeline does at one rank): the loss and every gradient equal the whole
+    model's, bit for bit."""
+    cfg = c1_config(layers=4, tie_embeddings=False)
+    torch.manual_seed(0)
+    whole = nm.GPTModel(cfg).to(device=device, dtype=torch.bfloat16).train()
+    first = nm.GPTModel(cfg, layer_end=2, owns_lm_head=False, owns_final_norm=False)
+    last = nm.GPTModel(cfg, layer_start=2, owns_embedding=False)
+    first = first.to(device=device, dtype=torch.bfloat16).train()
+    last = last.to(device=device, dtype=torch.bfloat16).train()
+    state = whole.state_dict()
+    first.load_state_dict({k: v for k, v in state.items()
+                           if k.startswith("embedding.") or k.split(".")[:2] in (["layers", "0"], ["layers", "1"])})
+    moved = {}
+    for k, v in state.items():
+        parts = k.split(".")
+        if parts[0] == "layers" and int(parts[1]) >= 2:
+            moved[".".join(["layers", str(int(parts[1]) - 2), *parts[2:]])] = v
+        elif parts[0] in ("final_norm", "lm_head"):
+            moved[k] = v
+    last.load_state_dict(moved)
+    ids, labels = c1_batch()
+    ids, labels = ids[:2].to(device), labels[:2].to(device)
+    loss = whole(ids, labels=labels).loss
+    loss.backward()
+    hidden = first(ids).hidden_states
+    assert first.lm_head is None and last.embedding is None
+    staged = last(hidden_states=hidden, labels=labels).loss
+    staged.backward()
+    assert torch.equal(loss, staged)
+    grads = dict(whole.named_parameters())
+    for name, p in first.named_parameters():
+        assert torch.equal(p.grad, grads[name].grad), name
+    for name, p in last.named_parameters():
+        parts = name.split(".")
+        src = ".".join(["layers", str(int(parts[1]) + 2), *parts[2:]]) if parts[0] == "layers" else name
+        assert torch.equal(p.grad, grads[src].grad), name
