@@ -828,12 +828,18 @@ def attention(
     scale: float | None = None,
 ) -> Tensor:
     """``local_attention`` for [B,H,S,D] tensors, GQA without repeated K/V.
-    The bf16 MFMA kernels take heads of 64 and 128; other head sizes (up to
-    128) run on the generic kernels of the masked entry points, without a
-    mask."""
+    The bf16 MFMA kernels take heads of 64 and 128; smaller bf16 heads run on
+    them zero-padded to the next of the two (the padded dimensions add zero to
+    every score and give zero output columns, which are cut off; the scale
+    stays 1/sqrt(D) of the true size), and autograd pads and cuts the
+    gradients the same way."""
     _check_attn(q, [k], [v])
-    if q.dtype == torch.bfloat16 and q.shape[-1] not in (64, 128):
-        return masked_attention(q, k, v, None, causal=causal, sequence_offset=sequence_offset, scale=scale)
+    d = q.shape[-1]
+    if q.dtype == torch.bfloat16 and d not in (64, 128) and d < 128:
+        dp = 64 if d < 64 else 128
+        scale = scale if scale else 1.0 / math.sqrt(d)
+        qp, kp, vp = (torch.nn.functional.pad(t, (0, dp - d)) for t in (q, k, v))
+        return AttentionFunction.apply(qp, causal, int(sequence_offset), scale, (0,), kp, vp)[..., :d]
     return AttentionFunction.apply(q, causal, int(sequence_offset), scale, (0,), k, v)
 
 

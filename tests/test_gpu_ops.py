@@ -868,7 +868,8 @@ def test_linear_with_feature_counts_not_multiples_of_8(device, n_in, n_out) -> N
 @pytest.mark.parametrize("d,hq,hkv,causal", [(96, 4, 2, True), (32, 2, 2, False), (80, 4, 1, True)])
 def test_attention_other_head_sizes_bf16(device, d, hq, hkv, causal) -> None:
     """local_attention at head sizes other than 64 and 128 in bf16 (SDPA takes
-    any): the generic kernels, forward and gradients against the oracle."""
+    any): the MFMA kernels on zero-padded heads, forward and gradients against
+    the oracle."""
     g = gen(d + hq)
     q = torch.randn(2, hq, 70, d, generator=g).bfloat16()
     k = torch.randn(2, hkv, 70, d, generator=g).bfloat16()
