@@ -433,3 +433,30 @@ def test_pipeline_stage_split_equals_the_whole_model(device) -> None:
         parts = name.split(".")
         src = ".".join(["layers", str(int(parts[1]) + 2), *parts[2:]]) if parts[0] == "layers" else name
         assert torch.equal(p.grad, grads[src].grad), name
+
+
+def test_activation_checkpoint_module_wrapper(device) -> None:
+    """nn/activation_checkpoint.py:103-131: the module wrapper runs the wrapped
+    layer under the checkpoint; output and gradients equal the unwrapped
+    layer's bit for bit."""
+    cfg = c1_config(layers=1)
+    torch.manual_seed(0)
+    model = nm.GPTModel(cfg).to(device=device, dtype=torch.bfloat16)
+    layer = model.layers[0]
+    x = torch.randn(2, 64, cfg.hidden_size, device=device).bfloat16()
+    calls = []
+    hook = layer.register_forward_hook(lambda *a: calls.append(1))
+    outs, grads = [], []
+    for wrapped in (False, True):
+        layer.zero_grad(set_to_none=True)
+        xi = x.clone().requires_grad_(True)
+        mod = nm.ActivationCheckpoint(layer) if wrapped else layer
+        y = mod(xi)
+        y.float().square().sum().backward()
+        outs.append(y.detach())
+        grads.append([xi.grad] + [p.grad.clone() for p in layer.parameters()])
+    hook.remove()
+    assert len(calls) >= 2
+    assert torch.equal(outs[0], outs[1])
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
