@@ -51,7 +51,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-kernels", action="store_true", help="skip the per-kernel roofline timing")
     p.add_argument("--no-eager", action="store_true", help="skip the no-checkpoint comparison run")
     p.add_argument("--no-legs", action="store_true",
-                   help="skip the config-4, config-5 and PyTorch legs of the default line")
+                   help="skip the config-4, config-5, PyTorch and vendor-GEMM legs of the default line")
     p.add_argument("--no-torch", action="store_true",
                    help="skip the plain PyTorch-ROCm implementation of the same step (context)")
     p.add_argument("--host-launch", action="store_true",
@@ -661,6 +661,64 @@ def c4_leg(args, device, eager: bool = True) -> dict:
     return leg
 
 
+def vendor_gemm_leg(device, calls: int = 20, rounds: int = 3) -> dict:
+    """This library's bf16 GEMM against ``torch.mm`` (the vendor BLAS that torch
+    picks on ROCm) on the twelve plain product shapes of the config-3 step
+    (forward, dX and weight-gradient products; the epilogue variants run as
+    plain products here so that both sides do the same work), same operand
+    views, best of ``rounds`` rounds of ``calls`` calls each, HIP events on the
+    current stream."""
+    import torch
+
+    from nano_megatron_amd import functional as Fn
+
+    bf = torch.bfloat16
+    gen = torch.Generator(device=device).manual_seed(0)
+    T, H, F = BATCH * SEQ, C3["hidden_size"], C3["ffn_hidden_size"]
+
+    def randn(*shape):
+        return (0.05 * torch.randn(*shape, device=device, generator=gen)).to(bf)
+
+    # (name, M, N, K, A stored transposed, B stored [K, N])
+    cases = [("qkv", T, 3 * H, H, False, False), ("o", T, H, H, False, False),
+             ("gate_up", T, 2 * F, H, False, False), ("down", T, H, F, False, False),
+             ("d_swiglu", T, F, H, False, True), ("d_norm2", T, H, 2 * F, False, True),
+             ("d_attn_out", T, H, H, False, True), ("d_norm1", T, H, 3 * H, False, True),
+             ("dw_gate_up", 2 * F, H, T, True, True), ("dw_down", H, F, T, True, True),
+             ("dw_o", H, H, T, True, True), ("dw_qkv", 3 * H, H, T, True, True)]
+
+    def best_us(fn):
+        best = None
+        for _ in range(rounds):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize(device)
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(calls):
+                fn()
+            e.record()
+            torch.cuda.synchronize(device)
+            t = s.elapsed_time(e) / calls * 1e3
+            best = t if best is None else min(best, t)
+        return best
+
+    shapes, ours_sum, torch_sum = [], 0.0, 0.0
+    for name, m, n, k, a_t, b_t in cases:
+        a = randn(k, m).t() if a_t else randn(m, k)
+        b = randn(k, n) if b_t else randn(n, k).t()
+        out, ref = torch.empty(m, n, dtype=bf, device=device), torch.empty(m, n, dtype=bf, device=device)
+        ours = best_us(lambda: Fn.mm(a, b, out=out))
+        theirs = best_us(lambda: torch.mm(a, b, out=ref))
+        ours_sum, torch_sum = ours_sum + ours, torch_sum + theirs
+        shapes.append(dict(name=name, m=m, n=n, k=k, ours_us=round(ours, 2), torch_us=round(theirs, 2),
+                           max_abs_diff=float((out.float() - ref.float()).abs().max())))
+        del a, b, out, ref
+    return dict(workload="the config-3 step's plain GEMM shapes, this library against torch.mm",
+                ours_us_sum=round(ours_sum, 1), torch_us_sum=round(torch_sum, 1),
+                ratio=round(ours_sum / torch_sum, 3), shapes=shapes)
+
+
 def torch_eager_leg(device, steps: int = 10, warmup: int = 3) -> dict:
     """The config-3 step written in plain PyTorch on the same GPU, for context:
     the reference's modules as torch operations (F.rms_norm, RoPE by tensor
@@ -896,6 +954,11 @@ def main() -> None:
         torch_ref = torch_eager_leg(device)
         print("torch_eager: " + json.dumps(torch_ref), file=sys.stderr, flush=True)
 
+    vendor = None
+    if not args.no_legs:
+        vendor = vendor_gemm_leg(device)
+        print("vendor_gemm: " + json.dumps(vendor), file=sys.stderr, flush=True)
+
     roofline = None
     if kernels:
         # the kernel with the most time per training step
@@ -949,6 +1012,7 @@ def main() -> None:
         c4=c4,
         c5=c5,
         torch_eager=torch_ref,
+        vendor_gemm=vendor,
     )
     if eager:
         line["no_checkpoint_tokens_per_s"] = round(eager["tokens_per_s"], 1)
