@@ -10,8 +10,6 @@ from nano_megatron_amd.config import (
     ActivationCheckpointConfig,
     GPTConfig,
     KernelConfig,
-    LearningRateSchedulerConfig,
-    OptimizerConfig,
 )
 from nano_megatron_amd.functional import (
     attention,
@@ -29,7 +27,7 @@ from nano_megatron_amd.gpt import (
     GPTOutput,
 )
 from nano_megatron_amd.kernels import HipKernelBackend, KernelBackend, build_kernel_backend
-from nano_megatron_amd.train import LearningRateScheduler, StepOutput, split_microbatches, train_step
+from nano_megatron_amd.train import StepOutput, train_step
 from nano_megatron_amd.nn import (
     ActivationCheckpoint,
     RMSNorm,
@@ -52,8 +50,6 @@ __all__ = [
     "HipKernelBackend",
     "KernelBackend",
     "KernelConfig",
-    "LearningRateSchedulerConfig",
-    "OptimizerConfig",
     "RMSNorm",
     "RotaryEmbedding",
     "activation_checkpoint",
@@ -61,8 +57,6 @@ __all__ = [
     "parallel_dropout",
     "ActivationCheckpoint",
     "StepOutput",
-    "LearningRateScheduler",
-    "split_microbatches",
     "train_step",
     "apply_rotary_pos_emb",
     "attention",

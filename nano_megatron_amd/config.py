@@ -2,9 +2,8 @@
 
 GPTConfig follows config/schema.py:205-273, ActivationCheckpointConfig
 config/schema.py:381-416, KernelConfig config/schema.py:298-307 (the
-reference's enum has only "torch"; this package adds "hip"), OptimizerConfig
-config/schema.py:438-463 and LearningRateSchedulerConfig config/schema.py:
-466-486.  Validation raises the same exception types as the reference.
+reference's enum has only "torch"; this package adds "hip").  Validation
+raises the same exception types as the reference.
 """
 
 from __future__ import annotations
@@ -120,64 +119,3 @@ class KernelConfig:
         if backend not in KERNEL_BACKENDS:
             raise ValueError(f"kernels.backend must be one of {KERNEL_BACKENDS}, got {backend!r}")
         object.__setattr__(self, "backend", backend)
-
-
-def _require_float(name: str, value, *, allow_zero: bool = False) -> None:
-    """config/schema.py:43-49."""
-    if isinstance(value, bool) or not isinstance(value, (int, float)):
-        raise TypeError(f"{name} must be a number, got {value!r}")
-    if not (value >= 0 if allow_zero else value > 0):
-        raise ValueError(f"{name} must be {'>=' if allow_zero else '>'} 0, got {value}")
-
-
-@dataclass(frozen=True)
-class OptimizerConfig:
-    """config/schema.py:438-463: AdamW and its gradient clip."""
-
-    name: str = "adamw"
-    lr: float = 3.0e-4
-    betas: tuple[float, float] = (0.9, 0.95)
-    eps: float = 1.0e-8
-    weight_decay: float = 0.1
-    clip_grad_norm: float | None = 1.0
-
-    def __post_init__(self) -> None:
-        if not isinstance(self.name, str):
-            raise TypeError("optimizer.name must be a string")
-        object.__setattr__(self, "name", self.name.lower())
-        object.__setattr__(self, "betas", tuple(self.betas))
-        if self.name != "adamw":
-            raise ValueError("optimizer.name must be 'adamw' in the first implementation phase")
-        _require_float("optimizer.lr", self.lr)
-        _require_float("optimizer.eps", self.eps)
-        _require_float("optimizer.weight_decay", self.weight_decay, allow_zero=True)
-        if len(self.betas) != 2 or any(
-            isinstance(b, bool) or not isinstance(b, (int, float)) or not 0 <= b < 1 for b in self.betas
-        ):
-            raise ValueError("optimizer.betas must contain two values in [0, 1)")
-        if self.clip_grad_norm is not None:
-            _require_float("optimizer.clip_grad_norm", self.clip_grad_norm)
-
-
-LR_SCHEDULES = ("constant", "cosine")
-
-
-@dataclass(frozen=True)
-class LearningRateSchedulerConfig:
-    """config/schema.py:466-486: warm-up, then constant or cosine decay to min_lr."""
-
-    schedule: str = "cosine"
-    warmup_steps: int = 0
-    decay_steps: int | None = None
-    min_lr: float = 0.0
-
-    def __post_init__(self) -> None:
-        value = str(getattr(self.schedule, "value", self.schedule)).lower()
-        if value not in LR_SCHEDULES:
-            raise ValueError(f"lr_scheduler.schedule must be one of: {', '.join(LR_SCHEDULES)}; "
-                             f"got {self.schedule!r}")
-        object.__setattr__(self, "schedule", value)
-        _require_int("lr_scheduler.warmup_steps", self.warmup_steps, minimum=0)
-        if self.decay_steps is not None:
-            _require_int("lr_scheduler.decay_steps", self.decay_steps)
-        _require_float("lr_scheduler.min_lr", self.min_lr, allow_zero=True)

@@ -52,15 +52,8 @@ class MasterAdamW:
         self._param_ptrs = [p.data_ptr() for p in self.params]
         self._graph: dict | None = None  # buffers of a captured step (prepare_graph)
 
-    @classmethod
-    def from_config(cls, params: Iterable[nn.Parameter], config) -> "MasterAdamW":
-        """From an OptimizerConfig (config/schema.py:438-463)."""
-        return cls(params, lr=config.lr, betas=tuple(config.betas), eps=config.eps,
-                   weight_decay=config.weight_decay, clip_grad_norm=config.clip_grad_norm)
-
     def set_learning_rate(self, lr: float) -> None:
-        """The rate of the next update (what LearningRateScheduler installs,
-        training/lr_scheduler.py:119-122)."""
+        """The rate of the next update (a schedule installs it between steps)."""
         if isinstance(lr, bool) or not lr >= 0.0:
             raise ValueError(f"learning rate must be >= 0, got {lr!r}")
         self.lr = float(lr)
@@ -70,9 +63,12 @@ class MasterAdamW:
         return self.stats[0]
 
     def state_dict(self) -> dict:
-        """The resumable state, as the ZeRO strategy keeps it at one rank
-        (data_parallel/_zero.py:234-251: the fp32 master and both moments,
-        the step count and the rate), as host tensors over the flat layout."""
+        """This optimizer's own resumable state: the fp32 master, both moments,
+        the step count and the rate, as host tensors over the flat layout of
+        the parameters (in their order), with their element counts.  It holds
+        what the reference's ZeRO strategy saves at one rank
+        (data_parallel/_zero.py:234-251) but not in its per-bucket layout:
+        neither side loads the other's state."""
         return {
             "mode": "master_adamw",
             "step": self.step_count,
@@ -85,9 +81,10 @@ class MasterAdamW:
 
     @torch.no_grad()
     def load_state_dict(self, state: dict) -> None:
-        """data_parallel/_zero.py:253-301: the layout must match the current
-        parameters; the master, both moments, the step and the rate are
-        restored (the parameters themselves come from the model's state dict)."""
+        """Restores what ``state_dict`` saved; the element counts must match
+        the current parameters.  The master, both moments, the step and the
+        rate come back (the parameters themselves come from the model's state
+        dict)."""
         if state.get("mode", "master_adamw") != "master_adamw":
             raise ValueError(f"cannot load {state.get('mode')!r} state into MasterAdamW")
         numels = [p.numel() for p in self.params]

@@ -1,5 +1,5 @@
-"""The training step's host logic on the CPU: micro-batch splitting as the
-reference's (training/microbatches.py:56-86), the schedules' backward order
+"""The training step's host logic on the CPU: micro-batch splitting, the
+schedules' backward order
 and loss scaling (pipeline_parallel/schedules/gpipe.py, one_f_one_b.py,
 base.py:111-126), and the token-weighted loss metric (training/metrics.py:
 68-121), checked on a small CPU model against closed forms."""
@@ -13,43 +13,35 @@ import torch
 from torch import nn
 
 import nano_megatron_amd as nm
+from nano_megatron_amd.train import _microbatches
 
 
-def test_split_microbatches_slices_every_batched_tensor() -> None:
+def _rows(batch, size):
+    """The micro-batches the step should see: consecutive row ranges."""
+    n = batch["input_ids"].size(0) // size
+    return [{k: v[i * size:(i + 1) * size] for k, v in batch.items()} for i in range(n)]
+
+
+def test_microbatches_are_row_views_and_pass_other_entries() -> None:
     ids = torch.arange(24).reshape(6, 4)
-    batch = {"input_ids": ids, "labels": ids + 1, "scale": torch.tensor(2.0), "name": "x"}
-    parts = nm.split_microbatches(batch, 2)
+    batch = {"input_ids": ids, "labels": ids + 1, "position_ids": torch.arange(4)[None], "scale": 2.0}
+    parts = _microbatches(batch, 2)
     assert len(parts) == 3
     for i, part in enumerate(parts):
         assert torch.equal(part["input_ids"], ids[2 * i:2 * i + 2])
         assert torch.equal(part["labels"], ids[2 * i:2 * i + 2] + 1)
-        assert part["scale"] is batch["scale"] and part["name"] == "x"
+        assert part["position_ids"] is batch["position_ids"] and part["scale"] == 2.0
         assert part["input_ids"].data_ptr() == ids[2 * i].data_ptr()  # views, no copies
 
 
-def test_split_microbatches_keeps_container_types() -> None:
-    from collections import namedtuple
-
-    Pair = namedtuple("Pair", "ids mask")
-    ids = torch.arange(8).reshape(4, 2)
-    # the batch size comes from the top-level tensors (the reference collects
-    # tensors from mappings only, microbatches.py:62-72); nested containers are sliced
-    batch = {"input_ids": ids, "pair": Pair(ids, ids > 3), "list": [ids, ids * 2], "tuple": (ids,)}
-    parts = nm.split_microbatches(batch, 2)
-    assert isinstance(parts[1]["pair"], Pair) and torch.equal(parts[1]["pair"].ids, ids[2:])
-    assert isinstance(parts[0]["list"], list) and torch.equal(parts[0]["list"][1], ids[:2] * 2)
-    assert isinstance(parts[1]["tuple"], tuple) and torch.equal(parts[1]["tuple"][0], ids[2:])
-
-
 @pytest.mark.parametrize("batch,mbs,match", [
-    ({"input_ids": torch.zeros(4, 2)}, 0, "micro_batch_size must be positive"),
-    ({"input_ids": torch.zeros(4, 2)}, 3, "divisible by micro_batch_size"),
-    ({"input_ids": torch.zeros(4, 2), "labels": torch.zeros(5, 2)}, 2, "same leading dimension"),
-    ({"input_ids": torch.tensor(1.0)}, 1, "no tensor with a leading batch dimension"),
+    ({"input_ids": torch.zeros(4, 2)}, 0, "does not split"),
+    ({"input_ids": torch.zeros(4, 2)}, 3, "does not split"),
+    ({"input_ids": torch.zeros(4, 2), "labels": torch.zeros(5, 2)}, 2, "labels has 5 rows"),
 ])
-def test_split_microbatches_rejects_what_the_reference_rejects(batch, mbs, match) -> None:
+def test_microbatches_reject_uneven_batches(batch, mbs, match) -> None:
     with pytest.raises(ValueError, match=match):
-        nm.split_microbatches(batch, mbs)
+        _microbatches(batch, mbs)
 
 
 class TinyLM(nn.Module):
@@ -93,7 +85,7 @@ def test_train_step_accumulates_the_mean_of_microbatch_losses(schedule) -> None:
     out = nm.train_step(model, opt, batch, micro_batch_size=2, gradient_accumulation_steps=3,
                         schedule=schedule, clip_grad_norm=None, step_index=4)
     assert model.calls == [12, 13, 14]
-    parts = nm.split_microbatches(batch, 2)
+    parts = _rows(batch, 2)
     losses = [ref(p["input_ids"], labels=p["labels"]).loss for p in parts]
     (sum(losses) / 3).backward()
     with torch.no_grad():
@@ -145,7 +137,7 @@ def test_train_step_clips_and_follows_the_lr_scheduler() -> None:
     out = nm.train_step(model, opt, _batch(), micro_batch_size=3, schedule="gpipe", clip_grad_norm=0.01,
                         lr_scheduler=sched, step_index=7)
     assert sched.completed == 8 and out.metrics["learning_rate"] == 0.05
-    parts = nm.split_microbatches(_batch(), 3)
+    parts = _rows(_batch(), 3)
     (sum(ref(p["input_ids"], labels=p["labels"]).loss for p in parts) / 2).backward()
     norm = torch.nn.utils.clip_grad_norm_(ref.parameters(), 0.01)
     assert out.metrics["grad_norm"] == pytest.approx(float(norm), rel=1e-12)
@@ -159,67 +151,9 @@ def test_train_step_clips_and_follows_the_lr_scheduler() -> None:
 def test_train_step_rejects_bad_arguments() -> None:
     model = TinyLM()
     opt = torch.optim.SGD(model.parameters(), lr=0.1)
-    with pytest.raises(ValueError, match="exactly gradient_accumulation_steps"):
+    with pytest.raises(ValueError, match="gradient_accumulation_steps is 2"):
         nm.train_step(model, opt, _batch(), micro_batch_size=2, gradient_accumulation_steps=2)
     with pytest.raises(ValueError, match="unknown schedule"):
         nm.train_step(model, opt, _batch(), micro_batch_size=2, schedule="interleaved")
     with pytest.raises(ValueError, match="labels"):
         nm.train_step(model, opt, {"input_ids": torch.zeros(2, 3, dtype=torch.long)}, micro_batch_size=1)
-
-
-class _Sink:
-    def __init__(self) -> None:
-        self.rates: list[float] = []
-
-    def set_learning_rate(self, lr: float) -> None:
-        self.rates.append(lr)
-
-
-def test_lr_scheduler_warmup_cosine_and_resume() -> None:
-    """training/lr_scheduler.py: warm-up base * (k + 1) / W, cosine from base
-    to min over [W, decay] (half-way = the mean, the end and after = min); the
-    rate for the next update is installed at every change; a state dict
-    restores it and refuses a changed configuration."""
-    cfg = nm.LearningRateSchedulerConfig(schedule="cosine", warmup_steps=4, decay_steps=20, min_lr=1e-5)
-    sink = _Sink()
-    s = nm.LearningRateScheduler(config=cfg, optimizer_config=nm.OptimizerConfig(lr=1e-3), data_parallel=sink,
-                                 max_steps=1000)
-    assert [s.rate_at(k) for k in range(4)] == pytest.approx([2.5e-4, 5e-4, 7.5e-4, 1e-3])
-    assert s.rate_at(4) == pytest.approx(1e-3)
-    assert s.rate_at(12) == pytest.approx((1e-3 + 1e-5) / 2)
-    assert s.rate_at(20) == pytest.approx(1e-5) and s.rate_at(500) == pytest.approx(1e-5)
-    assert sink.rates == [pytest.approx(2.5e-4)]
-    s.step()
-    s.step()
-    assert sink.rates[-1] == pytest.approx(7.5e-4) and s.completed_steps == 2
-    state = s.state_dict()
-    other = nm.LearningRateScheduler(config=cfg, optimizer_config=nm.OptimizerConfig(lr=1e-3),
-                                     data_parallel=_Sink(), max_steps=1000)
-    other.load_state_dict(state, expected_completed_steps=2)
-    assert other.learning_rate == s.learning_rate
-    changed = nm.LearningRateScheduler(config=cfg, optimizer_config=nm.OptimizerConfig(lr=2e-3),
-                                       data_parallel=_Sink(), max_steps=1000)
-    with pytest.raises(RuntimeError, match="changed across resume for base_lr"):
-        changed.load_state_dict(state)
-    const = nm.LearningRateScheduler(config=nm.LearningRateSchedulerConfig(schedule="constant"),
-                                     optimizer_config=nm.OptimizerConfig(lr=3e-4), data_parallel=_Sink(),
-                                     max_steps=10)
-    assert const.rate_at(0) == const.rate_at(9) == pytest.approx(3e-4)
-
-
-def test_optimizer_and_scheduler_configs_validate_like_the_reference() -> None:
-    with pytest.raises(ValueError, match="optimizer.lr must be > 0"):
-        nm.OptimizerConfig(lr=0.0)
-    with pytest.raises(ValueError, match="betas"):
-        nm.OptimizerConfig(betas=(0.9, 1.0))
-    with pytest.raises(ValueError, match="'adamw'"):
-        nm.OptimizerConfig(name="sgd")
-    with pytest.raises(ValueError, match="lr_scheduler.schedule must be one of"):
-        nm.LearningRateSchedulerConfig(schedule="linear")
-    with pytest.raises(ValueError, match="min_lr must be between"):
-        nm.LearningRateScheduler(config=nm.LearningRateSchedulerConfig(min_lr=1.0),
-                                 optimizer_config=nm.OptimizerConfig(lr=1e-3), data_parallel=_Sink(),
-                                 max_steps=10)
-    with pytest.raises(ValueError, match="warmup_steps cannot exceed decay_steps"):
-        nm.LearningRateScheduler(config=nm.LearningRateSchedulerConfig(warmup_steps=5, decay_steps=3),
-                                 optimizer_config=nm.OptimizerConfig(), data_parallel=_Sink(), max_steps=10)
