@@ -22,6 +22,7 @@ from nano_megatron_amd import functional as Fn
 from nano_megatron_amd.graph import CapturedTrainStep
 from nano_megatron_amd.optim import MasterAdamW
 from oracle import reference as R
+from parity import assert_bf16_grads, assert_close_scaled, assert_grads_scaled, assert_loss_close
 
 pytestmark = pytest.mark.gpu
 
@@ -30,11 +31,9 @@ def gen(seed):
     return torch.Generator().manual_seed(seed)
 
 
-def close(got, exp, dtype, scale_atol=False, msg=""):
-    t = dict(rtol=1e-5, atol=1e-5) if dtype == torch.float32 else dict(rtol=2e-2, atol=1e-2)
-    if scale_atol:
-        t["atol"] = t["atol"] * max(1.0, float(exp.abs().max()))
-    torch.testing.assert_close(got.detach().float().cpu(), exp.detach().float(), msg=msg, **t)
+def close(got, exp, dtype, scale_atol=True, msg=""):
+    """The dtype's bar with atol scaled to max|exp| (tests/parity.py)."""
+    assert_close_scaled(got, exp, dtype, msg=msg)
 
 
 # ---------------------------------------------------------------- elementwise dropout
@@ -199,6 +198,15 @@ def model_pair(device, dtype, mode, rng, kv_heads=None, dropout=0.1):
     return ours, ref
 
 
+def fp32_twin(ref, rng):
+    """The oracle in fp32 on the bf16 oracle's weights, with the same masks."""
+    seeds = (lambda layer, op: kernel_seed(rng.seed_of((layer, 0, 0, op)))) if rng is not None else None
+    twin = R.OracleGPTModel(ref.config, activation_checkpoint_config=ref.activation_checkpoint_config,
+                            dropout_seed=seeds)
+    twin.load_state_dict({k: v.float() for k, v in ref.state_dict().items()})
+    return twin.train()
+
+
 def batch():
     ids = torch.randint(0, 4096, (2, 65), generator=gen(10))
     return ids[:, :64].contiguous(), ids[:, 1:].contiguous()
@@ -219,14 +227,13 @@ def test_model_with_dropout_matches_oracle(device, dtype, mode, kv_heads) -> Non
     lr = ref(ids, labels=labels).loss
     lo.backward()
     lr.backward()
-    tol = dict(rtol=1e-5, atol=1e-5) if dtype == torch.float32 else dict(rtol=2e-2, atol=1e-2)
-    torch.testing.assert_close(lo.detach().float().cpu(), lr.detach().float(), **tol)
-    theirs = dict(ref.named_parameters())
-    for name, p in ours.named_parameters():
-        q = theirs[name]
-        t = dict(tol)
-        t["atol"] = t["atol"] * max(1.0, float(q.grad.abs().max()))
-        torch.testing.assert_close(p.grad.float().cpu(), q.grad.float(), msg=name, **t)
+    assert_loss_close(lo, lr, dtype)
+    if dtype == torch.float32:
+        assert_grads_scaled(ours, ref, dtype)
+    else:
+        twin = fp32_twin(ref, rng)
+        twin(ids, labels=labels).loss.backward()
+        assert_bf16_grads(ours, ref, twin)
     assert rng.forks > 0
 
 

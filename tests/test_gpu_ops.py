@@ -1,6 +1,8 @@
 """Kernel parity on the GPU: each HIP op against the CPU oracle on the same
-seeded inputs (fp32: rtol 1e-5; bf16: rtol 2e-2 / atol 1e-2), edge cases
-(ragged sizes, GQA, offsets, masks, ignored targets) and determinism."""
+seeded inputs (fp32: rtol 1e-5; bf16: rtol 2e-2 / atol 1e-2, the atol read
+relative to each tensor's largest magnitude and the relative L2 error held to
+rtol, tests/parity.py), edge cases (ragged sizes, GQA, offsets, masks, ignored
+targets) and determinism."""
 
 from __future__ import annotations
 
@@ -12,22 +14,15 @@ import torch
 import nano_megatron_amd as nm
 from nano_megatron_amd import functional as Fn
 from oracle import reference as R
+from parity import assert_close_scaled, assert_loss_close
 
 pytestmark = pytest.mark.gpu
 
-F32_TOL = dict(rtol=1e-5, atol=1e-5)
-BF16_TOL = dict(rtol=2e-2, atol=1e-2)
 
-
-def tol(dtype):
-    return F32_TOL if dtype == torch.float32 else BF16_TOL
-
-
-def close(got, exp, dtype, scale_atol=False, msg=""):
-    t = dict(tol(dtype))
-    if scale_atol:  # gradients: atol relative to the tensor's magnitude
-        t["atol"] = t["atol"] * max(1.0, float(exp.abs().max()))
-    torch.testing.assert_close(got.detach().float().cpu(), exp.detach().float(), msg=msg, **t)
+def close(got, exp, dtype, scale_atol=True, msg=""):
+    """The dtype's bar with atol scaled to max|exp| (for every tensor, outputs
+    and gradients alike; ``scale_atol`` is kept for the call sites)."""
+    assert_close_scaled(got, exp, dtype, msg=msg)
 
 
 def gen(seed):
@@ -345,13 +340,39 @@ def test_lm_head_cross_entropy_matches_oracle(device, rows, hidden, vocab, dtype
     xd, ed = x.to(device).requires_grad_(True), e.to(device).requires_grad_(True)
     ld = nm.lm_head_cross_entropy(xd, ed, t.to(device), chunk=chunk)
     ld.backward()
-    close(ld, lr, dtype)
-    close(xd.grad, xr.grad, dtype, scale_atol=True)
-    close(ed.grad, er.grad, dtype, scale_atol=True)
+    assert_loss_close(ld, lr, dtype)
+    close(xd.grad, xr.grad, dtype, msg="dx")
+    close(ed.grad, er.grad, dtype, msg="dE")
     per_tok = nm.lm_head_cross_entropy(xd.detach(), ed.detach(), t.to(device), reduction="none", chunk=chunk)
     assert torch.all(per_tok.cpu()[t == -100] == 0)
     with pytest.raises(ValueError, match="outside"):
         nm.lm_head_cross_entropy(xd.detach(), ed.detach(), torch.full_like(t, vocab).to(device))
+
+
+@pytest.mark.parametrize("reduction", ["sum", "mean"])
+def test_lm_head_cross_entropy_c2_bf16(device, reduction) -> None:
+    """Config 2's chunked cross entropy, [8192, 1024] x [1024, 8192] in bf16
+    (x ~ N(0, 1), E ~ N(0, 0.02), seed 1, uniform labels): with reduction
+    "sum" the logits' gradient is softmax - onehot per token, so dE is O(1)
+    and dX ~ 2e-2; the loss within rtol 1e-3 and dX, dE within the bf16 bar
+    scaled to each tensor, against the oracle's bf16 path (bf16 logits, fp32
+    softmax, the gradient cast to bf16: tensor_parallel/cross_entropy.py:
+    30-86, tests/unit/test_tensor_parallel_layers.py:139-166)."""
+    g = gen(1)
+    x = torch.randn(8192, 1024, generator=g).bfloat16()
+    e = (0.02 * torch.randn(8192, 1024, generator=g)).bfloat16()
+    t = torch.randint(0, 8192, (8192,), generator=g)
+    xr, er = x.clone().requires_grad_(True), e.clone().requires_grad_(True)
+    lr = R.cross_entropy_tokens(torch.nn.functional.linear(xr, er), t, reduction=reduction)
+    lr.backward()
+    xd, ed = x.to(device).requires_grad_(True), e.to(device).requires_grad_(True)
+    ld = nm.lm_head_cross_entropy(xd, ed, t.to(device), reduction=reduction)
+    ld.backward()
+    assert_loss_close(ld, lr, torch.bfloat16)
+    close(xd.grad, xr.grad, torch.bfloat16, msg="dx")
+    close(ed.grad, er.grad, torch.bfloat16, msg="dE")
+    if reduction == "sum":
+        assert float(er.grad.float().abs().max()) > 0.5  # O(1): a bar that a zeroed dE cannot pass
 
 
 # ---------------------------------------------------------------- GEMM
