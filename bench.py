@@ -375,17 +375,20 @@ def kernel_rooflines(device, only: str | None = None) -> list[dict]:
         ("embedding_bwd", mk_emb_bwd, T * H * E + 2 * V * H * E + T * 8, 1),
     ]
     cases = [(name, make, nbytes, 0, "hbm", per) for name, make, nbytes, per in hbm]
+    # attention at S 512 / D 64 sits below the ridge (127 FLOP/B forward, 159
+    # backward, against ~312 for 2.5 PFLOP/s over 8 TB/s), so its roofline is
+    # HBM: compulsory bytes over time; the FLOP rate is reported beside it
     cases += [
         ("attn_fwd", lambda: Fn.attn_fwd_bshd(q, [k], [v], (0,), causal=True, q_offset=0, scale=None, out=o,
                                               lse=lse),
-         4 * T * H * E + BATCH * nh * SEQ * 4, causal_flops, "mfma", 2 * L),
+         4 * T * H * E + BATCH * nh * SEQ * 4, causal_flops, "hbm", 2 * L),
         ("attn_fwd_from_lse", lambda: Fn.attn_fwd_from_lse_bshd(q, [k], [v], (0,), lse, causal=True, q_offset=0,
                                                                 scale=None, out=o),
-         4 * T * H * E + BATCH * nh * SEQ * 4, causal_flops, "mfma", 0),
+         4 * T * H * E + BATCH * nh * SEQ * 4, causal_flops, "hbm", 0),
         # the backward with the inverse RoPE of dq and dk in its stores, as the block runs it
         ("attn_bwd_rope", lambda: Fn.attn_bwd_rope_bshd(q, k, v, o, do, lse, dq, dk, dv, causal=True, q_offset=0,
                                                         scale=None, cos=tab.cos, sin=tab.sin),
-         8 * T * H * E + BATCH * nh * SEQ * 4, 2.5 * causal_flops, "mfma", L),
+         8 * T * H * E + BATCH * nh * SEQ * 4, 2.5 * causal_flops, "hbm", L),
     ] + gemms
     names = [c_[0] for c_ in cases] + ["adamw_step"]
     if only is not None and only not in names:
@@ -409,7 +412,7 @@ def kernel_rooflines(device, only: str | None = None) -> list[dict]:
             continue
         sets = 1
         fns = [fn]
-        if bound == "hbm":
+        if bound == "hbm" and not flops:
             sets = _input_sets(nbytes)
             fns = [fn() for _ in range(sets)]
         # launches captured in a HIP graph and replayed: the events then time GPU
@@ -559,12 +562,18 @@ def cpu_baseline(seconds: float = 25.0) -> dict:
     global-norm clip and AdamW (torch.optim.AdamW, the reference's fp32 mode,
     data_parallel/_common.py:242-252), timed with perf_counter after one
     warm-up step; the median of at least three steps, or as many as fit in
-    ``seconds``.  Reported with the threads used and the implied FLOP rate."""
+    ``seconds``.  Runs on every core the host reports
+    (``torch.set_num_threads(os.cpu_count())``); reports the core count, the
+    threads used, the cores this process may run on (affinity) and the
+    implied FLOP rate, and the batch in its own fields."""
     import torch
 
     from oracle import reference as R
 
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
     threads = torch.get_num_threads()
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else cores
 
     class Ck:
         mode = "full"
@@ -601,9 +610,16 @@ def cpu_baseline(seconds: float = 25.0) -> dict:
     return dict(
         value=round(SEQ / t_step, 1),
         unit="tokens/s",
-        cores=threads,
+        cores=cores,
+        threads=threads,
+        cores_usable=usable,
         kind="port",
-        sample=(f"CPU oracle (PyTorch fp32, {threads} threads on {_host_cpu_model()}): the full 24-layer "
+        dtype="f32",
+        batch=1,
+        seq_len=SEQ,
+        tokens_per_step=SEQ,
+        gpu_batch=BATCH,
+        sample=(f"CPU oracle (PyTorch fp32, {threads} threads on {cores} cores of {_host_cpu_model()}): the full 24-layer "
                 f"config-3 step (forward with per-layer recompute, backward, clip, AdamW) on one "
                 f"512-token sequence, median of {len(times)} steps after one warm-up: "
                 f"{t_step:.2f} s per step ({min(times):.2f}-{max(times):.2f} s), "
@@ -974,6 +990,11 @@ def main() -> None:
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline()
+    if kernels and ceilings:
+        # each HBM-bound kernel against what a plain device copy reaches on this box
+        for k_ in kernels:
+            if k_["bound"] == "hbm":
+                k_["copy_frac"] = round(k_["gbs"] / ceilings["copy_256mib_gbs"], 3)
     line = dict(
         metric=METRIC,
         value=round(full["tokens_per_s"], 1),

@@ -166,7 +166,9 @@ def dtype_code(dtype: torch.dtype) -> int:
         return NMB_BF16
     if dtype == torch.float32:
         return NMB_F32
-    raise ValueError(f"nano_megatron_amd kernels support float32 and bfloat16, got {dtype}")
+    raise ValueError(f"nano_megatron_amd kernels support float32 and bfloat16, got {dtype}; supported "
+                     "precisions: params=compute=float32, or params=compute=bfloat16 with the fp32-master "
+                     "optimizer")
 
 
 def stream_of(t: torch.Tensor) -> int:

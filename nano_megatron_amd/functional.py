@@ -35,6 +35,39 @@ def _require_gpu(*tensors: Tensor) -> None:
             )
 
 
+SUPPORTED_PRECISIONS = (
+    "params=float32 with compute=float32, or params=bfloat16 with compute=bfloat16 "
+    "(bf16 parameters and activations, the fp32-master optimizer; torch.autocast to bfloat16 "
+    "around it is accepted)"
+)
+
+
+def require_precision(*tensors: Tensor) -> None:
+    """The precision modes these kernels implement (config/schema.py:55-64,
+    training/trainer.py:49-57): every kernel computes in its inputs' dtype,
+    float32 or bfloat16.  Two reference modes are refused with a ValueError
+    instead of running something else silently: float16 (no kernels), and
+    float32 parameters under ``torch.autocast`` to a lower dtype (the
+    reference's params=float32/compute=bfloat16 mode, where autocast runs the
+    linears and attention in bf16 on an fp32 residual stream; these kernels
+    would run them in fp32)."""
+    for t in tensors:
+        if t is None:
+            continue
+        if t.dtype == torch.float16:
+            raise ValueError(f"precision float16 has no kernels in nano_megatron_amd; supported: "
+                             f"{SUPPORTED_PRECISIONS}")
+        device_type = t.device.type
+        if torch.is_autocast_enabled(device_type):
+            cast = torch.get_autocast_dtype(device_type)
+            if t.is_floating_point() and cast != t.dtype:
+                raise ValueError(
+                    f"torch.autocast({device_type}, dtype={cast}) around {t.dtype} tensors is the "
+                    f"reference's params={str(t.dtype).replace('torch.', '')}/compute="
+                    f"{str(cast).replace('torch.', '')} mode, which these kernels do not implement "
+                    f"(they compute in the tensors' own dtype); supported: {SUPPORTED_PRECISIONS}")
+
+
 def _workspace(nbytes: int, device: torch.device) -> Tensor:
     return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
 
@@ -221,6 +254,7 @@ class LinearFunction(torch.autograd.Function):
 def linear(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
     """``F.linear`` with the GEMM on this library's kernels (the bias, when a
     module has one, is added by a broadcast tensor add)."""
+    require_precision(x, weight)
     y = LinearFunction.apply(x, weight)
     return y if bias is None else y + bias
 
@@ -321,6 +355,7 @@ class RMSNormFunction(torch.autograd.Function):
 
 
 def rms_norm(x: Tensor, weight: Tensor, eps: float) -> Tensor:
+    require_precision(x, weight)
     return RMSNormFunction.apply(x, weight, eps)
 
 
@@ -605,11 +640,13 @@ class SwiGLUFunction(torch.autograd.Function):
 
 
 def swiglu(gate: Tensor, up: Tensor) -> Tensor:
+    require_precision(gate, up)
     return SwiGLUFunction.apply(gate, up)
 
 
 # ---------------------------------------------------------------- attention
 def _check_attn(q: Tensor, ks: Sequence[Tensor], vs: Sequence[Tensor]) -> tuple[int, ...]:
+    require_precision(q, *ks, *vs)
     if q.ndim != 4 or any(k.ndim != 4 for k in ks) or any(v.ndim != 4 for v in vs):
         raise ValueError("q, k and v must have [batch, heads, sequence, head_dim] shape")
     for k, v in zip(ks, vs):
@@ -939,6 +976,7 @@ def masked_attention(q: Tensor, k: Tensor, v: Tensor, attention_mask: Tensor | N
     [B,H,S,D] tensors; ``seed`` keys the dropout mask (default: dropout_seed())."""
     dropout_p = _check_dropout_p(dropout_p)
     _require_gpu(q, k, v, attention_mask)
+    require_precision(q, k, v)
     if causal and attention_mask is not None and attention_mask.dtype != torch.bool:
         # the reference combines the masks with `mask & causal_mask` (torch_backend.py:66)
         raise ValueError("a causal attention_mask must be boolean (it is ANDed with the causal mask)")
@@ -1217,6 +1255,7 @@ def lm_head_cross_entropy(
     (tensor_parallel/cross_entropy.py:89-123) without materialising logits."""
     if reduction not in ("none", "mean", "sum"):
         raise ValueError(f"unsupported reduction: {reduction}")
+    require_precision(hidden, weight)
     if hidden.shape[:-1] != targets.shape:
         raise ValueError(
             "targets must match all non-vocabulary logits dimensions: "

@@ -612,6 +612,7 @@ class GPTModel(nn.Module):
         elif hidden_states is None:
             raise ValueError("a non-first pipeline stage requires hidden_states")
         Fn._require_gpu(hidden_states)
+        Fn.require_precision(hidden_states)
         sequence = hidden_states.shape[1]
         # positions and the causal offset once per forward (models/gpt/model.py:193-200)
         plan = position_plan(hidden_states.device, sequence, position_ids, 0)

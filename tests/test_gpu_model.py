@@ -517,3 +517,39 @@ def test_activation_checkpoint_module_wrapper(device) -> None:
     assert torch.equal(outs[0], outs[1])
     for a, b in zip(*grads):
         assert torch.equal(a, b)
+
+
+def test_precision_modes_run_or_raise(device) -> None:
+    """The reference's precision modes (config/schema.py:55-64,
+    training/trainer.py:49-57): bf16 parameters under torch.autocast to
+    bfloat16 (the configurations' mode, as the reference's trainer wraps it)
+    run and equal the same step without autocast bit for bit; float32
+    parameters under autocast to bfloat16 (params=float32/compute=bfloat16)
+    and float16 parameters raise a ValueError naming the mode, at the model,
+    at the kernel seam's modules and at the functional entry points."""
+    cfg = c1_config(layers=2, kv_heads=2)
+    ids, labels = c1_batch()
+    ids, labels = ids.to(device), labels.to(device)
+    torch.manual_seed(0)
+    model = nm.GPTModel(cfg).to(device=device, dtype=torch.bfloat16).train()
+    plain = model(ids, labels=labels).loss
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        cast = model(ids, labels=labels).loss
+    assert torch.equal(plain, cast)
+    model32 = nm.GPTModel(cfg).to(device=device).train()
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        with pytest.raises(ValueError, match="params=float32/compute=bfloat16"):
+            model32(ids, labels=labels)
+        lin = nm.HipKernelBackend().linear(256, 64, bias=False, device=device)
+        with pytest.raises(ValueError, match="params=float32/compute=bfloat16"):
+            lin(torch.randn(8, 256, device=device))
+        q = torch.randn(1, 4, 64, 64, device=device)
+        with pytest.raises(ValueError, match="params=float32/compute=bfloat16"):
+            nm.HipKernelBackend().local_attention(q, q, q)
+        with pytest.raises(ValueError, match="params=float32/compute=bfloat16"):
+            nm.rms_norm(q, torch.ones(64, device=device), 1e-5)
+    model16 = nm.GPTModel(cfg).to(device=device, dtype=torch.float16).train()
+    with pytest.raises(ValueError, match="float16 .*supported"):
+        model16(ids, labels=labels)
+    with pytest.raises(ValueError, match="float16 .*supported"):
+        nm.attention(q.half(), q.half(), q.half())
