@@ -954,10 +954,14 @@ def main() -> None:
         return
     full = run_steps("full", args.steps, args.warmup, device, args.metrics_jsonl, graph=not args.host_launch)
     print("full: " + json.dumps(full), file=sys.stderr, flush=True)
-    eager = None
+    eager = selective = None
     if not args.no_eager:
         eager = run_steps("none", args.steps, args.warmup, device, graph=not args.host_launch)
         print("none: " + json.dumps(eager), file=sys.stderr, flush=True)
+        # activation_checkpoint.mode "selective" (attention and MLP sub-blocks
+        # checkpointed on their inputs, models/gpt/layer.py:68-89) on the fused block
+        selective = run_steps("selective", args.steps, args.warmup, device, graph=not args.host_launch)
+        print("selective: " + json.dumps(selective), file=sys.stderr, flush=True)
 
     c4 = c5 = None
     if not args.no_legs:
@@ -1039,6 +1043,16 @@ def main() -> None:
         line["no_checkpoint_tokens_per_s"] = round(eager["tokens_per_s"], 1)
         line["no_checkpoint_saved_act_mib_per_layer"] = round(block_saved_mib("none", device), 2)
         line["recompute_overhead"] = round(full["ms_per_step"] / eager["ms_per_step"] - 1.0, 4)
+    if selective:
+        line["selective"] = dict(
+            selective_ops=["attention", "mlp"],
+            tokens_per_s=round(selective["tokens_per_s"], 1),
+            ms_per_step=round(selective["ms_per_step"], 3),
+            host_launched_tokens_per_s=round(selective["eager_tokens_per_s"], 1),
+            recompute_overhead=round(selective["ms_per_step"] / eager["ms_per_step"] - 1.0, 4),
+            saved_act_mib_per_layer=round(block_saved_mib("selective", device), 2),
+            peak_act_gib_per_layer=round(selective["peak_act_gib_per_layer"], 4),
+        )
     print(json.dumps(line), flush=True)
 
 

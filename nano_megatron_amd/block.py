@@ -25,7 +25,9 @@ gradient.  With ``offload`` the saved input goes to
 pinned host memory (the reference's saved-tensor offload,
 nn/activation_checkpoint.py:24-41); the weights are parameters, never copied.
 ``EagerBlockFunction`` (activation_checkpoint.mode = "none") keeps the
-intermediates instead and shares the backward.
+intermediates instead and shares the backward; ``SelectiveBlockFunction``
+("selective") keeps the sub-block inputs and recomputes only the checkpointed
+sub-blocks' products.
 """
 
 from __future__ import annotations
@@ -105,6 +107,25 @@ def _qkv_views(qkv: Tensor, b: int, s: int, m: BlockMeta) -> tuple[Tensor, Tenso
     return q, k, v
 
 
+def _attention_part(n1: Tensor, w: tuple[Tensor, ...], m: BlockMeta, b: int, s: int) -> tuple:
+    """[q|k|v] (RoPE applied), the attention output o [B*S, Hq*D] and its lse
+    from the normalised block input n1."""
+    _, wq, wk, wv = w[:4]
+    # Q/K/V projection with RoPE of q and k as the GEMM epilogue
+    qkv = Fn.mm_rope(n1, joined((wq, wk, wv)).t(), seq=s, head_dim=m.head_dim,
+                     rope_cols=(m.heads + m.kv_heads) * m.head_dim, cos=m.cos, sin=m.sin,
+                     pos_offset=m.pos_offset, positions=m.positions)
+    q, k, v = _qkv_views(qkv, b, s, m)
+    o, lse = Fn.attn_fwd_bshd(q, [k], [v], (0,), causal=True, q_offset=m.sequence_offset, scale=None)
+    return qkv, o.view(b * s, m.heads * m.head_dim), lse
+
+
+def _gate_up_part(n2: Tensor, w: tuple[Tensor, ...], *, act: bool, gu: bool) -> tuple:
+    """(s, [g|u]) of the MLP's gate/up product; one GEMM plan whether or not
+    the activation is applied in the epilogue, so [g|u] has the same bits."""
+    return Fn.mm_gate_up(n2, joined((w[6], w[7])), act=act, gu=gu)
+
+
 def block_forward(x: Tensor, w: tuple[Tensor, ...], m: BlockMeta, *, recompute: bool,
                   keep_gu: bool = True) -> dict:
     """Run the block on x [B,S,H].  With recompute=True stop after [g|u] (no s, no y).
@@ -114,18 +135,10 @@ def block_forward(x: Tensor, w: tuple[Tensor, ...], m: BlockMeta, *, recompute: 
     b, s, hdim = x.shape
     x2 = x.reshape(b * s, hdim)
     n1 = Fn.rmsnorm_fwd(x2, w_in, m.eps)
-    # Q/K/V projection with RoPE of q and k as the GEMM epilogue
-    qkv = Fn.mm_rope(n1, joined((wq, wk, wv)).t(), seq=s, head_dim=m.head_dim,
-                     rope_cols=(m.heads + m.kv_heads) * m.head_dim, cos=m.cos, sin=m.sin,
-                     pos_offset=m.pos_offset, positions=m.positions)
-    q, k, v = _qkv_views(qkv, b, s, m)
-    o, lse = Fn.attn_fwd_bshd(q, [k], [v], (0,), causal=True, q_offset=m.sequence_offset, scale=None)
-    o2 = o.view(b * s, m.heads * m.head_dim)
+    qkv, o2, lse = _attention_part(n1, w, m, b, s)
     h = Fn.mm(o2, wo.t(), c=x2, beta=1.0)
     n2 = Fn.rmsnorm_fwd(h, w_post, m.eps)
-    # one gate/up GEMM plan for the forward and the recompute: the same [g|u]
-    # bits whether or not the activation is applied in the epilogue
-    act, gu = Fn.mm_gate_up(n2, joined((wg, wu)), act=not recompute, gu=recompute or keep_gu)
+    act, gu = _gate_up_part(n2, w, act=not recompute, gu=recompute or keep_gu)
     acts = dict(x2=x2, n1=n1, qkv=qkv, o2=o2, lse=lse, h=h, n2=n2)
     if gu is not None:
         acts["gu"] = gu
@@ -265,6 +278,71 @@ class CheckpointedBlockFunction(torch.autograd.Function):
             acts = block_forward(x, tuple(weights), ctx.meta, recompute=True)
             grads = block_backward(acts, dy, tuple(weights), ctx.meta, ctx.shape)
         return (grads[0], None, None, *grads[1:])
+
+
+class SelectiveBlockFunction(torch.autograd.Function):
+    """Selective recompute (activation_checkpoint.mode = "selective",
+    models/gpt/layer.py:68-89): the sub-blocks named in ``ops`` ("attention":
+    the Q/K/V projection, RoPE, attention and out projection; "mlp": gate/up,
+    SwiGLU and down projection) are checkpointed on their inputs, as the
+    reference's per-sub-block ``activation_checkpoint`` does.  Saved: the block
+    input x and the residual midpoint h (the norms' inputs, outside the
+    checkpoints), n1 and n2 (the checkpointed sub-blocks' inputs), and the
+    intermediates of a sub-block that is not checkpointed.  The backward
+    recomputes a checkpointed attention's [q|k|v], o and lse from n1 and a
+    checkpointed MLP's [g|u] from n2 with the forward's kernels (same bits),
+    never the norms, the out projection or the down projection, whose outputs
+    it does not read, then runs the shared block backward.  With ``offload``
+    the checkpointed sub-blocks' inputs wait in pinned host memory."""
+
+    @staticmethod
+    def forward(ctx: Any, x: Tensor, meta: BlockMeta, ops: tuple[str, ...], offload: bool,
+                *weights: Tensor) -> Tensor:
+        x = x.contiguous()
+        attn_ck, mlp_ck = "attention" in ops, "mlp" in ops
+        with torch.no_grad():
+            acts = block_forward(x, weights, meta, recompute=False, keep_gu=not mlp_ck)
+        ctx.meta = meta
+        ctx.shape = tuple(x.shape)
+        ctx.ops = (attn_ck, mlp_ck)
+        keep = ["h"] + ([] if attn_ck else ["n1", "qkv", "o2", "lse"]) + ([] if mlp_ck else ["n2", "gu"])
+        ck = ([acts["n1"]] if attn_ck else []) + ([acts["n2"]] if mlp_ck else [])
+        ctx.keys = keep
+        ctx.offloaded = None
+        if offload and ck:
+            # enqueued after the block's kernels on the same stream, which read them first
+            host = [torch.empty(t.shape, dtype=t.dtype, pin_memory=True) for t in ck]
+            for hst, t in zip(host, ck):
+                hst.copy_(t, non_blocking=True)
+            ctx.offloaded = (host, x.device)
+            ck = []
+        ctx.n_ck = len(ck)
+        ctx.save_for_backward(x, *(acts[k] for k in keep), *ck, *weights)
+        return acts["y"]
+
+    @staticmethod
+    def backward(ctx: Any, dy: Tensor):
+        saved = ctx.saved_tensors
+        x, weights = saved[0], tuple(saved[1 + len(ctx.keys) + ctx.n_ck:])
+        acts = dict(zip(ctx.keys, saved[1:1 + len(ctx.keys)]))
+        ck = list(saved[1 + len(ctx.keys):1 + len(ctx.keys) + ctx.n_ck])
+        if ctx.offloaded is not None:
+            host, device = ctx.offloaded
+            ck = [t.to(device, non_blocking=True) for t in host]
+            ctx.offloaded = None
+        attn_ck, mlp_ck = ctx.ops
+        b, s, hdim = ctx.shape
+        m = ctx.meta
+        acts["x2"] = x.reshape(b * s, hdim)
+        with torch.no_grad():
+            if attn_ck:
+                acts["n1"] = ck.pop(0)
+                acts["qkv"], acts["o2"], acts["lse"] = _attention_part(acts["n1"], weights, m, b, s)
+            if mlp_ck:
+                acts["n2"] = ck.pop(0)
+                _, acts["gu"] = _gate_up_part(acts["n2"], weights, act=False, gu=True)
+            grads = block_backward(acts, dy, weights, m, ctx.shape)
+        return (grads[0], None, None, None, *grads[1:])
 
 
 class EagerBlockFunction(torch.autograd.Function):

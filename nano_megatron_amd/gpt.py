@@ -17,9 +17,11 @@ standard layer as one fused block Function:
   inside backward);
 * otherwise -> ``EagerBlockFunction`` (same kernels, intermediates kept).
 
-``"selective"`` runs the layer module by module with the chosen sub-blocks
-under non-reentrant ``torch.utils.checkpoint``, as the reference does
-(models/gpt/layer.py:68-89).  With ``labels`` the loss comes from the chunked
+``"selective"`` (training) -> ``SelectiveBlockFunction``: the chosen
+sub-blocks checkpointed on their inputs, as the reference's per-sub-block
+checkpoints (models/gpt/layer.py:68-89) keep them; a layer the fused block
+does not cover runs module by module with those sub-blocks under
+non-reentrant ``torch.utils.checkpoint``, as the reference does.  With ``labels`` the loss comes from the chunked
 LM-head cross entropy and ``GPTOutput.logits`` is None (full logits are never
 built); without labels the logits are returned.
 """
@@ -39,6 +41,7 @@ from nano_megatron_amd.block import (
     BlockMeta,
     CheckpointedBlockFunction,
     EagerBlockFunction,
+    SelectiveBlockFunction,
     pack_adjacent,
 )
 from nano_megatron_amd.kernels import HipKernelBackend, KernelBackend
@@ -600,6 +603,8 @@ class GPTModel(nn.Module):
                 check = False
             else:
                 check = Fn.TargetCheck(labels, self.lm_head.weight.shape[0], Fn.IGNORE_INDEX)
+        if self.embedding is not None:
+            Fn.require_precision(self.embedding.weight)
         # the tied LM head passes its table gradient to the embedding's backward
         tie = None
         if (labels is not None and self.embedding is not None and self.lm_head is not None
@@ -631,7 +636,7 @@ class GPTModel(nn.Module):
         mode = getattr(self.activation_checkpoint_config, "mode", "none")
         offload = bool(getattr(self.activation_checkpoint_config, "offload_saved_tensors", False))
         for layer in self.layers:
-            if mode != "selective" and layer.fusable():
+            if layer.fusable():
                 weights = layer.block_weights()
                 if any(w.dtype != hidden_states.dtype for w in weights):
                     raise ValueError(
@@ -639,7 +644,10 @@ class GPTModel(nn.Module):
                         f"{weights[1].dtype} vs activations {hidden_states.dtype}"
                     )
                 meta = layer.block_meta(hidden_states.device, plan, offset)
-                if self._checkpoint_layer(layer):
+                if mode == "selective" and self.training:
+                    ops = tuple(getattr(self.activation_checkpoint_config, "selective_ops", ("attention", "mlp")))
+                    hidden_states = SelectiveBlockFunction.apply(hidden_states, meta, ops, offload, *weights)
+                elif self._checkpoint_layer(layer):
                     hidden_states = CheckpointedBlockFunction.apply(hidden_states, meta, offload, *weights)
                 else:
                     hidden_states = EagerBlockFunction.apply(hidden_states, meta, *weights)

@@ -18,7 +18,8 @@ What changes per replay and what does not:
   update, as in the eager forward, tensor_parallel/cross_entropy.py:109-114):
   made before each replay, since a host wait cannot be captured.
 The activation checkpoint options must not move tensors to the host
-(``offload_saved_tensors``), explicit ``position_ids`` (read on the host) are
+(``offload_saved_tensors``) nor recompute under ``torch.utils.checkpoint``
+(a layer outside the fused block in mode "full" or "selective"), explicit ``position_ids`` (read on the host) are
 not accepted, and neither is dropout > 0 (its masks are keyed by seeds passed
 at launch, which every replay would repeat); all raise ``ValueError``.  No reference to an earlier step's
 autograd graph (an undetached loss) may be alive when the step is captured:
@@ -50,6 +51,12 @@ class CapturedTrainStep:
                              "replay cannot reuse: capture without it")
         if getattr(model, "lm_head", None) is None:
             raise ValueError("CapturedTrainStep needs the stage that owns the LM head (the loss)")
+        mode = getattr(ckpt, "mode", "none")
+        if mode in ("full", "selective") and any(not layer.fusable() for layer in getattr(model, "layers", ())):
+            raise ValueError("a layer outside the fused block (biases, other head sizes or components) "
+                             "recomputes under torch.utils.checkpoint, whose RNG-state replay cannot be "
+                             f"captured: capture with activation_checkpoint.mode 'none' or fused layers only "
+                             f"(mode {mode!r})")
         rates = (getattr(m, "dropout", 0.0) for m in model.modules())
         if any(isinstance(r, (int, float)) and not isinstance(r, bool) and r > 0.0 for r in rates):
             raise ValueError("dropout masks are keyed by seeds passed from the host at launch, which "

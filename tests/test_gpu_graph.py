@@ -39,7 +39,7 @@ def optimizer(model):
                        clip_grad_norm=1.0)
 
 
-@pytest.mark.parametrize("mode", ["full", "none"])
+@pytest.mark.parametrize("mode", ["full", "none", "selective"])
 def test_captured_step_replays_match_eager_steps(device, mode) -> None:
     data = batches(device, 4)
     eager = small_model(device, mode)
@@ -97,6 +97,15 @@ def test_captured_step_refuses_offload_and_shape_changes(device) -> None:
     model = small_model(device, "full", offload=True)
     with pytest.raises(ValueError, match="offload_saved_tensors"):
         CapturedTrainStep(model, optimizer(model), x, y)
+    # a layer outside the fused block (biases) recomputes under torch's checkpoint
+    cfg = nm.GPTConfig(layers=1, hidden_size=256, ffn_hidden_size=688, heads=4, seq_length=128,
+                       vocab_size=VOCAB, bias=True)
+    for mode in ("full", "selective"):
+        torch.manual_seed(0)
+        biased = nm.GPTModel(cfg, activation_checkpoint_config=nm.ActivationCheckpointConfig(mode=mode))
+        biased = biased.to(device=device, dtype=torch.bfloat16).train()
+        with pytest.raises(ValueError, match="torch.utils.checkpoint"):
+            CapturedTrainStep(biased, optimizer(biased), x, y)
     model = small_model(device, "full")
     cap = CapturedTrainStep(model, optimizer(model), x, y)
     with pytest.raises(ValueError, match="shape"):

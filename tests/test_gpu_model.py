@@ -233,6 +233,50 @@ def test_full_recompute_keeps_only_block_input(device) -> None:
     assert none > 8 * x_bytes, none
 
 
+@pytest.mark.parametrize("ops", [("attention", "mlp"), ("attention",), ("mlp",)])
+def test_fused_selective_recompute_bit_identical_to_eager(device, ops) -> None:
+    """Selective checkpointing on the fused block (models/gpt/layer.py:68-89):
+    the chosen sub-blocks recomputed from their saved inputs with the
+    forward's kernels, so the loss and every gradient equal the eager (no
+    checkpoint) run's and the full-recompute run's bit for bit; offloading the
+    sub-block inputs changes nothing either."""
+    cfg = c1_config(layers=2, kv_heads=2)
+    ids, labels = c1_batch()
+    results = []
+    for ck in (nm.ActivationCheckpointConfig(mode="none"), nm.ActivationCheckpointConfig(mode="full"),
+               nm.ActivationCheckpointConfig(mode="selective", selective_ops=ops),
+               nm.ActivationCheckpointConfig(mode="selective", selective_ops=ops, offload_saved_tensors=True)):
+        torch.manual_seed(0)
+        model = nm.GPTModel(cfg, activation_checkpoint_config=ck).to(device=device, dtype=torch.bfloat16).train()
+        assert all(layer.fusable() for layer in model.layers)
+        loss = model(ids.to(device), labels=labels.to(device)).loss
+        loss.backward()
+        results.append((loss.detach(), [p.grad.clone() for p in model.parameters()]))
+    for loss, grads in results[1:]:
+        assert torch.equal(loss, results[0][0])
+        for a, b in zip(grads, results[0][1]):
+            assert torch.equal(a, b)
+
+
+def test_fused_selective_keeps_the_sub_block_inputs(device) -> None:
+    """Selective recompute of both sub-blocks keeps what the reference's
+    checkpoint boundaries keep: the block input, the residual midpoint and the
+    two checkpointed sub-blocks' inputs (4 x the input's bytes); with
+    offload_saved_tensors the sub-block inputs wait in host memory (2 x);
+    checkpointing only the MLP keeps the attention's intermediates too."""
+    cfg = dict(hidden_size=512, ffn_hidden_size=1376, heads=8, seq_length=256, vocab_size=4096)
+    ids = torch.randint(0, 4096, (4, 256), device=device)
+    x_bytes = 4 * 256 * 512 * 2
+    sel = _block_saved_bytes(device, cfg, ids, nm.ActivationCheckpointConfig(mode="selective"))
+    off = _block_saved_bytes(device, cfg, ids, nm.ActivationCheckpointConfig(mode="selective",
+                                                                              offload_saved_tensors=True))
+    mlp = _block_saved_bytes(device, cfg, ids, nm.ActivationCheckpointConfig(mode="selective",
+                                                                              selective_ops=("mlp",)))
+    assert sel == 4 * x_bytes, sel
+    assert off == 2 * x_bytes, off
+    assert mlp > 6 * x_bytes, mlp
+
+
 def test_offload_and_block_interval_match_oracle_and_full_recompute(device) -> None:
     """offload_saved_tensors=True and block_interval=2 (layers 0 and 2
     checkpointed, 1 and 3 eager; models/gpt/model.py:162-170) give the loss and
@@ -549,7 +593,7 @@ def test_precision_modes_run_or_raise(device) -> None:
         with pytest.raises(ValueError, match="params=float32/compute=bfloat16"):
             nm.rms_norm(q, torch.ones(64, device=device), 1e-5)
     model16 = nm.GPTModel(cfg).to(device=device, dtype=torch.float16).train()
-    with pytest.raises(ValueError, match="float16 .*supported"):
+    with pytest.raises(ValueError, match="float16.*supported"):
         model16(ids, labels=labels)
-    with pytest.raises(ValueError, match="float16 .*supported"):
+    with pytest.raises(ValueError, match="float16.*supported"):
         nm.attention(q.half(), q.half(), q.half())
