@@ -64,6 +64,17 @@ int nmb_rmsnorm_bwd(const void* x, const void* w, const void* dy, const void* re
                     void* dx, void* dw, void* workspace, size_t workspace_bytes, int64_t rows,
                     int64_t cols, float eps, int dtype, hipStream_t stream);
 
+/* nmb_rmsnorm_bwd in its two launches, for a caller that runs the weight
+ * gradient's column sum on another stream (ordered after the first by the
+ * caller): nmb_rmsnorm_bwd_rows writes dx and the per-workgroup dw partials
+ * into the workspace; nmb_rmsnorm_bwd_dw sums them into dw in a fixed order
+ * (the same bits as nmb_rmsnorm_bwd).  Same reference function. */
+int nmb_rmsnorm_bwd_rows(const void* x, const void* w, const void* dy, const void* residual_grad,
+                         void* dx, void* workspace, size_t workspace_bytes, int64_t rows,
+                         int64_t cols, float eps, int dtype, hipStream_t stream);
+int nmb_rmsnorm_bwd_dw(const void* workspace, size_t workspace_bytes, int64_t rows, int64_t cols,
+                       void* dw, int dtype, hipStream_t stream);
+
 /* ------------------------------------------------------------ RoPE
  * replaces RotaryEmbedding.forward + apply_rotary_pos_emb
  * (nn/rotary.py:27-38, 55-70) as called at models/gpt/attention.py:180-181.

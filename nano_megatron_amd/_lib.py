@@ -44,6 +44,8 @@ SIGNATURES: dict[str, list] = {
     "nmb_rmsnorm_fwd": [_p, _p, _p, _p, _i64, _i64, _f32, _i32, _p],
     "nmb_rmsnorm_bwd_workspace_bytes": [_i64, _i64, _psz],
     "nmb_rmsnorm_bwd": [_p, _p, _p, _p, _p, _p, _p, _sz, _i64, _i64, _f32, _i32, _p],
+    "nmb_rmsnorm_bwd_rows": [_p, _p, _p, _p, _p, _p, _sz, _i64, _i64, _f32, _i32, _p],
+    "nmb_rmsnorm_bwd_dw": [_p, _sz, _i64, _i64, _p, _i32, _p],
     "nmb_rope_table": [_p, _p, _p, _i64, _i64, _p],
     "nmb_rope_apply": [
         _p, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _pi64, _pi64, _i32, _i32, _p,

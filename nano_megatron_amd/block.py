@@ -188,6 +188,12 @@ class _SideProducts:
         self.used = True
         return out
 
+    def stream(self) -> torch.cuda.Stream:
+        """The side stream for work the caller enqueues there itself (joined
+        like the products)."""
+        self.used = True
+        return self.side
+
     def join(self) -> None:
         if self.used:
             self.main.wait_stream(self.side)
@@ -210,7 +216,8 @@ def block_backward(acts: dict, dy: Tensor, w: tuple[Tensor, ...], m: BlockMeta, 
     dwd = side.mm(dy2.t(), act)
     dn2 = Fn.mm(dgu, joined((wg, wu)))
     dwgu = side.mm(dgu.t(), n2)
-    dh, dw_post = Fn.rmsnorm_bwd(h, w_post, dn2, m.eps, residual_grad=dy2)
+    # the weight gradient's column sum beside the next products (second stream)
+    dh, dw_post = Fn.rmsnorm_bwd(h, w_post, dn2, m.eps, residual_grad=dy2, dw_stream=side.stream())
 
     # attention: h = x + o Wo^T
     do2 = Fn.mm(dh, wo)

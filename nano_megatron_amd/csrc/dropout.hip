@@ -9,6 +9,8 @@
 // flattened element index, so no mask is stored between forward, recompute
 // and backward.  Pure HBM streaming: one 16-byte vector per lane, a SplitMix64
 // evaluation per two elements.
+#include <algorithm>
+
 #include "common.h"
 #include "dropout_math.h"
 #include "vec.h"
@@ -23,34 +25,39 @@ __device__ __forceinline__ float dropout_elem(float x, float r, uint32_t bits, c
   return r + y;
 }
 
-// thread t < nvec handles vector t (V elements); thread nvec + e handles the
-// scalar tail element nvec * V + e.  out may alias x or res (each thread reads
-// its elements before it writes them), so the pointers are not restrict.
+// item t < nvec is vector t (V elements); item nvec + e is the scalar tail
+// element nvec * V + e.  Items are walked grid-stride (the grid is capped at
+// kMaxBlocks, so any n up to the entry point's limit launches).  out may alias
+// x or res (each item reads its elements before it writes them), so the
+// pointers are not restrict.
+constexpr int64_t kMaxBlocks = 65536;
+
 template <typename T>
 __global__ __launch_bounds__(256) void dropout_add_kernel(const T* x, const T* res, T* out, int64_t nvec,
                                                           int64_t n, DropoutParams d) {
   constexpr int V = VecTraits<T>::N;
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (t < nvec) {
-    float xv[V], rv[V], ov[V];
-    load_vec<T>(x + t * V, xv);
-    if (res != nullptr) {
-      load_vec<T>(res + t * V, rv);
+  const int64_t items = nvec + (n - nvec * V);
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; t < items;
+       t += static_cast<int64_t>(gridDim.x) * 256) {
+    if (t < nvec) {
+      float xv[V], rv[V], ov[V];
+      load_vec<T>(x + t * V, xv);
+      if (res != nullptr) {
+        load_vec<T>(res + t * V, rv);
+      } else {
+#pragma unroll
+        for (int e = 0; e < V; ++e) rv[e] = 0.f;
+      }
+      const uint64_t base = static_cast<uint64_t>(t) * V;  // even: element pairs share one draw
+#pragma unroll
+      for (int e = 0; e < V; e += 2) {
+        const uint64_t z = splitmix64(d.seed, (base + e) >> 1);
+        ov[e] = dropout_elem<T>(xv[e], rv[e], static_cast<uint32_t>(z), d);
+        ov[e + 1] = dropout_elem<T>(xv[e + 1], rv[e + 1], static_cast<uint32_t>(z >> 32), d);
+      }
+      store_vec<T>(out + t * V, ov);
     } else {
-#pragma unroll
-      for (int e = 0; e < V; ++e) rv[e] = 0.f;
-    }
-    const uint64_t base = static_cast<uint64_t>(t) * V;  // even: element pairs share one draw
-#pragma unroll
-    for (int e = 0; e < V; e += 2) {
-      const uint64_t z = splitmix64(d.seed, (base + e) >> 1);
-      ov[e] = dropout_elem<T>(xv[e], rv[e], static_cast<uint32_t>(z), d);
-      ov[e + 1] = dropout_elem<T>(xv[e + 1], rv[e + 1], static_cast<uint32_t>(z >> 32), d);
-    }
-    store_vec<T>(out + t * V, ov);
-  } else {
-    const int64_t i = nvec * V + (t - nvec);
-    if (i < n) {
+      const int64_t i = nvec * V + (t - nvec);
       const float r = res != nullptr ? to_f32(res[i]) : 0.f;
       out[i] = from_f32<T>(dropout_elem<T>(to_f32(x[i]), r, keep_bits(d.seed, static_cast<uint64_t>(i)), d));
     }
@@ -64,7 +71,7 @@ void launch(const void* x, const void* res, void* out, int64_t n, const DropoutP
   const bool vec = aligned16(x) && aligned16(out) && (res == nullptr || aligned16(res));
   const int64_t nvec = vec ? n / V : 0;
   const int64_t threads = nvec + (n - nvec * V);
-  const int64_t blocks = (threads + 255) / 256;
+  const int64_t blocks = std::min<int64_t>((threads + 255) / 256, kMaxBlocks);
   hipLaunchKernelGGL((dropout_add_kernel<T>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
                      static_cast<const T*>(x), static_cast<const T*>(res), static_cast<T*>(out), nvec, n, d);
 }

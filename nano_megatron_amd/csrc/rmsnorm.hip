@@ -374,12 +374,11 @@ int fwd_impl(const void* x, const void* w, void* y, float* rstd, int64_t rows, i
 }
 
 template <typename T>
-int bwd_impl(const void* x, const void* w, const void* dy, const void* dres, void* dx, void* dw,
-             void* ws, size_t ws_bytes, int64_t rows, int64_t cols, float eps,
-             hipStream_t stream) {
+int bwd_rows_impl(const void* x, const void* w, const void* dy, const void* dres, void* dx, void* ws,
+                  size_t ws_bytes, int64_t rows, int64_t cols, float eps, hipStream_t stream) {
   int st = check_common<T>(x, w, rows, cols);
   if (st != NMB_OK) return st;
-  NMB_REQUIRE(dy != nullptr && dx != nullptr && dw != nullptr, "rmsnorm_bwd: null tensor");
+  NMB_REQUIRE(dy != nullptr && dx != nullptr, "rmsnorm_bwd: null tensor");
   NMB_REQUIRE(aligned16(x) && aligned16(w) && aligned16(dy) && aligned16(dx) &&
                   (dres == nullptr || aligned16(dres)),
               "rmsnorm_bwd: tensors must be 16-byte aligned");
@@ -418,10 +417,33 @@ int bwd_impl(const void* x, const void* w, const void* dy, const void* dres, voi
 #undef NMB_LAUNCH
   }
   NMB_CHECK_LAUNCH("rmsnorm_bwd");
-  hipLaunchKernelGGL((column_sum_kernel<T>), dim3((c + 15) / 16), dim3(256), 0, stream, part,
-                     nblocks, c, static_cast<T*>(dw));
+  return NMB_OK;
+}
+
+template <typename T>
+int bwd_dw_impl(const void* ws, size_t ws_bytes, int64_t rows, int64_t cols, void* dw, hipStream_t stream) {
+  NMB_REQUIRE(dw != nullptr && rows >= 0 && cols > 0, "rmsnorm_bwd_dw: bad arguments");
+  int nblocks;
+  int64_t rpb;
+  bwd_grid(rows, &nblocks, &rpb);
+  const size_t need = static_cast<size_t>(nblocks) * static_cast<size_t>(cols) * sizeof(float);
+  NMB_REQUIRE(ws != nullptr && ws_bytes >= need,
+              "rmsnorm_bwd_dw: workspace of %zu bytes is smaller than the %zu required", ws_bytes, need);
+  const int c = static_cast<int>(cols);
+  hipLaunchKernelGGL((column_sum_kernel<T>), dim3((c + 15) / 16), dim3(256), 0, stream,
+                     static_cast<const float*>(ws), nblocks, c, static_cast<T*>(dw));
   NMB_CHECK_LAUNCH("rmsnorm_bwd(dw)");
   return NMB_OK;
+}
+
+template <typename T>
+int bwd_impl(const void* x, const void* w, const void* dy, const void* dres, void* dx, void* dw,
+             void* ws, size_t ws_bytes, int64_t rows, int64_t cols, float eps,
+             hipStream_t stream) {
+  NMB_REQUIRE(dw != nullptr, "rmsnorm_bwd: null tensor");
+  const int st = bwd_rows_impl<T>(x, w, dy, dres, dx, ws, ws_bytes, rows, cols, eps, stream);
+  if (st != NMB_OK) return st;
+  return bwd_dw_impl<T>(ws, ws_bytes, rows, cols, dw, stream);
 }
 
 }  // namespace
@@ -456,4 +478,25 @@ extern "C" int nmb_rmsnorm_bwd(const void* x, const void* w, const void* dy,
     return nmb::bwd_impl<float>(x, w, dy, residual_grad, dx, dw, workspace, workspace_bytes,
                                 rows, cols, eps, stream);
   NMB_REQUIRE_SUPPORTED(false, "rmsnorm_bwd: unsupported dtype code %d", dtype);
+}
+
+extern "C" int nmb_rmsnorm_bwd_rows(const void* x, const void* w, const void* dy,
+                                    const void* residual_grad, void* dx, void* workspace,
+                                    size_t workspace_bytes, int64_t rows, int64_t cols, float eps,
+                                    int dtype, hipStream_t stream) {
+  NMB_REQUIRE(eps > 0.f, "rmsnorm_bwd: eps must be positive, got %g", (double)eps);
+  if (dtype == NMB_BF16)
+    return nmb::bwd_rows_impl<nmb::bf16>(x, w, dy, residual_grad, dx, workspace, workspace_bytes, rows,
+                                         cols, eps, stream);
+  if (dtype == NMB_F32)
+    return nmb::bwd_rows_impl<float>(x, w, dy, residual_grad, dx, workspace, workspace_bytes, rows, cols,
+                                     eps, stream);
+  NMB_REQUIRE_SUPPORTED(false, "rmsnorm_bwd: unsupported dtype code %d", dtype);
+}
+
+extern "C" int nmb_rmsnorm_bwd_dw(const void* workspace, size_t workspace_bytes, int64_t rows,
+                                  int64_t cols, void* dw, int dtype, hipStream_t stream) {
+  if (dtype == NMB_BF16) return nmb::bwd_dw_impl<nmb::bf16>(workspace, workspace_bytes, rows, cols, dw, stream);
+  if (dtype == NMB_F32) return nmb::bwd_dw_impl<float>(workspace, workspace_bytes, rows, cols, dw, stream);
+  NMB_REQUIRE_SUPPORTED(false, "rmsnorm_bwd_dw: unsupported dtype code %d", dtype);
 }

@@ -315,9 +315,13 @@ def rmsnorm_fwd(x2: Tensor, weight: Tensor, eps: float) -> Tensor:
 
 
 def rmsnorm_bwd(
-    x2: Tensor, weight: Tensor, dy2: Tensor, eps: float, residual_grad: Tensor | None = None
+    x2: Tensor, weight: Tensor, dy2: Tensor, eps: float, residual_grad: Tensor | None = None,
+    dw_stream: "torch.cuda.Stream | None" = None,
 ) -> tuple[Tensor, Tensor]:
-    """(dx [+ residual_grad], dw) of RMSNorm, with dw reduced deterministically."""
+    """(dx [+ residual_grad], dw) of RMSNorm, with dw reduced deterministically.
+    With ``dw_stream`` the weight gradient's column sum runs there, after the
+    current stream's work so far (the caller joins that stream before dw is
+    read on another); the bits are the same."""
     _require_gpu(x2, weight, dy2)
     rows, cols = x2.shape
     nbytes = _lib.ctypes.c_size_t(0)
@@ -325,11 +329,24 @@ def rmsnorm_bwd(
     ws = _workspace(nbytes.value, x2.device)
     dx = torch.empty_like(x2)
     dw = torch.empty_like(weight)
+    code = _lib.dtype_code(x2.dtype)
+    if dw_stream is None:
+        _lib.call(
+            "nmb_rmsnorm_bwd", x2.data_ptr(), weight.data_ptr(), dy2.data_ptr(),
+            _lib.ptr(residual_grad), dx.data_ptr(), dw.data_ptr(), ws.data_ptr(), ws.numel(),
+            rows, cols, float(eps), code, _lib.stream_of(x2),
+        )
+        return dx, dw
     _lib.call(
-        "nmb_rmsnorm_bwd", x2.data_ptr(), weight.data_ptr(), dy2.data_ptr(),
-        _lib.ptr(residual_grad), dx.data_ptr(), dw.data_ptr(), ws.data_ptr(), ws.numel(),
-        rows, cols, float(eps), _lib.dtype_code(x2.dtype), _lib.stream_of(x2),
+        "nmb_rmsnorm_bwd_rows", x2.data_ptr(), weight.data_ptr(), dy2.data_ptr(),
+        _lib.ptr(residual_grad), dx.data_ptr(), ws.data_ptr(), ws.numel(), rows, cols, float(eps), code,
+        _lib.stream_of(x2),
     )
+    dw_stream.wait_stream(torch.cuda.current_stream(x2.device))
+    _lib.call("nmb_rmsnorm_bwd_dw", ws.data_ptr(), ws.numel(), rows, cols, dw.data_ptr(), code,
+              dw_stream.cuda_stream)
+    ws.record_stream(dw_stream)
+    dw.record_stream(dw_stream)
     return dx, dw
 
 
@@ -965,7 +982,11 @@ def dropout_seed() -> int:
     """A 63-bit key for the counter-based dropout masks, drawn from torch's
     default CPU generator, so that whatever replays that generator replays the
     mask: the recompute of a torch activation checkpoint (preserve_rng_state)
-    and a forked, explicitly seeded stream (nn.activation_rng_context)."""
+    and a forked, explicitly seeded stream (nn.activation_rng_context).  Each
+    draw advances that CPU generator, where the reference's F.dropout on the
+    GPU advances the CUDA generator instead: without an rng fork around the
+    dropout, later CPU randomness (data shuffles, initialisation) differs from
+    a reference run with the same seed."""
     return int(torch.randint(0, 2**63 - 1, (1,), dtype=torch.int64).item())
 
 

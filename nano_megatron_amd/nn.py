@@ -216,8 +216,10 @@ def activation_rng_context(rng: Any | None, tensor: Tensor, *, layer: int, micro
     its dropout mask does not depend on what ran before it.  The kernels draw
     their mask keys from torch's default CPU generator (functional.dropout_seed),
     the generator the fork reseeds; no CUDA generator is involved, so none is
-    forked.  Without an rng (or one without ``fork``) the default generator's
-    running stream is used, as the reference's F.dropout then does."""
+    forked.  Without an rng (or one without ``fork``) the default CPU
+    generator's running stream is used and advanced; the reference's F.dropout
+    then advances the CUDA generator instead, so later CPU randomness differs
+    from a reference run with the same seed."""
     del tensor
     if rng is None or not hasattr(rng, "fork"):
         yield

@@ -906,3 +906,19 @@ def test_attention_other_head_sizes_bf16(device, d, hq, hkv, causal) -> None:
     close(qd.grad, qr.grad, torch.bfloat16, scale_atol=True, msg="dq")
     close(kd.grad, kr.grad, torch.bfloat16, scale_atol=True, msg="dk")
     close(vd.grad, vr.grad, torch.bfloat16, scale_atol=True, msg="dv")
+
+
+def test_rmsnorm_bwd_dw_on_a_second_stream_is_bit_identical(device) -> None:
+    """nmb_rmsnorm_bwd_rows + nmb_rmsnorm_bwd_dw with the column sum on another
+    stream (as the block backward runs the post-attention norm) equal
+    nmb_rmsnorm_bwd bit for bit."""
+    g = torch.Generator(device=device).manual_seed(3)
+    x = torch.randn(8192, 1024, device=device, generator=g).bfloat16()
+    w = (1 + 0.1 * torch.randn(1024, device=device, generator=g)).bfloat16()
+    dy = torch.randn(8192, 1024, device=device, generator=g).bfloat16()
+    res = torch.randn(8192, 1024, device=device, generator=g).bfloat16()
+    side = torch.cuda.Stream(device)
+    dx0, dw0 = Fn.rmsnorm_bwd(x, w, dy, 1e-5, residual_grad=res)
+    dx1, dw1 = Fn.rmsnorm_bwd(x, w, dy, 1e-5, residual_grad=res, dw_stream=side)
+    torch.cuda.current_stream(device).wait_stream(side)
+    assert torch.equal(dx0, dx1) and torch.equal(dw0, dw1)
