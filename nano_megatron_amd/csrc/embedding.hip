@@ -9,11 +9,12 @@
 // the sum, in the order autograd accumulates them: bf16(lm + bf16(rows)).
 //
 // Backward without atomics (deterministic): workgroup (row block, column
-// chunk) owns RV table rows x CH columns.  It walks the token ids in order,
-// 256 at a time, compacts the tokens whose id falls in its rows into an LDS
-// list (wavefront ballots + a block prefix, so the list keeps token order),
-// and adds their gradient chunks to fp32 accumulators in LDS, then writes the
-// rows once.  Every output-gradient element is read by one workgroup; the ids
+// chunk) owns RV table rows x CH columns.  It takes the token ids in rounds of
+// 2048 (8 consecutive ids per thread, loaded together), lists the tokens whose
+// id falls in its rows in token order (a workgroup prefix sum of each
+// thread's hits), and adds their gradient chunks, eight rows' loads in flight
+// at a time, to fp32 accumulators in LDS in list order, then writes its rows
+// once.  Every output-gradient element is read by one workgroup; the ids
 // (8 bytes per token) are read by all of them from L2.
 #include "common.h"
 #include "vec.h"
@@ -21,8 +22,10 @@
 namespace nmb {
 namespace {
 
-constexpr int RV = 16;     // table rows per workgroup
-constexpr int CH = 1024;   // columns per workgroup (4 per thread)
+constexpr int RV = 16;        // table rows per workgroup
+constexpr int CH = 1024;      // columns per workgroup (4 per thread)
+constexpr int kPer = 8;       // token ids per thread per round
+constexpr int kRound = 256 * kPer;  // tokens per round
 
 template <typename T>
 __global__ __launch_bounds__(256) void embedding_fwd_kernel(const T* __restrict__ table,
@@ -51,61 +54,141 @@ __global__ __launch_bounds__(256) void embedding_fwd_kernel(const T* __restrict_
   }
 }
 
+// 4 consecutive elements of T (8 bytes of bf16, 16 of fp32) as floats
 template <typename T>
-__global__ __launch_bounds__(256) void embedding_bwd_kernel(const T* __restrict__ dout,
-                                                            const int64_t* __restrict__ ids,
-                                                            const T* __restrict__ grad_in,
-                                                            T* __restrict__ grad_out,
-                                                            int64_t n_tokens, int64_t vocab,
-                                                            int64_t hidden) {
-  __shared__ float acc[RV * CH];     // 64 KB
-  __shared__ int list_t[256];        // matching tokens of the current pass, in order
-  __shared__ int list_r[256];
-  __shared__ int wave_count[4];
+__device__ __forceinline__ void load4(const T* p, float (&v)[4]) {
+  if constexpr (sizeof(T) == 2) {
+    const uint2 raw = *reinterpret_cast<const uint2*>(p);
+    T e[4];
+    __builtin_memcpy(e, &raw, 8);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = to_f32(e[i]);
+  } else {
+    const float4 raw = *reinterpret_cast<const float4*>(p);
+    v[0] = raw.x;
+    v[1] = raw.y;
+    v[2] = raw.z;
+    v[3] = raw.w;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256, 2) void embedding_bwd_kernel(const T* __restrict__ dout,
+                                                               const int64_t* __restrict__ ids,
+                                                               const T* __restrict__ grad_in,
+                                                               T* __restrict__ grad_out,
+                                                               int64_t n_tokens, int64_t vocab,
+                                                               int64_t hidden) {
+  __shared__ float4 acc[RV * CH / 4];  // 64 KB: row r, this thread's 4 columns at [r * CH / 4 + thread]
+  __shared__ int list[kRound];     // matching tokens of the round, in order: offset * RV + row
+  __shared__ int wave_total[4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t row_blocks = (vocab + RV - 1) / RV;
   const int64_t v0 = (blockIdx.x % row_blocks) * RV;
   const int64_t c0 = (blockIdx.x / row_blocks) * CH;
   const int cols = static_cast<int>(min<int64_t>(CH, hidden - c0));
   const int c = threadIdx.x * 4;  // this thread's 4 columns
-  for (int i = threadIdx.x; i < RV * CH; i += 256) acc[i] = 0.f;
-
-  for (int64_t base = 0; base < n_tokens; base += 256) {
-    const int64_t t = base + threadIdx.x;
-    const int64_t id = t < n_tokens ? ids[t] : -1;
-    const bool hit = id >= v0 && id < v0 + RV;
-    const uint64_t mask = __ballot(hit);
-    const int before = __builtin_popcountll(mask & ((uint64_t{1} << lane) - 1));
-    if (lane == 0) wave_count[wave] = __builtin_popcountll(mask);
-    __syncthreads();  // wave counts ready; the previous pass's list is consumed
-    int off = 0;
-    for (int w = 0; w < wave; ++w) off += wave_count[w];
-    const int total = wave_count[0] + wave_count[1] + wave_count[2] + wave_count[3];
-    if (hit) {
-      list_t[off + before] = static_cast<int>(threadIdx.x);
-      list_r[off + before] = static_cast<int>(id - v0);
-    }
-    __syncthreads();
-    if (c < cols) {
-      for (int k = 0; k < total; ++k) {
-        const T* src = dout + (base + list_t[k]) * hidden + c0 + c;
-        float* a = acc + list_r[k] * CH + c;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) a[e] += to_f32(src[e]);
+  for (int r = 0; r < RV; ++r) acc[r * (CH / 4) + threadIdx.x] = make_float4(0.f, 0.f, 0.f, 0.f);
+
+  // the ids of a round: kPer consecutive tokens per thread, loaded together;
+  // the next round's are in flight while this round's rows are added
+  int64_t id[kPer], next[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) next[j] = -1;
+  auto load_ids = [&](int64_t base, int64_t (&dst)[kPer]) {
+    const int64_t t0 = base + threadIdx.x * kPer;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) dst[j] = t0 + j < n_tokens ? ids[t0 + j] : -1;
+  };
+  load_ids(0, id);
+  for (int64_t base = 0; base < n_tokens; base += kRound) {
+    const int t_off = threadIdx.x * kPer;
+    int hits = 0;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) hits += id[j] >= v0 && id[j] < v0 + RV;
+    // exclusive prefix of the hits over the workgroup (thread order = token order)
+    int incl = hits;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += y;
+    }
+    if (lane == 63) wave_total[wave] = incl;
+    __syncthreads();  // wave totals ready; the previous round's list is consumed
+    int pos = incl - hits;
+    for (int w = 0; w < wave; ++w) pos += wave_total[w];
+    const int total = wave_total[0] + wave_total[1] + wave_total[2] + wave_total[3];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j)
+      if (id[j] >= v0 && id[j] < v0 + RV) list[pos++] = (t_off + j) * RV + static_cast<int>(id[j] - v0);
+    __syncthreads();
+    if (base + kRound < n_tokens) load_ids(base + kRound, next);
+    if (c < cols) {
+      // the listed gradient rows in token order, loaded eight at a time
+      for (int k0 = 0; k0 < total; k0 += 8) {
+        float v[8][4];
+        int row[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int e = list[min(k0 + u, total - 1)];
+          row[u] = e % RV;
+          load4<T>(dout + (base + e / RV) * hidden + c0 + c, v[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (k0 + u >= total) break;
+          float4& a = acc[row[u] * (CH / 4) + threadIdx.x];
+          float4 t = a;
+          t.x += v[u][0];
+          t.y += v[u][1];
+          t.z += v[u][2];
+          t.w += v[u][3];
+          a = t;
+        }
       }
     }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) id[j] = next[j];
   }
   __syncthreads();
   if (c >= cols) return;
-  for (int r = 0; r < RV && v0 + r < vocab; ++r) {
+  // the tied LM head's rows, all loaded before any is used (rows past the
+  // table read its last row and are not stored)
+  float prior[RV][4];
+#pragma unroll
+  for (int r = 0; r < RV; ++r) {
+    const int64_t o = min(v0 + r, vocab - 1) * hidden + c0 + c;
+    if (grad_in != nullptr) {
+      load4<T>(grad_in + o, prior[r]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) prior[r][e] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RV; ++r) {
+    if (v0 + r >= vocab) break;
     const int64_t o = (v0 + r) * hidden + c0 + c;
+    const float4 a4 = acc[r * (CH / 4) + threadIdx.x];
+    const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+    float out[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       // the embedding's own gradient is rounded to the table dtype before the
       // tied LM-head gradient is added (autograd adds two gradient tensors)
-      const float mine = round_as<T>(acc[r * CH + c + e]);
-      const float prior = grad_in != nullptr ? to_f32(grad_in[o + e]) : 0.f;
-      grad_out[o + e] = from_f32<T>(grad_in != nullptr ? add_rn(prior, mine) : mine);
+      const float mine = round_as<T>(av[e]);
+      out[e] = grad_in != nullptr ? add_rn(prior[r][e], mine) : mine;
+    }
+    if constexpr (sizeof(T) == 2) {
+      T ov[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ov[e] = from_f32<T>(out[e]);
+      uint2 raw;
+      __builtin_memcpy(&raw, ov, 8);
+      *reinterpret_cast<uint2*>(grad_out + o) = raw;
+    } else {
+      *reinterpret_cast<float4*>(grad_out + o) = make_float4(out[0], out[1], out[2], out[3]);
     }
   }
 }
@@ -135,6 +218,13 @@ int bwd_impl(const void* dout, const int64_t* ids, const void* grad_in, void* gr
                         (long long)hidden);
   const int64_t blocks = ((vocab + RV - 1) / RV) * ((hidden + CH - 1) / CH);
   NMB_REQUIRE(blocks < (int64_t{1} << 31), "embedding_bwd: table too large");
+  // rows of 4 elements are read as one 8-byte (bf16) or 16-byte (fp32) access
+  const uintptr_t align = 4 * sizeof(T) - 1;
+  NMB_REQUIRE((reinterpret_cast<uintptr_t>(dout) & align) == 0 &&
+                  (reinterpret_cast<uintptr_t>(grad_out) & align) == 0 &&
+                  (grad_in == nullptr || (reinterpret_cast<uintptr_t>(grad_in) & align) == 0),
+              "embedding_bwd: dout, grad_in and grad_out must be aligned to %d bytes",
+              static_cast<int>(align + 1));
   if (blocks == 0) return NMB_OK;
   hipLaunchKernelGGL((embedding_bwd_kernel<T>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      stream, static_cast<const T*>(dout), ids, static_cast<const T*>(grad_in),
