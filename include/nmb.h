@@ -366,6 +366,22 @@ int nmb_gemm_bf16_swiglu_bwd(int b_layout, int64_t m, int64_t f, int64_t k, cons
                              int64_t lda, const void* b, int64_t ldb, const void* gu, int64_t ldgu,
                              void* dgu, int64_t lddgu, void* act, int64_t ldact, hipStream_t stream);
 
+/* The MLP backward of a recomputed block in one kernel (autograd of
+ * models/gpt/mlp.py:72-78 with the gate/up product recomputed, as a
+ * checkpointed layer's backward re-runs it): per 256 x 128 tile of F,
+ *   [g|u] = bf16(A1 Wgu^T)   A1 [M, K1] row-major (n2), Wgu [2F, K1] row-major
+ *                            ([Wg; Wu], paired as nmb_gemm_bf16_swiglu reads it),
+ *   ds = bf16(A2 op(Wd))     A2 [M, K2] row-major (dY), b_layout as above,
+ * then the SwiGLU backward: dgu [M, 2F] = (d gate | d up), act (nullable)
+ * [M, F] = silu(g) u.  Bit-identical to nmb_gemm_bf16_swiglu (product only)
+ * followed by nmb_gemm_bf16_swiglu_bwd, without the [M, 2F] product in
+ * memory; never split along K; F, K1, K2 and the leading dimensions
+ * multiples of 8; no workspace. */
+int nmb_gemm_bf16_gate_up_swiglu_bwd(int64_t m, int64_t f, int64_t k1, const void* a1, int64_t lda1,
+                                     const void* wgu, int64_t ldwgu, int64_t k2, const void* a2,
+                                     int64_t lda2, int b_layout, const void* wd, int64_t ldwd, void* dgu,
+                                     int64_t lddgu, void* act, int64_t ldact, hipStream_t stream);
+
 /* ------------------------------------------------------------ optimizer
  * replaces FlatShardZeROStrategy.clip_grad_norm + optimizer_step at DP=1
  * (data_parallel/_zero.py:130-199; defaults config/schema.py:439-445):

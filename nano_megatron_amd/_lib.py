@@ -105,6 +105,8 @@ SIGNATURES: dict[str, list] = {
     ],
     "nmb_gemm_bf16_swiglu": [_i64, _i64, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p],
     "nmb_gemm_bf16_swiglu_bwd": [_i32, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p],
+    "nmb_gemm_bf16_gate_up_swiglu_bwd": [_i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _i64, _i32, _p, _i64,
+                                         _p, _i64, _p, _i64, _p],
     "nmb_adamw_workspace_bytes": [_i64, _psz],
     "nmb_adamw_step": [
         _p, _p, _p, _i32, _i64, _p, _p, _p, _i32, _i32, _f64, _f64, _f64, _f64, _f64, _i64, _f32,

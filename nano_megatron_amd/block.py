@@ -16,12 +16,15 @@ models/gpt/layer.py:91-137):
 models/gpt/model.py:162-170, 215-233): it saves only the block input x.  Its
 backward re-runs the sequence above with the same kernels and shapes (so the
 recomputed tensors, the attention output and its lse included, are
-bit-identical to the forward's), except that the gate/up GEMM writes the
-product [g|u] instead of s (same plan, same bits), and never re-runs the down
-projection, whose output the backward does not need.  The down projection's
-backward GEMM runs the SwiGLU backward as its epilogue
-(``nmb_gemm_bf16_swiglu_bwd``: no ds in memory) and re-emits s for the Wd
-gradient.  With ``offload`` the saved input goes to
+bit-identical to the forward's) up to n2, and never re-runs the down
+projection, whose output the backward does not need.  The gate/up product is
+recomputed inside the MLP backward's GEMM (``nmb_gemm_bf16_gate_up_swiglu_bwd``:
+per output tile [g|u] = n2 [Wg;Wu]^T, ds = dY Wd and the SwiGLU backward with
+all three in registers, the same bits as the forward's gate/up product
+followed by the SwiGLU backward; neither [g|u] nor ds reaches memory), which
+re-emits s for the Wd gradient.  A block that keeps [g|u] (no checkpoint)
+runs the down projection's backward GEMM with the SwiGLU backward as its
+epilogue instead (``nmb_gemm_bf16_swiglu_bwd``).  With ``offload`` the saved input goes to
 pinned host memory (the reference's saved-tensor offload,
 nn/activation_checkpoint.py:24-41); the weights are parameters, never copied.
 ``EagerBlockFunction`` (activation_checkpoint.mode = "none") keeps the
@@ -127,10 +130,12 @@ def _gate_up_part(n2: Tensor, w: tuple[Tensor, ...], *, act: bool, gu: bool) -> 
 
 
 def block_forward(x: Tensor, w: tuple[Tensor, ...], m: BlockMeta, *, recompute: bool,
-                  keep_gu: bool = True) -> dict:
-    """Run the block on x [B,S,H].  With recompute=True stop after [g|u] (no s, no y).
-    With keep_gu=False (a forward whose intermediates are dropped) the gate/up
-    GEMM applies the activation in its epilogue and [g|u] is never written."""
+                  keep_gu: bool = True, gate_up: bool = True) -> dict:
+    """Run the block on x [B,S,H].  With recompute=True stop after [g|u] (no s, no y),
+    or after n2 with gate_up=False (the backward then recomputes [g|u] inside its
+    fused gate/up + SwiGLU-backward GEMM).  With keep_gu=False (a forward whose
+    intermediates are dropped) the gate/up GEMM applies the activation in its
+    epilogue and [g|u] is never written."""
     w_in, wq, wk, wv, wo, w_post, wg, wu, wd = w
     b, s, hdim = x.shape
     x2 = x.reshape(b * s, hdim)
@@ -138,8 +143,10 @@ def block_forward(x: Tensor, w: tuple[Tensor, ...], m: BlockMeta, *, recompute: 
     qkv, o2, lse = _attention_part(n1, w, m, b, s)
     h = Fn.mm(o2, wo.t(), c=x2, beta=1.0)
     n2 = Fn.rmsnorm_fwd(h, w_post, m.eps)
-    act, gu = _gate_up_part(n2, w, act=not recompute, gu=recompute or keep_gu)
     acts = dict(x2=x2, n1=n1, qkv=qkv, o2=o2, lse=lse, h=h, n2=n2)
+    if recompute and not gate_up:
+        return acts
+    act, gu = _gate_up_part(n2, w, act=not recompute, gu=recompute or keep_gu)
     if gu is not None:
         acts["gu"] = gu
     if recompute:
@@ -207,12 +214,17 @@ def block_backward(acts: dict, dy: Tensor, w: tuple[Tensor, ...], m: BlockMeta, 
     dy2 = dy.reshape(b * s, hdim)
     if not dy2.is_contiguous():
         dy2 = dy2.contiguous()
-    x2, n1, qkv, o2, lse, h, n2, gu = (acts[k] for k in ("x2", "n1", "qkv", "o2", "lse", "h", "n2", "gu"))
+    x2, n1, qkv, o2, lse, h, n2 = (acts[k] for k in ("x2", "n1", "qkv", "o2", "lse", "h", "n2"))
     side = _SideProducts(dy2.device)
 
     # MLP: y = h + s Wd^T, s = silu(g) * u, [g|u] = n2 [Wg;Wu]^T
-    # ds = dY Wd and the SwiGLU backward in one GEMM (its epilogue); act feeds dWd
-    dgu, act = Fn.mm_swiglu_bwd(dy2, wd, gu)
+    # ds = dY Wd and the SwiGLU backward in one GEMM (its epilogue); act feeds dWd.
+    # Without a kept [g|u] (a recomputed block) the same kernel first forms
+    # [g|u] for its tile from n2 (same bits), so the product never reaches memory.
+    if "gu" in acts:
+        dgu, act = Fn.mm_swiglu_bwd(dy2, wd, acts["gu"])
+    else:
+        dgu, act = Fn.mm_gate_up_swiglu_bwd(n2, joined((wg, wu)), dy2, wd)
     dwd = side.mm(dy2.t(), act)
     dn2 = Fn.mm(dgu, joined((wg, wu)))
     dwgu = side.mm(dgu.t(), n2)
@@ -281,8 +293,9 @@ class CheckpointedBlockFunction(torch.autograd.Function):
             x, weights = saved[0], saved[1:]
         with torch.no_grad():
             # the recompute re-runs the forward's attention kernel: o and lse come
-            # out bit-identical to the forward's, so the lse needs no saving
-            acts = block_forward(x, tuple(weights), ctx.meta, recompute=True)
+            # out bit-identical to the forward's, so the lse needs no saving; the
+            # gate/up product is recomputed inside the MLP backward's GEMM
+            acts = block_forward(x, tuple(weights), ctx.meta, recompute=True, gate_up=False)
             grads = block_backward(acts, dy, tuple(weights), ctx.meta, ctx.shape)
         return (grads[0], None, None, *grads[1:])
 
@@ -297,7 +310,8 @@ class SelectiveBlockFunction(torch.autograd.Function):
     checkpoints), n1 and n2 (the checkpointed sub-blocks' inputs), and the
     intermediates of a sub-block that is not checkpointed.  The backward
     recomputes a checkpointed attention's [q|k|v], o and lse from n1 and a
-    checkpointed MLP's [g|u] from n2 with the forward's kernels (same bits),
+    checkpointed MLP's [g|u] from n2 (inside the fused gate/up + SwiGLU
+    backward GEMM) with the forward's arithmetic (same bits),
     never the norms, the out projection or the down projection, whose outputs
     it does not read, then runs the shared block backward.  With ``offload``
     the checkpointed sub-blocks' inputs wait in pinned host memory."""
@@ -346,8 +360,8 @@ class SelectiveBlockFunction(torch.autograd.Function):
                 acts["n1"] = ck.pop(0)
                 acts["qkv"], acts["o2"], acts["lse"] = _attention_part(acts["n1"], weights, m, b, s)
             if mlp_ck:
+                # [g|u] is recomputed inside the MLP backward's GEMM
                 acts["n2"] = ck.pop(0)
-                _, acts["gu"] = _gate_up_part(acts["n2"], weights, act=False, gu=True)
             grads = block_backward(acts, dy, weights, m, ctx.shape)
         return (grads[0], None, None, None, *grads[1:])
 

@@ -242,69 +242,18 @@ struct Stages {
   static_assert(S >= 2, "two LDS stages at least");
 };
 
-// One workgroup's work: item L of the launch (XCD-ordered as below), on the
-// operand stages sA and sB in LDS.
-//
-// TBM x TBN output tile, NW wavefronts (4: 2 x 2, two workgroups per CU;
-// 8: 2 x 4 or 4 x 2, one workgroup per CU), BKT-deep K tiles.  RD > 0: RoPE
-// epilogue on heads of RD.  SWI: B is [2F, K] (gate rows, then up rows), N = F,
-// and D = swiglu(gate product, up product).
-template <int TBM, int TBN, int NW, int BKT, bool A_KC, bool B_KC, int RD, bool SWI, bool SWB>
-__device__ __forceinline__ void gemm_tile(const GemmArgs& g, int L,
-                                          bf16 (*sA)[TBM * BKT],
-                                          bf16 (*sB)[TBN * BKT]) {
-  constexpr int WAVES_N = NW == 4 ? 2 : (TBN == 256 ? 4 : 2);
-  constexpr int WAVES_M = NW / WAVES_N;
-  constexpr int WM = TBM / WAVES_M, WN = TBN / WAVES_N;  // wave tile
-  constexpr int TM = WM / 16, TN = WN / 16;              // 16 x 16 MFMA tiles per wave
+// The K loop of one tile: acc[i][j] += the wave's 16 x 16 MFMA tiles of
+// op(A) op(B) over [k_begin, k_end), the operands streamed through the S LDS
+// stages sA / sB by the loaders (the wave tile at rows wm, columns wn).
+// Returns with every load of the loop complete; the other waves may still
+// read the last stage.
+template <int TBM, int TBN, int NW, int BKT, bool A_KC, bool B_KC, int TM, int TN>
+__device__ __forceinline__ void k_loop(const Loader<TBM, A_KC, BKT, NW>& la,
+                                       const Loader<TBN, B_KC, BKT, NW>& lb, bf16 (*sA)[TBM * BKT],
+                                       bf16 (*sB)[TBN * BKT], f32x4 (&acc)[TM][TN], int wm, int wn,
+                                       int k_begin, int k_end, int wave, int lane) {
   constexpr int KSTEPS = BKT / 32;
   constexpr int S = Stages<TBM, TBN, NW, BKT>::S;
-
-  const int w = (L % 8) * g.per_xcd + L / 8;
-  if (w >= g.items) return;
-  const int split = w / g.tiles;
-  const int t = w % g.tiles;
-  // grouped order: 4 tile rows at a time, walking the rows fastest, so the
-  // 32 workgroups an XCD runs together cover 4 rows x 8 columns of tiles and
-  // share their operand blocks in its L2
-  constexpr int GM = 4;
-  const int tiles_m = g.tiles / g.tiles_n;
-  const int grp = t / (GM * g.tiles_n);
-  const int gsize = min(tiles_m - grp * GM, GM);
-  const int r = t - grp * GM * g.tiles_n;
-  const int m0 = (grp * GM + r % gsize) * TBM;
-  const int n0 = (r / gsize) * out_cols<TBN, SWI>();
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = (wave / WAVES_N) * WM, wn = (wave % WAVES_N) * WN;
-  const int k_begin = split * g.kps;
-  const int k_end = min(g.K, k_begin + g.kps);
-
-  Loader<TBM, A_KC, BKT, NW> la;
-  Loader<TBN, B_KC, BKT, NW> lb;
-  {
-    // tile origins and the extents (bytes) of the matrices from there
-    const bf16* a0 = A_KC ? g.a + static_cast<int64_t>(m0) * g.lda : g.a + m0;
-    const bf16* b0 = B_KC ? g.b + static_cast<int64_t>(n0) * g.ldb : g.b + n0;
-    const int va = min(TBM, g.M - m0), vb = min(TBN, g.N - n0);
-    const int64_t ea = A_KC ? (static_cast<int64_t>(va - 1) * g.lda + g.K) * 2
-                            : (static_cast<int64_t>(g.K - 1) * g.lda + (g.M - m0)) * 2;
-    const int64_t eb = B_KC ? (static_cast<int64_t>(vb - 1) * g.ldb + g.K) * 2
-                            : (static_cast<int64_t>(g.K - 1) * g.ldb + (g.N - n0)) * 2;
-    la.init(a0, g.lda, va, static_cast<uint32_t>(ea), wave, lane);
-    if constexpr (SWI) {
-      const int64_t e2 = (static_cast<int64_t>(2 * g.N - 1) * g.ldb + g.K) * 2;
-      lb.init_pairs(g.b, g.ldb, g.N, n0, static_cast<uint32_t>(e2), wave, lane);
-    } else {
-      lb.init(b0, g.ldb, vb, static_cast<uint32_t>(eb), wave, lane);
-    }
-  }
-
-  f32x4 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
   Frags<TBM, A_KC, TM, BKT> fra;
   Frags<TBN, B_KC, TN, BKT> frb;
   fra.init(wm, lane);
@@ -381,6 +330,72 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int L,
         for (int j = 0; j < TN; ++j) acc[i][j] = mfma16(fb[0][j], fa[0][i], acc[i][j]);
     }
   }
+
+}
+
+// One workgroup's work: item L of the launch (XCD-ordered as below), on the
+// operand stages sA and sB in LDS.
+//
+// TBM x TBN output tile, NW wavefronts (4: 2 x 2, two workgroups per CU;
+// 8: 2 x 4 or 4 x 2, one workgroup per CU), BKT-deep K tiles.  RD > 0: RoPE
+// epilogue on heads of RD.  SWI: B is [2F, K] (gate rows, then up rows), N = F,
+// and D = swiglu(gate product, up product).
+template <int TBM, int TBN, int NW, int BKT, bool A_KC, bool B_KC, int RD, bool SWI, bool SWB>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& g, int L,
+                                          bf16 (*sA)[TBM * BKT],
+                                          bf16 (*sB)[TBN * BKT]) {
+  constexpr int WAVES_N = NW == 4 ? 2 : (TBN == 256 ? 4 : 2);
+  constexpr int WAVES_M = NW / WAVES_N;
+  constexpr int WM = TBM / WAVES_M, WN = TBN / WAVES_N;  // wave tile
+  constexpr int TM = WM / 16, TN = WN / 16;              // 16 x 16 MFMA tiles per wave
+  constexpr int S = Stages<TBM, TBN, NW, BKT>::S;
+
+  const int w = (L % 8) * g.per_xcd + L / 8;
+  if (w >= g.items) return;
+  const int split = w / g.tiles;
+  const int t = w % g.tiles;
+  // grouped order: 4 tile rows at a time, walking the rows fastest, so the
+  // 32 workgroups an XCD runs together cover 4 rows x 8 columns of tiles and
+  // share their operand blocks in its L2
+  constexpr int GM = 4;
+  const int tiles_m = g.tiles / g.tiles_n;
+  const int grp = t / (GM * g.tiles_n);
+  const int gsize = min(tiles_m - grp * GM, GM);
+  const int r = t - grp * GM * g.tiles_n;
+  const int m0 = (grp * GM + r % gsize) * TBM;
+  const int n0 = (r / gsize) * out_cols<TBN, SWI>();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = (wave / WAVES_N) * WM, wn = (wave % WAVES_N) * WN;
+  const int k_begin = split * g.kps;
+  const int k_end = min(g.K, k_begin + g.kps);
+
+  Loader<TBM, A_KC, BKT, NW> la;
+  Loader<TBN, B_KC, BKT, NW> lb;
+  {
+    // tile origins and the extents (bytes) of the matrices from there
+    const bf16* a0 = A_KC ? g.a + static_cast<int64_t>(m0) * g.lda : g.a + m0;
+    const bf16* b0 = B_KC ? g.b + static_cast<int64_t>(n0) * g.ldb : g.b + n0;
+    const int va = min(TBM, g.M - m0), vb = min(TBN, g.N - n0);
+    const int64_t ea = A_KC ? (static_cast<int64_t>(va - 1) * g.lda + g.K) * 2
+                            : (static_cast<int64_t>(g.K - 1) * g.lda + (g.M - m0)) * 2;
+    const int64_t eb = B_KC ? (static_cast<int64_t>(vb - 1) * g.ldb + g.K) * 2
+                            : (static_cast<int64_t>(g.K - 1) * g.ldb + (g.N - n0)) * 2;
+    la.init(a0, g.lda, va, static_cast<uint32_t>(ea), wave, lane);
+    if constexpr (SWI) {
+      const int64_t e2 = (static_cast<int64_t>(2 * g.N - 1) * g.ldb + g.K) * 2;
+      lb.init_pairs(g.b, g.ldb, g.N, n0, static_cast<uint32_t>(e2), wave, lane);
+    } else {
+      lb.init(b0, g.ldb, vb, static_cast<uint32_t>(eb), wave, lane);
+    }
+  }
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  k_loop<TBM, TBN, NW, BKT, A_KC, B_KC, TM, TN>(la, lb, sA, sB, acc, wm, wn, k_begin, k_end, wave, lane);
 
   // acc[i][j][e] = D[m0 + wm + 16 i + l16][n0 + wn + 16 j + 4 q4 + e]
   const int l16 = lane & 15, q4 = lane >> 4;
@@ -755,6 +770,132 @@ __global__ __launch_bounds__(512, 1) void gemm_pair_kernel(GemmArgs g1, GemmArgs
   } else {
     gemm_tile<TBM2, TBN2, 8, BKT2, true, B_KC, 0, false, false>(
         g2, L - n1, reinterpret_cast<bf16(*)[TBM2 * BKT2]>(smem), reinterpret_cast<bf16(*)[TBN2 * BKT2]>(smem + A2));
+  }
+}
+
+// The MLP backward's two products for one 256-row x 128-column tile of F,
+// with the SwiGLU backward as the epilogue and nothing in between in memory:
+//   phase 1: [g|u] = A1 [Wg; Wu]^T (g1: A1 = n2 [M, K1], B = the paired
+//            [2F, K1] gate/up weight, as nmb_gemm_bf16_swiglu reads it),
+//   phase 2: ds = A2 Wd (g2: A2 = dY [M, K2], B = Wd [F, K2] or [K2, F]),
+//   epilogue: dg, du = swiglu_bwd(g, u, ds) into dgu [M, 2F] and
+//            silu(g) u into act [M, F] (the activation the Wd gradient reads).
+// Both phases use the same wave tiling (4 x 2 waves, 64 rows x 64 F columns
+// each), so the lane holding g, u of an element (phase 1's 16 x 16 tiles j
+// and j + 2 of a gate / up column pair) holds its ds too (phase 2's tile
+// (j & 1) + 2 (j >> 2)).  g, u and ds are rounded to bf16 as the separate
+// products store them and every K sum runs in the order of the other
+// kernels, so the outputs equal nmb_gemm_bf16_swiglu (product only) followed
+// by nmb_gemm_bf16_swiglu_bwd bit for bit, without [g|u] ever being written.
+template <bool B2_KC>
+__global__ __launch_bounds__(512, 1) void gemm_gu_swb_kernel(GemmArgs g1, GemmArgs g2) {
+  constexpr int TBM = 256, TB1 = 256, TB2 = 128, NW = 8, BKT = 64, WAVES_N = 2;
+  constexpr int WM = TBM / (NW / WAVES_N), WN1 = TB1 / WAVES_N, WN2 = TB2 / WAVES_N;
+  constexpr int TM = WM / 16, TN1 = WN1 / 16, TN2 = WN2 / 16;
+  constexpr int S1 = Stages<TBM, TB1, NW, BKT>::S, S2 = Stages<TBM, TB2, NW, BKT>::S;
+  constexpr int A1 = S1 * TBM * BKT, B1 = S1 * TB1 * BKT;
+  constexpr int A2 = S2 * TBM * BKT, B2 = S2 * TB2 * BKT;
+  constexpr int kElems = A1 + B1 > A2 + B2 ? A1 + B1 : A2 + B2;
+  static_assert(A1 % 512 == 0 && A2 % 512 == 0, "B stages stay 1 KB aligned");
+  static_assert(TN1 == 2 * TN2, "a wave's gate/up columns pair with its ds columns");
+  __shared__ __attribute__((aligned(1024))) bf16 smem[kElems];
+
+  const int L = static_cast<int>(blockIdx.x);
+  const int w = (L % 8) * g2.per_xcd + L / 8;
+  if (w >= g2.items) return;
+  // grouped order as in gemm_tile: 4 tile rows at a time
+  constexpr int GM = 4;
+  const int tiles_m = g2.tiles / g2.tiles_n;
+  const int grp = w / (GM * g2.tiles_n);
+  const int gsize = min(tiles_m - grp * GM, GM);
+  const int r = w - grp * GM * g2.tiles_n;
+  const int m0 = (grp * GM + r % gsize) * TBM;
+  const int f0 = (r / gsize) * TB2;
+  const int M = g2.M, F = g2.N;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = (wave / WAVES_N) * WM, wc = wave % WAVES_N;
+  const int va = min(TBM, M - m0);
+
+  // phase 1: the gate/up product of the tile's F columns (128 gate, 128 up)
+  f32x4 acc1[TM][TN1];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN1; ++j) acc1[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  {
+    Loader<TBM, true, BKT, NW> la;
+    Loader<TB1, true, BKT, NW> lb;
+    la.init(g1.a + static_cast<int64_t>(m0) * g1.lda, g1.lda, va,
+            static_cast<uint32_t>((static_cast<int64_t>(va - 1) * g1.lda + g1.K) * 2), wave, lane);
+    lb.init_pairs(g1.b, g1.ldb, F, f0,
+                  static_cast<uint32_t>((static_cast<int64_t>(2 * F - 1) * g1.ldb + g1.K) * 2), wave, lane);
+    k_loop<TBM, TB1, NW, BKT, true, true, TM, TN1>(
+        la, lb, reinterpret_cast<bf16(*)[TBM * BKT]>(smem), reinterpret_cast<bf16(*)[TB1 * BKT]>(smem + A1),
+        acc1, wm, wc * WN1, 0, g1.K, wave, lane);
+  }
+  // g and u as the product stores them (bf16); column tile jj of phase 2 is
+  // gate tile (jj & 1) + 4 (jj >> 1) of phase 1, its up partner 2 tiles on
+  bf16x4 gv[TM][TN2], uv[TM][TN2];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int jj = 0; jj < TN2; ++jj) {
+      const int j = (jj & 1) + 4 * (jj >> 1);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        gv[i][jj][e] = static_cast<bf16>(acc1[i][j][e]);
+        uv[i][jj][e] = static_cast<bf16>(acc1[i][j + 2][e]);
+      }
+    }
+  __syncthreads();  // every wave is done with phase 1's stages
+
+  // phase 2: ds = dY Wd for the same tile
+  f32x4 acc2[TM][TN2];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN2; ++j) acc2[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  {
+    Loader<TBM, true, BKT, NW> la;
+    Loader<TB2, B2_KC, BKT, NW> lb;
+    la.init(g2.a + static_cast<int64_t>(m0) * g2.lda, g2.lda, va,
+            static_cast<uint32_t>((static_cast<int64_t>(va - 1) * g2.lda + g2.K) * 2), wave, lane);
+    const int vb = min(TB2, F - f0);
+    const bf16* b0 = B2_KC ? g2.b + static_cast<int64_t>(f0) * g2.ldb : g2.b + f0;
+    const int64_t eb = B2_KC ? (static_cast<int64_t>(vb - 1) * g2.ldb + g2.K) * 2
+                             : (static_cast<int64_t>(g2.K - 1) * g2.ldb + (F - f0)) * 2;
+    lb.init(b0, g2.ldb, vb, static_cast<uint32_t>(eb), wave, lane);
+    k_loop<TBM, TB2, NW, BKT, true, B2_KC, TM, TN2>(
+        la, lb, reinterpret_cast<bf16(*)[TBM * BKT]>(smem), reinterpret_cast<bf16(*)[TB2 * BKT]>(smem + A2),
+        acc2, wm, wc * WN2, 0, g2.K, wave, lane);
+  }
+
+  // the SwiGLU backward on the tile: lane (l16, q4) holds row wm + 16 i + l16,
+  // F columns wc 64 + 16 jj + 4 q4 .. + 3 of every (i, jj)
+  const int l16 = lane & 15, q4 = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = m0 + wm + 16 * i + l16;
+    if (m >= M) continue;
+    bf16* drow = g2.swb_dgu + static_cast<int64_t>(m) * g2.swb_lddgu;
+#pragma unroll
+    for (int jj = 0; jj < TN2; ++jj) {
+      const int n = f0 + wc * WN2 + 16 * jj + 4 * q4;
+      if (n >= F) continue;
+      bf16x4 dgo, duo, oo;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float dgf, duf, of;
+        swiglu_bwd_elem<bf16>(static_cast<float>(gv[i][jj][e]), static_cast<float>(uv[i][jj][e]),
+                              round_as<bf16>(acc2[i][jj][e]), dgf, duf, of);
+        dgo[e] = static_cast<bf16>(dgf);
+        duo[e] = static_cast<bf16>(duf);
+        oo[e] = static_cast<bf16>(of);
+      }
+      *reinterpret_cast<bf16x4*>(drow + n) = dgo;
+      *reinterpret_cast<bf16x4*>(drow + F + n) = duo;
+      if (g2.d != nullptr) *reinterpret_cast<bf16x4*>(g2.d + static_cast<int64_t>(m) * g2.ldd + n) = oo;
+    }
   }
 }
 
@@ -1233,4 +1374,38 @@ extern "C" int nmb_gemm_bf16_swiglu_bwd(int b_layout, int64_t m, int64_t f, int6
   g.swb_dgu = static_cast<nmb::bf16*>(dgu);
   g.swb_lddgu = lddgu;
   return nmb::dispatch_swiglu_bwd(p.config, b_kc, g, stream);
+}
+
+extern "C" int nmb_gemm_bf16_gate_up_swiglu_bwd(int64_t m, int64_t f, int64_t k1, const void* a1, int64_t lda1,
+                                                const void* wgu, int64_t ldwgu, int64_t k2, const void* a2,
+                                                int64_t lda2, int b_layout, const void* wd, int64_t ldwd,
+                                                void* dgu, int64_t lddgu, void* act, int64_t ldact,
+                                                hipStream_t stream) {
+  // [g|u] = a1 wgu^T ([M, K1] x [2F, K1]), ds = a2 wd ([M, K2] x op(wd) [K2, F]); dgu [M, 2F], act [M, F]
+  NMB_REQUIRE(dgu != nullptr, "gemm_gate_up_swiglu_bwd: null dgu");
+  int st = nmb::check_gemm(0, 0, m, f, k1, a1, lda1, wgu, ldwgu, false, nullptr, 0, dgu, lddgu);
+  if (st != NMB_OK) return st;
+  st = nmb::check_gemm(0, b_layout, m, f, k2, a2, lda2, wd, ldwd, false, nullptr, 0, dgu, lddgu);
+  if (st != NMB_OK) return st;
+  NMB_REQUIRE(lddgu >= 2 * f, "gemm_gate_up_swiglu_bwd: dgu needs a leading dimension >= 2F");
+  NMB_REQUIRE(act == nullptr || (ldact >= f && ldact % 8 == 0 && nmb::aligned16(act)),
+              "gemm_gate_up_swiglu_bwd: act must be 16-byte aligned [M, F] with a leading dimension multiple of 8");
+  NMB_REQUIRE_SUPPORTED(2 * (2 * f * ldwgu) < (int64_t{1} << 31),
+                        "gemm_gate_up_swiglu_bwd: the gate/up weight spans more than 2 GiB");
+  if (m == 0 || f == 0) return NMB_OK;
+  const nmb::Plan none{0, 1, 0, 0.0};
+  nmb::GemmArgs g1 = nmb::make_args(m, f, k1, 1.f, a1, lda1, wgu, ldwgu, 0.f, nullptr, 0, nullptr, 0, nullptr, none);
+  nmb::GemmArgs g2 = nmb::make_args(m, f, k2, 1.f, a2, lda2, wd, ldwd, 0.f, nullptr, 0, act, ldact, nullptr, none);
+  g2.swb_dgu = static_cast<nmb::bf16*>(dgu);
+  g2.swb_lddgu = lddgu;
+  st = nmb::prepare<256, 128>(g2);
+  if (st != NMB_OK) return st;
+  if (b_layout == 0)
+    hipLaunchKernelGGL((nmb::gemm_gu_swb_kernel<true>), dim3(static_cast<unsigned>(g2.per_xcd * 8)), dim3(512),
+                       0, stream, g1, g2);
+  else
+    hipLaunchKernelGGL((nmb::gemm_gu_swb_kernel<false>), dim3(static_cast<unsigned>(g2.per_xcd * 8)), dim3(512),
+                       0, stream, g1, g2);
+  NMB_CHECK_LAUNCH("gemm gate_up swiglu_bwd");
+  return NMB_OK;
 }

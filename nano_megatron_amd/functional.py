@@ -572,6 +572,38 @@ def mm_swiglu_bwd(dy: Tensor, wd: Tensor, gu: Tensor, *, act: bool = True) -> tu
     return dgu, out
 
 
+def mm_gate_up_swiglu_bwd(a: Tensor, w_gu: Tensor, dy: Tensor, wd: Tensor, *, act: bool = True
+                          ) -> tuple[Tensor, Tensor | None]:
+    """The MLP backward of a recomputed block in one pass: the gate/up product
+    ``[g|u] = a [Wg; Wu]^T`` (``w_gu`` [2F, K], as ``mm_gate_up`` computes it),
+    ``ds = dy @ wd`` and the SwiGLU backward, for each tile of the output with
+    g, u and ds in registers (``nmb_gemm_bf16_gate_up_swiglu_bwd``): the same
+    (``dgu`` [M, 2F], ``silu(g) * u`` [M, F] if act) as ``mm_gate_up`` (product
+    only) then ``mm_swiglu_bwd``, bit for bit, without [g|u] in memory.  Other
+    dtypes run those two."""
+    m, k = a.shape
+    f2, k2 = w_gu.shape
+    m2, h = dy.shape
+    h2, f = wd.shape
+    if k != k2 or f2 != 2 * f or m2 != m or h2 != h:
+        raise ValueError("mm_gate_up_swiglu_bwd: a [M, K], w_gu [2F, K], dy [M, H] and wd [H, F] expected")
+    if a.dtype != torch.bfloat16:
+        _, gu = mm_gate_up(a, w_gu, act=False, gu=True)
+        return mm_swiglu_bwd(dy, wd, gu, act=act)
+    _require_gpu(a, w_gu, dy, wd)
+    if any(t.stride(1) != 1 or t.dtype != a.dtype for t in (a, w_gu, dy, wd)):
+        raise ValueError("mm_gate_up_swiglu_bwd: operands must be row-major and of one dtype")
+    dgu = torch.empty(m, f2, dtype=a.dtype, device=a.device)
+    out = torch.empty(m, f, dtype=a.dtype, device=a.device) if act else None
+    _lib.call(
+        "nmb_gemm_bf16_gate_up_swiglu_bwd", m, f, k, a.data_ptr(), max(a.stride(0), k), w_gu.data_ptr(),
+        max(w_gu.stride(0), k), h, dy.data_ptr(), max(dy.stride(0), h), 1, wd.data_ptr(), max(wd.stride(0), f),
+        dgu.data_ptr(), dgu.stride(0), _lib.ptr(out), out.stride(0) if out is not None else 0,
+        _lib.stream_of(a),
+    )
+    return dgu, out
+
+
 def mm_gate_up(a: Tensor, w_gu: Tensor, *, act: bool = True, gu: bool = False,
                act_out: Tensor | None = None, gu_out: Tensor | None = None
                ) -> tuple[Tensor | None, Tensor | None]:

@@ -922,3 +922,24 @@ def test_rmsnorm_bwd_dw_on_a_second_stream_is_bit_identical(device) -> None:
     dx1, dw1 = Fn.rmsnorm_bwd(x, w, dy, 1e-5, residual_grad=res, dw_stream=side)
     torch.cuda.current_stream(device).wait_stream(side)
     assert torch.equal(dx0, dx1) and torch.equal(dw0, dw1)
+
+
+@pytest.mark.parametrize("m,f,h", [(8192, 2736, 1024), (8192, 5632, 2048), (300, 200, 136), (512, 136, 264)])
+def test_gate_up_swiglu_bwd_equals_gate_up_then_swiglu_bwd(device, m, f, h) -> None:
+    """nmb_gemm_bf16_gate_up_swiglu_bwd (the recomputed gate/up product, ds =
+    dY Wd and the SwiGLU backward in one kernel, [g|u] never in memory) equals
+    the gate/up product followed by nmb_gemm_bf16_swiglu_bwd bit for bit, at
+    the config-3 and config-4 shapes and ragged ones (partial row and F tiles)."""
+    g = torch.Generator(device=device).manual_seed(m + f + h)
+    bf = torch.bfloat16
+    n2 = torch.randn(m, h, device=device, generator=g).to(bf)
+    wgu = (0.05 * torch.randn(2 * f, h, device=device, generator=g)).to(bf)
+    dy = torch.randn(m, h, device=device, generator=g).to(bf)
+    wd = (0.05 * torch.randn(h, f, device=device, generator=g)).to(bf)
+    _, gu = Fn.mm_gate_up(n2, wgu, act=False, gu=True)
+    dgu_ref, act_ref = Fn.mm_swiglu_bwd(dy, wd, gu)
+    dgu, act = Fn.mm_gate_up_swiglu_bwd(n2, wgu, dy, wd)
+    assert torch.equal(dgu, dgu_ref)
+    assert torch.equal(act, act_ref)
+    dgu2, none = Fn.mm_gate_up_swiglu_bwd(n2, wgu, dy, wd, act=False)
+    assert none is None and torch.equal(dgu2, dgu)
