@@ -330,16 +330,22 @@ def kernel_rooflines(device, only: str | None = None) -> list[dict]:
          (T * H + 3 * H * H + 3 * T * H) * E, 2.0 * T * 3 * H * H, "mfma", 2 * L),
         gemm_case("gemm_o_residual", T, H, H, False, False, 2 * L, residual=True),
         # the gate/up projection: the forward's applies SwiGLU in its epilogue; the
-        # recompute's writes the product [g|u] (same kernel and plan)
+        # product [g|u] alone (same kernel and plan) is what a block without
+        # checkpointing keeps (not in the full-recompute step)
         ("gemm_gate_up", lambda: Fn.mm_gate_up(x, w_gu, act=False, gu=True, gu_out=gu_buf),
-         (T * H + 2 * F * H + 2 * T * F) * E, 2.0 * T * 2 * F * H, "mfma", L),
+         (T * H + 2 * F * H + 2 * T * F) * E, 2.0 * T * 2 * F * H, "mfma", 0),
         ("gemm_gate_up_swiglu", lambda: Fn.mm_gate_up(x, w_gu, act=True, act_out=act),
          (T * H + 2 * F * H + T * F) * E, 2.0 * T * 2 * F * H, "mfma", L),
         gemm_case("gemm_down_residual", T, H, F, False, False, L, residual=True),
-        # ds = dY Wd with the SwiGLU backward as its epilogue (reads [g|u], writes
-        # [dg|du] and the re-emitted activation; ds never reaches memory)
+        # the recomputed block's MLP backward in one kernel: [g|u] = n2 [Wg;Wu]^T
+        # and ds = dY Wd per tile, the SwiGLU backward on both, [dg|du] and the
+        # re-emitted activation written; neither [g|u] nor ds reaches memory
+        ("gemm_gate_up_swiglu_bwd", lambda: Fn.mm_gate_up_swiglu_bwd(x, w_gu, dy_swb, wd_swb),
+         (2 * T * H + 2 * F * H + H * F + 3 * T * F) * E, 2.0 * T * 2 * F * H + 2.0 * T * F * H, "mfma", L),
+        # ds = dY Wd with the SwiGLU backward as its epilogue, reading a kept [g|u]
+        # (a block without checkpointing; not in the full-recompute step)
         ("gemm_d_swiglu_bwd", lambda: Fn.mm_swiglu_bwd(dy_swb, wd_swb, gu_swb),
-         (T * H + H * F + 5 * T * F) * E, 2.0 * T * F * H, "mfma", L),
+         (T * H + H * F + 5 * T * F) * E, 2.0 * T * F * H, "mfma", 0),
         gemm_case("gemm_dw_down", H, F, T, True, True, L),
         gemm_case("gemm_d_norm2", T, H, 2 * F, False, True, L),
         gemm_case("gemm_dw_gate_up", 2 * F, H, T, True, True, L),
