@@ -307,6 +307,11 @@ __global__ __launch_bounds__(64 * NWV, (D == 64 && NWV == 4) ? (TQ <= 2 ? 3 : 2)
 #pragma unroll
     for (int dt = 0; dt < NA; ++dt) acc[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
+  // Q (and the given LSE) land before the first K/V tile load is issued.  The
+  // compiler counts only its own loads: one still pending where the loop
+  // starts makes it wait for every outstanding load, the K/V tiles in flight
+  // included, before the first MFMA of every iteration.
+  wait_vmcnt<0>();
   const int64_t qa_wg_last = p.q_offset + min(qt * BQ + BQ - 1, p.Sq - 1);
   const int64_t kv_off = b * p.kv_sb + hk * p.kv_sh;
   // bytes from (b, key 0, hk) to the end of the last key row of a block (< 2^31, checked by the host)
@@ -314,6 +319,49 @@ __global__ __launch_bounds__(64 * NWV, (D == 64 && NWV == 4) ? (TQ <= 2 ? 3 : 2)
   const uint32_t row_bytes = static_cast<uint32_t>(p.kv_ss * 2);
   TileStream<D, NWV> ld;
   ld.init(p.kv_ss, wave, lane);
+
+  bf16* ob = o + b * p.o_sb + h * p.o_sh;
+  float* lb = lse + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
+  // O (and the LSE) of column tile t, normalised by its row sum
+  auto store_tile = [&](int t) {
+    int qi = qbase + CT * t + l16;
+    // opaque to the optimiser: the store addresses are formed here, not
+    // hoisted out of the key-tile loop into registers held across it
+    asm volatile("" : "+v"(qi));
+    // the row sum sits in element 0 of the sum tile in lane group 0; every
+    // lane group of the query needs it
+    float l = 0.f;
+    if constexpr (!FL) l = xor32_sum(xor16_sum(g == 0 ? acc[t][NA - 1][0] : 0.f));
+    if (qi >= p.Sq) return;
+    const float inv = FL ? 1.f : (l > 0.f ? 1.f / l : 0.f);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      bf16x4 wv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) wv[e] = static_cast<bf16>(acc[t][dt][e] * inv);
+      *reinterpret_cast<bf16x4*>(ob + static_cast<int64_t>(qi) * p.o_ss + dt * 16 + g * 4) = wv;
+    }
+    if (!FL && g == 0) lb[qi] = l > 0.f ? (m[t] * c + log2f(l)) * kLn2 : -__builtin_inff();
+  };
+  // With one K/V block the key tiles come in ascending order, and under
+  // causal masking a column tile is finished at the last tile it sees: its
+  // output is stored then, so that the stores overlap the remaining tiles'
+  // work instead of all following the loop (for the four-column-tile waves of
+  // short sequences, where that burst is a large part of the kernel).  (The stores count in vmcnt
+  // beside the tile loads; as loads complete in order, the wait at the top
+  // of the loop still implies that the oldest tile has landed.)
+  bool stored[TQ];
+  int fin[TQ];  // first key (tile-relative to the block) of column tile t's last tile, or -1
+#pragma unroll
+  for (int t = 0; t < TQ; ++t) {
+    stored[t] = false;
+    fin[t] = -1;
+    if (p.nblk == 1) {
+      int64_t last_key = p.Sk - 1;
+      if (p.causal) last_key = min(last_key, p.q_offset + min(qbase + CT * t + 15, p.Sq - 1) - kv.koff[0]);
+      if (last_key >= 0) fin[t] = static_cast<int>(last_key / BK) * BK;
+    }
+  }
 
   // compute cursor (blk, kt) and load cursor (pblk, pkt) over the visible tiles
   int nt = 0;
@@ -492,29 +540,20 @@ __global__ __launch_bounds__(64 * NWV, (D == 64 && NWV == 4) ? (TQ <= 2 ? 3 : 2)
         }
       }
     }
+    if constexpr (!kPhased) {
+#pragma unroll
+      for (int t = 0; t < TQ; ++t)
+        if (live[t] && k0 == fin[t]) {
+          store_tile(t);
+          stored[t] = true;
+        }
+    }
   }
   // no load may still write this workgroup's LDS when it ends
   wait_vmcnt<0>();
-  bf16* ob = o + b * p.o_sb + h * p.o_sh;
-  float* lb = lse + (static_cast<int64_t>(b) * p.Hq + h) * p.Sq;
 #pragma unroll
-  for (int t = 0; t < TQ; ++t) {
-    const int qi = qbase + CT * t + l16;
-    // the row sum sits in element 0 of the sum tile in lane group 0; every
-    // lane group of the query needs it
-    float l = 0.f;
-    if constexpr (!FL) l = xor32_sum(xor16_sum(g == 0 ? acc[t][NA - 1][0] : 0.f));
-    if (qi >= p.Sq) continue;
-    const float inv = FL ? 1.f : (l > 0.f ? 1.f / l : 0.f);
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      bf16x4 wv;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) wv[e] = static_cast<bf16>(acc[t][dt][e] * inv);
-      *reinterpret_cast<bf16x4*>(ob + static_cast<int64_t>(qi) * p.o_ss + dt * 16 + g * 4) = wv;
-    }
-    if (!FL && g == 0) lb[qi] = l > 0.f ? (m[t] * c + log2f(l)) * kLn2 : -__builtin_inff();
-  }
+  for (int t = 0; t < TQ; ++t)
+    if (!stored[t]) store_tile(t);
 }
 
 // ---------------------------------------------------------------- delta (fp32 path)
@@ -931,6 +970,10 @@ __global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel
     }
   };
   start(0);
+  // K/V in registers before the first Q/dO tile load is issued (as in the
+  // forward: a pending compiler-visible load at the loop would make every
+  // iteration wait for the tiles in flight)
+  wait_vmcnt<0>();
 #pragma unroll
   for (int st = 0; st < kStages - 1; ++st) issue(st, st);
   bool switched = false;
