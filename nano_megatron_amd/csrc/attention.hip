@@ -1008,6 +1008,10 @@ __global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel
       any = any || live[j];
     }
     if (!any) continue;
+    // The MFMAs below run for every key tile of the wave, live or not, with no
+    // branch between them, so that LDS reads and MFMAs are scheduled together;
+    // a tile that is not live gets zero P and dS (its keys are all masked) and
+    // adds nothing to dK and dV.
 
     if constexpr (kSliced) {
       // tile-relative queries [qmin, qend) see key tile j's key of this lane
@@ -1046,17 +1050,19 @@ __global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel
             const bf16x8 aq = Tile::row8(tq, mq * 16 + l16, ks * 32 + g * 8);
             const bf16x8 ad = Tile::row8(td, mq * 16 + l16, ks * 32 + g * 8);
 #pragma unroll
-            for (int j = 0; j < KT; ++j)
-              if (live[j]) {
-                s[m2][j] = mfma16(aq, kf[j][ks], s[m2][j]);
-                dp[m2][j] = mfma16(ad, vf[j][ks], dp[m2][j]);
-              }
+            for (int j = 0; j < KT; ++j) {
+              s[m2][j] = mfma16(aq, kf[j][ks], s[m2][j]);
+              dp[m2][j] = mfma16(ad, vf[j][ks], dp[m2][j]);
+            }
           }
         }
         bf16x8 pa[KT], da[KT];
 #pragma unroll
         for (int j = 0; j < KT; ++j) {
-          if (!live[j]) continue;
+          if (!live[j]) {  // formed, not visible: adds nothing
+            pa[j] = da[j] = zero8();
+            continue;
+          }
 #pragma unroll
           for (int m2 = 0; m2 < 2; ++m2)
 #pragma unroll
@@ -1073,11 +1079,10 @@ __global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel
           const bf16x8 bd = Tile::col8(td, 32 * s2, dt * 16, l16, g);
           const bf16x8 bq = Tile::col8(tq, 32 * s2, dt * 16, l16, g);
 #pragma unroll
-          for (int j = 0; j < KT; ++j)
-            if (live[j]) {
-              dva[j][dt] = mfma16(pa[j], bd, dva[j][dt]);
-              dka[j][dt] = mfma16(da[j], bq, dka[j][dt]);
-            }
+          for (int j = 0; j < KT; ++j) {
+            dva[j][dt] = mfma16(pa[j], bd, dva[j][dt]);
+            dka[j][dt] = mfma16(da[j], bq, dka[j][dt]);
+          }
         }
       }
     } else {
@@ -1097,17 +1102,20 @@ __global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel
           const bf16x8 aq = Tile::row8(tq, mq * 16 + l16, ks * 32 + g * 8);
           const bf16x8 ad = Tile::row8(td, mq * 16 + l16, ks * 32 + g * 8);
 #pragma unroll
-          for (int j = 0; j < KT; ++j)
-            if (live[j]) {
-              s[mq][j] = mfma16(aq, kf[j][ks], s[mq][j]);
-              dp[mq][j] = mfma16(ad, vf[j][ks], dp[mq][j]);
-            }
+          for (int j = 0; j < KT; ++j) {
+            s[mq][j] = mfma16(aq, kf[j][ks], s[mq][j]);
+            dp[mq][j] = mfma16(ad, vf[j][ks], dp[mq][j]);
+          }
         }
       }
       bf16x8 pa[2][KT], da[2][KT];
 #pragma unroll
       for (int j = 0; j < KT; ++j) {
-        if (!live[j]) continue;
+        if (!live[j]) {
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) pa[s2][j] = da[s2][j] = zero8();
+          continue;
+        }
         // tile-relative queries [qmin, qend) see this lane's key (qend: the
         // queries past Sq, whose zero-filled rows must not count)
         int qmin = 0;
@@ -1145,11 +1153,10 @@ __global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel
           const bf16x8 bd = Tile::col8(td, 32 * s2, dt * 16, l16, g);
           const bf16x8 bq = Tile::col8(tq, 32 * s2, dt * 16, l16, g);
 #pragma unroll
-          for (int j = 0; j < KT; ++j)
-            if (live[j]) {
-              dva[j][dt] = mfma16(pa[s2][j], bd, dva[j][dt]);
-              dka[j][dt] = mfma16(da[s2][j], bq, dka[j][dt]);
-            }
+          for (int j = 0; j < KT; ++j) {
+            dva[j][dt] = mfma16(pa[s2][j], bd, dva[j][dt]);
+            dka[j][dt] = mfma16(da[s2][j], bq, dka[j][dt]);
+          }
         }
       }
     }
