@@ -51,16 +51,16 @@ class CapturedTrainStep:
                              "replay cannot reuse: capture without it")
         if getattr(model, "lm_head", None) is None:
             raise ValueError("CapturedTrainStep needs the stage that owns the LM head (the loss)")
+        rates = (getattr(m, "dropout", 0.0) for m in model.modules())
+        if any(isinstance(r, (int, float)) and not isinstance(r, bool) and r > 0.0 for r in rates):
+            raise ValueError("dropout masks are keyed by seeds passed from the host at launch, which "
+                             "every replay of a captured graph would repeat: capture with dropout 0")
         mode = getattr(ckpt, "mode", "none")
         if mode in ("full", "selective") and any(not layer.fusable() for layer in getattr(model, "layers", ())):
             raise ValueError("a layer outside the fused block (biases, other head sizes or components) "
                              "recomputes under torch.utils.checkpoint, whose RNG-state replay cannot be "
                              f"captured: capture with activation_checkpoint.mode 'none' or fused layers only "
                              f"(mode {mode!r})")
-        rates = (getattr(m, "dropout", 0.0) for m in model.modules())
-        if any(isinstance(r, (int, float)) and not isinstance(r, bool) and r > 0.0 for r in rates):
-            raise ValueError("dropout masks are keyed by seeds passed from the host at launch, which "
-                             "every replay of a captured graph would repeat: capture with dropout 0")
         self.model, self.optimizer = model, optimizer
         self.device = input_ids.device
         self.vocab = model.lm_head.weight.shape[0]
