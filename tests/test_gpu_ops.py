@@ -170,6 +170,12 @@ ATTN_CASES = [
     (3, 2, 2, 33, 33, 128, torch.bfloat16, 0, True),
     (1, 16, 2, 96, 96, 64, torch.bfloat16, 0, True),
     (1, 2, 1, 200, 64, 128, torch.bfloat16, 0, False),
+    # 512-1023 queries at head dim 64 (eight waves of four column tiles, each
+    # column tile storing its output at its last key tile): an offset query
+    # block over a ragged key range, and the non-causal case (every tile stores
+    # at the last key tile)
+    (1, 4, 2, 700, 764, 64, torch.bfloat16, 64, True),
+    (1, 2, 2, 600, 600, 64, torch.bfloat16, 0, False),
 ]
 
 
