@@ -413,14 +413,7 @@ def kernel_rooflines(device, only: str | None = None) -> list[dict]:
             entry.update(flops=int(flops), tflops=round(tf, 1), mfma_frac=round(tf / BF16_PEAK_TFLOPS, 4))
         out.append(entry)
 
-    for name, fn, nbytes, flops, bound, per_step in cases:
-        if only is not None and name != only:
-            continue
-        sets = 1
-        fns = [fn]
-        if bound == "hbm" and not flops:
-            sets = _input_sets(nbytes)
-            fns = [fn() for _ in range(sets)]
+    def time_launches(fns, sets):
         # launches captured in a HIP graph and replayed: the events then time GPU
         # work only, not the host cost of issuing each launch
         n = sets * max(1, math.ceil(20 / sets))
@@ -447,8 +440,35 @@ def kernel_rooflines(device, only: str | None = None) -> list[dict]:
             end.record(stream)
             end.synchronize()
             us = min(us, start.elapsed_time(end) * 1e3 / (n * reps))
-        del graph, fns
+        del graph
+        return us
+
+    def mk_copy(nbytes):
+        # a plain device copy moving the same bytes (half read, half written)
+        def make():
+            src = torch.empty(max(nbytes // 2, 1), dtype=torch.uint8, device=device).fill_(1)
+            dst = torch.empty_like(src)
+            return lambda: dst.copy_(src)
+        return make
+
+    for name, fn, nbytes, flops, bound, per_step in cases:
+        if only is not None and name != only:
+            continue
+        sets = 1
+        fns = [fn]
+        if bound == "hbm" and not flops:
+            sets = _input_sets(nbytes)
+            fns = [fn() for _ in range(sets)]
+        us = time_launches(fns, sets)
+        del fns
         record(name, us, nbytes, flops, bound, per_step, sets)
+        if bound == "hbm":
+            # the same bytes moved by a plain copy, timed the same way: the
+            # ceiling at this transfer size (launch ramp and tail included)
+            cfns = [mk_copy(nbytes)() for _ in range(_input_sets(nbytes))]
+            cus = time_launches(cfns, len(cfns))
+            del cfns
+            out[-1].update(same_size_copy_us=round(cus, 2), same_size_copy_frac=round(cus / us, 3))
 
     if only is None or only == "adamw_step":
         # the optimizer of the step: global grad-norm clip + fp32-master AdamW over the
