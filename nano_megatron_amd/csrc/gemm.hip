@@ -242,16 +242,38 @@ struct Stages {
   static_assert(S >= 2, "two LDS stages at least");
 };
 
+// Byte offsets of K-tile stage st of the A and B operand tiles from sA and
+// sB: consecutive stages.
+template <int TBM, int TBN, int BKT>
+struct LinearStages {
+  __device__ static uint32_t a(int st) { return static_cast<uint32_t>(st) * (TBM * BKT * 2u); }
+  __device__ static uint32_t b(int st) { return static_cast<uint32_t>(st) * (TBN * BKT * 2u); }
+};
+
+// Called at the start of every K tile, after the barrier (no-op).
+struct NoHook {
+  __device__ void operator()(int, int) const {}
+};
+
+__device__ __forceinline__ const bf16* at_byte(const void* base, uint32_t off) {
+  return reinterpret_cast<const bf16*>(reinterpret_cast<const char*>(base) + off);
+}
+
 // The K loop of one tile: acc[i][j] += the wave's 16 x 16 MFMA tiles of
 // op(A) op(B) over [k_begin, k_end), the operands streamed through the S LDS
-// stages sA / sB by the loaders (the wave tile at rows wm, columns wn).
-// Returns with every load of the loop complete; the other waves may still
-// read the last stage.
-template <int TBM, int TBN, int NW, int BKT, bool A_KC, bool B_KC, int TM, int TN>
+// stages (at sA + Map::a(stage), sB + Map::b(stage)) by the loaders (the
+// wave tile at rows wm, columns wn).  The first `pre` K tiles may have been
+// issued by the caller already (into their stages, by the same loaders, with
+// nothing issued after them); hook(kt, nk) runs at the start of each K tile,
+// after the barrier.  Returns with every load of the loop complete; the other
+// waves may still read the last stage.
+template <int TBM, int TBN, int NW, int BKT, bool A_KC, bool B_KC, int TM, int TN,
+          class Map = LinearStages<TBM, TBN, BKT>, class Hook = NoHook>
 __device__ __forceinline__ void k_loop(const Loader<TBM, A_KC, BKT, NW>& la,
                                        const Loader<TBN, B_KC, BKT, NW>& lb, bf16 (*sA)[TBM * BKT],
                                        bf16 (*sB)[TBN * BKT], f32x4 (&acc)[TM][TN], int wm, int wn,
-                                       int k_begin, int k_end, int wave, int lane) {
+                                       int k_begin, int k_end, int wave, int lane, int pre = 0,
+                                       const Hook& hook = Hook{}) {
   constexpr int KSTEPS = BKT / 32;
   constexpr int S = Stages<TBM, TBN, NW, BKT>::S;
   Frags<TBM, A_KC, TM, BKT> fra;
@@ -275,16 +297,16 @@ __device__ __forceinline__ void k_loop(const Loader<TBM, A_KC, BKT, NW>& la,
   auto issue = [&](int kt) {
     const int st = kt % S;
     if constexpr (kScalarIssue) {
-      la.issue_s(a_lds + st * (TBM * BKT * 2u), k_begin + kt * BKT, k_end);
-      lb.issue_s(b_lds + st * (TBN * BKT * 2u), k_begin + kt * BKT, k_end);
+      la.issue_s(a_lds + Map::a(st), k_begin + kt * BKT, k_end);
+      lb.issue_s(b_lds + Map::b(st), k_begin + kt * BKT, k_end);
     } else {
-      la.issue(&sA[st][0], k_begin + kt * BKT, k_end, wave);
-      lb.issue(&sB[st][0], k_begin + kt * BKT, k_end, wave);
+      la.issue(at_byte(&sA[0][0], Map::a(st)), k_begin + kt * BKT, k_end, wave);
+      lb.issue(at_byte(&sB[0][0], Map::b(st)), k_begin + kt * BKT, k_end, wave);
     }
   };
 #pragma unroll
   for (int p = 0; p < S - 1; ++p)
-    if (p < nk) issue(p);
+    if (p >= pre && p < nk) issue(p);
   for (int kt = 0; kt < nk; ++kt) {
     // tiles issued after tile kt: min(nk - 1, kt + S - 2) - kt
     const int after = min(nk - 1, kt + S - 2) - kt;
@@ -292,14 +314,17 @@ __device__ __forceinline__ void k_loop(const Loader<TBM, A_KC, BKT, NW>& la,
     else if (after == 1) wait_vmcnt<kLoads>();
     else wait_vmcnt<0>();
     lds_barrier();
+    hook(kt, nk);
     const int st = kt % S;
+    const bf16* ta = at_byte(&sA[0][0], Map::a(st));
+    const bf16* tb = at_byte(&sB[0][0], Map::b(st));
     bf16x8 fa[KSTEPS][TM], fb[KSTEPS][TN];
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j) fb[ks][j] = frb.get(&sB[st][0], j, 32 * ks);
+      for (int j = 0; j < TN; ++j) fb[ks][j] = frb.get(tb, j, 32 * ks);
 #pragma unroll
-      for (int i = 0; i < TM; ++i) fa[ks][i] = fra.get(&sA[st][0], i, 32 * ks);
+      for (int i = 0; i < TM; ++i) fa[ks][i] = fra.get(ta, i, 32 * ks);
     }
     if constexpr (KSTEPS == 2) {
       // The wave issues in order and a full LDS queue stalls it, MFMAs
@@ -787,6 +812,15 @@ __global__ __launch_bounds__(512, 1) void gemm_pair_kernel(GemmArgs g1, GemmArgs
 // products store them and every K sum runs in the order of the other
 // kernels, so the outputs equal nmb_gemm_bf16_swiglu (product only) followed
 // by nmb_gemm_bf16_swiglu_bwd bit for bit, without [g|u] ever being written.
+// Phase 2's three stages in the 160 KB of LDS, placed so that its first two
+// (A 32 KB + B 16 KB each) fall where phase 1's last K tile does not read
+// (phase 1 reads stage 1 in its last tile when its tile count is even: A at
+// [32, 64) KB and B at [96, 128) KB): A at 0, 64, 32 KB, B at 128, 144, 96 KB.
+struct GuSwbPhase2Stages {
+  __device__ static uint32_t a(int st) { return st == 0 ? 0u : (st == 1 ? 65536u : 32768u); }
+  __device__ static uint32_t b(int st) { return st == 0 ? 131072u : (st == 1 ? 147456u : 98304u); }
+};
+
 template <bool B2_KC>
 __global__ __launch_bounds__(512, 1) void gemm_gu_swb_kernel(GemmArgs g1, GemmArgs g2) {
   constexpr int TBM = 256, TB1 = 256, TB2 = 128, NW = 8, BKT = 64, WAVES_N = 2;
@@ -794,9 +828,9 @@ __global__ __launch_bounds__(512, 1) void gemm_gu_swb_kernel(GemmArgs g1, GemmAr
   constexpr int TM = WM / 16, TN1 = WN1 / 16, TN2 = WN2 / 16;
   constexpr int S1 = Stages<TBM, TB1, NW, BKT>::S, S2 = Stages<TBM, TB2, NW, BKT>::S;
   constexpr int A1 = S1 * TBM * BKT, B1 = S1 * TB1 * BKT;
-  constexpr int A2 = S2 * TBM * BKT, B2 = S2 * TB2 * BKT;
-  constexpr int kElems = A1 + B1 > A2 + B2 ? A1 + B1 : A2 + B2;
-  static_assert(A1 % 512 == 0 && A2 % 512 == 0, "B stages stay 1 KB aligned");
+  constexpr int kElems = 160 * 1024 / 2;
+  static_assert(S1 == 2 && S2 == 3 && A1 + B1 <= kElems, "the stage placement assumes 2 + 3 stages");
+  static_assert(A1 % 512 == 0, "B stages stay 1 KB aligned");
   static_assert(TN1 == 2 * TN2, "a wave's gate/up columns pair with its ds columns");
   __shared__ __attribute__((aligned(1024))) bf16 smem[kElems];
 
@@ -816,6 +850,41 @@ __global__ __launch_bounds__(512, 1) void gemm_gu_swb_kernel(GemmArgs g1, GemmAr
   const int wm = (wave / WAVES_N) * WM, wc = wave % WAVES_N;
   const int va = min(TBM, M - m0);
 
+  // phase 2's loaders (ds = dY Wd for the same tile)
+  auto init2 = [&](Loader<TBM, true, BKT, NW>& la, Loader<TB2, B2_KC, BKT, NW>& lb, int lane) {
+    la.init(g2.a + static_cast<int64_t>(m0) * g2.lda, g2.lda, va,
+            static_cast<uint32_t>((static_cast<int64_t>(va - 1) * g2.lda + g2.K) * 2), wave, lane);
+    const int vb = min(TB2, F - f0);
+    const bf16* b0 = B2_KC ? g2.b + static_cast<int64_t>(f0) * g2.ldb : g2.b + f0;
+    const int64_t eb = B2_KC ? (static_cast<int64_t>(vb - 1) * g2.ldb + g2.K) * 2
+                             : (static_cast<int64_t>(g2.K - 1) * g2.ldb + (F - f0)) * 2;
+    lb.init(b0, g2.ldb, vb, static_cast<uint32_t>(eb), wave, lane);
+  };
+  // Phase 2's first two K tiles are loaded during phase 1's last K tile (into
+  // stages that tile does not read), so that phase 2 starts on landed data
+  // instead of waiting a full load latency.  Phase 1 ends in its stage 1 when
+  // it has an even number of K tiles; otherwise phase 2 loads them itself.
+  const int nk1 = (g1.K + BKT - 1) / BKT, nk2 = (g2.K + BKT - 1) / BKT;
+  const int pre2 = (nk1 >= 2 && nk1 % 2 == 0) ? min(S2 - 1, nk2) : 0;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  auto prefetch2 = [&](int kt, int nk) {
+    if (pre2 == 0 || kt != nk - 1) return;
+    Loader<TBM, true, BKT, NW> la;
+    Loader<TB2, B2_KC, BKT, NW> lb;
+    // the lane index made opaque, so that the offsets are formed here and not
+    // hoisted out of phase 1's loop into registers held (or spilled) across it
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    init2(la, lb, ln);
+    // as k_loop issues them (scalar issue for 256 x 128 tiles)
+    const uint32_t a_lds = lds_offset(smem) + 1024u * wave_u * Loader<TBM, true, BKT, NW>::kPer;
+    const uint32_t b_lds = lds_offset(smem) + 1024u * wave_u * Loader<TB2, B2_KC, BKT, NW>::kPer;
+    for (int p = 0; p < pre2; ++p) {
+      la.issue_s(a_lds + GuSwbPhase2Stages::a(p), p * BKT, g2.K);
+      lb.issue_s(b_lds + GuSwbPhase2Stages::b(p), p * BKT, g2.K);
+    }
+  };
+
   // phase 1: the gate/up product of the tile's F columns (128 gate, 128 up)
   f32x4 acc1[TM][TN1];
 #pragma unroll
@@ -829,9 +898,9 @@ __global__ __launch_bounds__(512, 1) void gemm_gu_swb_kernel(GemmArgs g1, GemmAr
             static_cast<uint32_t>((static_cast<int64_t>(va - 1) * g1.lda + g1.K) * 2), wave, lane);
     lb.init_pairs(g1.b, g1.ldb, F, f0,
                   static_cast<uint32_t>((static_cast<int64_t>(2 * F - 1) * g1.ldb + g1.K) * 2), wave, lane);
-    k_loop<TBM, TB1, NW, BKT, true, true, TM, TN1>(
+    k_loop<TBM, TB1, NW, BKT, true, true, TM, TN1, LinearStages<TBM, TB1, BKT>, decltype(prefetch2)>(
         la, lb, reinterpret_cast<bf16(*)[TBM * BKT]>(smem), reinterpret_cast<bf16(*)[TB1 * BKT]>(smem + A1),
-        acc1, wm, wc * WN1, 0, g1.K, wave, lane);
+        acc1, wm, wc * WN1, 0, g1.K, wave, lane, 0, prefetch2);
   }
   // g and u as the product stores them (bf16); column tile jj of phase 2 is
   // gate tile (jj & 1) + 4 (jj >> 1) of phase 1, its up partner 2 tiles on
@@ -858,16 +927,10 @@ __global__ __launch_bounds__(512, 1) void gemm_gu_swb_kernel(GemmArgs g1, GemmAr
   {
     Loader<TBM, true, BKT, NW> la;
     Loader<TB2, B2_KC, BKT, NW> lb;
-    la.init(g2.a + static_cast<int64_t>(m0) * g2.lda, g2.lda, va,
-            static_cast<uint32_t>((static_cast<int64_t>(va - 1) * g2.lda + g2.K) * 2), wave, lane);
-    const int vb = min(TB2, F - f0);
-    const bf16* b0 = B2_KC ? g2.b + static_cast<int64_t>(f0) * g2.ldb : g2.b + f0;
-    const int64_t eb = B2_KC ? (static_cast<int64_t>(vb - 1) * g2.ldb + g2.K) * 2
-                             : (static_cast<int64_t>(g2.K - 1) * g2.ldb + (F - f0)) * 2;
-    lb.init(b0, g2.ldb, vb, static_cast<uint32_t>(eb), wave, lane);
-    k_loop<TBM, TB2, NW, BKT, true, B2_KC, TM, TN2>(
-        la, lb, reinterpret_cast<bf16(*)[TBM * BKT]>(smem), reinterpret_cast<bf16(*)[TB2 * BKT]>(smem + A2),
-        acc2, wm, wc * WN2, 0, g2.K, wave, lane);
+    init2(la, lb, lane);
+    k_loop<TBM, TB2, NW, BKT, true, B2_KC, TM, TN2, GuSwbPhase2Stages>(
+        la, lb, reinterpret_cast<bf16(*)[TBM * BKT]>(smem), reinterpret_cast<bf16(*)[TB2 * BKT]>(smem),
+        acc2, wm, wc * WN2, 0, g2.K, wave, lane, pre2);
   }
 
   // the SwiGLU backward on the tile: lane (l16, q4) holds row wm + 16 i + l16,
