@@ -930,7 +930,10 @@ def test_rmsnorm_bwd_dw_on_a_second_stream_is_bit_identical(device) -> None:
     assert torch.equal(dx0, dx1) and torch.equal(dw0, dw1)
 
 
-@pytest.mark.parametrize("m,f,h", [(8192, 2736, 1024), (8192, 5632, 2048), (300, 200, 136), (512, 136, 264)])
+# the config shapes, odd K-tile counts (136, 264: the second product loads its
+# own first tiles), two K tiles (128: both preloaded) and one (64)
+@pytest.mark.parametrize("m,f,h", [(8192, 2736, 1024), (8192, 5632, 2048), (300, 200, 136), (512, 136, 264),
+                                   (256, 136, 128), (300, 72, 64)])
 def test_gate_up_swiglu_bwd_equals_gate_up_then_swiglu_bwd(device, m, f, h) -> None:
     """nmb_gemm_bf16_gate_up_swiglu_bwd (the recomputed gate/up product, ds =
     dY Wd and the SwiGLU backward in one kernel, [g|u] never in memory) equals
