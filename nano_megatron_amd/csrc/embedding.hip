@@ -12,9 +12,9 @@
 // chunk) owns RV table rows x CH columns.  It takes the token ids in rounds of
 // 2048 (8 consecutive ids per thread, loaded together), lists the tokens whose
 // id falls in its rows in token order (a workgroup prefix sum of each
-// thread's hits), and adds their gradient chunks, eight rows' loads in flight
-// at a time, to fp32 accumulators in LDS in list order, then writes its rows
-// once.  Every output-gradient element is read by one workgroup; the ids
+// thread's hits), and once the ids are done (or the list is full) adds their
+// gradient chunks, sixteen rows' loads in flight at a time, to fp32
+// accumulators in LDS in list order, then writes its rows once.  Every output-gradient element is read by one workgroup; the ids
 // (8 bytes per token) are read by all of them from L2.
 #include "common.h"
 #include "vec.h"
@@ -26,6 +26,8 @@ constexpr int RV = 16;        // table rows per workgroup
 constexpr int CH = 1024;      // columns per workgroup (4 per thread)
 constexpr int kPer = 8;       // token ids per thread per round
 constexpr int kRound = 256 * kPer;  // tokens per round
+constexpr int kList = 3072;    // listed tokens held before their rows are added (12 KB of LDS)
+constexpr int kBatch = 16;     // gradient rows loaded together
 
 template <typename T>
 __global__ __launch_bounds__(256) void embedding_fwd_kernel(const T* __restrict__ table,
@@ -80,7 +82,7 @@ __global__ __launch_bounds__(256, 2) void embedding_bwd_kernel(const T* __restri
                                                                int64_t n_tokens, int64_t vocab,
                                                                int64_t hidden) {
   __shared__ float4 acc[RV * CH / 4];  // 64 KB: row r, this thread's 4 columns at [r * CH / 4 + thread]
-  __shared__ int list[kRound];     // matching tokens of the round, in order: offset * RV + row
+  __shared__ int list[kList];          // matching tokens in token order: token * RV + row
   __shared__ int wave_total[4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t row_blocks = (vocab + RV - 1) / RV;
@@ -88,11 +90,58 @@ __global__ __launch_bounds__(256, 2) void embedding_bwd_kernel(const T* __restri
   const int64_t c0 = (blockIdx.x / row_blocks) * CH;
   const int cols = static_cast<int>(min<int64_t>(CH, hidden - c0));
   const int c = threadIdx.x * 4;  // this thread's 4 columns
+  const int cc = c < cols ? c : 0;  // (a thread past the chunk's columns loads column 0, unused)
 #pragma unroll
   for (int r = 0; r < RV; ++r) acc[r * (CH / 4) + threadIdx.x] = make_float4(0.f, 0.f, 0.f, 0.f);
 
-  // the ids of a round: kPer consecutive tokens per thread, loaded together;
-  // the next round's are in flight while this round's rows are added
+  // the tied LM head's rows of this block, loaded first: nothing depends on
+  // them until the end (rows past the table read its last row, not stored)
+  float prior[RV][4];
+#pragma unroll
+  for (int r = 0; r < RV; ++r) {
+    if (grad_in != nullptr) {
+      load4<T>(grad_in + min(v0 + r, vocab - 1) * hidden + c0 + cc, prior[r]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) prior[r][e] = 0.f;
+    }
+  }
+
+  // the listed gradient rows, in token order, into the accumulators: all of
+  // a batch's loads in flight together
+  int listed = 0;  // workgroup-uniform
+  auto add_listed = [&]() {
+    if (c < cols) {
+      for (int k0 = 0; k0 < listed; k0 += kBatch) {
+        float v[kBatch][4];
+        int row[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          const int e = list[min(k0 + u, listed - 1)];
+          row[u] = e % RV;
+          load4<T>(dout + static_cast<int64_t>(e / RV) * hidden + c0 + c, v[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          if (k0 + u < listed) {  // (no break: the loaded rows stay in registers)
+            float4& a = acc[row[u] * (CH / 4) + threadIdx.x];
+            float4 t = a;
+            t.x += v[u][0];
+            t.y += v[u][1];
+            t.z += v[u][2];
+            t.w += v[u][3];
+            a = t;
+          }
+        }
+      }
+    }
+    listed = 0;
+  };
+
+  // the ids in rounds of kPer consecutive tokens per thread, the next round's
+  // in flight while this round's are listed; the rows are added once the
+  // list is full or the ids are done, so that their loads are not spread
+  // over the rounds one latency each
   int64_t id[kPer], next[kPer];
 #pragma unroll
   for (int j = 0; j < kPer; ++j) next[j] = -1;
@@ -103,7 +152,13 @@ __global__ __launch_bounds__(256, 2) void embedding_bwd_kernel(const T* __restri
   };
   load_ids(0, id);
   for (int64_t base = 0; base < n_tokens; base += kRound) {
-    const int t_off = threadIdx.x * kPer;
+    if (listed > kList - kRound) {
+      // a full round may not fit: add what is listed first (every thread is
+      // past the previous round's list writes: second barrier below)
+      add_listed();
+      __syncthreads();  // every thread is done reading the list
+    }
+    const int t_off = static_cast<int>(base) + threadIdx.x * kPer;
     int hits = 0;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) hits += id[j] >= v0 && id[j] < v0 + RV;
@@ -115,57 +170,22 @@ __global__ __launch_bounds__(256, 2) void embedding_bwd_kernel(const T* __restri
       if (lane >= d) incl += y;
     }
     if (lane == 63) wave_total[wave] = incl;
-    __syncthreads();  // wave totals ready; the previous round's list is consumed
-    int pos = incl - hits;
+    __syncthreads();  // wave totals ready
+    int pos = listed + incl - hits;
     for (int w = 0; w < wave; ++w) pos += wave_total[w];
     const int total = wave_total[0] + wave_total[1] + wave_total[2] + wave_total[3];
 #pragma unroll
     for (int j = 0; j < kPer; ++j)
       if (id[j] >= v0 && id[j] < v0 + RV) list[pos++] = (t_off + j) * RV + static_cast<int>(id[j] - v0);
-    __syncthreads();
+    listed += total;
+    __syncthreads();  // the round's list entries are visible; wave totals read
     if (base + kRound < n_tokens) load_ids(base + kRound, next);
-    if (c < cols) {
-      // the listed gradient rows in token order, loaded eight at a time
-      for (int k0 = 0; k0 < total; k0 += 8) {
-        float v[8][4];
-        int row[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int e = list[min(k0 + u, total - 1)];
-          row[u] = e % RV;
-          load4<T>(dout + (base + e / RV) * hidden + c0 + c, v[u]);
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          if (k0 + u >= total) break;
-          float4& a = acc[row[u] * (CH / 4) + threadIdx.x];
-          float4 t = a;
-          t.x += v[u][0];
-          t.y += v[u][1];
-          t.z += v[u][2];
-          t.w += v[u][3];
-          a = t;
-        }
-      }
-    }
 #pragma unroll
     for (int j = 0; j < kPer; ++j) id[j] = next[j];
   }
+  add_listed();
   __syncthreads();
   if (c >= cols) return;
-  // the tied LM head's rows, all loaded before any is used (rows past the
-  // table read its last row and are not stored)
-  float prior[RV][4];
-#pragma unroll
-  for (int r = 0; r < RV; ++r) {
-    const int64_t o = min(v0 + r, vocab - 1) * hidden + c0 + c;
-    if (grad_in != nullptr) {
-      load4<T>(grad_in + o, prior[r]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) prior[r][e] = 0.f;
-    }
-  }
 #pragma unroll
   for (int r = 0; r < RV; ++r) {
     if (v0 + r >= vocab) break;
@@ -218,6 +238,9 @@ int bwd_impl(const void* dout, const int64_t* ids, const void* grad_in, void* gr
                         (long long)hidden);
   const int64_t blocks = ((vocab + RV - 1) / RV) * ((hidden + CH - 1) / CH);
   NMB_REQUIRE(blocks < (int64_t{1} << 31), "embedding_bwd: table too large");
+  // the token list holds token * RV + row in 32 bits
+  NMB_REQUIRE_SUPPORTED(n_tokens < (int64_t{1} << 27), "embedding_bwd: %lld tokens exceed the supported 2^27",
+                        (long long)n_tokens);
   // rows of 4 elements are read as one 8-byte (bf16) or 16-byte (fp32) access
   const uintptr_t align = 4 * sizeof(T) - 1;
   NMB_REQUIRE((reinterpret_cast<uintptr_t>(dout) & align) == 0 &&
