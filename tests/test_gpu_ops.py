@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import pytest
 import torch
 
@@ -650,6 +651,31 @@ def test_embedding_matches_torch(device, dtype, vocab, hidden, tokens) -> None:
         Fn._lib.call("nmb_embedding_bwd", dout.data_ptr(), ids.data_ptr(), Fn._lib.ptr(grad_in), again.data_ptr(),
                      tokens, vocab, hidden, Fn._lib.dtype_code(dtype), Fn._lib.stream_of(dout))
         assert torch.equal(grad, again)  # deterministic
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_embedding_backward_hot_row_in_token_order(device, dtype) -> None:
+    """One id taking 12,000 of 20,000 tokens (its 16-row block lists more
+    tokens than one pass holds, so the rows are added in several batches):
+    that row equals the fp32 sum of its gradient rows taken one after another
+    in token order (numpy's sequential accumulate), rounded to the dtype, bit
+    for bit; every other row is the fp64 scatter-add within the dtype's bar."""
+    vocab, hidden, tokens, hot = 512, 256, 20000, 5
+    g = torch.Generator(device=device).manual_seed(41)
+    ids = torch.randint(0, vocab, (tokens,), device=device, generator=g)
+    ids[:12000] = hot
+    dout = torch.randn(tokens, hidden, device=device, generator=g).to(dtype)
+    grad = torch.empty(vocab, hidden, device=device, dtype=dtype)
+    Fn._lib.call("nmb_embedding_bwd", dout.data_ptr(), ids.data_ptr(), None, grad.data_ptr(),
+                 tokens, vocab, hidden, Fn._lib.dtype_code(dtype), Fn._lib.stream_of(dout))
+    rows = dout[ids == hot].float().cpu().numpy()
+    seq = np.add.accumulate(rows, axis=0, dtype=np.float32)[-1]
+    assert torch.equal(grad[hot].cpu(), torch.from_numpy(seq).to(dtype))
+    sums = torch.zeros(vocab, hidden, dtype=torch.float64, device=device).index_add_(0, ids, dout.double())
+    tol = dict(rtol=1e-2, atol=2e-2) if dtype == torch.bfloat16 else dict(rtol=1e-5, atol=1e-5)
+    keep = torch.arange(vocab, device=device) != hot
+    torch.testing.assert_close(grad[keep].float(), sums[keep].to(dtype).float(), **tol)
 
 
 @pytest.mark.gpu
