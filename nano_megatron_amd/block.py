@@ -35,8 +35,9 @@ sub-blocks' products.
 
 from __future__ import annotations
 
+import weakref
 from dataclasses import dataclass
-from typing import Any
+from typing import Any, Callable
 
 import torch
 from torch import Tensor
@@ -217,8 +218,12 @@ class _SideProducts:
             self.main.wait_stream(self.side)
 
 
-def block_backward(acts: dict, dy: Tensor, w: tuple[Tensor, ...], m: BlockMeta, shape) -> tuple:
-    """Gradients (dx, dw_in, dWq, dWk, dWv, dWo, dw_post, dWg, dWu, dWd) of the block."""
+def block_backward(acts: dict, dy: Tensor, w: tuple[Tensor, ...], m: BlockMeta, shape,
+                   prefetch: Callable[[], None] | None = None) -> tuple:
+    """Gradients (dx, dw_in, dWq, dWk, dWv, dWo, dw_post, dWg, dWu, dWd) of the
+    block.  ``prefetch`` (the recompute prefetch of a captured step) is called
+    once the out-projection's products are queued, before the attention
+    backward."""
     w_in, wq, wk, wv, wo, w_post, wg, wu, wd = w
     b, s, hdim = shape
     f = wg.shape[0]
@@ -253,6 +258,8 @@ def block_backward(acts: dict, dy: Tensor, w: tuple[Tensor, ...], m: BlockMeta, 
     do2 = Fn.mm(dh, wo)
     # on the main stream: beside the attention backward it measured slower
     dwo = Fn.mm(dh.t(), o2)
+    if prefetch is not None:
+        prefetch()
     q, k, v = _qkv_views(qkv, b, s, m)
     dqkv = torch.empty_like(qkv)
     dq, dk, dv = _qkv_views(dqkv, b, s, m)
@@ -278,9 +285,51 @@ def block_backward(acts: dict, dy: Tensor, w: tuple[Tensor, ...], m: BlockMeta, 
     )
 
 
+_PREFETCH_STREAMS: dict[int, torch.cuda.Stream] = {}
+# device index -> weak reference to the latest CheckpointedBlockFunction
+# context of the forward pass being captured
+_LAST_CHECKPOINTED: dict[int, Any] = {}
+
+
+def begin_forward_pass(device: torch.device) -> None:
+    """Called by the model at the start of each forward: the recompute prefetch
+    links the checkpointed blocks of one forward pass only."""
+    if device.type == "cuda":
+        _LAST_CHECKPOINTED.pop(device.index, None)
+
+
+def _prefetch_recompute(ctx: Any, device: torch.device) -> None:
+    """Queues the recompute of the checkpointed block ``ctx`` on a third
+    stream; its backward waits for the recorded event, then uses the result.
+
+    In a captured step, a block's backward starts the recompute of the
+    checkpointed block before it (in forward order) once its own
+    out-projection products are queued, so that the recompute's launches
+    overlap the attention backward, the QKV products and the norm backward of
+    the block being differentiated instead of following them (replayed config-3
+    step -2.1%, same process, bit-identical: the same kernels on the same
+    inputs; started before the block's MLP backward instead, -0.7%; launched
+    from the host, 2.1% slower, so host-launched steps recompute in place).
+    Costs one block's recompute outputs held at the peak."""
+    main = torch.cuda.current_stream(device)
+    stream = _PREFETCH_STREAMS.get(device.index)
+    if stream is None:
+        stream = _PREFETCH_STREAMS[device.index] = torch.cuda.Stream(device)
+    saved = ctx.saved_tensors
+    x, weights = saved[0], tuple(saved[1:])
+    stream.wait_stream(main)
+    with torch.cuda.stream(stream):
+        acts = block_forward(x, weights, ctx.meta, recompute=True, gate_up=False)
+        done = torch.cuda.Event()
+        done.record(stream)
+    ctx.prefetched = (acts, weights, done)
+
+
 class CheckpointedBlockFunction(torch.autograd.Function):
     """Full per-layer recompute: saves x (the block input) only; with
-    ``offload`` x waits for the backward in pinned host memory."""
+    ``offload`` x waits for the backward in pinned host memory.  In a captured
+    step the recompute of the block before runs early, on a third stream
+    (``_prefetch_recompute``)."""
 
     @staticmethod
     def forward(ctx: Any, x: Tensor, meta: BlockMeta, offload: bool, *weights: Tensor) -> Tensor:
@@ -298,23 +347,43 @@ class CheckpointedBlockFunction(torch.autograd.Function):
             ctx.save_for_backward(*weights)
         else:
             ctx.save_for_backward(x, *weights)
+        ctx.prefetched = None
+        ctx.prefetch_prev = None
+        if not offload and x.is_cuda and torch.cuda.is_current_stream_capturing():
+            ctx.prefetch_prev = _LAST_CHECKPOINTED.get(x.device.index)
+            _LAST_CHECKPOINTED[x.device.index] = weakref.ref(ctx)
         return acts["y"]
 
     @staticmethod
     def backward(ctx: Any, dy: Tensor):
-        saved = ctx.saved_tensors
-        if ctx.offloaded is not None:
-            host, device = ctx.offloaded
-            x, weights = host.to(device, non_blocking=True), saved
-            ctx.offloaded = None
-        else:
-            x, weights = saved[0], saved[1:]
+        prev = ctx.prefetch_prev() if ctx.prefetch_prev is not None else None
+        ctx.prefetch_prev = None
         with torch.no_grad():
-            # the recompute re-runs the forward's attention kernel: o and lse come
-            # out bit-identical to the forward's, so the lse needs no saving; the
-            # gate/up product is recomputed inside the MLP backward's GEMM
-            acts = block_forward(x, tuple(weights), ctx.meta, recompute=True, gate_up=False)
-            grads = block_backward(acts, dy, tuple(weights), ctx.meta, ctx.shape)
+            if ctx.prefetched is not None:
+                acts, weights, done = ctx.prefetched
+                ctx.prefetched = None
+                main = torch.cuda.current_stream(dy.device)
+                main.wait_event(done)
+                for t in acts.values():
+                    t.record_stream(main)
+            else:
+                saved = ctx.saved_tensors
+                if ctx.offloaded is not None:
+                    host, device = ctx.offloaded
+                    x, weights = host.to(device, non_blocking=True), saved
+                    ctx.offloaded = None
+                else:
+                    x, weights = saved[0], saved[1:]
+                weights = tuple(weights)
+                # the recompute re-runs the forward's attention kernel: o and lse come
+                # out bit-identical to the forward's, so the lse needs no saving; the
+                # gate/up product is recomputed inside the MLP backward's GEMM
+                acts = block_forward(x, weights, ctx.meta, recompute=True, gate_up=False)
+            prefetch = None
+            if (prev is not None and prev.prefetched is None and prev.offloaded is None
+                    and any(prev.needs_input_grad) and torch.cuda.is_current_stream_capturing()):
+                prefetch = lambda: _prefetch_recompute(prev, dy.device)  # noqa: E731
+            grads = block_backward(acts, dy, weights, ctx.meta, ctx.shape, prefetch=prefetch)
         return (grads[0], None, None, *grads[1:])
 
 

@@ -42,6 +42,7 @@ from nano_megatron_amd.block import (
     CheckpointedBlockFunction,
     EagerBlockFunction,
     SelectiveBlockFunction,
+    begin_forward_pass,
     pack_adjacent,
 )
 from nano_megatron_amd.kernels import HipKernelBackend, KernelBackend
@@ -633,6 +634,7 @@ class GPTModel(nn.Module):
             )
 
         self._pack_block_weights()
+        begin_forward_pass(hidden_states.device)
         mode = getattr(self.activation_checkpoint_config, "mode", "none")
         offload = bool(getattr(self.activation_checkpoint_config, "offload_saved_tensors", False))
         for layer in self.layers:

@@ -17,10 +17,10 @@ pytestmark = pytest.mark.gpu
 VOCAB = 1024
 
 
-def small_model(device, mode: str, offload: bool = False):
-    cfg = nm.GPTConfig(layers=2, hidden_size=256, ffn_hidden_size=688, heads=4, seq_length=128,
+def small_model(device, mode: str, offload: bool = False, layers: int = 2, block_interval: int = 1):
+    cfg = nm.GPTConfig(layers=layers, hidden_size=256, ffn_hidden_size=688, heads=4, seq_length=128,
                        vocab_size=VOCAB, norm_epsilon=1e-5, rope_theta=1e4)
-    ck = nm.ActivationCheckpointConfig(mode=mode, offload_saved_tensors=offload)
+    ck = nm.ActivationCheckpointConfig(mode=mode, offload_saved_tensors=offload, block_interval=block_interval)
     torch.manual_seed(0)
     return nm.GPTModel(cfg, activation_checkpoint_config=ck).to(device=device, dtype=torch.bfloat16).train()
 
@@ -71,6 +71,40 @@ def test_captured_step_replays_match_eager_steps(device, mode) -> None:
     for attr in ("master", "exp_avg", "exp_avg_sq"):
         assert torch.equal(getattr(opt_e, attr), getattr(opt, attr)), attr
     assert torch.equal(opt_e.last_grad_norm, opt.last_grad_norm)
+
+
+@pytest.mark.parametrize("block_interval", [1, 2])
+def test_captured_step_prefetches_recompute(device, monkeypatch, block_interval) -> None:
+    """A captured full-recompute step starts each checkpointed block's recompute
+    during the backward of the checkpointed block after it (one prefetch per
+    checkpointed block but the last in forward order, none in an eager step),
+    and its replays still give the eager steps' parameters bit for bit, with
+    checkpointed and eager blocks alternating (block_interval 2) too."""
+    from nano_megatron_amd import block as B
+
+    calls = []
+    orig = B._prefetch_recompute
+    monkeypatch.setattr(B, "_prefetch_recompute", lambda ctx, dev: (calls.append(1), orig(ctx, dev)))
+    layers = 4
+    checkpointed = len(range(0, layers, block_interval))
+    data = batches(device, 3)
+    eager = small_model(device, "full", layers=layers, block_interval=block_interval)
+    opt_e = optimizer(eager)
+    for x, y in data:
+        opt_e.zero_grad()
+        eager(x, labels=y).loss.backward()
+        opt_e.step()
+    assert not calls
+
+    model = small_model(device, "full", layers=layers, block_interval=block_interval)
+    opt = optimizer(model)
+    cap = CapturedTrainStep(model, opt, data[0][0], data[0][1])
+    assert len(calls) == checkpointed - 1
+    for x, y in data:
+        cap.step(x, y)
+    torch.cuda.synchronize()
+    for (name, p), q in zip(eager.named_parameters(), model.parameters()):
+        assert torch.equal(p, q), name
 
 
 def test_captured_step_rejects_out_of_range_labels(device) -> None:
