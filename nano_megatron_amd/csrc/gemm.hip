@@ -577,15 +577,59 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int L,
     // (D = bf16(alpha * acc + beta * C), one rounding)
     if (g.beta != 0.f) {
       constexpr int LPR = TBN / 8, RPI = 64 / LPR, ROWS_PER_WAVE = PR / NW;
+      constexpr int IT = ROWS_PER_WAVE / RPI;
       static_assert(ROWS_PER_WAVE % RPI == 0, "whole store instructions per wave");
       const int sl = lane % LPR;
+      if constexpr (PR == TBM) {
+        // One pass (the whole tile): every C row of the wave is loaded while
+        // the products are staged and every row computed before the first
+        // store (loads and stores share one counter and complete out of
+        // order, so a wait after a store would also wait for it).  Lanes past
+        // the matrix load element (m0, n0), which exists, and store nothing.
+        bf16x8 cv[IT];
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+          const int lr = wave * ROWS_PER_WAVE + it * RPI + lane / LPR;
+          const int m = m0 + lr, n = n0 + 8 * sl;
+          const bool ok = m < g.M && n < g.N;
+          cv[it] = *reinterpret_cast<const bf16x8*>(g.c + static_cast<int64_t>(ok ? m : m0) * g.ldc +
+                                                    (ok ? n : n0));
+        }
+        __syncthreads();  // every wave is done with the operand stages
+        stage_f32(0);
+        __syncthreads();
+        bf16x8 ov[IT];
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+          const int lr = wave * ROWS_PER_WAVE + it * RPI + lane / LPR;
+          const f32x4 lo = *reinterpret_cast<const f32x4*>(slot_at(lr, 2 * sl));
+          const f32x4 hi = *reinterpret_cast<const f32x4*>(slot_at(lr, 2 * sl + 1));
+          float v[8];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[e] = g.alpha * lo[e];
+            v[4 + e] = g.alpha * hi[e];
+          }
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ov[it][e] = static_cast<bf16>(v[e] + g.beta * static_cast<float>(cv[it][e]));
+        }
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+          const int lr = wave * ROWS_PER_WAVE + it * RPI + lane / LPR;
+          const int m = m0 + lr, n = n0 + 8 * sl;
+          if (m < g.M && n < g.N) *reinterpret_cast<bf16x8*>(g.d + static_cast<int64_t>(m) * g.ldd + n) = ov[it];
+        }
+        return;
+      }
+      // several passes (the later passes' accumulators are still held: no
+      // registers for a pass of C rows)
 #pragma unroll
       for (int p0 = 0; p0 < TBM; p0 += PR) {
         __syncthreads();  // the operand stages (first pass) or the last pass's rows are free
         stage_f32(p0);
         __syncthreads();
 #pragma unroll
-        for (int it = 0; it < ROWS_PER_WAVE / RPI; ++it) {
+        for (int it = 0; it < IT; ++it) {
           const int lr = wave * ROWS_PER_WAVE + it * RPI + lane / LPR;
           const int m = m0 + p0 + lr, n = n0 + 8 * sl;
           if (m >= g.M || n >= g.N) continue;
