@@ -675,20 +675,39 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int L,
     // product and after the sum.  Column pairs (d, d + RD/2) of a head are
     // tiles j and j + RD/32 of the same lane.
     constexpr int HALF = RD / 2;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int r = wm + 16 * i + l16;
-      const int m = m0 + r;
-      if (m >= g.M) continue;
+    constexpr int JP = HALF / 16;  // first-half column tiles of a head
+    // The cos/sin values of row tile i + 1 are loaded before row tile i is
+    // rotated, so the table loads of consecutive row tiles overlap instead of
+    // each row tile waiting for its own.  A lane reads 4 consecutive values
+    // per first-half column tile (16-byte loads; the host checks the tables'
+    // alignment); rows past the matrix read a valid row and are not stored.
+    f32x4 tc[2][JP], ts[2][JP];
+    bool tbad[2];
+    auto load_tab = [&](int i, int b) {
+      const int m = min(m0 + wm + 16 * i + l16, g.M - 1);
       const int sq = m % g.rope_seq;
       int pos = g.rope_pos != nullptr
                     ? g.rope_pos[static_cast<int64_t>(m / g.rope_seq) * g.rope_pos_bstride + sq]
                     : g.rope_offset + sq;
       // an out-of-table position is a caller error: read a valid row and poison the result
-      const bool bad = pos < 0 || pos >= g.rope_n_pos;
-      if (bad) pos = 0;
-      const float* crow = g.rope_cos + static_cast<int64_t>(pos) * HALF;
-      const float* srow = g.rope_sin + static_cast<int64_t>(pos) * HALF;
+      tbad[b] = pos < 0 || pos >= g.rope_n_pos;
+      if (tbad[b]) pos = 0;
+      const float* crow = g.rope_cos + static_cast<int64_t>(pos) * HALF + 4 * q4;
+      const float* srow = g.rope_sin + static_cast<int64_t>(pos) * HALF + 4 * q4;
+#pragma unroll
+      for (int h = 0; h < JP; ++h) {
+        tc[b][h] = *reinterpret_cast<const f32x4*>(crow + 16 * h);
+        ts[b][h] = *reinterpret_cast<const f32x4*>(srow + 16 * h);
+      }
+    };
+    load_tab(0, 0);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int b = i & 1;
+      if (i + 1 < TM) load_tab(i + 1, b ^ 1);
+      const int r = wm + 16 * i + l16;
+      const int m = m0 + r;
+      if (m >= g.M) continue;
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int c = wn + 16 * j + 4 * q4;
@@ -696,18 +715,17 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int L,
         if ((16 * j) % RD >= HALF) {
           if (n0 + wn + 16 * j < g.rope_cols) continue;  // written with its first-half partner
         } else if (n0 + wn + 16 * j < g.rope_cols) {
-          constexpr int JP = HALF / 16;
-          const int d = (16 * j) % RD + 4 * q4;
+          const int h = ((16 * j) % RD) / 16;
           bf16x4 o1, o2;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float x1 = round_as<bf16>(acc[i][j][e]);
             const float x2 = round_as<bf16>(acc[i][(j + JP) % TN][e]);
-            const float cs = round_as<bf16>(crow[d + e]);
-            const float sn = round_as<bf16>(srow[d + e]);
+            const float cs = round_as<bf16>(tc[b][h][e]);
+            const float sn = round_as<bf16>(ts[b][h][e]);
             float r1 = round_as<bf16>(add_rn(round_as<bf16>(mul_rn(x1, cs)), round_as<bf16>(mul_rn(-x2, sn))));
             float r2 = round_as<bf16>(add_rn(round_as<bf16>(mul_rn(x2, cs)), round_as<bf16>(mul_rn(x1, sn))));
-            if (bad) r1 = r2 = __builtin_nanf("");
+            if (tbad[b]) r1 = r2 = __builtin_nanf("");
             o1[e] = static_cast<bf16>(r1);
             o2[e] = static_cast<bf16>(r2);
           }
@@ -1373,6 +1391,9 @@ extern "C" int nmb_gemm_bf16_rope(int b_layout, int64_t m, int64_t n, int64_t k,
   if (st != NMB_OK) return st;
   NMB_REQUIRE(cos_table != nullptr && sin_table != nullptr && n_pos > 0 && n_pos < (1 << 30),
               "gemm_rope: cos/sin tables of n_pos rows needed");
+  // the epilogue reads 4 table values per 16-byte load
+  NMB_REQUIRE(nmb::aligned16(cos_table) && nmb::aligned16(sin_table),
+              "gemm_rope: cos/sin tables must be 16-byte aligned");
   NMB_REQUIRE_SUPPORTED(head_dim == 64 || head_dim == 128, "gemm_rope: head_dim %lld (64 or 128 supported)",
                         (long long)head_dim);
   NMB_REQUIRE(rope_cols >= 0 && rope_cols <= n && rope_cols % head_dim == 0,
