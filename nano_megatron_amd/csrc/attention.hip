@@ -655,36 +655,57 @@ __global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
   };
   // lane holds dQ[q0 + 16 t + l16][d = 16 dt + 4 g + e]; d and d + D/2 are dt and dt + DT/2
   auto finish = [&]() {
+    if constexpr (ROPE) {
+      // every cos/sin value (4 consecutive d per 16-byte load) is loaded and
+      // every output computed before the first store: loads and stores share
+      // one counter, so a wait after a store would also wait for it.  A query
+      // past the sequence reads a valid row and stores nothing.
+      f32x4 cw[2][DT / 2], sw[2][DT / 2];
+      bool bad[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int64_t pos = rope_pos(rg, b, min(q0 + 16 * t + l16, p.Sq - 1), &bad[t]);
+#pragma unroll
+        for (int dt = 0; dt < DT / 2; ++dt) {
+          cw[t][dt] = *reinterpret_cast<const f32x4*>(rg.cos + pos * (D / 2) + dt * 16 + g * 4);
+          sw[t][dt] = *reinterpret_cast<const f32x4*>(rg.sin + pos * (D / 2) + dt * 16 + g * 4);
+        }
+      }
+      bf16x4 w1[2][DT / 2], w2[2][DT / 2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int dt = 0; dt < DT / 2; ++dt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            bf16 r1, r2;
+            rope_back(round_as<bf16>(acc[t][dt][e] * p.scale), round_as<bf16>(acc[t][dt + DT / 2][e] * p.scale),
+                      cw[t][dt][e], sw[t][dt][e], bad[t], r1, r2);
+            w1[t][dt][e] = r1;
+            w2[t][dt][e] = r2;
+          }
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int qi = q0 + 16 * t + l16;
+        if (qi >= p.Sq) continue;
+#pragma unroll
+        for (int dt = 0; dt < DT / 2; ++dt) {
+          *reinterpret_cast<bf16x4*>(dqb + static_cast<int64_t>(qi) * p.q_ss + dt * 16 + g * 4) = w1[t][dt];
+          *reinterpret_cast<bf16x4*>(dqb + static_cast<int64_t>(qi) * p.q_ss + D / 2 + dt * 16 + g * 4) = w2[t][dt];
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int qi = q0 + 16 * t + l16;
       if (qi >= p.Sq) continue;
-      if constexpr (ROPE) {
-        bool bad;
-        const int64_t pos = rope_pos(rg, b, qi, &bad);
 #pragma unroll
-        for (int dt = 0; dt < DT / 2; ++dt) {
-          bf16x4 w1, w2;
+      for (int dt = 0; dt < DT; ++dt) {
+        bf16x4 wv;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int d = dt * 16 + g * 4 + e;
-            bf16 r1, r2;
-            rope_back(round_as<bf16>(acc[t][dt][e] * p.scale), round_as<bf16>(acc[t][dt + DT / 2][e] * p.scale),
-                      rg.cos[pos * (D / 2) + d], rg.sin[pos * (D / 2) + d], bad, r1, r2);
-            w1[e] = r1;
-            w2[e] = r2;
-          }
-          *reinterpret_cast<bf16x4*>(dqb + static_cast<int64_t>(qi) * p.q_ss + dt * 16 + g * 4) = w1;
-          *reinterpret_cast<bf16x4*>(dqb + static_cast<int64_t>(qi) * p.q_ss + D / 2 + dt * 16 + g * 4) = w2;
-        }
-      } else {
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          bf16x4 wv;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) wv[e] = static_cast<bf16>(acc[t][dt][e] * p.scale);
-          *reinterpret_cast<bf16x4*>(dqb + static_cast<int64_t>(qi) * p.q_ss + dt * 16 + g * 4) = wv;
-        }
+        for (int e = 0; e < 4; ++e) wv[e] = static_cast<bf16>(acc[t][dt][e] * p.scale);
+        *reinterpret_cast<bf16x4*>(dqb + static_cast<int64_t>(qi) * p.q_ss + dt * 16 + g * 4) = wv;
       }
     }
   };
@@ -907,6 +928,52 @@ __global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel
   };
   // lane holds dK[key = kbase + KSTR j + 4 g + e][d = 16 dt + l16]
   auto finish = [&]() {
+    if constexpr (ROPE) {
+      // d = 16 dt + l16 and d + D/2 are dt and dt + DT/2 (one K/V block: key =
+      // token index).  Every cos/sin value is loaded and every output computed
+      // before the first store (a wait after a store would also wait for it);
+      // a key past the sequence reads a valid row and stores nothing.
+      float cw[KT][4][DT / 2], sw[KT][4][DT / 2];
+      bool bad[KT][4];
+#pragma unroll
+      for (int j = 0; j < KT; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t pos = rope_pos(rg, b, min(kbase + KSTR * j + g * 4 + e, p.Sk - 1), &bad[j][e]);
+#pragma unroll
+          for (int dt = 0; dt < DT / 2; ++dt) {
+            cw[j][e][dt] = rg.cos[pos * (D / 2) + dt * 16 + l16];
+            sw[j][e][dt] = rg.sin[pos * (D / 2) + dt * 16 + l16];
+          }
+        }
+      bf16 ko[KT][4][DT], vo[KT][4][DT];
+#pragma unroll
+      for (int j = 0; j < KT; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+#pragma unroll
+          for (int dt = 0; dt < DT / 2; ++dt)
+            rope_back(round_as<bf16>(dka[j][dt][e] * p.scale), round_as<bf16>(dka[j][dt + DT / 2][e] * p.scale),
+                      cw[j][e][dt], sw[j][e][dt], bad[j][e], ko[j][e][dt], ko[j][e][dt + DT / 2]);
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) vo[j][e][dt] = static_cast<bf16>(dva[j][dt][e]);
+        }
+#pragma unroll
+      for (int j = 0; j < KT; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int key = kbase + KSTR * j + g * 4 + e;
+          if (key >= p.Sk) continue;
+          bf16* dkr = dkb + static_cast<int64_t>(key) * p.kv_ss;
+          bf16* dvr = dvb + static_cast<int64_t>(key) * p.kv_ss;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) {
+            dkr[dt * 16 + l16] = ko[j][e][dt];
+            dvr[dt * 16 + l16] = vo[j][e][dt];
+          }
+        }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < KT; ++j)
 #pragma unroll
@@ -914,20 +981,8 @@ __global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel
         const int key = kbase + KSTR * j + g * 4 + e;
         if (key >= p.Sk) continue;
         bf16* dkr = dkb + static_cast<int64_t>(key) * p.kv_ss;
-        if constexpr (ROPE) {
-          // d = 16 dt + l16 and d + D/2 are dt and dt + DT/2 (one K/V block: key = token index)
-          bool bad;
-          const int64_t pos = rope_pos(rg, b, key, &bad);
 #pragma unroll
-          for (int dt = 0; dt < DT / 2; ++dt) {
-            const int d = dt * 16 + l16;
-            rope_back(round_as<bf16>(dka[j][dt][e] * p.scale), round_as<bf16>(dka[j][dt + DT / 2][e] * p.scale),
-                      rg.cos[pos * (D / 2) + d], rg.sin[pos * (D / 2) + d], bad, dkr[d], dkr[d + D / 2]);
-          }
-        } else {
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) dkr[dt * 16 + l16] = static_cast<bf16>(dka[j][dt][e] * p.scale);
-        }
+        for (int dt = 0; dt < DT; ++dt) dkr[dt * 16 + l16] = static_cast<bf16>(dka[j][dt][e] * p.scale);
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
           dvb[static_cast<int64_t>(key) * p.kv_ss + dt * 16 + l16] = static_cast<bf16>(dva[j][dt][e]);
@@ -1838,6 +1893,9 @@ extern "C" int nmb_attn_bwd_rope(const void* q, const void* k, const void* v, co
                                  int64_t pos_offset, hipStream_t stream) {
   NMB_REQUIRE(cos_table != nullptr && sin_table != nullptr && n_pos > 0 && n_pos < (1 << 30),
               "attn_bwd_rope: cos/sin tables of n_pos rows needed");
+  // the dQ stores read 4 table values per 16-byte load
+  NMB_REQUIRE(nmb::aligned16(cos_table) && nmb::aligned16(sin_table),
+              "attn_bwd_rope: cos/sin tables must be 16-byte aligned");
   NMB_REQUIRE_SUPPORTED(head_dim == 64 || head_dim == 128, "attn_bwd_rope: head_dim %lld (64 or 128 supported)",
                         (long long)head_dim);
   if (positions == nullptr) {
