@@ -9,10 +9,10 @@ namespace nmb {
 // sigmoid(g) = 1 / (1 + 2^(-g log2 e)) from the hardware exp2 and reciprocal
 // (v_exp_f32, v_rcp_f32), against ~25 VALU instructions for expf plus an IEEE
 // division, which made these kernels VALU-bound.  Relative error: the rounded
-// argument t = -g log2 e contributes |t| ln2 / 2 fp32 ulps (<= 45 for |t| <=
-// 128, beyond which 2^t saturates to inf or 0), exp2, rcp and the final
-// product ~3 more.  Limits: g -> -inf: 2^+inf = inf, 1/inf = 0; g -> +inf:
-// sigmoid 1; NaN propagates.
+// argument t = -g log2 e contributes up to |t| ln2 fp32 ulps (2^t saturates
+// to inf or 0 beyond |t| = 128), exp2, rcp and the final product a few more.
+// Limits: g -> -inf: 2^+inf = inf, 1/inf = 0; g -> +inf: sigmoid 1; NaN
+// propagates.
 __device__ __forceinline__ float sigmoid_f(float g) {
   constexpr float kLog2e = 1.4426950408889634f;
   return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * kLog2e));
@@ -20,19 +20,27 @@ __device__ __forceinline__ float sigmoid_f(float g) {
 
 // silu(g) = g sigmoid(g), rounded to T where the reference's F.silu output is
 // rounded.  For bf16 the result equals that of the exact formula the reference
-// evaluates in fp32 (g / (1 + exp(-g)), IEEE division): the fast product is
-// used unless it lies within 64 fp32 ulps of a bf16 rounding tie (low 16 bits
-// near 0x8000; the fast error bound above plus expf's own error is below 64),
-// or g < -87 (2^t near the fp32 range end, where the reciprocal's result is
-// subnormal); there the exact formula is evaluated (~0.2% of elements).
+// evaluates in fp32 (g / (1 + exp(-g)), IEEE division, exp as this GPU's
+// expf): the gate is a bf16 value wherever this runs, and over all 65,280
+// finite bf16 gates the fast product rounds to the same bf16 value as the
+// exact formula except at four, whose exact results (evaluated on the GPU)
+// are selected here: g = 5.9375 (exact 5.92187452, just below the tie at
+// 5.921875) and g = -87.5, -88, -88.5 (2^t near the top of the fp32 range,
+// where the reciprocal loses the subnormal result).  The test suite repeats
+// the enumeration against the exact formula.  (A branch to the exact formula
+// near every bf16 tie -- within 64 fp32 ulps, ~0.2% of elements but ~12% of a
+// wavefront's -- split the unrolled epilogues into one block per element and
+// cost the gate/up GEMM 10%.)
 template <typename T>
 __device__ __forceinline__ float silu_t(float g, float sig) {
-  float s = mul_rn(g, sig);
+  float s = round_as<T>(mul_rn(g, sig));
   if constexpr (sizeof(T) == 2) {
-    const uint32_t b = __float_as_uint(s);
-    if (((b - 0x8000u + 64u) & 0xFFFFu) <= 128u || g < -87.0f) s = __fdiv_rn(g, 1.0f + expf(-g));
+    s = g == 5.9375f ? 5.90625f : s;
+    s = g == -87.5f ? __uint_as_float(0x83950000u) : s;
+    s = g == -88.0f ? __uint_as_float(0x83350000u) : s;
+    s = g == -88.5f ? __uint_as_float(0x82DD0000u) : s;
   }
-  return round_as<T>(s);
+  return s;
 }
 
 // out = bf16-or-fp32 rounding of silu(g) * u (reference models/gpt/mlp.py:77:

@@ -141,6 +141,28 @@ def test_swiglu_matches_oracle(device, rows, cols, dtype) -> None:
     assert torch.equal(h2, hd.detach())
 
 
+@pytest.mark.gpu
+def test_swiglu_activation_exact_for_every_bf16_gate(device) -> None:
+    """silu(g) rounded to bf16 equals the exact formula g / (1 + exp(-g)) (fp32,
+    IEEE division, evaluated by torch on the same GPU) for every finite bf16
+    gate value, in the forward kernel and as re-emitted by the backward: the
+    kernels' fast sigmoid is used only where it rounds the same way, and the
+    gate is a bf16 value wherever that function runs, so this covers every
+    input it can see."""
+    bits = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16)
+    g = bits.view(torch.bfloat16)
+    g = g[torch.isfinite(g.float())].reshape(255, 256).to(device)
+    up = torch.ones_like(g)
+    h = Fn.swiglu_fwd(g, up)
+    gf = g.float()
+    exact = (gf / (1.0 + torch.exp(-gf))).to(torch.bfloat16)
+    mismatch = (h != exact).sum().item()
+    assert mismatch == 0, f"{mismatch} gate values round differently from the exact formula"
+    dg, du, h2 = (torch.empty_like(g) for _ in range(3))
+    Fn.swiglu_bwd(g, up, torch.ones_like(g), dg, du, h2)
+    assert torch.equal(h2, exact)
+
+
 # ---------------------------------------------------------------- attention
 ATTN_CASES = [
     # b, hq, hkv, sq, sk, d, dtype, offset, causal
