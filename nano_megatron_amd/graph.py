@@ -68,6 +68,7 @@ class CapturedTrainStep:
         self.labels = labels.detach().clone()
         self.loss = torch.zeros((), dtype=torch.float32, device=self.device)
         Fn.TargetCheck(self.labels, self.vocab, Fn.IGNORE_INDEX).raise_if_invalid()
+        self._labels_checked = True  # the labels buffer holds checked targets
 
         # One forward and backward outside the capture, on a side stream, for the
         # device state the first call creates (packed block weights, RoPE
@@ -92,10 +93,12 @@ class CapturedTrainStep:
             self.loss.copy_(loss.detach())
 
     def step(self, input_ids: Tensor | None = None, labels: Tensor | None = None) -> Tensor:
-        """One training step on the batch (the previous one when omitted).  The
-        host waits for the target check, hence for the previous replay, before
-        it advances the optimizer and replays.  Returns the loss (a device
-        scalar, overwritten by the next replay)."""
+        """One training step on the batch (the previous one when omitted).  New
+        labels are copied in and checked before the replay (the host waits for
+        the check, hence for the previous replay, and raises the ValueError
+        before any update); labels already checked are not checked again, and
+        the replay is then queued behind the previous one without a host wait.
+        Returns the loss (a device scalar, overwritten by the next replay)."""
         if input_ids is not None:
             if input_ids.shape != self.input_ids.shape:
                 raise ValueError(f"input_ids shape {tuple(input_ids.shape)} differs from the captured "
@@ -105,8 +108,11 @@ class CapturedTrainStep:
             if labels.shape != self.labels.shape:
                 raise ValueError(f"labels shape {tuple(labels.shape)} differs from the captured "
                                  f"{tuple(self.labels.shape)}")
+            self._labels_checked = False
             self.labels.copy_(labels)
-        Fn.TargetCheck(self.labels, self.vocab, Fn.IGNORE_INDEX).raise_if_invalid()
+        if not self._labels_checked:
+            Fn.TargetCheck(self.labels, self.vocab, Fn.IGNORE_INDEX).raise_if_invalid()
+            self._labels_checked = True
         self.optimizer.advance_graph_step()
         self.graph.replay()
         return self.loss

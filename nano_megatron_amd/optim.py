@@ -121,7 +121,11 @@ class MasterAdamW:
         _lib.call("nmb_adamw_hyper_bytes", _lib.ctypes.byref(nb))
         n = len(self.params)
         self._graph = dict(
-            hyper_host=torch.empty(nb.value, dtype=torch.uint8, pin_memory=True),
+            # two host records, alternating: one may still wait for its copy to
+            # the device while the next step's scalars are written to the other
+            hyper_host=[torch.empty(nb.value, dtype=torch.uint8, pin_memory=True) for _ in range(2)],
+            hyper_copied=[None, None],
+            hyper_next=0,
             hyper_dev=torch.empty(nb.value, dtype=torch.uint8, device=self.device),
             table_host=torch.empty(n, dtype=torch.int64, pin_memory=True),
             table_dev=torch.empty(n, dtype=torch.int64, device=self.device),
@@ -130,15 +134,26 @@ class MasterAdamW:
     def advance_graph_step(self) -> None:
         """Before a replay of a captured step: the step count advances as an
         eager ``step`` would advance it, and the update's scalars for that
-        step go to the device on the current stream.  The caller has waited
-        for the previous replay (the host record is reused)."""
+        step go to the device on the current stream (stream-ordered after the
+        previous replay, whose update has read the device record by then).
+        The host records alternate; before one is rewritten the host waits for
+        the copy that last read it, two steps back, so it never waits for the
+        replay in flight."""
         if self._graph is None:
             raise ValueError("MasterAdamW.advance_graph_step: call prepare_graph() before capturing")
         self.step_count += 1
-        host = self._graph["hyper_host"]
+        i = self._graph["hyper_next"]
+        self._graph["hyper_next"] = 1 - i
+        host = self._graph["hyper_host"][i]
+        copied = self._graph["hyper_copied"][i]
+        if copied is not None:
+            copied.synchronize()
         _lib.call("nmb_adamw_hyper", self.lr, self.betas[0], self.betas[1], self.eps,
                   self.weight_decay, self.step_count, host.data_ptr())
         self._graph["hyper_dev"].copy_(host, non_blocking=True)
+        copied = torch.cuda.Event()
+        copied.record(torch.cuda.current_stream(self.device))
+        self._graph["hyper_copied"][i] = copied
 
     @torch.no_grad()
     def step(self) -> None:

@@ -73,6 +73,30 @@ def test_captured_step_replays_match_eager_steps(device, mode) -> None:
     assert torch.equal(opt_e.last_grad_norm, opt.last_grad_norm)
 
 
+def test_captured_steps_on_the_same_batch_match_eager_steps(device) -> None:
+    """Replays on the captured batch (no new labels: no check, no host wait
+    between them, the optimizer's step scalars staged through alternating host
+    records) give the eager steps' parameters and optimizer state bit for bit."""
+    (x, y), = batches(device, 1)
+    eager = small_model(device, "full")
+    opt_e = optimizer(eager)
+    for _ in range(5):
+        opt_e.zero_grad()
+        eager(x, labels=y).loss.backward()
+        opt_e.step()
+    model = small_model(device, "full")
+    opt = optimizer(model)
+    cap = CapturedTrainStep(model, opt, x, y)
+    for _ in range(5):
+        cap.step()
+    torch.cuda.synchronize()
+    assert opt.step_count == opt_e.step_count == 5
+    for (name, p), q in zip(eager.named_parameters(), model.parameters()):
+        assert torch.equal(p, q), name
+    for attr in ("master", "exp_avg", "exp_avg_sq"):
+        assert torch.equal(getattr(opt_e, attr), getattr(opt, attr)), attr
+
+
 @pytest.mark.parametrize("block_interval", [1, 2])
 def test_captured_step_prefetches_recompute(device, monkeypatch, block_interval) -> None:
     """A captured full-recompute step starts each checkpointed block's recompute
@@ -117,6 +141,10 @@ def test_captured_step_rejects_out_of_range_labels(device) -> None:
     bad[1, 5] = VOCAB
     with pytest.raises(ValueError, match="outside"):
         cap.step(x, bad)
+    # the captured labels buffer now holds the rejected targets: a step without
+    # new labels checks them again instead of replaying
+    with pytest.raises(ValueError, match="outside"):
+        cap.step()
     torch.cuda.synchronize()
     assert opt.step_count == 0
     for a, p in zip(before, model.parameters()):
