@@ -788,7 +788,9 @@ __global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
       lim[t] = need_mask ? mask_limit(p, koff, k0, p.q_offset + q0 + 16 * t + l16) : BK;
     // per 16-key slice mk: S^T and dP^T (K and V row fragments), then
     // dS = P (dP - delta) packed into the B operand of the dQ MFMAs; only one
-    // slice's scores are live at a time
+    // slice's scores are live at a time.  At D 64 a tile that every query of
+    // the wave sees in full takes the element loop without the mask selects.
+    auto slices = [&](auto masked) {
 #pragma unroll
     for (int mk = 0; mk < 4; ++mk) {
       f32x4 s[2], dp[2];
@@ -812,9 +814,16 @@ __global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           float pv = fast_exp2(fmaf(s[t][e], c, -lse2[t]));
-          pv = (mk * 16 + g * 4 + e > lim[t]) ? 0.f : pv;
+          if constexpr (decltype(masked)::value) pv = (mk * 16 + g * 4 + e > lim[t]) ? 0.f : pv;
           dsf[mk >> 1][t][4 * (mk & 1) + e] = static_cast<bf16>(pv * (dp[t][e] - dl[t]));
         }
+    }
+    };
+    if constexpr (D == 64) {
+      if (need_mask) slices(std::true_type{});
+      else slices(std::false_type{});
+    } else {
+      slices(std::true_type{});  // at D 128 a second copy of the loop would spill
     }
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
@@ -1181,16 +1190,29 @@ __global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel
           if (key >= p.Sk) f = BQ;
           qmin = f < 0 ? 0 : (f > BQ ? BQ : static_cast<int>(f));
         }
+        if (!need_mask[j] && qend == BQ) {
+          // every query of the tile sees every key of the tile: no selects
 #pragma unroll
-        for (int mq = 0; mq < 4; ++mq)
+          for (int mq = 0; mq < 4; ++mq)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int ql = mq * 16 + g * 4 + e;
-            float pv = fast_exp2(fmaf(s[mq][j][e], c, -sL[ql]));
-            pv = (ql < qmin || ql >= qend) ? 0.f : pv;
-            s[mq][j][e] = pv;
-            dp[mq][j][e] = pv * (dp[mq][j][e] - sDl[ql]);
-          }
+            for (int e = 0; e < 4; ++e) {
+              const int ql = mq * 16 + g * 4 + e;
+              const float pv = fast_exp2(fmaf(s[mq][j][e], c, -sL[ql]));
+              s[mq][j][e] = pv;
+              dp[mq][j][e] = pv * (dp[mq][j][e] - sDl[ql]);
+            }
+        } else {
+#pragma unroll
+          for (int mq = 0; mq < 4; ++mq)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int ql = mq * 16 + g * 4 + e;
+              float pv = fast_exp2(fmaf(s[mq][j][e], c, -sL[ql]));
+              pv = (ql < qmin || ql >= qend) ? 0.f : pv;
+              s[mq][j][e] = pv;
+              dp[mq][j][e] = pv * (dp[mq][j][e] - sDl[ql]);
+            }
+        }
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
