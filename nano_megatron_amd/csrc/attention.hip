@@ -1127,16 +1127,29 @@ __global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel
             pa[j] = da[j] = zero8();
             continue;
           }
+          if (!need_mask[j] && qend == BQ) {
+            // every query of the tile sees every key of the tile: no selects
 #pragma unroll
-          for (int m2 = 0; m2 < 2; ++m2)
+            for (int m2 = 0; m2 < 2; ++m2)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int ql = (2 * s2 + m2) * 16 + g * 4 + e;
-              float pv = fast_exp2(fmaf(s[m2][j][e], c, -sL[ql]));
-              pv = (ql < qmin[j] || ql >= qend) ? 0.f : pv;
-              pa[j][4 * m2 + e] = static_cast<bf16>(pv);
-              da[j][4 * m2 + e] = static_cast<bf16>(pv * (dp[m2][j][e] - sDl[ql]));
-            }
+              for (int e = 0; e < 4; ++e) {
+                const int ql = (2 * s2 + m2) * 16 + g * 4 + e;
+                const float pv = fast_exp2(fmaf(s[m2][j][e], c, -sL[ql]));
+                pa[j][4 * m2 + e] = static_cast<bf16>(pv);
+                da[j][4 * m2 + e] = static_cast<bf16>(pv * (dp[m2][j][e] - sDl[ql]));
+              }
+          } else {
+#pragma unroll
+            for (int m2 = 0; m2 < 2; ++m2)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int ql = (2 * s2 + m2) * 16 + g * 4 + e;
+                float pv = fast_exp2(fmaf(s[m2][j][e], c, -sL[ql]));
+                pv = (ql < qmin[j] || ql >= qend) ? 0.f : pv;
+                pa[j][4 * m2 + e] = static_cast<bf16>(pv);
+                da[j][4 * m2 + e] = static_cast<bf16>(pv * (dp[m2][j][e] - sDl[ql]));
+              }
+          }
         }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
