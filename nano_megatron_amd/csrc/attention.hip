@@ -788,8 +788,10 @@ __global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
       lim[t] = need_mask ? mask_limit(p, koff, k0, p.q_offset + q0 + 16 * t + l16) : BK;
     // per 16-key slice mk: S^T and dP^T (K and V row fragments), then
     // dS = P (dP - delta) packed into the B operand of the dQ MFMAs; only one
-    // slice's scores are live at a time.  At D 64 a tile that every query of
-    // the wave sees in full takes the element loop without the mask selects.
+    // slice's scores are live at a time.  A tile that every query of the wave
+    // sees in full takes the element loop without the mask selects: at D 64
+    // a second copy of the whole slice loop, at D 128 (where that copy would
+    // spill) a branch per slice around the element loop.
     auto slices = [&](auto masked) {
 #pragma unroll
     for (int mk = 0; mk < 4; ++mk) {
@@ -809,21 +811,29 @@ __global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(
           dp[t] = mfma16(av, df[t][ks], dp[t]);
         }
       }
+      auto elems = [&](auto sel) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float pv = fast_exp2(fmaf(s[t][e], c, -lse2[t]));
-          if constexpr (decltype(masked)::value) pv = (mk * 16 + g * 4 + e > lim[t]) ? 0.f : pv;
-          dsf[mk >> 1][t][4 * (mk & 1) + e] = static_cast<bf16>(pv * (dp[t][e] - dl[t]));
-        }
+          for (int e = 0; e < 4; ++e) {
+            float pv = fast_exp2(fmaf(s[t][e], c, -lse2[t]));
+            if constexpr (decltype(sel)::value) pv = (mk * 16 + g * 4 + e > lim[t]) ? 0.f : pv;
+            dsf[mk >> 1][t][4 * (mk & 1) + e] = static_cast<bf16>(pv * (dp[t][e] - dl[t]));
+          }
+      };
+      if constexpr (decltype(masked)::value && D == 128) {
+        if (need_mask) elems(std::true_type{});
+        else elems(std::false_type{});
+      } else {
+        elems(masked);
+      }
     }
     };
     if constexpr (D == 64) {
       if (need_mask) slices(std::true_type{});
       else slices(std::false_type{});
     } else {
-      slices(std::true_type{});  // at D 128 a second copy of the loop would spill
+      slices(std::true_type{});
     }
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
