@@ -1007,17 +1007,16 @@ __global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel
           dvb[static_cast<int64_t>(key) * p.kv_ss + dt * 16 + l16] = static_cast<bf16>(dva[j][dt][e]);
       }
   };
-  // stream iteration it: query head hk * group + i / per_head, query tile
-  // qt_begin + i % per_head of its sub-item (i = it, or it - n_iter0)
-  auto locate = [&](int it, int& h, int& q0) {
-    const bool second = it >= n_iter0;
-    const int i = second ? it - n_iter0 : it;
-    const int qtb = second ? qtb1 : qtb0;
-    const int per_head = n_qt - qtb;
-    h = hk * group + i / per_head;
-    q0 = (qtb + i % per_head) * BQ;
+  // Stream tile i is query tile qt of query head hk * group + ih: the first
+  // sub-item's tiles qtb0 .. n_qt - 1 of each head of the group in turn, then
+  // from stream tile n_iter0 on the second's from qtb1.  The loads and the
+  // compute each walk it one tile per step (no division per iteration).
+  const int qt_first = n_iter0 > 0 ? qtb0 : qtb1;
+  auto step_qt = [&](int next, int& qt) {  // qt of stream tile next, from that of next - 1
+    const bool wrap = next == n_iter0 || qt + 1 == n_qt;
+    qt = wrap ? (next < n_iter0 ? qtb0 : qtb1) : qt + 1;
+    return wrap;
   };
-
   // Q / dO tiles and their row statistics stream through LDS (kStages deep),
   // across the two sub-items.  Past the last iteration the loads read zeros.
   TileStream<D, NW> lq, ldo;
@@ -1025,10 +1024,11 @@ __global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel
   ldo.init(p.o_ss, wave, lane);
   const uint32_t q_bytes = static_cast<uint32_t>(((p.Sq - 1) * p.q_ss + D) * 2);
   const uint32_t o_bytes = static_cast<uint32_t>(((p.Sq - 1) * p.o_ss + D) * 2);
+  int l_ih = 0, l_qt = qt_first;  // the next tile to load
   auto issue = [&](int it, int stage) {
     if (it < total) {
-      int h, q0;
-      locate(it, h, q0);
+      const int h = hk * group + l_ih, q0 = l_qt * BQ;
+      if (step_qt(it + 1, l_qt)) l_ih = it + 1 == n_iter0 ? 0 : l_ih + 1;
       lq.issue(make_rsrc(q + b * p.q_sb + h * p.q_sh, q_bytes), sQ[stage], q0, p.Sq,
                static_cast<uint32_t>(q0) * static_cast<uint32_t>(p.q_ss * 2), wave);
       ldo.issue(make_rsrc(dout + b * p.o_sb + h * p.o_sh, o_bytes), sD[stage], q0, p.Sq,
@@ -1051,6 +1051,7 @@ __global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel
 #pragma unroll
   for (int st = 0; st < kStages - 1; ++st) issue(st, st);
   bool switched = false;
+  int c_qt = qt_first;  // the tile computed
   for (int it = 0; it < total; ++it) {
     if (it == n_iter0 && n_sub == 2) {
       // first iteration of the second key tile: store the first one's dK/dV
@@ -1069,8 +1070,8 @@ __global__ __launch_bounds__(64 * NW, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel
     const bf16* td = sD[it % kStages];
     const float* sL = sStat[it % kStages][0];
     const float* sDl = sStat[it % kStages][1];
-    int h_unused, q0;
-    locate(it, h_unused, q0);
+    const int q0 = c_qt * BQ;
+    step_qt(it + 1, c_qt);
     const int64_t qa_last = p.q_offset + min(q0 + BQ - 1, p.Sq - 1);
     bool live[KT], need_mask[KT];
     bool any = false;
