@@ -225,6 +225,33 @@ def test_attention_matches_oracle(device, b, hq, hkv, sq, sk, d, dtype, offset, 
     close(vd.grad, vr.grad, dtype, scale_atol=True, msg="dv")
 
 
+@pytest.mark.parametrize("hq,hkv,sq,sk,d", [(4, 2, 64, 320, 64), (4, 1, 100, 400, 128)])
+def test_attention_keys_past_every_query(device, hq, hkv, sq, sk, d) -> None:
+    """Causal attention at offset 0 with more keys than queries: keys past the
+    last query position are seen by no query, so whole 128-key tiles have an
+    empty query-tile stream in the dK/dV kernel (alone or as the second key
+    tile of a work item).  Their dK and dV are exactly zero, and everything
+    matches the oracle within the bf16 bars."""
+    g = gen(3)
+    q = torch.randn(1, hq, sq, d, generator=g).bfloat16()
+    k = torch.randn(1, hkv, sk, d, generator=g).bfloat16()
+    v = torch.randn(1, hkv, sk, d, generator=g).bfloat16()
+    do = torch.randn(1, hq, sq, d, generator=g).bfloat16()
+    qr, kr, vr = (t.clone().requires_grad_(True) for t in (q, k, v))
+    o_ref = R.local_attention(qr, kr, vr, causal=True, sequence_offset=0)
+    o_ref.backward(do)
+    qd, kd, vd = (t.to(device).requires_grad_(True) for t in (q, k, v))
+    o = nm.attention(qd, kd, vd, causal=True, sequence_offset=0)
+    o.backward(do.to(device))
+    close(o, o_ref, torch.bfloat16)
+    close(qd.grad, qr.grad, torch.bfloat16, scale_atol=True, msg="dq")
+    close(kd.grad, kr.grad, torch.bfloat16, scale_atol=True, msg="dk")
+    close(vd.grad, vr.grad, torch.bfloat16, scale_atol=True, msg="dv")
+    assert torch.count_nonzero(kd.grad[:, :, sq:].cpu()) == 0
+    assert torch.count_nonzero(vd.grad[:, :, sq:].cpu()) == 0
+    assert torch.count_nonzero(kd.grad[:, :, :sq].cpu()) > 0
+
+
 MASK_CASES = [
     # (dtype, causal, offset, kind, hq, hkv, sq, sk, d)
     (torch.bfloat16, True, 0, "bool", 4, 2, 64, 64, 64),
