@@ -184,20 +184,20 @@ __device__ __forceinline__ float lse_to_log2(float v) {
 // (buffer_load ... lds: no register round trip), kStages deep, so kStages - 1
 // tiles are in flight while one is computed.  A tile keeps the row-major
 // layout with its 16-byte chunks swizzled: chunk c of row r in slot
-// c ^ swz(r).  The swizzle serves both fragment kinds without bank conflicts:
+// c ^ swz(r).  The swizzle serves both fragment kinds without bank conflicts
+// (SQ_LDS_BANK_CONFLICT reads zero for each kind alone on gfx950):
 //  * row fragments (an MFMA operand holding 8 consecutive columns of a row per
 //    lane; 16 rows per lane group): one ds_read_b128;
 //  * column fragments (8 rows of one column per lane: rows r0 + 4g .. +3 and
 //    r0 + 16 + 4g .. +3 of a 32-row chunk, the key/query order in which the
 //    score accumulators hold P and dS): two ds_read_b64_tr_b16.
+// (2 ((r >> 1) & 3) + ((r >> 3) & 1) at D 64 and 2 (r & 7) + ((r >> 3) & 1) at
+// D 128 keep the column reads conflict-free but give every row read a two-way
+// conflict; r & 15 at D 128 the reverse.)
 template <int D>
 struct Tile64 {
   static constexpr int kElems = 64 * D;
-  // rows of a 16-lane group take 16 distinct (row parity, slot) pairs; the 8
-  // rows of a half-wave column read take 8 distinct (row parity, slot pair)s
-  __device__ static int swz(int r) {
-    return D == 64 ? 2 * ((r >> 1) & 3) + ((r >> 3) & 1) : 2 * (r & 7) + ((r >> 3) & 1);
-  }
+  __device__ static int swz(int r) { return D == 64 ? (r & 7) : 2 * (r & 7); }
   __device__ static int at(int r, int col) { return r * D + 8 * ((col >> 3) ^ swz(r)) + (col & 7); }
   // row r, columns col .. col + 7 (col a multiple of 8)
   __device__ static bf16x8 row8(const bf16* t, int r, int col) { return ld8(t + at(r, col)); }
